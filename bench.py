@@ -1,0 +1,269 @@
+"""Sparse-MLA decode benchmark on one MI355X.
+
+Workload: the 32K-context decode step, B=8 sequences, H=64 heads, latent rows 576 (512 + 64 rope)
+in bf16.  Raw latent cache [8, 32768, 576] (window rows), block-4 mean-pooled compressed cache
+[8, 8192, 576], fp8-e4m3 indexer keys [8, 8192, 64] with per-row pow2 scales, top-k 2048 plus the
+128-row window at position 32767.
+
+One step = indexer score -> exact top-k (+ window ids) -> split-K MFMA attention + LSE merge,
+for all 8 sequences; metric value = tokens/s = B * K / (time of K steps).  Inputs are resident in
+HBM; R copies of the caches (> 512 MB of distinct rows touched per rotation) are rotated so the
+256 MB MALL cannot serve the gather.  The K steps are replayed from HIP graphs.
+
+Also reported:
+* roofline of the dominant kernel (the MFMA attention kernel): algorithmic bytes per launch /
+  its average duration measured with HIP events recorded around that kernel alone;
+* cpu_baseline: the CPU oracle running the same step on a bounded sample.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+PKG = os.path.join(ROOT, "deepseek-v4-flash-mlx_amd")
+sys.path.insert(0, PKG)
+
+METRIC = "sparse-MLA decode tok/s/GPU @32K ctx top-k 2048; HBM GB/s; prefill MFMA util"
+HBM_PEAK_GBS = 8000.0
+
+
+def algorithmic_attention_bytes(B, H, T, D=576, DV=512, row_bytes=1152):
+    """Rows gathered + q read + output written + index list read, per launch."""
+    return B * T * row_bytes + B * H * D * 2 + B * H * DV * 2 + B * T * 4
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=96)
+    ap.add_argument("--warmup", type=int, default=24)
+    ap.add_argument("--rot", type=int, default=24, help="cache copies rotated across steps")
+    ap.add_argument("--kernel-iters", type=int, default=96)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-steps", type=int, default=3)
+    return ap.parse_args()
+
+
+def cpu_baseline(w, nthreads, reps):
+    """Time the oracle on one full decode step (all 8 sequences): C indexer chain + C top-k +
+    torch sparse attention, median of `reps` after one warm-up."""
+    import numpy as np
+    import torch
+    sys.path.insert(0, ROOT)
+    from oracle import indexer as oidx
+    from oracle import sparse_attn as osa
+    from oracle import compressor as ocomp
+    os.environ["OMP_NUM_THREADS"] = str(nthreads)
+    torch.set_num_threads(nthreads)
+    B, k, win = w["q"].shape[0], w["k"], w["window"]
+    n_raw = w["raw"].shape[1]
+    comp = ocomp.mean_pool(w["raw"], 4).to(torch.bfloat16)
+    keys = w["k_codes"].view(torch.float8_e4m3fn).float().numpy()
+    ks = w["kscale"].numpy()
+    qi = w["q_idx"].float().numpy()
+    wt = w["w"].numpy()
+    raw_f = [w["raw"][b, n_raw - win:].float() for b in range(B)]
+    comp_f = [comp[b].float() for b in range(B)]
+    qf = w["q"].float()
+
+    def one_step():
+        for b in range(B):
+            sc = oidx.indexer_score(qi[b], keys[b], ks[b], wt[b])
+            sel = oidx.topk(sc, k)[0]
+            kv = torch.cat([raw_f[b], comp_f[b][torch.from_numpy(sel).long()]])
+            ids = torch.arange(kv.shape[0], dtype=torch.int32)[None]
+            osa.sparse_attn(qf[b], kv, None, ids, w["scale"], dv=512)
+
+    one_step()
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        one_step()
+        times.append(time.perf_counter() - t0)
+    med = float(np.median(times))
+    return med
+
+
+def main():
+    args = parse()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world > 1:
+        print(json.dumps({"error": "this build measures one GPU; --gpus must be 1 "
+                                   "(the multi-GPU sharding is described in DESIGN.md, not run)"}))
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+    import smla
+    from smla import _lib
+    from smla import compressor as scomp
+    from smla import indexer as sidx
+    from smla import sparse_attn as ssa
+    from smla import workloads as wl
+
+    smla.load()
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    print("[bench] generating decode_32k inputs", file=sys.stderr, flush=True)
+    w = wl.decode_32k()
+    B, k, win = w["q"].shape[0], w["k"], w["window"]
+    H = w["q"].shape[2]
+    n_raw = w["raw"].shape[1]
+    T = win + k
+
+    raw0 = w["raw"].to(dev)
+    comp0 = scomp.block_mean_pool(raw0, 4)
+    keys0 = w["k_codes"].to(dev)
+    ks0 = w["kscale"].to(dev)
+    copies = [(raw0, comp0, keys0, ks0)]
+    for _ in range(args.rot - 1):
+        copies.append(tuple(t.clone() for t in copies[0]))
+    q = w["q"].to(dev)
+    qi = w["q_idx"].to(dev)
+    wt = w["w"].to(dev)
+    pos = torch.full((B,), w["pos"], dtype=torch.int32, device=dev)
+    print(f"[bench] {args.rot} cache copies resident ({args.rot * sum(t.numel() * t.element_size() for t in copies[0]) / 2**30:.1f} GiB)",
+          file=sys.stderr, flush=True)
+
+    def step(r):
+        raw, comp, keys, ks = copies[r]
+        sc = sidx.indexer_score(qi, keys, ks, wt)
+        idx = sidx.select_decode_indices(sc[:, 0], k, pos, win, n_raw)
+        return ssa.sparse_attn_two_source(q, raw, comp, None, idx[:, None, :], w["scale"], dv=512)
+
+    ref_out = step(0)
+    torch.cuda.synchronize()
+
+    # ---- capture R consecutive steps (one per cache copy) into a graph
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for r in range(args.rot):
+            step(r)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    graphs = {}
+
+    def graph_for(nsteps):
+        if nsteps not in graphs:
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                outs = [step(r) for r in range(nsteps)]
+            graphs[nsteps] = (g, outs)
+        return graphs[nsteps]
+
+    def run_steps(n):
+        full, tail = divmod(n, args.rot)
+        for _ in range(full):
+            graph_for(args.rot)[0].replay()
+        if tail:
+            graph_for(tail)[0].replay()
+
+    g_full, outs = graph_for(args.rot)
+    # every replay must reproduce the eager result (copies hold identical data)
+    for rep in range(2):
+        g_full.replay()
+        torch.cuda.synchronize()
+        for o in outs:
+            if not torch.equal(o, ref_out):
+                raise SystemExit("graph replay differs from the eager step")
+    print("[bench] graph replays match the eager step", file=sys.stderr, flush=True)
+
+    run_steps(args.warmup)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record()
+    run_steps(args.steps)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1)
+    ms_per_step = ms / args.steps
+    tok_s = B * args.steps / (ms / 1000.0)
+    print(f"[bench] {args.steps} steps in {ms:.3f} ms", file=sys.stderr, flush=True)
+
+    # ---- dominant kernel: MFMA attention, events around the kernel alone (eager, rotated copies)
+    lib = _lib.lib()
+    ns, rps = _lib.ctypes.c_int(0), _lib.ctypes.c_int(0)
+    lib.smla_attn_plan(B, 1, H, 576, 512, T, _lib.BF16, _lib.BF16, _lib.ctypes.byref(ns), _lib.ctypes.byref(rps))
+    idx_all = []
+    for r in range(args.rot):
+        raw, comp, keys, ks = copies[r]
+        sc = sidx.indexer_score(qi, keys, ks, wt)
+        idx_all.append(sidx.select_decode_indices(sc[:, 0], k, pos, win, n_raw))
+    torch.cuda.synchronize()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(args.kernel_iters)]
+    for a, b in evs:     # materialise the underlying hipEvents
+        a.record()
+        b.record()
+    torch.cuda.synchronize()
+    full_ev = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+    for i in range(8):
+        r = i % args.rot
+        ssa.sparse_attn_two_source(q, copies[r][0], copies[r][1], None, idx_all[r][:, None, :], w["scale"], dv=512)
+    torch.cuda.synchronize()
+    for i, (a, b) in enumerate(evs):
+        r = i % args.rot
+        lib.smla_profile_set_attn_events(a.cuda_event, b.cuda_event)
+        ssa.sparse_attn_two_source(q, copies[r][0], copies[r][1], None, idx_all[r][:, None, :], w["scale"], dv=512)
+    lib.smla_profile_set_attn_events(None, None)
+    torch.cuda.synchronize()
+    k_ms = [a.elapsed_time(b) for a, b in evs]
+    k_us = 1000.0 * float(np.mean(k_ms))
+    # main + merge, per op (eager)
+    full_ev[0].record()
+    for i in range(args.kernel_iters):
+        r = i % args.rot
+        ssa.sparse_attn_two_source(q, copies[r][0], copies[r][1], None, idx_all[r][:, None, :], w["scale"], dv=512)
+    full_ev[1].record()
+    torch.cuda.synchronize()
+    attn_op_us = 1000.0 * full_ev[0].elapsed_time(full_ev[1]) / args.kernel_iters
+
+    alg_bytes = algorithmic_attention_bytes(B, H, T)
+    achieved = alg_bytes / (k_us * 1e-6) / 1e9
+    roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                "kernel": "attn_mfma_kernel<576,512,bf16>", "kernel_us": round(k_us, 3),
+                "algorithmic_bytes": alg_bytes, "nsplit": ns.value, "rows_per_split": rps.value}
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        ncores = len(os.sched_getaffinity(0))
+        ncores = min(ncores, 16)
+        print(f"[bench] cpu baseline on {ncores} threads", file=sys.stderr, flush=True)
+        med = cpu_baseline(w, ncores, args.cpu_steps)
+        cpu = {"value": round(B / med, 2), "unit": "tok/s", "cores": ncores, "kind": "port",
+               "sample": f"one full decode step (8 sequences: indexer chain + top-k + attention), "
+                         f"median of {args.cpu_steps} after 1 warm-up; {med * 1e3:.1f} ms/step"}
+
+    line = {
+        "metric": METRIC,
+        "value": round(tok_s, 1),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic: seeded N(0,1)*0.05 q/latent rows (bf16), fp8 indexer keys, seed 1",
+        "config": {"workload": "decode_32k: B=8 H=64 rows 576 bf16, raw [8,32768,576], mean-pooled "
+                               "[8,8192,576], fp8 keys [8,8192,64], top-k 2048 + window 128",
+                   "global_batch": B, "seq_len": 32768, "parallelism": "single GPU"},
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "attention_op_us": round(attn_op_us, 3),
+        "rotated_copies": args.rot,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,338 @@
+// KV compressor kernels.
+//
+//  * block_mean_kernel : out[b,g,:] = (x[rg] + ... + x[rg+r-1]) * (1/r), fp32 in row order.
+//                        HBM bound: reads N*D*es, writes N/r*D*es'.  16-byte vector lanes.
+//  * gated_pool_kernel : ref_torch/compressor.py:41-49 from the projections — overlapped
+//                        per-channel softmax over 2r slots (slots 0..r-1: previous group's first
+//                        half channels, r..2r-1: own group's second half, ref_torch/compressor.py:
+//                        12-18; group 0 has no previous slots), weighted sum, RMSNorm, RoPE of the
+//                        last rd channels at position g*r, optional fp8 round trip of the first
+//                        d-rd channels (v4mlx/compressor.py:60-62).  One workgroup per output row.
+//  * ring_step_kernel  : oracle/decode_engine.py:96-105 — write the token into ring slot
+//                        r + pos%r, and on a group boundary pool the ring into one row (same
+//                        epilogue, RoPE position pos+1-r), append it to the compressed cache and
+//                        shift the ring.  One workgroup per sequence; no host synchronisation.
+//  * quant_kernel      : act_quant_sim's stored form (v4mlx/compressor.py:11-20): per 64-block pow2
+//                        scale and e4m3 codes, one wave per block-row.
+#include "smla_internal.h"
+
+namespace {
+
+constexpr int kPoolThreads = 256;
+
+template <int XDT, int ODT>
+__global__ void block_mean_kernel(const void* __restrict__ x, int64_t B, int64_t N, int64_t D, int ratio,
+                                  void* __restrict__ out) {
+  // one thread per 8 output elements
+  const int64_t G = N / ratio;
+  const int64_t per_row = D / 8;
+  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= B * G * per_row) return;
+  int64_t c = i % per_row;
+  int64_t bg = i / per_row;
+  int64_t b = bg / G, g = bg % G;
+  float acc[8];
+  const float inv = 1.0f / (float)ratio;
+  for (int j = 0; j < ratio; j++) {
+    int64_t row = b * N + g * ratio + j;
+    float v[8];
+    if constexpr (XDT == SMLA_BF16) {
+      u32x4_t w = *(const u32x4_t*)((const uint16_t*)x + row * D + c * 8);
+#pragma unroll
+      for (int k = 0; k < 4; k++) {
+        v[2 * k] = bf16_bits_to_f32((uint16_t)(w[k] & 0xffffu));
+        v[2 * k + 1] = bf16_bits_to_f32((uint16_t)(w[k] >> 16));
+      }
+    } else {
+      const f32x4_t* p = (const f32x4_t*)((const float*)x + row * D + c * 8);
+      f32x4_t a = p[0], bq = p[1];
+#pragma unroll
+      for (int k = 0; k < 4; k++) {
+        v[k] = a[k];
+        v[4 + k] = bq[k];
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < 8; k++) acc[k] = (j == 0) ? v[k] : acc[k] + v[k];
+  }
+  int64_t orow = b * G + g;
+  if constexpr (ODT == SMLA_BF16) {
+    u32x4_t w;
+#pragma unroll
+    for (int k = 0; k < 4; k++) w[k] = pack_bf16x2(acc[2 * k] * inv, acc[2 * k + 1] * inv);
+    *(u32x4_t*)((uint16_t*)out + orow * D + c * 8) = w;
+  } else {
+    f32x4_t a, bq;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      a[k] = acc[k] * inv;
+      bq[k] = acc[4 + k] * inv;
+    }
+    f32x4_t* p = (f32x4_t*)((float*)out + orow * D + c * 8);
+    p[0] = a;
+    p[1] = bq;
+  }
+}
+
+__device__ inline float block_sum(float v, float* red) {
+  v = wave_sum(v);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (lane == 0) red[wave] = v;
+  __syncthreads();
+  float s = 0.f;
+  for (int w = 0; w < (int)(blockDim.x >> 6); w++) s += red[w];
+  __syncthreads();
+  return s;
+}
+
+// Epilogue shared by the prefill pool and the ring step: RMSNorm(norm_w), RoPE of the last rd
+// channels at position `pos`, optional fp8 round trip of channels [0, d-rd).  Thread t owns
+// channels 2t and 2t+1 (d == 2*blockDim.x).  `v0,v1` are the pooled values; the result is written
+// to dst[2t], dst[2t+1].
+__device__ inline void pool_epilogue(float v0, float v1, int d, int rd, float eps, int fp8_sim,
+                                     const float* __restrict__ norm_w, const float* __restrict__ cos_t,
+                                     const float* __restrict__ sin_t, int64_t pos, float* red, float* dst) {
+  const int t = threadIdx.x;
+  const int c0 = 2 * t;
+  float ss = block_sum(v0 * v0 + v1 * v1, red);
+  float inv = rsqrtf(ss / (float)d + eps);
+  float y0 = norm_w[c0] * (v0 * inv);
+  float y1 = norm_w[c0 + 1] * (v1 * inv);
+  const int nope = d - rd;
+  if (c0 >= nope) {
+    int pi = (c0 - nope) >> 1;
+    float cs = cos_t[pos * (rd / 2) + pi], sn = sin_t[pos * (rd / 2) + pi];
+    float r0 = y0 * cs - y1 * sn;
+    float r1 = y0 * sn + y1 * cs;
+    y0 = r0;
+    y1 = r1;
+  } else if (fp8_sim) {
+    // 64-channel blocks = 32 consecutive threads (half a wave)
+    float a = fmaxf(fabsf(y0), fabsf(y1));
+#pragma unroll
+    for (int o = 16; o >= 1; o >>= 1) a = fmaxf(a, __shfl_xor(a, o, 64));
+    a = fmaxf(a, 1e-4f);
+    float s = pow2_ceil(a / 448.0f);
+    float z0 = fminf(fmaxf(y0 / s, -448.f), 448.f);
+    float z1 = fminf(fmaxf(y1 / s, -448.f), 448.f);
+    y0 = e4m3_to_f32(f32_to_e4m3(z0)) * s;
+    y1 = e4m3_to_f32(f32_to_e4m3(z1)) * s;
+  }
+  dst[c0] = y0;
+  dst[c0 + 1] = y1;
+}
+
+// slot-weighted pooling for one channel over `ns` (value, score) pairs held in registers
+template <int MAXS>
+__device__ inline float softmax_pool(const float* v, const float* s, int ns) {
+  float m = -SMLA_INF;
+  for (int j = 0; j < ns; j++) m = fmaxf(m, s[j]);
+  float den = 0.f, num = 0.f;
+  for (int j = 0; j < ns; j++) {
+    float e = __expf(s[j] - m);
+    den += e;
+    num = fmaf(v[j], e, num);
+  }
+  return num / den;
+}
+
+constexpr int kMaxRatio = 8;
+
+__global__ __launch_bounds__(kPoolThreads) void gated_pool_kernel(
+    const float* __restrict__ kv, const float* __restrict__ score, const float* __restrict__ ape,
+    const float* __restrict__ norm_w, const float* __restrict__ cos_t, const float* __restrict__ sin_t, int64_t N,
+    int d, int ratio, int rd, float eps, int fp8_sim, float* __restrict__ out) {
+  __shared__ float red[kPoolThreads / 64];
+  const int64_t G = N / ratio;
+  const int64_t bg = blockIdx.x;
+  const int64_t b = bg / G, g = bg % G;
+  const int t = threadIdx.x;
+  const int64_t two_d = 2 * (int64_t)d;
+  float pooled[2];
+  for (int k = 0; k < 2; k++) {
+    const int c = 2 * t + k;
+    float v[2 * kMaxRatio], s[2 * kMaxRatio];
+    int ns = 0;
+    if (g > 0) {
+      for (int j = 0; j < ratio; j++) {
+        int64_t row = b * N + (g - 1) * ratio + j;
+        v[ns] = kv[row * two_d + c];
+        s[ns] = score[row * two_d + c] + ape[j * two_d + c];
+        ns++;
+      }
+    }
+    for (int j = 0; j < ratio; j++) {
+      int64_t row = b * N + g * ratio + j;
+      v[ns] = kv[row * two_d + d + c];
+      s[ns] = score[row * two_d + d + c] + ape[j * two_d + d + c];
+      ns++;
+    }
+    pooled[k] = softmax_pool<2 * kMaxRatio>(v, s, ns);
+  }
+  pool_epilogue(pooled[0], pooled[1], d, rd, eps, fp8_sim, norm_w, cos_t, sin_t, g * ratio, red,
+                out + bg * (int64_t)d);
+}
+
+__global__ __launch_bounds__(kPoolThreads) void ring_step_kernel(
+    float* __restrict__ ring_kv, float* __restrict__ ring_sc, const float* __restrict__ kv_p,
+    const float* __restrict__ score_p, const int32_t* __restrict__ pos_arr, const float* __restrict__ ape,
+    const float* __restrict__ norm_w, const float* __restrict__ cos_t, const float* __restrict__ sin_t,
+    int64_t n_pos, int d, int ratio, int rd, float eps, int fp8_sim, float* __restrict__ comp, int64_t comp_cap) {
+  __shared__ float red[kPoolThreads / 64];
+  const int64_t b = blockIdx.x;
+  const int t = threadIdx.x;
+  const int64_t two_d = 2 * (int64_t)d;
+  const int64_t pos = pos_arr[b];
+  if (pos < 0 || pos + 1 - ratio >= n_pos) return;  // block-uniform guard
+  float* rk = ring_kv + b * (2 * ratio) * two_d;
+  float* rs = ring_sc + b * (2 * ratio) * two_d;
+  const int slot = ratio + (int)(pos % ratio);
+  // thread t owns channels {2t, 2t+1} and {d+2t, d+2t+1} of every slot
+  for (int k = 0; k < 2; k++) {
+    const int c = 2 * t + k;
+    for (int h = 0; h < 2; h++) {
+      int64_t cc = c + h * (int64_t)d;
+      rk[slot * two_d + cc] = kv_p[b * two_d + cc];
+      rs[slot * two_d + cc] = score_p[b * two_d + cc] + ape[(pos % ratio) * two_d + cc];
+    }
+  }
+  if ((pos + 1) % ratio != 0) return;  // block-uniform
+  float pooled[2];
+  for (int k = 0; k < 2; k++) {
+    const int c = 2 * t + k;
+    float v[2 * kMaxRatio], s[2 * kMaxRatio];
+    for (int j = 0; j < ratio; j++) {
+      v[j] = rk[j * two_d + c];
+      s[j] = rs[j * two_d + c];
+      v[ratio + j] = rk[(ratio + j) * two_d + d + c];
+      s[ratio + j] = rs[(ratio + j) * two_d + d + c];
+    }
+    pooled[k] = softmax_pool<2 * kMaxRatio>(v, s, 2 * ratio);
+  }
+  const int64_t grp = (pos + 1) / ratio - 1;
+  __shared__ float rowbuf[2 * kPoolThreads];
+  pool_epilogue(pooled[0], pooled[1], d, rd, eps, fp8_sim, norm_w, cos_t, sin_t, pos + 1 - ratio, red, rowbuf);
+  if (grp < comp_cap) {
+    float* dst = comp + (b * comp_cap + grp) * (int64_t)d;
+    dst[2 * t] = rowbuf[2 * t];
+    dst[2 * t + 1] = rowbuf[2 * t + 1];
+  }
+  // shift: slots r..2r-1 -> 0..r-1 (own channels only)
+  for (int k = 0; k < 2; k++) {
+    const int c = 2 * t + k;
+    for (int h = 0; h < 2; h++) {
+      int64_t cc = c + h * (int64_t)d;
+      for (int j = 0; j < ratio; j++) {
+        rk[j * two_d + cc] = rk[(ratio + j) * two_d + cc];
+        rs[j * two_d + cc] = rs[(ratio + j) * two_d + cc];
+      }
+    }
+  }
+}
+
+// one thread per 64-element block
+__global__ void quant_kernel(const void* __restrict__ x, int x_dtype, int64_t nblocks, uint8_t* __restrict__ codes,
+                             float* __restrict__ scales) {
+  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= nblocks) return;
+  float v[64];
+  float a = 0.f;
+#pragma unroll
+  for (int j = 0; j < 64; j++) {
+    v[j] = load_as_f32(x, i * 64 + j, x_dtype);
+    a = fmaxf(a, fabsf(v[j]));
+  }
+  a = fmaxf(a, 1e-4f);
+  float s = pow2_ceil(a / 448.0f);
+  scales[i] = s;
+  u32x4_t* dst = (u32x4_t*)(codes + i * 64);
+#pragma unroll
+  for (int q = 0; q < 4; q++) {
+    u32x4_t w;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      uint32_t word = 0;
+#pragma unroll
+      for (int by = 0; by < 4; by++) {
+        float z = fminf(fmaxf(v[16 * q + 4 * k + by] / s, -448.f), 448.f);
+        word |= f32_to_e4m3(z) << (8 * by);
+      }
+      w[k] = word;
+    }
+    dst[q] = w;
+  }
+}
+
+}  // namespace
+
+extern "C" int smla_block_mean_pool(const void* x, int x_dtype, int64_t B, int64_t N, int64_t D, int64_t ratio,
+                                    void* out, int out_dtype, void* stream) {
+  if (!x || !out) return SMLA_E_NULL;
+  if (B <= 0 || N <= 0 || D <= 0 || ratio <= 0 || N < ratio) return SMLA_E_SHAPE;
+  if (D % 8 != 0 || ratio > 64) return SMLA_E_UNSUPPORTED;
+  if ((x_dtype != SMLA_F32 && x_dtype != SMLA_BF16) || (out_dtype != SMLA_F32 && out_dtype != SMLA_BF16))
+    return SMLA_E_DTYPE;
+  int64_t total = B * (N / ratio) * (D / 8);
+  dim3 grid((unsigned)((total + 255) / 256)), blk(256);
+  hipStream_t st = (hipStream_t)stream;
+  if (x_dtype == SMLA_BF16 && out_dtype == SMLA_BF16)
+    hipLaunchKernelGGL((block_mean_kernel<SMLA_BF16, SMLA_BF16>), grid, blk, 0, st, x, B, N, D, (int)ratio, out);
+  else if (x_dtype == SMLA_BF16)
+    hipLaunchKernelGGL((block_mean_kernel<SMLA_BF16, SMLA_F32>), grid, blk, 0, st, x, B, N, D, (int)ratio, out);
+  else if (out_dtype == SMLA_BF16)
+    hipLaunchKernelGGL((block_mean_kernel<SMLA_F32, SMLA_BF16>), grid, blk, 0, st, x, B, N, D, (int)ratio, out);
+  else
+    hipLaunchKernelGGL((block_mean_kernel<SMLA_F32, SMLA_F32>), grid, blk, 0, st, x, B, N, D, (int)ratio, out);
+  SMLA_HIP_CHECK_LAUNCH();
+  return SMLA_OK;
+}
+
+static int check_pool_dims(int64_t d, int64_t ratio, int64_t rd) {
+  if (d <= 0 || ratio <= 0 || rd <= 0 || rd > d || rd % 2 != 0) return SMLA_E_SHAPE;
+  if (d != 2 * kPoolThreads || ratio > kMaxRatio || (d - rd) % 64 != 0) return SMLA_E_UNSUPPORTED;
+  return SMLA_OK;
+}
+
+extern "C" int smla_gated_pool(const float* kv, const float* score, const float* ape, const float* norm_w,
+                               const float* cos_t, const float* sin_t, int64_t B, int64_t N, int64_t d, int64_t ratio,
+                               int64_t rd, float eps, int fp8_sim, float* out, void* stream) {
+  if (!kv || !score || !ape || !norm_w || !cos_t || !sin_t || !out) return SMLA_E_NULL;
+  if (B <= 0 || N <= 0) return SMLA_E_SHAPE;
+  int rc = check_pool_dims(d, ratio, rd);
+  if (rc) return rc;
+  if (N % ratio != 0) return SMLA_E_SHAPE;
+  int64_t rows = B * (N / ratio);
+  if (rows <= 0) return SMLA_OK;
+  hipLaunchKernelGGL(gated_pool_kernel, dim3((unsigned)rows), dim3(kPoolThreads), 0, (hipStream_t)stream, kv, score,
+                     ape, norm_w, cos_t, sin_t, N, (int)d, (int)ratio, (int)rd, eps, fp8_sim, out);
+  SMLA_HIP_CHECK_LAUNCH();
+  return SMLA_OK;
+}
+
+extern "C" int smla_ring_step(float* ring_kv, float* ring_sc, const float* kv_p, const float* score_p,
+                              const int32_t* pos, const float* ape, const float* norm_w, const float* cos_t,
+                              const float* sin_t, int64_t n_pos, int64_t B, int64_t d, int64_t ratio, int64_t rd,
+                              float eps, int fp8_sim, float* comp_cache, int64_t comp_cap, void* stream) {
+  if (!ring_kv || !ring_sc || !kv_p || !score_p || !pos || !ape || !norm_w || !cos_t || !sin_t || !comp_cache)
+    return SMLA_E_NULL;
+  if (B <= 0 || comp_cap < 0 || n_pos <= 0) return SMLA_E_SHAPE;
+  int rc = check_pool_dims(d, ratio, rd);
+  if (rc) return rc;
+  hipLaunchKernelGGL(ring_step_kernel, dim3((unsigned)B), dim3(kPoolThreads), 0, (hipStream_t)stream, ring_kv,
+                     ring_sc, kv_p, score_p, pos, ape, norm_w, cos_t, sin_t, n_pos, (int)d, (int)ratio, (int)rd,
+                     eps, fp8_sim, comp_cache, comp_cap);
+  SMLA_HIP_CHECK_LAUNCH();
+  return SMLA_OK;
+}
+
+extern "C" int smla_quant_fp8_pow2(const void* x, int x_dtype, int64_t rows, int64_t D, uint8_t* codes,
+                                   float* scales, void* stream) {
+  if (!x || !codes || !scales) return SMLA_E_NULL;
+  if (rows <= 0 || D <= 0 || D % 64 != 0) return SMLA_E_SHAPE;
+  if (x_dtype != SMLA_F32 && x_dtype != SMLA_BF16) return SMLA_E_DTYPE;
+  int64_t nb = rows * (D / 64);
+  hipLaunchKernelGGL(quant_kernel, dim3((unsigned)((nb + 127) / 128)), dim3(128), 0, (hipStream_t)stream, x, x_dtype,
+                     nb, codes, scales);
+  SMLA_HIP_CHECK_LAUNCH();
+  return SMLA_OK;
+}

@@ -1,0 +1,132 @@
+// Shared device helpers for the smla HIP kernels (gfx950 only).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/smla.h"
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+
+#define SMLA_INF __builtin_inff()
+
+// ---------------------------------------------------------------------------------------------
+// bf16 <-> fp32 (bit level; fp32 -> bf16 rounds to nearest even, NaN stays NaN)
+__host__ __device__ inline float bf16_bits_to_f32(uint16_t b) {
+  uint32_t u = (uint32_t)b << 16;
+  float f;
+  __builtin_memcpy(&f, &u, 4);
+  return f;
+}
+__host__ __device__ inline uint16_t f32_to_bf16_bits(float f) {
+  uint32_t u;
+  __builtin_memcpy(&u, &f, 4);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40);  // quiet NaN
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+// pack two fp32 into two bf16 (lo in bits 0..15)
+__device__ inline uint32_t pack_bf16x2(float lo, float hi) {
+  return (uint32_t)f32_to_bf16_bits(lo) | ((uint32_t)f32_to_bf16_bits(hi) << 16);
+}
+
+// ---------------------------------------------------------------------------------------------
+// fp8 e4m3fn (OCP): decode and round-to-nearest-even encode, integer arithmetic only.
+__host__ __device__ inline float e4m3_to_f32(uint32_t code) {
+  uint32_t s = (code >> 7) & 1u, e = (code >> 3) & 0xFu, m = code & 7u;
+  float v;
+  if (e == 0) {
+    v = (float)m * 0.001953125f;  // m * 2^-9
+  } else if (e == 15 && m == 7) {
+    v = __builtin_nanf("");
+  } else {
+    uint32_t bits = ((e + 120u) << 23) | (m << 20);  // 2^(e-7) * (1 + m/8)
+    __builtin_memcpy(&v, &bits, 4);
+  }
+  return s ? -v : v;
+}
+
+// |x| <= 448 expected (callers clip); larger magnitudes saturate to 448.
+__host__ __device__ inline uint32_t f32_to_e4m3(float x) {
+  uint32_t u;
+  __builtin_memcpy(&u, &x, 4);
+  uint32_t sign = (u >> 24) & 0x80u;
+  uint32_t mag = u & 0x7fffffffu;
+  if (mag >= 0x43e00000u) return sign | 0x7eu;  // >= 448 -> 448
+  int32_t exp = (int32_t)(mag >> 23) - 127;
+  if (exp < -10) return sign;  // < 2^-10: rounds to 0 (2^-10 itself is the 0/2^-9 midpoint)
+  uint32_t man = (mag & 0x7fffffu) | 0x800000u;  // 24-bit significand, value = man * 2^(exp-23)
+  if ((mag >> 23) == 0) return sign;              // fp32 subnormal
+  // quantum of the e4m3 grid: 2^(max(exp,-6)-3);  q = value / quantum = man * 2^(exp-23-qe)
+  int32_t qe = (exp < -6 ? -6 : exp) - 3;
+  int32_t sh = qe - (exp - 23);  // >= 20 for normals, larger for subnormal range
+  uint32_t q = man >> sh;
+  uint32_t rem = man & ((1u << sh) - 1u);
+  uint32_t half = 1u << (sh - 1);
+  if (rem > half || (rem == half && (q & 1u))) q++;
+  // q counts quanta at exponent qe: value = q * 2^qe.  Re-encode.
+  if (qe == -9) {
+    // quantum 2^-9 covers the subnormals (q < 8) and exponent field 1 (8 <= q < 16); q == 16
+    // carries into exponent field 2.  Field/mantissa bits are contiguous, so code = q works for
+    // q < 8 and code = 8 + (q - 8) = q for the rest: the code is q itself.
+    return sign | q;
+  }
+  // normal: q in [8, 16]; q == 16 carries into the next binade
+  uint32_t ef = (uint32_t)(qe + 3 + 7);
+  if (q >= 16) { q >>= 1; ef += 1; }
+  if (ef > 15 || (ef == 15 && (q - 8u) > 6u)) return sign | 0x7eu;
+  return sign | (ef << 3) | (q - 8u);
+}
+
+// exact 2^ceil(log2(v)) for finite v > 0 (normal range)
+__host__ __device__ inline float pow2_ceil(float v) {
+  uint32_t u;
+  __builtin_memcpy(&u, &v, 4);
+  uint32_t e = (u >> 23) & 0xffu;
+  if (u & 0x7fffffu) e += 1;
+  uint32_t r = e << 23;
+  float f;
+  __builtin_memcpy(&f, &r, 4);
+  return f;
+}
+
+// ---------------------------------------------------------------------------------------------
+// wave64 reductions
+__device__ inline float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+__device__ inline float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+// ---------------------------------------------------------------------------------------------
+// load one element of a given dtype as fp32
+__device__ inline float load_as_f32(const void* p, int64_t i, int dtype) {
+  switch (dtype) {
+    case SMLA_F32: return ((const float*)p)[i];
+    case SMLA_BF16: return bf16_bits_to_f32(((const uint16_t*)p)[i]);
+    case SMLA_FP8_E4M3: return e4m3_to_f32(((const uint8_t*)p)[i]);
+    case SMLA_F16: return (float)((const _Float16*)p)[i];
+  }
+  return 0.f;
+}
+__device__ inline void store_from_f32(void* p, int64_t i, int dtype, float v) {
+  if (dtype == SMLA_F32) ((float*)p)[i] = v;
+  else if (dtype == SMLA_BF16) ((uint16_t*)p)[i] = f32_to_bf16_bits(v);
+  else if (dtype == SMLA_F16) ((_Float16*)p)[i] = (_Float16)v;
+}
+
+#define SMLA_HIP_CHECK_LAUNCH()                         \
+  do {                                                  \
+    hipError_t _e = hipGetLastError();                  \
+    if (_e != hipSuccess) return (int)_e;               \
+  } while (0)

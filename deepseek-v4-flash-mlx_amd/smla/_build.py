@@ -1,0 +1,27 @@
+"""Builds libsmla.so in-tree with hipcc for gfx950."""
+import os
+import subprocess
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+CSRC = os.path.join(os.path.dirname(_HERE), "csrc")
+SOURCES = ["attn.hip", "prefill.hip", "indexer.hip", "topk.hip", "pool.hip", "capi.hip"]
+OUT = os.path.join(_HERE, "libsmla.so")
+
+FLAGS = ["-O3", "--offload-arch=gfx950", "-std=c++17", "-shared", "-fPIC",
+         # packed fp32 VALU ops are disabled for every kernel (hipcc's host pass warns that it does
+         # not know the feature; that is harmless)
+         "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
+
+
+def build(verbose=False):
+    hipcc = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+    srcs = [os.path.join(CSRC, s) for s in SOURCES if os.path.exists(os.path.join(CSRC, s))]
+    tmp = OUT + ".tmp"
+    cmd = [hipcc, *FLAGS, "-o", tmp, *srcs]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError("hipcc failed:\n" + res.stdout + res.stderr)
+    if verbose:
+        print(" ".join(cmd))
+    os.replace(tmp, OUT)
+    return OUT

@@ -1,0 +1,35 @@
+"""Indexer scoring and top-k selection over compressed positions (HIP).
+
+The reference has no indexer: its engine attends every causally visible compressed row
+(``oracle/decode_engine.py:112-114``).  ``indexer_score`` implements the build's definition
+(ReLU-gated per-head dot products, per-head weights, per-key scale, one fixed fp32 order) and
+``topk`` the exact selection (score desc, index asc, ascending output, -1 padding), which equals
+the reference's index build whenever the visible count is at most k.
+"""
+import torch
+
+from . import ops
+
+
+def indexer_score(q_idx, keys, kscale, weights, nvis=None):
+    """q_idx [B,S,Hi,Di], keys [B,N,Di] (fp32/bf16/fp8 codes), kscale [B,N] or None,
+    weights [B,S,Hi], nvis [B,S] or None -> [B,S,N] fp32."""
+    return ops.indexer_score_op(q_idx, keys, kscale, weights, nvis)
+
+
+def topk(scores, k, nvis=None, id_offset=0):
+    """scores [..., N] -> int32 [..., k]."""
+    return ops.topk_op(scores, k, nvis, id_offset)
+
+
+def select_decode_indices(scores, k, pos, window, n_raw, out=None):
+    """The decode attention index list per sequence: the raw-cache window rows pos-window+1..pos
+    (columns 0..window-1) followed by the top-k compressed rows offset by ``n_raw`` (the raw
+    cache length, so ids index the virtual [raw; compressed] buffer).
+    scores [B, N] fp32, pos [B] int32 -> out [B, window + k] int32."""
+    B = scores.shape[0]
+    if out is None:
+        out = torch.empty(B, window + k, dtype=torch.int32, device=scores.device)
+    ops.decode_window_idxs(pos, window, out=out[:, :window])
+    ops.topk_into(scores, k, out[:, window:], id_offset=n_raw)
+    return out

@@ -1,0 +1,251 @@
+"""torch.library custom ops over libsmla (GPU only; no CPU fallback inside any op).
+
+Each op validates shapes/dtypes on the host, allocates its outputs (and workspace) with torch's
+caching allocator, and launches on ``torch.cuda.current_stream()``.  Fake (meta) kernels give
+output shapes for tracing.
+"""
+from typing import Optional
+
+import torch
+
+from . import _lib
+
+_DT = {torch.float32: _lib.F32, torch.bfloat16: _lib.BF16, torch.float16: _lib.F16,
+       torch.uint8: _lib.FP8_E4M3}
+if hasattr(torch, "float8_e4m3fn"):
+    _DT[torch.float8_e4m3fn] = _lib.FP8_E4M3
+
+
+def dtype_code(t):
+    try:
+        return _DT[t.dtype]
+    except KeyError:
+        raise TypeError(f"unsupported dtype {t.dtype}") from None
+
+
+def _p(t):
+    return None if t is None else t.data_ptr()
+
+
+def _stream(t):
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _on_gpu(*ts):
+    for t in ts:
+        if t is not None and t.device.type != "cuda":
+            raise RuntimeError("smla ops run on the GPU only (got a tensor on %s)" % t.device)
+
+
+def _c(t):
+    return None if t is None else t.contiguous()
+
+
+# ----------------------------------------------------------------------------------------------
+@torch.library.custom_op("smla::sparse_attn", mutates_args=(), device_types="cuda")
+def sparse_attn_op(q: torch.Tensor, kv0: torch.Tensor, kv1: Optional[torch.Tensor],
+                   kv0_scale: Optional[torch.Tensor], kv1_scale: Optional[torch.Tensor],
+                   attn_sink: Optional[torch.Tensor], topk_idxs: torch.Tensor, scale: float,
+                   dv: int) -> torch.Tensor:
+    """q [B,S,H,D], kv0 [B,n0,D], kv1 [B,n1,D]|None, scales [B,n,D/64] (fp8 rows),
+    attn_sink [H]|None, topk_idxs [B,S,T] -> out [B,S,H,dv] in q's dtype."""
+    _on_gpu(q, kv0, kv1, kv0_scale, kv1_scale, attn_sink, topk_idxs)
+    q, kv0, kv1 = q.contiguous(), kv0.contiguous(), _c(kv1)
+    kv0_scale, kv1_scale, attn_sink = _c(kv0_scale), _c(kv1_scale), _c(attn_sink)
+    if topk_idxs.dtype != torch.int32:
+        topk_idxs = topk_idxs.to(torch.int32)
+    topk_idxs = topk_idxs.contiguous()
+    if attn_sink is not None and attn_sink.dtype != torch.float32:
+        attn_sink = attn_sink.float()
+    B, S, H, D = q.shape
+    T = topk_idxs.shape[-1]
+    n0 = kv0.shape[1]
+    n1 = 0 if kv1 is None else kv1.shape[1]
+    out = torch.empty(B, S, H, dv, dtype=q.dtype, device=q.device)
+    qd, kd, od = dtype_code(q), dtype_code(kv0), dtype_code(out)
+    wsb = _lib.lib().smla_sparse_attn_workspace(B, S, H, D, dv, T, qd, kd)
+    ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device=q.device)
+    _lib.call("smla_sparse_attn", _p(q), qd, _p(kv0), n0, _p(kv1), n1, kd, _p(kv0_scale),
+              _p(kv1_scale), _p(attn_sink), _p(topk_idxs), T, B, S, H, D, dv, float(scale),
+              _p(out), od, _p(ws), wsb, _stream(q))
+    return out
+
+
+@sparse_attn_op.register_fake
+def _(q, kv0, kv1, kv0_scale, kv1_scale, attn_sink, topk_idxs, scale, dv):
+    B, S, H, _D = q.shape
+    return q.new_empty(B, S, H, dv)
+
+
+# ----------------------------------------------------------------------------------------------
+@torch.library.custom_op("smla::indexer_score", mutates_args=(), device_types="cuda")
+def indexer_score_op(q: torch.Tensor, keys: torch.Tensor, kscale: Optional[torch.Tensor],
+                     weights: torch.Tensor, nvis: Optional[torch.Tensor]) -> torch.Tensor:
+    """q [B,S,Hi,Di] f32|bf16, keys [B,N,Di] f32|bf16|fp8, kscale [B,N]|None, weights [B,S,Hi],
+    nvis [B,S]|None -> scores [B,S,N] fp32 (-inf past nvis)."""
+    _on_gpu(q, keys, kscale, weights, nvis)
+    q, keys, kscale, weights = q.contiguous(), keys.contiguous(), _c(kscale), weights.float().contiguous()
+    if nvis is not None:
+        nvis = nvis.to(torch.int32).contiguous()
+    if kscale is not None:
+        kscale = kscale.float().contiguous()
+    B, S, Hi, Di = q.shape
+    N = keys.shape[1]
+    out = torch.empty(B, S, N, dtype=torch.float32, device=q.device)
+    _lib.call("smla_indexer_score", _p(q), dtype_code(q), _p(keys), dtype_code(keys), _p(kscale),
+              _p(weights), _p(nvis), B, S, Hi, Di, N, _p(out), _stream(q))
+    return out
+
+
+@indexer_score_op.register_fake
+def _(q, keys, kscale, weights, nvis):
+    return q.new_empty(q.shape[0], q.shape[1], keys.shape[1], dtype=torch.float32)
+
+
+# ----------------------------------------------------------------------------------------------
+@torch.library.custom_op("smla::topk", mutates_args=(), device_types="cuda")
+def topk_op(scores: torch.Tensor, k: int, nvis: Optional[torch.Tensor], id_offset: int) -> torch.Tensor:
+    """scores [..., N] fp32 -> [..., k] int32 ascending ids (+ id_offset), -1 padded."""
+    _on_gpu(scores, nvis)
+    scores = scores.float().contiguous()
+    N = scores.shape[-1]
+    R = scores.numel() // N
+    if nvis is not None:
+        nvis = nvis.to(torch.int32).contiguous()
+    out = torch.empty(*scores.shape[:-1], k, dtype=torch.int32, device=scores.device)
+    _lib.call("smla_topk", _p(scores), R, N, _p(nvis), k, _p(out), k, int(id_offset), _stream(scores))
+    return out
+
+
+@topk_op.register_fake
+def _(scores, k, nvis, id_offset):
+    return scores.new_empty(*scores.shape[:-1], k, dtype=torch.int32)
+
+
+# ----------------------------------------------------------------------------------------------
+@torch.library.custom_op("smla::block_mean_pool", mutates_args=(), device_types="cuda")
+def block_mean_pool_op(x: torch.Tensor, ratio: int) -> torch.Tensor:
+    """x [B,N,D] -> [B,N//ratio,D] in x's dtype (fp32 sum in row order, times 1/ratio)."""
+    _on_gpu(x)
+    x = x.contiguous()
+    B, N, D = x.shape
+    out = torch.empty(B, N // ratio, D, dtype=x.dtype, device=x.device)
+    _lib.call("smla_block_mean_pool", _p(x), dtype_code(x), B, N, D, ratio, _p(out), dtype_code(out),
+              _stream(x))
+    return out
+
+
+@block_mean_pool_op.register_fake
+def _(x, ratio):
+    return x.new_empty(x.shape[0], x.shape[1] // ratio, x.shape[2])
+
+
+# ----------------------------------------------------------------------------------------------
+@torch.library.custom_op("smla::gated_pool", mutates_args=(), device_types="cuda")
+def gated_pool_op(kv: torch.Tensor, score: torch.Tensor, ape: torch.Tensor, norm_w: torch.Tensor,
+                  cos_t: torch.Tensor, sin_t: torch.Tensor, ratio: int, rope_head_dim: int, eps: float,
+                  fp8_sim: bool) -> torch.Tensor:
+    """kv, score [B,N,2d] fp32 (N % ratio == 0) -> [B,N//ratio,d] fp32."""
+    _on_gpu(kv, score, ape, norm_w, cos_t, sin_t)
+    kv, score = kv.float().contiguous(), score.float().contiguous()
+    ape, norm_w = ape.float().contiguous(), norm_w.float().contiguous()
+    cos_t, sin_t = cos_t.float().contiguous(), sin_t.float().contiguous()
+    B, N, two_d = kv.shape
+    d = two_d // 2
+    if cos_t.shape[0] < N:
+        raise ValueError("rotation tables must cover every token position")
+    out = torch.empty(B, N // ratio, d, dtype=torch.float32, device=kv.device)
+    _lib.call("smla_gated_pool", _p(kv), _p(score), _p(ape), _p(norm_w), _p(cos_t), _p(sin_t), B, N, d,
+              ratio, rope_head_dim, float(eps), int(bool(fp8_sim)), _p(out), _stream(kv))
+    return out
+
+
+@gated_pool_op.register_fake
+def _(kv, score, ape, norm_w, cos_t, sin_t, ratio, rope_head_dim, eps, fp8_sim):
+    return kv.new_empty(kv.shape[0], kv.shape[1] // ratio, kv.shape[2] // 2, dtype=torch.float32)
+
+
+# ----------------------------------------------------------------------------------------------
+@torch.library.custom_op("smla::ring_step", mutates_args=("ring_kv", "ring_sc", "comp_cache"),
+                         device_types="cuda")
+def ring_step_op(ring_kv: torch.Tensor, ring_sc: torch.Tensor, kv_p: torch.Tensor, score_p: torch.Tensor,
+                 pos: torch.Tensor, ape: torch.Tensor, norm_w: torch.Tensor, cos_t: torch.Tensor,
+                 sin_t: torch.Tensor, ratio: int, rope_head_dim: int, eps: float, fp8_sim: bool,
+                 comp_cache: torch.Tensor) -> None:
+    """In-place decode ring update for B sequences; appends emitted rows to comp_cache [B,cap,d]."""
+    _on_gpu(ring_kv, ring_sc, kv_p, score_p, pos, ape, norm_w, cos_t, sin_t, comp_cache)
+    for t in (ring_kv, ring_sc, comp_cache):
+        if not t.is_contiguous() or t.dtype != torch.float32:
+            raise ValueError("ring and cache tensors must be contiguous fp32")
+    B = ring_kv.shape[0]
+    d = ring_kv.shape[-1] // 2
+    kv_p, score_p = kv_p.float().contiguous(), score_p.float().contiguous()
+    pos = pos.to(torch.int32).contiguous()
+    _lib.call("smla_ring_step", _p(ring_kv), _p(ring_sc), _p(kv_p), _p(score_p), _p(pos),
+              _p(ape.float().contiguous()), _p(norm_w.float().contiguous()), _p(cos_t.float().contiguous()),
+              _p(sin_t.float().contiguous()), cos_t.shape[0], B, d, ratio, rope_head_dim, float(eps),
+              int(bool(fp8_sim)), _p(comp_cache), comp_cache.shape[1], _stream(ring_kv))
+
+
+@ring_step_op.register_fake
+def _(ring_kv, ring_sc, kv_p, score_p, pos, ape, norm_w, cos_t, sin_t, ratio, rope_head_dim, eps, fp8_sim,
+      comp_cache):
+    return None
+
+
+# ----------------------------------------------------------------------------------------------
+@torch.library.custom_op("smla::quant_fp8_pow2", mutates_args=(), device_types="cuda")
+def quant_fp8_pow2_op(x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """x [..., D] (D % 64 == 0) -> (codes uint8 [..., D], scales fp32 [..., D/64])."""
+    _on_gpu(x)
+    x = x.contiguous()
+    D = x.shape[-1]
+    rows = x.numel() // D
+    codes = torch.empty(x.shape, dtype=torch.uint8, device=x.device)
+    scales = torch.empty(*x.shape[:-1], D // 64, dtype=torch.float32, device=x.device)
+    _lib.call("smla_quant_fp8_pow2", _p(x), dtype_code(x), rows, D, _p(codes), _p(scales), _stream(x))
+    return codes, scales
+
+
+@quant_fp8_pow2_op.register_fake
+def _(x):
+    return (x.new_empty(x.shape, dtype=torch.uint8),
+            x.new_empty(*x.shape[:-1], x.shape[-1] // 64, dtype=torch.float32))
+
+
+# ----------------------------------------------------------------------------------------------
+def window_topk_idxs(window_size, bsz, seqlen, start_pos, device="cuda"):
+    """Device-built window index matrix (int32); see sparse_attn.get_window_topk_idxs."""
+    if start_pos > 0:
+        out = torch.empty(bsz, 1, window_size, dtype=torch.int32, device=device)
+    else:
+        out = torch.empty(bsz, seqlen, min(seqlen, window_size), dtype=torch.int32, device=device)
+    _on_gpu(out)
+    _lib.call("smla_window_topk_idxs", window_size, bsz, seqlen, start_pos, _p(out), _stream(out))
+    return out
+
+
+def decode_window_idxs(pos, window, out=None):
+    """pos [R] int32 (device) -> out [R, window] int32 with pos-window+1..pos (-1 where < 0)."""
+    _on_gpu(pos)
+    pos = pos.to(torch.int32).contiguous()
+    R = pos.numel()
+    stride = window
+    if out is None:
+        out = torch.empty(R, window, dtype=torch.int32, device=pos.device)
+    else:
+        stride = out.stride(0)
+    _lib.call("smla_decode_window_idxs", _p(pos), R, window, _p(out), stride, _stream(pos))
+    return out
+
+
+def topk_into(scores, k, out, id_offset=0, nvis=None):
+    """Write the top-k selection of scores [R, N] into the int32 view out [R, >=k] (row stride
+    out.stride(0)); no allocation."""
+    _on_gpu(scores, out, nvis)
+    if out.dtype != torch.int32 or out.stride(-1) != 1:
+        raise ValueError("out must be an int32 view with unit inner stride")
+    R, N = scores.shape
+    _lib.call("smla_topk", _p(scores), R, N, _p(nvis), k, _p(out), out.stride(0), int(id_offset),
+              _stream(scores))
+    return out

@@ -1,0 +1,178 @@
+/* smla — MI355X (gfx950) sparse multi-head latent attention for DeepSeek-V4-Flash.
+ *
+ * C ABI of libsmla.so.  Every entry point takes device pointers, element counts and a HIP
+ * stream (as void*, NULL = the default stream), enqueues its kernels on that stream and returns
+ * without synchronising.  The caller owns every buffer (inputs, outputs, workspace); the library
+ * never allocates or frees caller memory.  Tensors are dense and row-major in the shapes given.
+ *
+ * Return value: SMLA_OK (0); a negative SMLA_E_* code for an argument error, detected on the
+ * host before anything is launched; or a positive hipError_t from the launch.
+ *
+ * Reference counterparts (the reference is plain Python; these replace its functions):
+ *   smla_sparse_attn          ref_torch/sparse_attn.py:23-34   sparse_attn(q, kv, attn_sink, topk_idxs, scale)
+ *                             v4mlx/sparse_attn.py:26-39       (MLX twin)
+ *   smla_window_topk_idxs     ref_torch/sparse_attn.py:9-20    get_window_topk_idxs(window_size, bsz, seqlen, start_pos)
+ *   smla_decode_window_idxs   oracle/decode_engine.py:110-111  widx = range(max(0, p-127), p+1)
+ *   smla_indexer_score        (none: the reference attends every visible compressed row,
+ *                              oracle/decode_engine.py:112-114; the indexer is the build's)
+ *   smla_topk                 oracle/decode_engine.py:112-114  cidx selection (take-all when nvis <= k)
+ *   smla_block_mean_pool      (none: block mean of the 32K decode workload)
+ *   smla_gated_pool           ref_torch/compressor.py:41-49    pooling + RMSNorm + RoPE of compressor_prefill
+ *   smla_ring_step            oracle/decode_engine.py:96-105   decode compressor ring step and cache append
+ *   smla_quant_fp8_pow2       v4mlx/compressor.py:11-20        act_quant_sim (stored form: codes + pow2 scales)
+ */
+#ifndef SMLA_H
+#define SMLA_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SMLA_API_VERSION 1
+
+/* element types */
+enum {
+  SMLA_F32 = 0,
+  SMLA_BF16 = 1,
+  SMLA_FP8_E4M3 = 2, /* OCP e4m3fn (max 448), one byte per element */
+  SMLA_F16 = 3,
+  SMLA_I32 = 4
+};
+
+/* status codes */
+enum {
+  SMLA_OK = 0,
+  SMLA_E_NULL = -1,        /* a required pointer is NULL */
+  SMLA_E_SHAPE = -2,       /* a size is non-positive or inconsistent */
+  SMLA_E_DTYPE = -3,       /* unsupported element type for this argument */
+  SMLA_E_UNSUPPORTED = -4, /* valid but unimplemented combination */
+  SMLA_E_WORKSPACE = -5,   /* workspace missing or too small */
+  SMLA_E_RANGE = -6        /* a scalar argument is out of its valid range */
+};
+
+/* Human-readable text for a status code (static storage). */
+const char* smla_strerror(int status);
+
+/* SMLA_API_VERSION of the loaded library. */
+int smla_api_version(void);
+
+/* ---------------------------------------------------------------------------------------------
+ * Sparse attention over gathered latent rows (absorbed MLA).
+ * Replaces ref_torch/sparse_attn.py:23-34 (sparse_attn) and v4mlx/sparse_attn.py:26-39.
+ *
+ *   q          [B, S, H, D]          q_dtype: F32 or BF16
+ *   kv0        [B, n0, D]            kv rows; kv_dtype: F32, BF16 or FP8_E4M3
+ *   kv1        [B, n1, D] or NULL    second row source; the index space is the virtual
+ *                                    concatenation [kv0; kv1] (the engine's [window; compressed]
+ *                                    buffer, oracle/decode_engine.py:108-109) without copying
+ *   kv0_scale, kv1_scale             FP8 only: [B, n, D/64] fp32 scale per 64-element tile
+ *                                    (row value = decode(code) * scale); NULL otherwise
+ *   attn_sink  [H] fp32 or NULL      NULL = -inf (no sink)
+ *   topk_idxs  [B, S, T] int32       row ids in [0, n0+n1); negative = masked.  Ids outside the
+ *                                    range are treated as masked (the reference raises instead).
+ *   out        [B, S, H, DV]         out_dtype: F32 or BF16; value = first DV columns of the rows
+ *   scale      softmax scale applied to q.kv
+ *
+ * out[b,s,h,:] = sum_t p_t kv[idx_t, :DV] / (sum_t p_t + exp(sink_h - m)),
+ *   p_t = exp(scale q.kv[idx_t] - m), m = max over valid t.  No valid index -> NaN.
+ * Duplicate ids count once per occurrence.
+ *
+ * workspace: smla_sparse_attn_workspace() bytes (split-K partial states), may be 0.
+ */
+int smla_sparse_attn(const void* q, int q_dtype,
+                     const void* kv0, int64_t n0, const void* kv1, int64_t n1, int kv_dtype,
+                     const float* kv0_scale, const float* kv1_scale,
+                     const float* attn_sink, const int32_t* topk_idxs, int64_t T,
+                     int64_t B, int64_t S, int64_t H, int64_t D, int64_t DV, float scale,
+                     void* out, int out_dtype, void* workspace, size_t workspace_bytes,
+                     void* stream);
+
+size_t smla_sparse_attn_workspace(int64_t B, int64_t S, int64_t H, int64_t D, int64_t DV,
+                                  int64_t T, int q_dtype, int kv_dtype);
+
+/* ---------------------------------------------------------------------------------------------
+ * Window index matrix.  Replaces ref_torch/sparse_attn.py:9-20 (get_window_topk_idxs).
+ * out: [bsz, w] int32 when start_pos > 0 (ring or partial window), [bsz, seqlen, min(seqlen, w)]
+ * when start_pos == 0 (prefill causal band, -1 above the diagonal).
+ */
+int smla_window_topk_idxs(int64_t window_size, int64_t bsz, int64_t seqlen, int64_t start_pos,
+                          int32_t* out, void* stream);
+
+/* Engine decode window: for each row r, out[r*out_stride + j] = pos[r]-window+1+j (j < window),
+ * or -1 where that is negative.  Replaces the widx list of oracle/decode_engine.py:110-111 with
+ * ids into an un-ringed raw cache.  pos: [R] int32 on the device. */
+int smla_decode_window_idxs(const int32_t* pos, int64_t R, int64_t window, int32_t* out,
+                            int64_t out_stride, void* stream);
+
+/* ---------------------------------------------------------------------------------------------
+ * Indexer score (no reference counterpart; the build's definition, fixed fp32 order):
+ *   dot_h = fma chain over d of q[b,s,h,d]*k[b,n,d];  r_h = max(dot_h, +0)
+ *   acc   = fma chain over h of w[b,s,h]*r_h;          score = acc * kscale[b,n]
+ *   score = -inf for n >= nvis[b,s].
+ *   q [B,S,Hi,Di] F32|BF16;  keys [B,N,Di] F32|BF16|FP8_E4M3;  kscale [B,N] fp32 or NULL (= 1);
+ *   weights [B,S,Hi] fp32;  nvis [B,S] int32 or NULL (= N);  scores [B,S,N] fp32.
+ */
+int smla_indexer_score(const void* q, int q_dtype, const void* keys, int k_dtype,
+                       const float* kscale, const float* weights, const int32_t* nvis,
+                       int64_t B, int64_t S, int64_t Hi, int64_t Di, int64_t N,
+                       float* scores, void* stream);
+
+/* ---------------------------------------------------------------------------------------------
+ * Top-k selection over rows of scores [R, N]: rank the first nvis[r] entries (NULL = N) by
+ * (score desc, index asc), -0 == +0; keep min(k, nvis); write them in ascending index order as
+ * out[r*out_stride + j] = id + id_offset, then -1 up to k.  Bit-exact.  Replaces the compressed
+ * index selection of oracle/decode_engine.py:112-114 (identical when nvis <= k).
+ * Scores must not be NaN.  workspace: none.
+ */
+int smla_topk(const float* scores, int64_t R, int64_t N, const int32_t* nvis, int64_t k,
+              int32_t* out, int64_t out_stride, int32_t id_offset, void* stream);
+
+/* ---------------------------------------------------------------------------------------------
+ * Compressor.
+ *
+ * smla_block_mean_pool: out[b,g,:] = (x[b,rg] + x[b,rg+1] + ... + x[b,rg+r-1]) * (1/r), fp32
+ * sum in row order, g < N/r.  x [B,N,D] F32|BF16, out [B,N/r,D] F32|BF16.
+ */
+int smla_block_mean_pool(const void* x, int x_dtype, int64_t B, int64_t N, int64_t D,
+                         int64_t ratio, void* out, int out_dtype, void* stream);
+
+/* smla_gated_pool: the pooling half of ref_torch/compressor.py:21-50 (compressor_prefill), from
+ * the projections kv = x@wkv^T and score = x@wgate^T:
+ *   kv, score [B,N,2d] fp32 (N a multiple of ratio);  ape [ratio,2d];  norm_w [d];
+ *   cos, sin [>= N, rd/2] fp32 rotation tables indexed by token position (row g uses position
+ *   g*ratio);  out [B, N/ratio, d] fp32 (or, with fp8_sim != 0, the d-rd non-rope channels
+ *   fp8 round-tripped with pow2 block-64 scales as v4mlx/compressor.py:60-62).
+ */
+int smla_gated_pool(const float* kv, const float* score, const float* ape, const float* norm_w,
+                    const float* cos_t, const float* sin_t, int64_t B, int64_t N, int64_t d,
+                    int64_t ratio, int64_t rd, float eps, int fp8_sim, float* out, void* stream);
+
+/* smla_ring_step: one decode token of the compressor ring (oracle/decode_engine.py:96-105) for
+ * B sequences at positions pos[b]:
+ *   ring_kv, ring_sc [B, 2*ratio, 2d] fp32 (updated);  kv_p, score_p [B, 2d] fp32 projections;
+ *   when (pos+1) % ratio == 0 the ring emits a row (softmax pool, RMSNorm(norm_w), RoPE with
+ *   cos/sin [n_pos, rd/2] at position pos+1-ratio, optional fp8 round trip of the non-rope
+ *   channels) written to comp_cache[b, (pos+1)/ratio - 1, :] ([B, comp_cap, d] fp32), then
+ *   shifts.  Rows that would land at or past comp_cap are not written.  A sequence whose pos is
+ *   negative or whose RoPE position is not below n_pos is left untouched. */
+int smla_ring_step(float* ring_kv, float* ring_sc, const float* kv_p, const float* score_p,
+                   const int32_t* pos, const float* ape, const float* norm_w,
+                   const float* cos_t, const float* sin_t, int64_t n_pos, int64_t B, int64_t d,
+                   int64_t ratio, int64_t rd, float eps, int fp8_sim, float* comp_cache,
+                   int64_t comp_cap, void* stream);
+
+/* smla_quant_fp8_pow2: per 64-element block, s = 2^ceil(log2(max(|x|,1e-4)/448)),
+ * code = e4m3(clip(x/s, +-448)) (round to nearest even).  x [rows, D] F32|BF16 (D % 64 == 0),
+ * codes [rows, D] uint8, scales [rows, D/64] fp32.  The stored form of act_quant_sim,
+ * v4mlx/compressor.py:11-20. */
+int smla_quant_fp8_pow2(const void* x, int x_dtype, int64_t rows, int64_t D, uint8_t* codes,
+                        float* scales, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SMLA_H */

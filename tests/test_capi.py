@@ -1,0 +1,130 @@
+"""CPU tier: the C-ABI library loads, exports every symbol the header declares, maps status codes
+and rejects bad arguments on the host before launching anything; the device fp8/bf16 codecs are
+checked on the host against the oracle.  No compute call is made without a GPU."""
+import ctypes
+import os
+import re
+import subprocess
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import ROOT
+from oracle import fp8
+
+HEADER = os.path.join(ROOT, "include", "smla.h")
+
+
+def _declared():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:int|size_t|const char\*)\s+(smla_\w+)\s*\(", text, re.M)))
+
+
+def test_library_exports_every_declared_symbol():
+    from smla import _lib
+    lib = _lib.lib()
+    names = _declared()
+    assert len(names) >= 12
+    for n in names:
+        assert hasattr(lib, n), n
+    assert set(names) == set(_lib.exported_symbols())
+    assert lib.smla_api_version() == 1
+
+
+def test_strerror_and_status_codes():
+    from smla import _lib
+    lib = _lib.lib()
+    assert lib.smla_strerror(0) == b"ok"
+    for code in range(-6, 0):
+        assert lib.smla_strerror(code) and lib.smla_strerror(code) != b"unknown smla status"
+    assert lib.smla_strerror(-99) == b"unknown smla status"
+
+
+def test_host_validation_rejects_bad_arguments():
+    from smla import _lib
+    lib = _lib.lib()
+    fake = ctypes.c_void_p(16)   # never dereferenced: validation fails first
+    # NULL inputs
+    assert lib.smla_sparse_attn(None, 1, fake, 10, None, 0, 1, None, None, None, fake, 4, 1, 1, 64, 576, 512,
+                                1.0, fake, 1, None, 0, None) == -1
+    # DV > D
+    assert lib.smla_sparse_attn(fake, 1, fake, 10, None, 0, 1, None, None, None, fake, 4, 1, 1, 64, 512, 576,
+                                1.0, fake, 1, None, 0, None) == -2
+    # second source without pointer
+    assert lib.smla_sparse_attn(fake, 1, fake, 10, None, 5, 1, None, None, None, fake, 4, 1, 1, 64, 576, 512,
+                                1.0, fake, 1, None, 0, None) == -1
+    # bad dtype
+    assert lib.smla_sparse_attn(fake, 9, fake, 10, None, 0, 1, None, None, None, fake, 4, 1, 1, 64, 576, 512,
+                                1.0, fake, 1, None, 0, None) == -3
+    # fp8 rows without scales
+    assert lib.smla_sparse_attn(fake, 1, fake, 10, None, 0, 2, None, None, None, fake, 4, 1, 1, 64, 576, 512,
+                                1.0, fake, 1, None, 0, None) == -1
+    assert lib.smla_topk(fake, 2, 100, None, 10, fake, 5, 0, None) == -2        # stride < k
+    assert lib.smla_topk(None, 2, 100, None, 10, fake, 10, 0, None) == -1
+    assert lib.smla_topk(fake, 1, 70000, None, 10, fake, 10, 0, None) == -4     # N > 65536
+    assert lib.smla_indexer_score(fake, 1, fake, 7, None, fake, None, 1, 1, 4, 64, 10, fake, None) == -3
+    assert lib.smla_indexer_score(fake, 1, fake, 2, None, fake, None, 1, 1, 4, 48, 10, fake, None) == -4
+    assert lib.smla_block_mean_pool(fake, 1, 1, 8, 12, 4, fake, 1, None) == -4   # D % 8
+    assert lib.smla_gated_pool(fake, fake, fake, fake, fake, fake, 1, 8, 512, 4, 63, 1e-6, 0, fake, None) == -2
+    assert lib.smla_gated_pool(fake, fake, fake, fake, fake, fake, 1, 8, 256, 4, 64, 1e-6, 0, fake, None) == -4
+    assert lib.smla_quant_fp8_pow2(fake, 1, 4, 100, fake, fake, None) == -2
+    assert lib.smla_window_topk_idxs(0, 1, 1, 0, fake, None) == -2
+    assert lib.smla_decode_window_idxs(fake, 2, 128, fake, 64, None) == -2
+
+
+def test_python_ops_refuse_cpu_tensors():
+    from smla import sparse_attn as ssa
+    q = torch.zeros(1, 16, 576)
+    kv = torch.zeros(8, 576)
+    idx = torch.zeros(1, 4, dtype=torch.int32)
+    with pytest.raises(Exception):
+        ssa.sparse_attn(q, kv, None, idx, 1.0)
+
+
+@pytest.fixture(scope="module")
+def codec(tmp_path_factory):
+    out = tmp_path_factory.mktemp("codec") / "libcodec.so"
+    src = os.path.join(ROOT, "tests", "native", "codec_host.hip")
+    subprocess.run(["/opt/rocm/bin/hipcc", "-O2", "-fPIC", "-shared", "--offload-arch=gfx950", "-o", str(out), src],
+                   check=True, capture_output=True)
+    lib = ctypes.CDLL(str(out))
+    lib.host_f32_to_e4m3.restype = ctypes.c_uint32
+    lib.host_f32_to_e4m3.argtypes = [ctypes.c_float]
+    lib.host_e4m3_to_f32.restype = ctypes.c_float
+    lib.host_e4m3_to_f32.argtypes = [ctypes.c_uint32]
+    lib.host_pow2_ceil.restype = ctypes.c_float
+    lib.host_pow2_ceil.argtypes = [ctypes.c_float]
+    lib.host_f32_to_bf16.restype = ctypes.c_uint16
+    lib.host_f32_to_bf16.argtypes = [ctypes.c_float]
+    return lib
+
+
+def test_device_fp8_codec_matches_oracle(codec):
+    codes = np.arange(256, dtype=np.uint8)
+    ref = fp8.e4m3_decode(codes)
+    for c in range(256):
+        v = codec.host_e4m3_to_f32(c)
+        assert (np.isnan(v) and np.isnan(ref[c])) or v == ref[c], c
+    vals = ref[np.isfinite(ref)]
+    pos = np.unique(np.abs(vals))
+    mids = ((pos[1:].astype(np.float64) + pos[:-1]) / 2).astype(np.float32)
+    rng = np.random.default_rng(3)
+    rnd = np.clip(rng.standard_normal(4000).astype(np.float32) * 50, -448, 448)
+    x = np.concatenate([vals, mids, -mids, np.nextafter(mids, 0), np.nextafter(mids, 1), rnd,
+                        np.float32([2.0 ** -10, 3 * 2.0 ** -10, 1e-30, -0.0])])
+    want = fp8.e4m3_encode(x)
+    got = np.array([codec.host_f32_to_e4m3(float(v)) for v in x], dtype=np.uint32)
+    np.testing.assert_array_equal(got, want.astype(np.uint32))
+
+
+def test_device_pow2_and_bf16_match_oracle(codec):
+    rng = np.random.default_rng(4)
+    amax = np.concatenate([np.exp2(rng.uniform(-13, 12, 500)), np.exp2(np.arange(-13, 12)) * 448.0]).astype(np.float32)
+    e = fp8.pow2_scale_exponent(amax)
+    for a, ee in zip(amax, e):
+        assert codec.host_pow2_ceil(float(np.float32(a / np.float32(448.0)))) == 2.0 ** ee
+    x = rng.standard_normal(2000).astype(np.float32)
+    ref = torch.from_numpy(x).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    got = np.array([codec.host_f32_to_bf16(float(v)) for v in x], dtype=np.uint16)
+    np.testing.assert_array_equal(got, ref)

@@ -1,0 +1,108 @@
+"""GPU parity of the indexer score (bit-exact to the canonical chain), top-k (exact sets) and the
+window index builders."""
+import numpy as np
+import pytest
+import torch
+
+from conftest import announce
+from oracle import indexer as oidx
+from oracle import sparse_attn as osa
+
+pytestmark = pytest.mark.gpu
+
+
+def _bits(a):
+    return np.ascontiguousarray(a, dtype=np.float32).view(np.uint32)
+
+
+@pytest.mark.parametrize("qdt,kdt,use_scale,Hi,Di,N", [
+    ("f32", "f32", False, 16, 64, 4096),
+    ("bf16", "fp8", True, 64, 64, 8192),
+    ("bf16", "bf16", False, 8, 128, 1000),
+    ("f32", "fp8", True, 3, 32, 333),
+    ("bf16", "f32", True, 64, 64, 257),
+])
+def test_indexer_bit_exact(dev, qdt, kdt, use_scale, Hi, Di, N):
+    from smla import indexer as sidx
+    from smla import workloads as wl
+    announce(f"indexer q={qdt} k={kdt} scale={use_scale} Hi={Hi} Di={Di} N={N}")
+    g = torch.Generator().manual_seed(N + Hi)
+    B, S = 2, 2
+    q = torch.randn(B, S, Hi, Di, generator=g)
+    if qdt == "bf16":
+        q = q.to(torch.bfloat16)
+    kf = torch.randn(B, N, Di, generator=g)
+    if kdt == "fp8":
+        keys, _ = wl.quant_e4m3_pow2(kf, block=Di)
+        kvals = keys.view(torch.float8_e4m3fn).float()
+    elif kdt == "bf16":
+        keys = kf.to(torch.bfloat16)
+        kvals = keys.float()
+    else:
+        keys = kf
+        kvals = kf
+    ks = (torch.rand(B, N, generator=g) + 0.5) if use_scale else None
+    w = torch.randn(B, S, Hi, generator=g)
+    nvis = torch.randint(0, N + 1, (B, S), generator=g, dtype=torch.int32)
+    nvis[0, 0] = N
+    out = sidx.indexer_score(q.to(dev), keys.to(dev), None if ks is None else ks.to(dev), w.to(dev), nvis.to(dev))
+    out = out.cpu().numpy()
+    for b in range(B):
+        ref = oidx.indexer_score(q[b].float().numpy(), kvals[b].numpy(), None if ks is None else ks[b].numpy(),
+                                 w[b].numpy(), nvis[b].numpy())
+        np.testing.assert_array_equal(_bits(out[b]), _bits(ref))
+
+
+@pytest.mark.parametrize("R,N,k,ties", [
+    (1, 100, 10, False), (3, 1024, 512, True), (2, 1025, 1000, True), (8, 8192, 2048, False),
+    (8, 8192, 2048, True), (1, 16384, 2048, True), (2, 65536, 2048, False), (4, 3000, 1, True),
+    (2, 50000, 7000, True)])
+def test_topk_exact(dev, R, N, k, ties):
+    from smla import indexer as sidx
+    announce(f"topk R={R} N={N} k={k} ties={ties}")
+    rng = np.random.default_rng(N + k)
+    if ties:
+        s = (rng.integers(-40, 41, (R, N)) * 0.25).astype(np.float32)
+        s[s == 0] = np.where(rng.random((s == 0).sum()) < 0.5, -0.0, 0.0).astype(np.float32)
+    else:
+        s = rng.standard_normal((R, N)).astype(np.float32)
+    nvis = rng.integers(0, N + 1, R).astype(np.int32)
+    nvis[0] = N
+    if R > 1:
+        nvis[1] = min(k, N)           # exactly k visible
+    got = sidx.topk(torch.from_numpy(s).to(dev), k, torch.from_numpy(nvis).to(dev)).cpu().numpy()
+    np.testing.assert_array_equal(got, oidx.topk(s, k, nvis))
+    got0 = sidx.topk(torch.from_numpy(s).to(dev), k, id_offset=5).cpu().numpy()
+    ref0 = oidx.topk(s, k)
+    np.testing.assert_array_equal(got0, np.where(ref0 >= 0, ref0 + 5, -1))
+
+
+def test_topk_all_equal_and_ragged(dev):
+    from smla import indexer as sidx
+    announce("topk all equal")
+    s = np.zeros((2, 5000), np.float32)
+    s[1, ::2] = -0.0
+    got = sidx.topk(torch.from_numpy(s).to(dev), 300).cpu().numpy()
+    np.testing.assert_array_equal(got, np.tile(np.arange(300, dtype=np.int32), (2, 1)))
+
+
+@pytest.mark.parametrize("w,bsz,seqlen,start_pos", [
+    (128, 2, 1, 32767), (8, 1, 1, 9), (8, 3, 1, 3), (128, 1, 1, 1), (8, 2, 5, 0), (128, 1, 300, 0)])
+def test_window_idxs(dev, w, bsz, seqlen, start_pos):
+    from smla import sparse_attn as ssa
+    announce(f"window idx w={w} start={start_pos}")
+    got = ssa.get_window_topk_idxs(w, bsz, seqlen, start_pos, device=dev).cpu()
+    ref = osa.get_window_topk_idxs(w, bsz, seqlen, start_pos)
+    assert got.shape == ref.shape
+    np.testing.assert_array_equal(got.numpy(), ref.numpy())
+
+
+def test_decode_window_idxs(dev):
+    from smla import ops
+    announce("decode window idx")
+    pos = torch.tensor([0, 5, 127, 128, 32767], dtype=torch.int32, device=dev)
+    got = ops.decode_window_idxs(pos, 128).cpu().numpy()
+    for r, p in enumerate([0, 5, 127, 128, 32767]):
+        ref = np.arange(p - 127, p + 1)
+        ref[ref < 0] = -1
+        np.testing.assert_array_equal(got[r], ref)
