@@ -209,6 +209,9 @@ def main():
     torch.cuda.synchronize()
     for i, (a, b) in enumerate(evs):
         r = i % args.rot
+        # keep the stream busy while the host enqueues the events and the kernel, so that the
+        # events bracket the kernel's execution rather than host launch latency
+        torch.cuda._sleep(100000)
         lib.smla_profile_set_attn_events(a.cuda_event, b.cuda_event)
         ssa.sparse_attn_two_source(q, copies[r][0], copies[r][1], None, idx_all[r][:, None, :], w["scale"], dv=512)
     lib.smla_profile_set_attn_events(None, None)

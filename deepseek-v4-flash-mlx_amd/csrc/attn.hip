@@ -17,21 +17,14 @@
 //    Online softmax keeps a reference max per head that moves only when a tile's max exceeds it
 //    by more than 8 (exact: numerator and denominator use the same reference).
 //  * attn_merge_kernel   — log-sum-exp merge of the split partial states.
-#include "smla_internal.h"
+#include "attn_common.h"
 
 namespace {
 
-constexpr int kTileRows = 32;
-constexpr int kThreads = 256;
-constexpr float kRescaleSlack = 8.0f;
-
-struct RowSrc {
-  const void* kv0;
-  const void* kv1;
-  const float* sc0;
-  const float* sc1;
-  int64_t n0, n1;
-};
+using smla_attn::kRescaleSlack;
+using smla_attn::kThreads;
+using smla_attn::kTileRows;
+using smla_attn::RowSrc;
 
 // pointer to row `r` (virtual concatenation [kv0; kv1]) of batch b; element size es bytes
 __device__ inline const uint8_t* row_ptr(const RowSrc& src, int64_t b, int64_t r, int64_t D, int es,
@@ -441,39 +434,84 @@ __global__ __launch_bounds__(kThreads, 1) void attn_mfma_kernel(
   }
 }
 
-// one workgroup (128 threads, 4 dv each) per (query row, head)
+// one workgroup (128 threads, 4 dv each) per (query row, head): split weights w_j = exp(m_j - M)
+// once into LDS, then every thread streams its float4 of each split's partial output with
+// independent (unrolled) loads.
+constexpr int kMaxSplits = 1024;
 __global__ __launch_bounds__(128) void attn_merge_kernel(const float* __restrict__ part, int nsplit,
                                                          int64_t BS, int H, int DV,
                                                          const float* __restrict__ sink,
-                                                         void* __restrict__ out, int out_dtype) {
+                                                         void* __restrict__ out, int out_dtype, int part_bf16) {
+  __shared__ float w_s[kMaxSplits];
+  __shared__ float red[2];
+  const int tid = threadIdx.x;
   const int64_t rh = blockIdx.x;  // bs*H + head
   const int head = (int)(rh % H);
   const float* ml = part + rh * nsplit * 2;
   const float* op = part + BS * H * nsplit * 2 + rh * nsplit * DV;
-  float M = -SMLA_INF;
-  for (int j = 0; j < nsplit; j++) M = fmaxf(M, ml[2 * j]);
+  float mx = -SMLA_INF;
+  for (int j = tid; j < nsplit; j += 128) mx = fmaxf(mx, ml[2 * j]);
+  mx = wave_max(mx);
+  if ((tid & 63) == 0) red[tid >> 6] = mx;
+  __syncthreads();
+  const float M = fmaxf(red[0], red[1]);
+  __syncthreads();
   const bool empty = !(M > -SMLA_INF);
-  float L = 0.f;
-  for (int j = 0; j < nsplit; j++) {
-    float mj = ml[2 * j];
-    if (mj > -SMLA_INF) L += ml[2 * j + 1] * __expf(mj - M);
+  float ls = 0.f;
+  for (int j = tid; j < nsplit; j += 128) {
+    const float mj = ml[2 * j];
+    const float w = (mj > -SMLA_INF) ? __expf(mj - M) : 0.f;
+    w_s[j] = w;
+    ls += w * ml[2 * j + 1];
   }
-  float snk = sink ? sink[head] : -SMLA_INF;
+  ls = wave_sum(ls);
+  if ((tid & 63) == 0) red[tid >> 6] = ls;
+  __syncthreads();
+  float L = red[0] + red[1];
+  const float snk = sink ? sink[head] : -SMLA_INF;
   if (!empty) L += __expf(snk - M);
-  float inv = 1.0f / L;
-  for (int dv0 = threadIdx.x * 4; dv0 < DV; dv0 += blockDim.x * 4) {
+  const float inv = 1.0f / L;
+  // partial O records are bf16 when the output is bf16 (written so by the bf16 decode kernel)
+  const bool obf = part_bf16 != 0;
+  const uint16_t* opb = (const uint16_t*)(part + BS * H * nsplit * 2) + rh * nsplit * DV;
+  for (int dv0 = tid * 4; dv0 < DV; dv0 += 128 * 4) {
     f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
-    for (int j = 0; j < nsplit; j++) {
-      float mj = ml[2 * j];
-      if (!(mj > -SMLA_INF)) continue;
-      float w = __expf(mj - M);
-      f32x4_t v = *(const f32x4_t*)(op + (int64_t)j * DV + dv0);
-      acc += v * w;
+    int j = 0;
+    if (obf) {
+      for (; j + 8 <= nsplit; j += 8) {
+        u32x2_t v[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) v[u] = *(const u32x2_t*)(opb + (int64_t)(j + u) * DV + dv0);
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+          const f32x4_t f = {bf16_bits_to_f32((uint16_t)(v[u][0] & 0xffffu)), bf16_bits_to_f32((uint16_t)(v[u][0] >> 16)),
+                             bf16_bits_to_f32((uint16_t)(v[u][1] & 0xffffu)), bf16_bits_to_f32((uint16_t)(v[u][1] >> 16))};
+          acc += f * w_s[j + u];
+        }
+      }
+      for (; j < nsplit; j++) {
+        const u32x2_t v = *(const u32x2_t*)(opb + (int64_t)j * DV + dv0);
+        const f32x4_t f = {bf16_bits_to_f32((uint16_t)(v[0] & 0xffffu)), bf16_bits_to_f32((uint16_t)(v[0] >> 16)),
+                           bf16_bits_to_f32((uint16_t)(v[1] & 0xffffu)), bf16_bits_to_f32((uint16_t)(v[1] >> 16))};
+        acc += f * w_s[j];
+      }
     }
-    for (int r = 0; r < 4; r++) {
-      float v = empty ? __builtin_nanf("") : acc[r] * inv;
-      if (out_dtype == SMLA_BF16) ((uint16_t*)out)[rh * DV + dv0 + r] = f32_to_bf16_bits(v);
-      else ((float*)out)[rh * DV + dv0 + r] = v;
+    for (; j + 8 <= nsplit; j += 8) {
+      f32x4_t v[8];
+#pragma unroll
+      for (int u = 0; u < 8; u++) v[u] = *(const f32x4_t*)(op + (int64_t)(j + u) * DV + dv0);
+#pragma unroll
+      for (int u = 0; u < 8; u++) acc += v[u] * w_s[j + u];
+    }
+    for (; j < nsplit; j++) acc += *(const f32x4_t*)(op + (int64_t)j * DV + dv0) * w_s[j];
+    const int64_t o = rh * DV + dv0;
+    if (out_dtype == SMLA_BF16) {
+      uint32_t w0 = empty ? 0x7fc07fc0u : pack_bf16x2(acc[0] * inv, acc[1] * inv);
+      uint32_t w1 = empty ? 0x7fc07fc0u : pack_bf16x2(acc[2] * inv, acc[3] * inv);
+      *(u32x2_t*)((uint16_t*)out + o) = u32x2_t{w0, w1};
+    } else {
+      const float nan = __builtin_nanf("");
+      *(f32x4_t*)((float*)out + o) = empty ? f32x4_t{nan, nan, nan, nan} : acc * inv;
     }
   }
 }
@@ -512,16 +550,35 @@ Plan make_plan(int64_t B, int64_t S, int64_t H, int64_t D, int64_t DV, int64_t T
   // tiles per split so that rows * nsplit ~ target workgroups
   int64_t per = (tiles * rows + target - 1) / target;
   if (per < 1) per = 1;
+  if ((tiles + per - 1) / per > kMaxSplits) per = (tiles + kMaxSplits - 1) / kMaxSplits;
   if (per > tiles) per = tiles;
+  if (per > smla_attn::kDecodeMaxRowsPerSplit / kTileRows) per = smla_attn::kDecodeMaxRowsPerSplit / kTileRows;
   p.rows_per_split = (int)(per * kTileRows);
   p.nsplit = (int)((tiles + per - 1) / per);
+  if (p.nsplit > kMaxSplits) p.mfma = false;  // beyond the merge kernel's capacity: generic kernel
   return p;
+}
+
+int launch_merge(const Plan& p, int64_t B, int64_t S, int64_t H, const float* sink, void* out, int out_dtype,
+                 void* ws, hipStream_t stream, int part_bf16) {
+  if (p.nsplit > 1) {
+    hipLaunchKernelGGL(attn_merge_kernel, dim3((unsigned)(B * S * H)), dim3(128), 0, stream,
+                       (const float*)ws, p.nsplit, B * S, (int)H, 512, sink, out, out_dtype, part_bf16);
+    SMLA_HIP_CHECK_LAUNCH();
+  }
+  return SMLA_OK;
 }
 
 template <int D, bool FP8>
 int launch_mfma(const Plan& p, const void* q, RowSrc src, const float* sink, const int32_t* idx,
                 int64_t T, int64_t B, int64_t S, int64_t H, float scale, void* out, int out_dtype,
                 void* ws, hipStream_t stream) {
+  if constexpr (!FP8) {
+    int rc = smla_attn::launch_decode_bf16(D, p.nsplit, p.rows_per_split, q, src, sink, idx, T, B, S, H, scale, out,
+                                           out_dtype, (float*)ws, stream, g_ev_before, g_ev_after);
+    if (rc != SMLA_OK) return rc;
+    return launch_merge(p, B, S, H, sink, out, out_dtype, ws, stream, out_dtype == SMLA_BF16);
+  }
   using C = MfmaCfg<D, 512>;
   auto kern = attn_mfma_kernel<D, 512, FP8>;
   static bool attr_set = false;
@@ -536,12 +593,7 @@ int launch_mfma(const Plan& p, const void* q, RowSrc src, const float* sink, con
                      idx, (int)T, (int)S, (int)H, p.rows_per_split, scale, (float*)ws, out, out_dtype);
   SMLA_HIP_CHECK_LAUNCH();
   if (g_ev_after) (void)hipEventRecord(g_ev_after, stream);
-  if (p.nsplit > 1) {
-    hipLaunchKernelGGL(attn_merge_kernel, dim3((unsigned)(B * S * H)), dim3(128), 0, stream,
-                       (const float*)ws, p.nsplit, B * S, (int)H, 512, sink, out, out_dtype);
-    SMLA_HIP_CHECK_LAUNCH();
-  }
-  return SMLA_OK;
+  return launch_merge(p, B, S, H, sink, out, out_dtype, ws, stream, 0);
 }
 
 }  // namespace

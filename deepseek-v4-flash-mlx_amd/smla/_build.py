@@ -4,7 +4,7 @@ import subprocess
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(os.path.dirname(_HERE), "csrc")
-SOURCES = ["attn.hip", "prefill.hip", "indexer.hip", "topk.hip", "pool.hip", "capi.hip"]
+SOURCES = ["attn.hip", "attn_bf16.hip", "prefill.hip", "indexer.hip", "topk.hip", "pool.hip", "capi.hip"]
 OUT = os.path.join(_HERE, "libsmla.so")
 
 FLAGS = ["-O3", "--offload-arch=gfx950", "-std=c++17", "-shared", "-fPIC",
