@@ -7,42 +7,46 @@
 //   score = acc * kscale[n]   (or acc when kscale == NULL);  -inf for n >= nvis
 //
 // The order is fixed so that every score is reproducible bit for bit by the CPU oracle; the top-k
-// that follows can then be compared exactly.  One thread per key: the key row lives in VGPRs as
-// fp32, q (fp32, [Hi][Di]) and w sit in LDS and are read as wave-wide broadcasts.  HBM traffic
-// per (query row): N * (Di * sizeof(key) + 4) bytes of keys and scales, N * 4 bytes of scores.
+// that follows can then be compared exactly.  A workgroup scores 64 keys (one per lane, key row in
+// VGPRs as fp32); its waves split the heads 16 at a time (q and w staged in LDS as fp32, read as
+// wave-wide broadcasts) and wave 0 runs each key's chain over the heads.  HBM traffic per query
+// row: N * (Di * sizeof(key) + 4) bytes of keys and scales, N * 4 bytes of scores.
+// The fp32 FMA work (N * Hi * Di per query row) is the bound: VALU, fixed order, no MFMA.
 #include "smla_internal.h"
 
 namespace {
 
-constexpr int kThreads = 256;
 constexpr int kMaxDi = 128;
 constexpr int kMaxQ = 64 * 128;  // Hi * Di fp32 in LDS (32 KiB)
+constexpr int kKeys = 64;        // keys per workgroup (one per lane)
+constexpr int kHG = 16;          // heads per wave
 
+// One workgroup = 64 keys x all heads.  Wave w computes r_h = ReLU(dot_h) for heads
+// 16w .. 16w+15 (lane = key, key row in VGPRs, q rows read from LDS as wave-wide broadcasts);
+// the r_h go through LDS and wave 0 runs the per-key chain over h = 0..Hi-1.  Each dot product is
+// the same sequential fma chain over d as the oracle's, so scores are bit-identical.
 template <int DI, int KDT>
-__global__ __launch_bounds__(kThreads) void indexer_kernel(const void* __restrict__ q, int q_dtype,
-                                                           const void* __restrict__ keys,
-                                                           const float* __restrict__ kscale,
-                                                           const float* __restrict__ weights,
-                                                           const int32_t* __restrict__ nvis, int64_t S,
-                                                           int Hi, int64_t N, float* __restrict__ scores) {
+__global__ __launch_bounds__(256) void indexer_kernel(const void* __restrict__ q, int q_dtype,
+                                                      const void* __restrict__ keys,
+                                                      const float* __restrict__ kscale,
+                                                      const float* __restrict__ weights,
+                                                      const int32_t* __restrict__ nvis, int64_t S, int Hi,
+                                                      int64_t N, float* __restrict__ scores) {
   __shared__ __align__(16) float sq[kMaxQ];
   __shared__ float sw[256];
+  __shared__ float sr[kKeys][65];  // r[key][head] (padded: lanes read different keys)
   const int64_t bs = blockIdx.y;
   const int64_t b = bs / S;
-  const int tid = threadIdx.x;
-  for (int i = tid; i < Hi * DI; i += kThreads) sq[i] = load_as_f32(q, bs * Hi * DI + i, q_dtype);
-  for (int i = tid; i < Hi; i += kThreads) sw[i] = weights[bs * Hi + i];
-  __syncthreads();
-  const int64_t n = (int64_t)blockIdx.x * kThreads + tid;
-  if (n >= N) return;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int nwaves = blockDim.x >> 6;
+  const int64_t n = (int64_t)blockIdx.x * kKeys + lane;
   const int64_t nv = nvis ? (int64_t)nvis[bs] : N;
-  float* out = scores + bs * N + n;
-  if (n >= nv) {
-    *out = -SMLA_INF;
-    return;
-  }
+  const bool live = n < N && n < nv;
+  const int64_t nrow = n < N ? n : N - 1;
+
+  // key row -> VGPRs (issued first so its latency overlaps the q staging)
   float kr[DI];
-  const int64_t row = b * N + n;
+  const int64_t row = b * N + nrow;
   if constexpr (KDT == SMLA_FP8_E4M3) {
     const u32x4_t* kp = (const u32x4_t*)((const uint8_t*)keys + row * DI);
 #pragma unroll
@@ -80,40 +84,88 @@ __global__ __launch_bounds__(kThreads) void indexer_kernel(const void* __restric
       kr[4 * v + 3] = w[3];
     }
   }
+  for (int i = tid; i < Hi * DI; i += blockDim.x) sq[i] = load_as_f32(q, bs * Hi * DI + i, q_dtype);
+  for (int i = tid; i < Hi; i += blockDim.x) sw[i] = weights[bs * Hi + i];
+  __syncthreads();
+
+  // r_h for this wave's heads
+  for (int h0 = wave * kHG; h0 < Hi; h0 += nwaves * kHG) {
+    const int hn = min(kHG, Hi - h0);
+    for (int hh = 0; hh < hn; hh++) {
+      const int h = h0 + hh;
+      const f32x4_t* qh = (const f32x4_t*)(sq + h * DI);
+      float dot = 0.f;
+#pragma unroll
+      for (int v = 0; v < DI / 4; v++) {
+        const f32x4_t qq = qh[v];
+        dot = __builtin_fmaf(qq[0], kr[4 * v], dot);
+        dot = __builtin_fmaf(qq[1], kr[4 * v + 1], dot);
+        dot = __builtin_fmaf(qq[2], kr[4 * v + 2], dot);
+        dot = __builtin_fmaf(qq[3], kr[4 * v + 3], dot);
+      }
+      sr[lane][h] = dot > 0.f ? dot : 0.f;
+    }
+  }
+  __syncthreads();
+  if (wave != 0) return;
+  float acc = 0.f;
+  for (int h = 0; h < Hi; h++) acc = __builtin_fmaf(sw[h], sr[lane][h], acc);
+  if (n < N) scores[bs * N + n] = live ? (kscale ? acc * kscale[row] : acc) : -SMLA_INF;
+}
+
+// Hi > 64: one thread per key, sequential over all heads (same arithmetic order)
+template <int DI, int KDT>
+__global__ __launch_bounds__(256) void indexer_wide_kernel(const void* __restrict__ q, int q_dtype,
+                                                           const void* __restrict__ keys,
+                                                           const float* __restrict__ kscale,
+                                                           const float* __restrict__ weights,
+                                                           const int32_t* __restrict__ nvis, int64_t S, int Hi,
+                                                           int64_t N, float* __restrict__ scores) {
+  const int64_t bs = blockIdx.y;
+  const int64_t b = bs / S;
+  const int64_t n = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (n >= N) return;
+  const int64_t nv = nvis ? (int64_t)nvis[bs] : N;
+  if (n >= nv) {
+    scores[bs * N + n] = -SMLA_INF;
+    return;
+  }
+  const int64_t row = b * N + n;
   float acc = 0.f;
   for (int h = 0; h < Hi; h++) {
-    const f32x4_t* qh = (const f32x4_t*)(sq + h * DI);
     float dot = 0.f;
-#pragma unroll
-    for (int v = 0; v < DI / 4; v++) {
-      f32x4_t qq = qh[v];
-      dot = __builtin_fmaf(qq[0], kr[4 * v], dot);
-      dot = __builtin_fmaf(qq[1], kr[4 * v + 1], dot);
-      dot = __builtin_fmaf(qq[2], kr[4 * v + 2], dot);
-      dot = __builtin_fmaf(qq[3], kr[4 * v + 3], dot);
-    }
-    float r = dot > 0.f ? dot : 0.f;
-    acc = __builtin_fmaf(sw[h], r, acc);
+    for (int d = 0; d < DI; d++)
+      dot = __builtin_fmaf(load_as_f32(q, (bs * Hi + h) * DI + d, q_dtype), load_as_f32(keys, row * DI + d, KDT), dot);
+    acc = __builtin_fmaf(weights[bs * Hi + h], dot > 0.f ? dot : 0.f, acc);
   }
-  *out = kscale ? acc * kscale[row] : acc;
+  scores[bs * N + n] = kscale ? acc * kscale[row] : acc;
+}
+
+template <int DI, int KDT>
+int launch_k(const void* q, int q_dtype, const void* keys, const float* kscale, const float* w,
+             const int32_t* nvis, int64_t B, int64_t S, int64_t Hi, int64_t N, float* scores, hipStream_t st) {
+  if (Hi <= 64) {
+    dim3 grid((unsigned)((N + kKeys - 1) / kKeys), (unsigned)(B * S));
+    const int threads = (int)(((Hi + kHG - 1) / kHG) * 64);
+    hipLaunchKernelGGL((indexer_kernel<DI, KDT>), grid, dim3(threads), 0, st, q, q_dtype, keys, kscale, w, nvis, S,
+                       (int)Hi, N, scores);
+  } else {
+    dim3 grid((unsigned)((N + 255) / 256), (unsigned)(B * S));
+    hipLaunchKernelGGL((indexer_wide_kernel<DI, KDT>), grid, dim3(256), 0, st, q, q_dtype, keys, kscale, w, nvis, S,
+                       (int)Hi, N, scores);
+  }
+  SMLA_HIP_CHECK_LAUNCH();
+  return SMLA_OK;
 }
 
 template <int DI>
 int launch_di(const void* q, int q_dtype, const void* keys, int k_dtype, const float* kscale,
               const float* w, const int32_t* nvis, int64_t B, int64_t S, int64_t Hi, int64_t N,
               float* scores, hipStream_t st) {
-  dim3 grid((unsigned)((N + kThreads - 1) / kThreads), (unsigned)(B * S));
   if (k_dtype == SMLA_FP8_E4M3)
-    hipLaunchKernelGGL((indexer_kernel<DI, SMLA_FP8_E4M3>), grid, dim3(kThreads), 0, st, q, q_dtype, keys,
-                       kscale, w, nvis, S, (int)Hi, N, scores);
-  else if (k_dtype == SMLA_BF16)
-    hipLaunchKernelGGL((indexer_kernel<DI, SMLA_BF16>), grid, dim3(kThreads), 0, st, q, q_dtype, keys, kscale,
-                       w, nvis, S, (int)Hi, N, scores);
-  else
-    hipLaunchKernelGGL((indexer_kernel<DI, SMLA_F32>), grid, dim3(kThreads), 0, st, q, q_dtype, keys, kscale,
-                       w, nvis, S, (int)Hi, N, scores);
-  SMLA_HIP_CHECK_LAUNCH();
-  return SMLA_OK;
+    return launch_k<DI, SMLA_FP8_E4M3>(q, q_dtype, keys, kscale, w, nvis, B, S, Hi, N, scores, st);
+  if (k_dtype == SMLA_BF16) return launch_k<DI, SMLA_BF16>(q, q_dtype, keys, kscale, w, nvis, B, S, Hi, N, scores, st);
+  return launch_k<DI, SMLA_F32>(q, q_dtype, keys, kscale, w, nvis, B, S, Hi, N, scores, st);
 }
 
 }  // namespace
@@ -125,7 +177,8 @@ extern "C" int smla_indexer_score(const void* q, int q_dtype, const void* keys, 
   if (B <= 0 || S <= 0 || Hi <= 0 || Di <= 0 || N <= 0) return SMLA_E_SHAPE;
   if (q_dtype != SMLA_F32 && q_dtype != SMLA_BF16) return SMLA_E_DTYPE;
   if (k_dtype != SMLA_F32 && k_dtype != SMLA_BF16 && k_dtype != SMLA_FP8_E4M3) return SMLA_E_DTYPE;
-  if (Hi > 256 || Hi * Di > kMaxQ || (N + kThreads - 1) / kThreads > 0x7fffffff) return SMLA_E_UNSUPPORTED;
+  if (Hi > 256 || (Hi <= 64 && Hi * Di > kMaxQ) || (N + 63) / 64 > 0x7fffffff || B * S > 65535)
+    return SMLA_E_UNSUPPORTED;
   hipStream_t st = (hipStream_t)stream;
   switch (Di) {
     case 32: return launch_di<32>(q, q_dtype, keys, k_dtype, kscale, weights, nvis, B, S, Hi, N, scores, st);

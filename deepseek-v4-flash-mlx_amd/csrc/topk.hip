@@ -2,14 +2,14 @@
 //
 // smla_topk: per row, rank the first nvis scores by (score desc, index asc) with -0 == +0, keep
 // min(k, nvis), emit ascending ids (+ id_offset), -1 padded to k.  One workgroup of 1024 threads
-// per row; each thread owns a contiguous run of PER keys in registers.
-//   1. key = order-preserving uint32 with larger score -> smaller key;
-//   2. 4 radix passes (8-bit digits, per-wave LDS histograms) find the k-th smallest key K and the
-//      number `need` of entries equal to K that still fit;
-//   3. two block-wide exclusive scans in index order: rank the K-ties (lowest index first), then
-//      place every selected id at its ascending position.
-// Bit-exact by construction: only comparisons and counts.  When nvis <= k every visible id is
-// taken (oracle/decode_engine.py:112-114, "all causally visible compressed rows").
+// per row; each thread owns a contiguous run of PER keys in registers (key = order-preserving
+// uint32, larger score -> smaller key).  The k-th best entry (Kt, It) is found by a bucket select
+// (monotone value buckets, exact ranking of the boundary bucket) or, for degenerate spreads, by
+// 4 radix passes plus a tie rank; a block-wide scan in index order then places every selected id
+// at its ascending position.  Bit-exact by construction: only comparisons and counts.  When
+// nvis <= k every visible id is taken (oracle/decode_engine.py:112-114, "all causally visible
+// compressed rows").  smla_select_decode also writes the decode window ids in front (one launch
+// for the engine's whole index build, oracle/decode_engine.py:110-114).
 //
 // smla_window_topk_idxs mirrors ref_torch/sparse_attn.py:9-20; smla_decode_window_idxs builds the
 // engine's decode window oracle/decode_engine.py:110-111 over an un-ringed raw cache.
@@ -57,14 +57,41 @@ __device__ inline int block_excl_scan(int v, int* tmp, int* total) {
   return res;
 }
 
+constexpr int kBuckets = 2048;
+constexpr int kMaxCand = 256;
+
+// inverse of desc_key (the score with -0 folded to +0)
+__device__ inline float key_score(uint32_t key) {
+  const uint32_t asc = ~key;
+  return __uint_as_float((asc & 0x80000000u) ? (asc ^ 0x80000000u) : ~asc);
+}
+
+// monotone bucket of a finite score: 0 holds the largest scores
+__device__ inline int bucket_of(uint32_t key, float lmax, float bscale) {
+  int bb = (int)((lmax - key_score(key)) * bscale);
+  return bb < 0 ? 0 : (bb >= kBuckets ? kBuckets - 1 : bb);
+}
+
+// Row selection.  Produces the threshold pair (Kt, It) of the k-th best entry in the order
+// (key asc == score desc, index asc); entry n is selected iff key < Kt or (key == Kt && n <= It).
+//  * fast path: monotone buckets of (max - s) * 2048 / (max - min); the bucket holding the k-th
+//    entry is found from a histogram + scan, and its (few) candidates are ranked exactly;
+//  * fallback (degenerate spreads, > 256 candidates in the boundary bucket): 4 radix passes of 8
+//    bits over the keys, then the tie rank among entries equal to the k-th key.
+// Output: window ids (optional), then the selected ids ascending (+ id_offset), then -1.
 template <int PER>
 __global__ __launch_bounds__(kTopkThreads) void topk_kernel(const float* __restrict__ scores, int64_t N,
                                                             const int32_t* __restrict__ nvis, int k,
                                                             int32_t* __restrict__ out, int64_t out_stride,
-                                                            int32_t id_offset) {
+                                                            int32_t id_offset, const int32_t* __restrict__ wpos,
+                                                            int window) {
   __shared__ int hist[kWaves][256];
+  __shared__ int bhist[kBuckets];
   __shared__ int tmp[kWaves + 1];
-  __shared__ int sel_digit, sel_before;
+  __shared__ float redf[2 * kWaves];
+  __shared__ uint32_t cand_key[kMaxCand];
+  __shared__ int cand_idx[kMaxCand];
+  __shared__ int s_int[4];
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int64_t r = blockIdx.x;
@@ -73,100 +100,202 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(const float* __restr
   if (nv < 0) nv = 0;
   const float* sr = scores + r * N;
   int32_t* orow = out + r * out_stride;
+  if (wpos) {
+    const int64_t p = wpos[r];
+    for (int j = tid; j < window; j += kTopkThreads) {
+      const int64_t v = p - window + 1 + j;
+      orow[j] = v < 0 ? -1 : (int32_t)v;
+    }
+    orow += window;
+  }
   const int take = (int)(nv < k ? nv : k);
 
   const int64_t base = (int64_t)tid * PER;
   if (nv <= k) {
-    // take every visible id, already ascending
     for (int64_t j = tid; j < k; j += kTopkThreads) orow[j] = j < nv ? (int32_t)j + id_offset : -1;
     return;
   }
   uint32_t key[PER];
+  float lmin = SMLA_INF, lmax = -SMLA_INF;
+  bool nan_seen = false;
 #pragma unroll
   for (int j = 0; j < PER; j++) {
-    int64_t n = base + j;
-    key[j] = n < nv ? desc_key(sr[n]) : 0xffffffffu;
+    const int64_t n = base + j;
+    const float f = n < nv ? sr[n] : 0.f;
+    key[j] = n < nv ? desc_key(f) : 0xffffffffu;
+    if (n < nv) {
+      lmin = fminf(lmin, f);
+      lmax = fmaxf(lmax, f);
+      nan_seen |= f != f;
+    }
   }
-  // ---- radix select for the k-th smallest key among visible entries
-  uint32_t prefix = 0, pmask = 0;
-  int remaining = k;
-#pragma unroll 1
-  for (int shift = 24; shift >= 0; shift -= 8) {
-    for (int i = lane; i < 256; i += 64) hist[wave][i] = 0;
-    __syncthreads();
+  nan_seen = __syncthreads_or(nan_seen);
+  // ---- row min / max
+  {
+    float a = lmin, bmx = lmax;
 #pragma unroll
-    for (int j = 0; j < PER; j++) {
-      int64_t n = base + j;
-      if (n < nv && (key[j] & pmask) == prefix) atomicAdd(&hist[wave][(key[j] >> shift) & 255u], 1);
+    for (int o = 32; o >= 1; o >>= 1) {
+      a = fminf(a, __shfl_xor(a, o, 64));
+      bmx = fmaxf(bmx, __shfl_xor(bmx, o, 64));
+    }
+    if (lane == 0) {
+      redf[wave] = a;
+      redf[kWaves + wave] = bmx;
+    }
+    for (int i = tid; i < kBuckets; i += kTopkThreads) bhist[i] = 0;
+    __syncthreads();
+    lmin = redf[0];
+    lmax = redf[kWaves];
+    for (int w = 1; w < kWaves; w++) {
+      lmin = fminf(lmin, redf[w]);
+      lmax = fmaxf(lmax, redf[kWaves + w]);
+    }
+  }
+  uint32_t Kt = 0;
+  int It = -1;
+  bool done = false;
+  if (lmax == lmin && !nan_seen) {
+    // every visible score equal: the k lowest indices
+    Kt = desc_key(lmax);
+    It = k - 1;
+    done = true;
+  }
+  const float bscale = (float)kBuckets / (lmax - lmin);
+  if (!done && !nan_seen && bscale < SMLA_INF && bscale > 0.f && lmin > -SMLA_INF && lmax < SMLA_INF) {
+    // ---- bucket histogram (bucket 0 holds the largest scores)
+#pragma unroll
+    for (int j = 0; j < PER; j++)
+      if (base + j < nv) atomicAdd(&bhist[bucket_of(key[j], lmax, bscale)], 1);
+    __syncthreads();
+    // thread t owns buckets 2t, 2t+1
+    const int c0 = bhist[2 * tid], c1 = bhist[2 * tid + 1];
+    int tot;
+    const int before = block_excl_scan(c0 + c1, tmp, &tot);
+    if (tid == 0) s_int[3] = 0;  // candidate counter
+    if (before < k && k <= before + c0) {
+      s_int[0] = 2 * tid;
+      s_int[1] = k - before;
+    } else if (before + c0 < k && k <= before + c0 + c1) {
+      s_int[0] = 2 * tid + 1;
+      s_int[1] = k - before - c0;
     }
     __syncthreads();
-    if (wave == 0) {
-      // bins lane*4 .. lane*4+3
-      int c[4];
-      int tot = 0;
+    const int bb = s_int[0], need = s_int[1];
+    const int cb = bhist[bb];
+    if (cb <= kMaxCand) {
+      // gather the boundary bucket's entries and rank them exactly
 #pragma unroll
-      for (int i = 0; i < 4; i++) {
-        int s = 0;
-        for (int w = 0; w < kWaves; w++) s += hist[w][lane * 4 + i];
-        c[i] = s;
-        tot += s;
+      for (int j = 0; j < PER; j++) {
+        if (base + j < nv && bucket_of(key[j], lmax, bscale) == bb) {
+          const int slot = atomicAdd(&s_int[3], 1);
+          cand_key[slot] = key[j];
+          cand_idx[slot] = (int)(base + j);
+        }
       }
-      int incl = tot;
+      __syncthreads();
+      if (tid < cb) {
+        const uint32_t kk = cand_key[tid];
+        const int ii = cand_idx[tid];
+        int rank = 0;
+#pragma unroll 4
+        for (int j = 0; j < cb; j++) {
+          const uint32_t k2 = cand_key[j];
+          rank += (k2 < kk) || (k2 == kk && cand_idx[j] < ii);
+        }
+        if (rank == need - 1) {
+          s_int[0] = (int)kk;
+          s_int[1] = ii;
+        }
+      }
+      __syncthreads();
+      Kt = (uint32_t)s_int[0];
+      It = s_int[1];
+      done = true;
+    }
+    __syncthreads();
+  }
+  if (!done) {
+    // ---- radix select over the 32-bit keys
+    uint32_t prefix = 0, pmask = 0;
+    int remaining = k;
+#pragma unroll 1
+    for (int shift = 24; shift >= 0; shift -= 8) {
+      for (int i = lane; i < 256; i += 64) hist[wave][i] = 0;
+      __syncthreads();
 #pragma unroll
-      for (int o = 1; o < 64; o <<= 1) {
-        int y = __shfl_up(incl, o, 64);
-        if (lane >= o) incl += y;
+      for (int j = 0; j < PER; j++) {
+        if (base + j < nv && (key[j] & pmask) == prefix) atomicAdd(&hist[wave][(key[j] >> shift) & 255u], 1);
       }
-      int before = incl - tot;
-      // the digit where the cumulative count first reaches `remaining`
-      if (before < remaining && remaining <= incl) {
-        int cum = before;
+      __syncthreads();
+      if (wave == 0) {
+        int cc[4];
+        int t4 = 0;
+#pragma unroll 1
         for (int i = 0; i < 4; i++) {
-          if (remaining <= cum + c[i]) {
-            sel_digit = lane * 4 + i;
-            sel_before = cum;
-            break;
+          int sacc = 0;
+#pragma unroll 4
+          for (int w = 0; w < kWaves; w++) sacc += hist[w][lane * 4 + i];
+          cc[i] = sacc;
+          t4 += sacc;
+        }
+        int incl = t4;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+          const int y = __shfl_up(incl, o, 64);
+          if (lane >= o) incl += y;
+        }
+        const int bef = incl - t4;
+        if (bef < remaining && remaining <= incl) {
+          int cum = bef;
+          for (int i = 0; i < 4; i++) {
+            if (remaining <= cum + cc[i]) {
+              s_int[0] = lane * 4 + i;
+              s_int[1] = cum;
+              break;
+            }
+            cum += cc[i];
           }
-          cum += c[i];
+        }
+      }
+      __syncthreads();
+      prefix |= (uint32_t)s_int[0] << shift;
+      pmask |= 255u << shift;
+      remaining -= s_int[1];
+      __syncthreads();
+    }
+    // index of the `remaining`-th entry equal to the k-th key (index order)
+    int nt = 0;
+#pragma unroll
+    for (int j = 0; j < PER; j++) nt += (base + j < nv && key[j] == prefix);
+    int tot_ties;
+    const int trank = block_excl_scan(nt, tmp, &tot_ties);
+    if (trank < remaining && remaining <= trank + nt) {
+      int cnt = trank;
+#pragma unroll
+      for (int j = 0; j < PER; j++) {
+        if (base + j < nv && key[j] == prefix) {
+          cnt++;
+          if (cnt == remaining) s_int[2] = (int)(base + j);
         }
       }
     }
     __syncthreads();
-    prefix |= (uint32_t)sel_digit << shift;
-    pmask |= 255u << shift;
-    remaining -= sel_before;
-    __syncthreads();
+    Kt = prefix;
+    It = s_int[2];
   }
-  const uint32_t K = prefix;
-  const int need = remaining;  // entries equal to K to take, lowest index first
-  // ---- rank ties in index order
-  int nt = 0;
-#pragma unroll
-  for (int j = 0; j < PER; j++) nt += (base + j < nv && key[j] == K);
-  int tot_ties;
-  int tie_rank = block_excl_scan(nt, tmp, &tot_ties);
+  // ---- emit the selected ids in ascending order
   int nsel = 0;
-  {
-    int tr = tie_rank;
 #pragma unroll
-    for (int j = 0; j < PER; j++) {
-      bool vis = base + j < nv;
-      bool s = vis && (key[j] < K || (key[j] == K && tr < need));
-      if (vis && key[j] == K) tr++;
-      nsel += s;
-    }
+  for (int j = 0; j < PER; j++) {
+    const int64_t n = base + j;
+    nsel += (n < nv) && (key[j] < Kt || (key[j] == Kt && n <= It));
   }
   int tot_sel;
   int pos = block_excl_scan(nsel, tmp, &tot_sel);
-  {
-    int tr = tie_rank;
 #pragma unroll
-    for (int j = 0; j < PER; j++) {
-      bool vis = base + j < nv;
-      bool s = vis && (key[j] < K || (key[j] == K && tr < need));
-      if (vis && key[j] == K) tr++;
-      if (s) orow[pos++] = (int32_t)(base + j) + id_offset;
-    }
+  for (int j = 0; j < PER; j++) {
+    const int64_t n = base + j;
+    if ((n < nv) && (key[j] < Kt || (key[j] == Kt && n <= It))) orow[pos++] = (int32_t)n + id_offset;
   }
   for (int64_t j = take + tid; j < k; j += kTopkThreads) orow[j] = -1;
 }
@@ -204,17 +333,26 @@ __global__ void decode_window_kernel(const int32_t* __restrict__ pos, int64_t R,
 
 }  // namespace
 
+static int launch_select(const float* scores, int64_t R, int64_t N, const int32_t* nvis, int64_t k, int32_t* out,
+                         int64_t out_stride, int32_t id_offset, const int32_t* wpos, int window, hipStream_t st);
+
 extern "C" int smla_topk(const float* scores, int64_t R, int64_t N, const int32_t* nvis, int64_t k, int32_t* out,
                          int64_t out_stride, int32_t id_offset, void* stream) {
   if (!scores || !out) return SMLA_E_NULL;
   if (R <= 0 || N <= 0 || k <= 0 || out_stride < k) return SMLA_E_SHAPE;
   if (R > 0x7fffffff || k > 0x7fffffff) return SMLA_E_UNSUPPORTED;
   hipStream_t st = (hipStream_t)stream;
+  return launch_select(scores, R, N, nvis, k, out, out_stride, id_offset, nullptr, 0, st);
+}
+
+static int launch_select(const float* scores, int64_t R, int64_t N, const int32_t* nvis, int64_t k, int32_t* out,
+                         int64_t out_stride, int32_t id_offset, const int32_t* wpos, int window, hipStream_t st) {
   int64_t per = (N + kTopkThreads - 1) / kTopkThreads;
   dim3 grid((unsigned)R), blk(kTopkThreads);
 #define SMLA_TOPK_CASE(P)                                                                          \
   if (per <= P) {                                                                                  \
-    hipLaunchKernelGGL(topk_kernel<P>, grid, blk, 0, st, scores, N, nvis, (int)k, out, out_stride, id_offset); \
+    hipLaunchKernelGGL(topk_kernel<P>, grid, blk, 0, st, scores, N, nvis, (int)k, out, out_stride, id_offset, \
+                       wpos, window);                                                              \
     SMLA_HIP_CHECK_LAUNCH();                                                                       \
     return SMLA_OK;                                                                                \
   }
@@ -226,6 +364,16 @@ extern "C" int smla_topk(const float* scores, int64_t R, int64_t N, const int32_
   SMLA_TOPK_CASE(64)
 #undef SMLA_TOPK_CASE
   return SMLA_E_UNSUPPORTED;  // N > 65536
+}
+
+extern "C" int smla_select_decode(const float* scores, int64_t R, int64_t N, const int32_t* nvis, int64_t k,
+                                  const int32_t* pos, int64_t window, int32_t* out, int64_t out_stride,
+                                  int32_t id_offset, void* stream) {
+  if (!scores || !out || !pos) return SMLA_E_NULL;
+  if (R <= 0 || N <= 0 || k <= 0 || window < 0 || out_stride < k + window) return SMLA_E_SHAPE;
+  if (R > 0x7fffffff || k > 0x7fffffff || window > 0x7fffffff) return SMLA_E_UNSUPPORTED;
+  if ((N + kTopkThreads - 1) / kTopkThreads > 64) return SMLA_E_UNSUPPORTED;
+  return launch_select(scores, R, N, nvis, k, out, out_stride, id_offset, pos, (int)window, (hipStream_t)stream);
 }
 
 extern "C" int smla_window_topk_idxs(int64_t window_size, int64_t bsz, int64_t seqlen, int64_t start_pos,

@@ -30,6 +30,7 @@ _SIGNATURES = {
     "smla_indexer_score": (_int, [_vp, _int, _vp, _int, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64,
                                   _vp, _vp]),
     "smla_topk": (_int, [_vp, _i64, _i64, _vp, _i64, _vp, _i64, _i32, _vp]),
+    "smla_select_decode": (_int, [_vp, _i64, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _i32, _vp]),
     "smla_block_mean_pool": (_int, [_vp, _int, _i64, _i64, _i64, _i64, _vp, _int, _vp]),
     "smla_gated_pool": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _f32,
                                _int, _vp, _vp]),

@@ -30,6 +30,5 @@ def select_decode_indices(scores, k, pos, window, n_raw, out=None):
     B = scores.shape[0]
     if out is None:
         out = torch.empty(B, window + k, dtype=torch.int32, device=scores.device)
-    ops.decode_window_idxs(pos, window, out=out[:, :window])
-    ops.topk_into(scores, k, out[:, window:], id_offset=n_raw)
+    ops.select_decode_into(scores.contiguous(), k, pos, window, out, id_offset=n_raw)
     return out

@@ -239,6 +239,21 @@ def decode_window_idxs(pos, window, out=None):
     return out
 
 
+def select_decode_into(scores, k, pos, window, out, id_offset=0, nvis=None):
+    """Window ids then top-k ids per row, in one launch: scores [R, N], pos [R] int32,
+    out int32 [R, >= window + k] (row stride out.stride(0))."""
+    _on_gpu(scores, pos, out, nvis)
+    if out.dtype != torch.int32 or out.stride(-1) != 1:
+        raise ValueError("out must be an int32 view with unit inner stride")
+    R, N = scores.shape
+    if nvis is not None:
+        nvis = nvis.to(torch.int32).contiguous()
+    pos = pos.to(torch.int32).contiguous()
+    _lib.call("smla_select_decode", _p(scores), R, N, _p(nvis), k, _p(pos), window, _p(out), out.stride(0),
+              int(id_offset), _stream(scores))
+    return out
+
+
 def topk_into(scores, k, out, id_offset=0, nvis=None):
     """Write the top-k selection of scores [R, N] into the int32 view out [R, >=k] (row stride
     out.stride(0)); no allocation."""

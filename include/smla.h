@@ -16,6 +16,7 @@
  *   smla_indexer_score        (none: the reference attends every visible compressed row,
  *                              oracle/decode_engine.py:112-114; the indexer is the build's)
  *   smla_topk                 oracle/decode_engine.py:112-114  cidx selection (take-all when nvis <= k)
+ *   smla_select_decode        oracle/decode_engine.py:110-114  widx + cidx in one launch
  *   smla_block_mean_pool      (none: block mean of the 32K decode workload)
  *   smla_gated_pool           ref_torch/compressor.py:41-49    pooling + RMSNorm + RoPE of compressor_prefill
  *   smla_ring_step            oracle/decode_engine.py:96-105   decode compressor ring step and cache append
@@ -129,6 +130,14 @@ int smla_indexer_score(const void* q, int q_dtype, const void* keys, int k_dtype
  */
 int smla_topk(const float* scores, int64_t R, int64_t N, const int32_t* nvis, int64_t k,
               int32_t* out, int64_t out_stride, int32_t id_offset, void* stream);
+
+/* The whole decode index build of oracle/decode_engine.py:110-114 in one launch: for row r,
+ * out[r*out_stride + j] = pos[r]-window+1+j (or -1 where negative) for j < window, then the
+ * smla_topk selection of scores row r (ids + id_offset, -1 padded) at columns window..window+k-1.
+ * pos: [R] int32 on the device; out_stride >= window + k. */
+int smla_select_decode(const float* scores, int64_t R, int64_t N, const int32_t* nvis, int64_t k,
+                       const int32_t* pos, int64_t window, int32_t* out, int64_t out_stride,
+                       int32_t id_offset, void* stream);
 
 /* ---------------------------------------------------------------------------------------------
  * Compressor.

@@ -106,3 +106,49 @@ def test_decode_window_idxs(dev):
         ref = np.arange(p - 127, p + 1)
         ref[ref < 0] = -1
         np.testing.assert_array_equal(got[r], ref)
+
+
+@pytest.mark.parametrize("case", ["outlier", "inf", "nan", "crowded"])
+def test_topk_fallback_spreads(dev, case):
+    """Rows whose value spread defeats the bucket pass (one huge outlier, infinities, NaN, more
+    than 256 entries sharing the boundary bucket) take the radix path; sets stay exact."""
+    from smla import indexer as sidx
+    announce(f"topk fallback {case}")
+    rng = np.random.default_rng(7)
+    R, N, k = 3, 8192, 2048
+    s = rng.standard_normal((R, N)).astype(np.float32)
+    if case == "outlier":
+        s[:, 17] = 3.0e38
+    elif case == "inf":
+        s[:, ::97] = np.inf
+        s[:, 5::89] = -np.inf
+    elif case == "nan":
+        s[:, ::101] = np.nan
+        s[1, 3::53] = -np.nan
+    else:
+        s = (rng.integers(0, 4, (R, N)) * 1e-3).astype(np.float32)
+        s[:, 0] = 1.0e6
+    nvis = np.array([N, N - 100, 3000], np.int32)
+    got = sidx.topk(torch.from_numpy(s).to(dev), k, torch.from_numpy(nvis).to(dev)).cpu().numpy()
+    np.testing.assert_array_equal(got, oidx.topk(s, k, nvis))
+
+
+@pytest.mark.parametrize("R,N,k,window", [(8, 8192, 2048, 128), (3, 100, 512, 128), (2, 4096, 64, 7)])
+def test_select_decode_fused(dev, R, N, k, window):
+    """One launch writes the decode window ids then the top-k ids (offset into the raw cache)."""
+    from smla import indexer as sidx
+    announce(f"select_decode R={R} N={N} k={k} window={window}")
+    rng = np.random.default_rng(R * N + k)
+    s = rng.standard_normal((R, N)).astype(np.float32)
+    pos = rng.integers(0, 4 * N, R).astype(np.int32)
+    pos[0] = 3
+    n_raw = 4 * N + 1
+    got = sidx.select_decode_indices(torch.from_numpy(s).to(dev), k, torch.from_numpy(pos).to(dev), window,
+                                     n_raw).cpu().numpy()
+    assert got.shape == (R, window + k)
+    sel = oidx.topk(s, k)
+    for r in range(R):
+        win = np.arange(pos[r] - window + 1, pos[r] + 1)
+        win[win < 0] = -1
+        np.testing.assert_array_equal(got[r, :window], win)
+        np.testing.assert_array_equal(got[r, window:], np.where(sel[r] >= 0, sel[r] + n_raw, -1))
