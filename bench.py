@@ -11,8 +11,9 @@ HBM; R copies of the caches (> 512 MB of distinct rows touched per rotation) are
 256 MB MALL cannot serve the gather.  The K steps are replayed from HIP graphs.
 
 Also reported:
-* roofline of the dominant kernel (the MFMA attention kernel): algorithmic bytes per launch /
-  its average duration measured with HIP events recorded around that kernel alone;
+* roofline of the dominant kernel (the MFMA attention split kernel): algorithmic bytes per launch /
+  its average duration, measured with HIP events around graph replays of that kernel alone (one
+  launch per rotated cache copy, back to back);
 * cpu_baseline: the CPU oracle running the same step on a bounded sample.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
@@ -36,6 +37,20 @@ def algorithmic_attention_bytes(B, H, T, D=576, DV=512, row_bytes=1152):
     return B * T * row_bytes + B * H * D * 2 + B * H * DV * 2 + B * T * 4
 
 
+def measured_traffic(kernel="attn_decode_bf16_kernel<576>", workload="decode_32k"):
+    """HBM bytes per launch of `kernel`, from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary
+    (both counters scaled by a plain-copy calibration); None when the summary has no such line."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", f"{workload}_hbm_counters.md")
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith(f"traffic_bytes_per_launch {kernel} {workload}:"):
+                    return int(line.rsplit(":", 1)[1])
+    except OSError:
+        return None
+    return None
+
+
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -45,7 +60,22 @@ def parse():
     ap.add_argument("--kernel-iters", type=int, default=96)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-steps", type=int, default=3)
+    ap.add_argument("--copy-mib", type=int, default=0,
+                    help="only run a plain device copy of this many MiB, 8 times (HBM counter calibration)")
     return ap.parse_args()
+
+
+def copy_calibration(mib):
+    """A plain copy kernel of known size: `rocprofv3 --pmc FETCH_SIZE` / `WRITE_SIZE` on this run gives
+    the counter reading per byte moved, which scales the same counters read on the attention kernel."""
+    import torch
+    dev = torch.device("cuda:0")
+    src = torch.ones(mib << 18, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(8):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_bytes_per_launch": mib << 20, "launches": 8}), flush=True)
 
 
 def cpu_baseline(w, nthreads, reps):
@@ -90,6 +120,9 @@ def cpu_baseline(w, nthreads, reps):
 
 def main():
     args = parse()
+    if args.copy_mib:
+        copy_calibration(args.copy_mib)
+        return
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world > 1:
         print(json.dumps({"error": "this build measures one GPU; --gpus must be 1 "
@@ -196,28 +229,28 @@ def main():
         sc = sidx.indexer_score(qi, keys, ks, wt)
         idx_all.append(sidx.select_decode_indices(sc[:, 0], k, pos, win, n_raw))
     torch.cuda.synchronize()
-    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-           for _ in range(args.kernel_iters)]
-    for a, b in evs:     # materialise the underlying hipEvents
-        a.record()
-        b.record()
+    # the split kernel alone: a graph of `rot` launches (one per cache copy, main kernel only), replayed
+    # back to back between two events on the replay stream
+    lib.smla_profile_set_attn_main_only(1)
+    try:
+        gk = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gk):
+            for r in range(args.rot):
+                ssa.sparse_attn_two_source(q, copies[r][0], copies[r][1], None, idx_all[r][:, None, :], w["scale"],
+                                           dv=512)
+    finally:
+        lib.smla_profile_set_attn_main_only(0)
+    gk.replay()
     torch.cuda.synchronize()
+    reps = max(1, args.kernel_iters // args.rot)
+    ka, kb = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ka.record()
+    for _ in range(reps):
+        gk.replay()
+    kb.record()
+    torch.cuda.synchronize()
+    k_us = 1000.0 * ka.elapsed_time(kb) / (reps * args.rot)
     full_ev = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-    for i in range(8):
-        r = i % args.rot
-        ssa.sparse_attn_two_source(q, copies[r][0], copies[r][1], None, idx_all[r][:, None, :], w["scale"], dv=512)
-    torch.cuda.synchronize()
-    for i, (a, b) in enumerate(evs):
-        r = i % args.rot
-        # keep the stream busy while the host enqueues the events and the kernel, so that the
-        # events bracket the kernel's execution rather than host launch latency
-        torch.cuda._sleep(100000)
-        lib.smla_profile_set_attn_events(a.cuda_event, b.cuda_event)
-        ssa.sparse_attn_two_source(q, copies[r][0], copies[r][1], None, idx_all[r][:, None, :], w["scale"], dv=512)
-    lib.smla_profile_set_attn_events(None, None)
-    torch.cuda.synchronize()
-    k_ms = [a.elapsed_time(b) for a, b in evs]
-    k_us = 1000.0 * float(np.mean(k_ms))
     # main + merge, per op (eager)
     full_ev[0].record()
     for i in range(args.kernel_iters):
@@ -230,8 +263,9 @@ def main():
     alg_bytes = algorithmic_attention_bytes(B, H, T)
     achieved = alg_bytes / (k_us * 1e-6) / 1e9
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                "kernel": "attn_mfma_kernel<576,512,bf16>", "kernel_us": round(k_us, 3),
+                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
+                "traffic_source": "profiles/decode_32k_hbm_counters.md (rocprofv3 --pmc, copy-calibrated)",
+                "kernel": "attn_decode_bf16_kernel<576>", "kernel_us": round(k_us, 3),
                 "algorithmic_bytes": alg_bytes, "nsplit": ns.value, "rows_per_split": rps.value}
 
     cpu = None

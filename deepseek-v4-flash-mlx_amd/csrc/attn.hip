@@ -527,6 +527,7 @@ struct Plan {
 
 int g_target_wgs = 0;  // 0 = default (number of CUs); settable for tuning
 hipEvent_t g_ev_before = nullptr, g_ev_after = nullptr;  // profiling: bracket the main kernel
+bool g_main_only = false;  // profiling: launch the split kernel alone (partials, no merge)
 
 int num_cus() {
   static int n = 0;
@@ -576,7 +577,7 @@ int launch_mfma(const Plan& p, const void* q, RowSrc src, const float* sink, con
   if constexpr (!FP8) {
     int rc = smla_attn::launch_decode_bf16(D, p.nsplit, p.rows_per_split, q, src, sink, idx, T, B, S, H, scale, out,
                                            out_dtype, (float*)ws, stream, g_ev_before, g_ev_after);
-    if (rc != SMLA_OK) return rc;
+    if (rc != SMLA_OK || g_main_only) return rc;
     return launch_merge(p, B, S, H, sink, out, out_dtype, ws, stream, out_dtype == SMLA_BF16);
   }
   using C = MfmaCfg<D, 512>;
@@ -655,6 +656,11 @@ extern "C" void smla_profile_set_attn_events(void* before, void* after) {
   g_ev_before = (hipEvent_t)before;
   g_ev_after = (hipEvent_t)after;
 }
+
+// profiling hook (not part of the public header): when on, the MFMA attention path launches only
+// its split kernel (the workspace partials are written, the output is not), so that a sequence of
+// such launches times that kernel alone
+extern "C" void smla_profile_set_attn_main_only(int on) { g_main_only = on != 0; }
 
 // split plan of the MFMA path for these sizes: writes nsplit and rows per split (0 if the generic
 // kernel would run)

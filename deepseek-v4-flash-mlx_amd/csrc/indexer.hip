@@ -16,8 +16,7 @@
 
 namespace {
 
-constexpr int kMaxDi = 128;
-constexpr int kMaxQ = 64 * 128;  // Hi * Di fp32 in LDS (32 KiB)
+constexpr int kMaxQ = 64 * 128;  // Hi * Di fp32 in LDS (at most 32 KiB)
 constexpr int kKeys = 64;        // keys per workgroup (one per lane)
 constexpr int kHG = 16;          // heads per wave
 
@@ -25,14 +24,14 @@ constexpr int kHG = 16;          // heads per wave
 // 16w .. 16w+15 (lane = key, key row in VGPRs, q rows read from LDS as wave-wide broadcasts);
 // the r_h go through LDS and wave 0 runs the per-key chain over h = 0..Hi-1.  Each dot product is
 // the same sequential fma chain over d as the oracle's, so scores are bit-identical.
-template <int DI, int KDT>
+template <int DI, int KDT, int QDT>
 __global__ __launch_bounds__(256) void indexer_kernel(const void* __restrict__ q, int q_dtype,
                                                       const void* __restrict__ keys,
                                                       const float* __restrict__ kscale,
                                                       const float* __restrict__ weights,
                                                       const int32_t* __restrict__ nvis, int64_t S, int Hi,
                                                       int64_t N, float* __restrict__ scores) {
-  __shared__ __align__(16) float sq[kMaxQ];
+  __shared__ __align__(16) float sq[64 * DI];
   __shared__ float sw[256];
   __shared__ float sr[kKeys][65];  // r[key][head] (padded: lanes read different keys)
   const int64_t bs = blockIdx.y;
@@ -84,24 +83,67 @@ __global__ __launch_bounds__(256) void indexer_kernel(const void* __restrict__ q
       kr[4 * v + 3] = w[3];
     }
   }
-  for (int i = tid; i < Hi * DI; i += blockDim.x) sq[i] = load_as_f32(q, bs * Hi * DI + i, q_dtype);
+  // q rows -> LDS as fp32, 8 elements per thread per step (Hi * DI is a multiple of 8 since DI is)
+  {
+    const int nq8 = Hi * DI / 8;
+    if constexpr (QDT == SMLA_BF16) {
+      const u32x4_t* qp = (const u32x4_t*)((const uint16_t*)q + bs * Hi * DI);
+      for (int i = tid; i < nq8; i += blockDim.x) {
+        const u32x4_t v = qp[i];
+        f32x4_t lo, hi;
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+          lo[2 * j] = bf16_bits_to_f32((uint16_t)(v[j] & 0xffffu));
+          lo[2 * j + 1] = bf16_bits_to_f32((uint16_t)(v[j] >> 16));
+          hi[2 * j] = bf16_bits_to_f32((uint16_t)(v[j + 2] & 0xffffu));
+          hi[2 * j + 1] = bf16_bits_to_f32((uint16_t)(v[j + 2] >> 16));
+        }
+        *(f32x4_t*)(sq + 8 * i) = lo;
+        *(f32x4_t*)(sq + 8 * i + 4) = hi;
+      }
+    } else {
+      const f32x4_t* qp = (const f32x4_t*)((const float*)q + bs * Hi * DI);
+      for (int i = tid; i < nq8; i += blockDim.x) {
+        const f32x4_t a = qp[2 * i], c = qp[2 * i + 1];
+        *(f32x4_t*)(sq + 8 * i) = a;
+        *(f32x4_t*)(sq + 8 * i + 4) = c;
+      }
+    }
+    (void)q_dtype;
+  }
   for (int i = tid; i < Hi; i += blockDim.x) sw[i] = weights[bs * Hi + i];
   __syncthreads();
 
   // r_h for this wave's heads
   for (int h0 = wave * kHG; h0 < Hi; h0 += nwaves * kHG) {
     const int hn = min(kHG, Hi - h0);
-    for (int hh = 0; hh < hn; hh++) {
+    int hh = 0;
+    for (; hh + 1 < hn; hh += 2) {  // two independent chains per step
+      const int h = h0 + hh;
+      const f32x4_t* qa = (const f32x4_t*)(sq + h * DI);
+      const f32x4_t* qb = (const f32x4_t*)(sq + (h + 1) * DI);
+      float da = 0.f, db = 0.f;
+#pragma unroll
+      for (int v = 0; v < DI / 4; v++) {
+        const f32x4_t xa = qa[v], xb = qb[v];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+          da = __builtin_fmaf(xa[j], kr[4 * v + j], da);
+          db = __builtin_fmaf(xb[j], kr[4 * v + j], db);
+        }
+      }
+      sr[lane][h] = da > 0.f ? da : 0.f;
+      sr[lane][h + 1] = db > 0.f ? db : 0.f;
+    }
+    if (hh < hn) {
       const int h = h0 + hh;
       const f32x4_t* qh = (const f32x4_t*)(sq + h * DI);
       float dot = 0.f;
 #pragma unroll
       for (int v = 0; v < DI / 4; v++) {
         const f32x4_t qq = qh[v];
-        dot = __builtin_fmaf(qq[0], kr[4 * v], dot);
-        dot = __builtin_fmaf(qq[1], kr[4 * v + 1], dot);
-        dot = __builtin_fmaf(qq[2], kr[4 * v + 2], dot);
-        dot = __builtin_fmaf(qq[3], kr[4 * v + 3], dot);
+#pragma unroll
+        for (int j = 0; j < 4; j++) dot = __builtin_fmaf(qq[j], kr[4 * v + j], dot);
       }
       sr[lane][h] = dot > 0.f ? dot : 0.f;
     }
@@ -109,6 +151,7 @@ __global__ __launch_bounds__(256) void indexer_kernel(const void* __restrict__ q
   __syncthreads();
   if (wave != 0) return;
   float acc = 0.f;
+#pragma unroll 8
   for (int h = 0; h < Hi; h++) acc = __builtin_fmaf(sw[h], sr[lane][h], acc);
   if (n < N) scores[bs * N + n] = live ? (kscale ? acc * kscale[row] : acc) : -SMLA_INF;
 }
@@ -147,8 +190,12 @@ int launch_k(const void* q, int q_dtype, const void* keys, const float* kscale, 
   if (Hi <= 64) {
     dim3 grid((unsigned)((N + kKeys - 1) / kKeys), (unsigned)(B * S));
     const int threads = (int)(((Hi + kHG - 1) / kHG) * 64);
-    hipLaunchKernelGGL((indexer_kernel<DI, KDT>), grid, dim3(threads), 0, st, q, q_dtype, keys, kscale, w, nvis, S,
-                       (int)Hi, N, scores);
+    if (q_dtype == SMLA_BF16)
+      hipLaunchKernelGGL((indexer_kernel<DI, KDT, SMLA_BF16>), grid, dim3(threads), 0, st, q, q_dtype, keys, kscale,
+                         w, nvis, S, (int)Hi, N, scores);
+    else
+      hipLaunchKernelGGL((indexer_kernel<DI, KDT, SMLA_F32>), grid, dim3(threads), 0, st, q, q_dtype, keys, kscale,
+                         w, nvis, S, (int)Hi, N, scores);
   } else {
     dim3 grid((unsigned)((N + 255) / 256), (unsigned)(B * S));
     hipLaunchKernelGGL((indexer_wide_kernel<DI, KDT>), grid, dim3(256), 0, st, q, q_dtype, keys, kscale, w, nvis, S,
