@@ -37,7 +37,10 @@ def algorithmic_attention_bytes(B, H, T, D=576, DV=512, row_bytes=1152):
     return B * T * row_bytes + B * H * D * 2 + B * H * DV * 2 + B * T * 4
 
 
-def measured_traffic(kernel="attn_decode_bf16_kernel<576>", workload="decode_32k"):
+KERNEL_NAMES = {0: "attn_decode_kernel<576>", 1: "attn_decode_bf16_kernel<576>"}
+
+
+def measured_traffic(kernel, workload="decode_32k"):
     """HBM bytes per launch of `kernel`, from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary
     (both counters scaled by a plain-copy calibration); None when the summary has no such line."""
     path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", f"{workload}_hbm_counters.md")
@@ -60,6 +63,10 @@ def parse():
     ap.add_argument("--kernel-iters", type=int, default=96)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-steps", type=int, default=3)
+    ap.add_argument("--decode-kernel", type=int, default=0,
+                    help="bf16-row decode kernel: 0 = role-split score/value waves (default), 1 = 64-head lockstep tiles")
+    ap.add_argument("--target-wgs", type=int, default=0,
+                    help="attention split plan: target workgroups (0 = one per CU)")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="only run a plain device copy of this many MiB, 8 times (HBM counter calibration)")
     return ap.parse_args()
@@ -139,6 +146,8 @@ def main():
     from smla import workloads as wl
 
     smla.load()
+    _lib.lib().smla_set_attn_decode_kernel(args.decode_kernel)
+    _lib.lib().smla_set_attn_target_wgs(args.target_wgs)
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     print("[bench] generating decode_32k inputs", file=sys.stderr, flush=True)
@@ -263,9 +272,9 @@ def main():
     alg_bytes = algorithmic_attention_bytes(B, H, T)
     achieved = alg_bytes / (k_us * 1e-6) / 1e9
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
+                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(KERNEL_NAMES[args.decode_kernel]),
                 "traffic_source": "profiles/decode_32k_hbm_counters.md (rocprofv3 --pmc, copy-calibrated)",
-                "kernel": "attn_decode_bf16_kernel<576>", "kernel_us": round(k_us, 3),
+                "kernel": KERNEL_NAMES[args.decode_kernel], "kernel_us": round(k_us, 3),
                 "algorithmic_bytes": alg_bytes, "nsplit": ns.value, "rows_per_split": rps.value}
 
     cpu = None

@@ -383,7 +383,7 @@ __global__ __launch_bounds__(kThreads, 1) void attn_mfma_kernel(
 #pragma unroll
     for (int i = 0; i < 8; i++) {
       float e = (m_ref > -SMLA_INF) ? __expf(x[i] - m_ref) : 0.f;
-      p[i] = bf16_bits_to_f32(f32_to_bf16_bits(e));  // value used by the P.V product
+      p[i] = bf16_round(e);  // value used by the P.V product
       l_lane += p[i];
     }
     u32x4_t pw = {pack_bf16x2(p[0], p[1]), pack_bf16x2(p[2], p[3]), pack_bf16x2(p[4], p[5]),
@@ -416,13 +416,13 @@ __global__ __launch_bounds__(kThreads, 1) void attn_mfma_kernel(
       for (int r = 0; r < 4; r++) {
         float v = empty ? __builtin_nanf("") : o[i][r] * inv;
         int64_t dv = 16 * i + 4 * g + r;
-        if (out_dtype == SMLA_BF16) ((uint16_t*)out)[obase + dv] = f32_to_bf16_bits(v);
+        if (out_dtype == SMLA_BF16) ((uint16_t*)out)[obase + dv] = bf16_rne(v);
         else ((float*)out)[obase + dv] = v;
       }
     }
   } else {
     // partial state: [bs][H][nsplit] records of (m, l) and O[DV]
-    int64_t rec = (bs * H + head) * nsplit + split;
+    int64_t rec = (bs * nsplit + split) * H + head;  // split-major partial records
     float* ml = part + rec * 2;
     float* op = part + (int64_t)gridDim.y * H * nsplit * 2 + rec * DV;
     if (g == 0) {
@@ -438,81 +438,93 @@ __global__ __launch_bounds__(kThreads, 1) void attn_mfma_kernel(
 // once into LDS, then every thread streams its float4 of each split's partial output with
 // independent (unrolled) loads.
 constexpr int kMaxSplits = 1024;
-__global__ __launch_bounds__(128) void attn_merge_kernel(const float* __restrict__ part, int nsplit,
-                                                         int64_t BS, int H, int DV,
-                                                         const float* __restrict__ sink,
-                                                         void* __restrict__ out, int out_dtype, int part_bf16) {
+// One wave per (query row, head): the nsplit partial states (m_j, l_j, O_j) of that head, stored
+// split-major ([row][split][head], so each split kernel writes one contiguous block), merge as
+//   M = max m_j,  w_j = exp(m_j - M),  O = sum w_j O_j / (sum w_j l_j + exp(sink - M)).
+// Lane l owns value columns 8l .. 8l+7 (DV = 512); the split loads are issued 8 at a time.
+__global__ __launch_bounds__(64) void attn_merge_kernel(const float* __restrict__ part, int nsplit,
+                                                        int64_t BS, int H, int DV,
+                                                        const float* __restrict__ sink,
+                                                        void* __restrict__ out, int out_dtype, int part_bf16) {
   __shared__ float w_s[kMaxSplits];
-  __shared__ float red[2];
-  const int tid = threadIdx.x;
+  const int lane = threadIdx.x;
   const int64_t rh = blockIdx.x;  // bs*H + head
+  const int64_t bs = rh / H;
   const int head = (int)(rh % H);
-  const float* ml = part + rh * nsplit * 2;
-  const float* op = part + BS * H * nsplit * 2 + rh * nsplit * DV;
+  const int64_t rstride = H;                              // records between consecutive splits
+  const int64_t rec0 = bs * nsplit * (int64_t)H + head;  // record of split 0
+  const float* ml = part + rec0 * 2;
   float mx = -SMLA_INF;
-  for (int j = tid; j < nsplit; j += 128) mx = fmaxf(mx, ml[2 * j]);
-  mx = wave_max(mx);
-  if ((tid & 63) == 0) red[tid >> 6] = mx;
-  __syncthreads();
-  const float M = fmaxf(red[0], red[1]);
-  __syncthreads();
+  for (int j = lane; j < nsplit; j += 64) mx = fmaxf(mx, ml[j * rstride * 2]);
+  const float M = wave_max(mx);
   const bool empty = !(M > -SMLA_INF);
   float ls = 0.f;
-  for (int j = tid; j < nsplit; j += 128) {
-    const float mj = ml[2 * j];
+  for (int j = lane; j < nsplit; j += 64) {
+    const float mj = ml[j * rstride * 2];
     const float w = (mj > -SMLA_INF) ? __expf(mj - M) : 0.f;
     w_s[j] = w;
-    ls += w * ml[2 * j + 1];
+    ls += w * ml[j * rstride * 2 + 1];
   }
-  ls = wave_sum(ls);
-  if ((tid & 63) == 0) red[tid >> 6] = ls;
+  float L = wave_sum(ls);
   __syncthreads();
-  float L = red[0] + red[1];
   const float snk = sink ? sink[head] : -SMLA_INF;
   if (!empty) L += __expf(snk - M);
   const float inv = 1.0f / L;
-  // partial O records are bf16 when the output is bf16 (written so by the bf16 decode kernel)
-  const bool obf = part_bf16 != 0;
-  const uint16_t* opb = (const uint16_t*)(part + BS * H * nsplit * 2) + rh * nsplit * DV;
-  for (int dv0 = tid * 4; dv0 < DV; dv0 += 128 * 4) {
-    f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+  const int dv0 = lane * 8;
+  const float* obase = part + BS * H * nsplit * 2;
+  f32x4_t a0 = {0.f, 0.f, 0.f, 0.f}, a1 = a0;
+  if (part_bf16) {
+    const uint16_t* op = (const uint16_t*)obase + rec0 * DV + dv0;
+    const int64_t js = rstride * DV;
     int j = 0;
-    if (obf) {
-      for (; j + 8 <= nsplit; j += 8) {
-        u32x2_t v[8];
+    for (; j < nsplit; j += 8) {
+      u32x4_t v[8];
 #pragma unroll
-        for (int u = 0; u < 8; u++) v[u] = *(const u32x2_t*)(opb + (int64_t)(j + u) * DV + dv0);
+      for (int u = 0; u < 8; u++) v[u] = (j + u < nsplit) ? *(const u32x4_t*)(op + (j + u) * js) : u32x4_t{0u, 0u, 0u, 0u};
 #pragma unroll
-        for (int u = 0; u < 8; u++) {
-          const f32x4_t f = {bf16_bits_to_f32((uint16_t)(v[u][0] & 0xffffu)), bf16_bits_to_f32((uint16_t)(v[u][0] >> 16)),
-                             bf16_bits_to_f32((uint16_t)(v[u][1] & 0xffffu)), bf16_bits_to_f32((uint16_t)(v[u][1] >> 16))};
-          acc += f * w_s[j + u];
-        }
-      }
-      for (; j < nsplit; j++) {
-        const u32x2_t v = *(const u32x2_t*)(opb + (int64_t)j * DV + dv0);
-        const f32x4_t f = {bf16_bits_to_f32((uint16_t)(v[0] & 0xffffu)), bf16_bits_to_f32((uint16_t)(v[0] >> 16)),
-                           bf16_bits_to_f32((uint16_t)(v[1] & 0xffffu)), bf16_bits_to_f32((uint16_t)(v[1] >> 16))};
-        acc += f * w_s[j];
+      for (int u = 0; u < 8; u++) {
+        if (j + u >= nsplit) break;
+        const float w = w_s[j + u];
+        a0 += w * f32x4_t{bf16_bits_to_f32((uint16_t)(v[u][0] & 0xffffu)), bf16_bits_to_f32((uint16_t)(v[u][0] >> 16)),
+                          bf16_bits_to_f32((uint16_t)(v[u][1] & 0xffffu)), bf16_bits_to_f32((uint16_t)(v[u][1] >> 16))};
+        a1 += w * f32x4_t{bf16_bits_to_f32((uint16_t)(v[u][2] & 0xffffu)), bf16_bits_to_f32((uint16_t)(v[u][2] >> 16)),
+                          bf16_bits_to_f32((uint16_t)(v[u][3] & 0xffffu)), bf16_bits_to_f32((uint16_t)(v[u][3] >> 16))};
       }
     }
-    for (; j + 8 <= nsplit; j += 8) {
-      f32x4_t v[8];
+  } else {
+    const float* op = obase + rec0 * DV + dv0;
+    const int64_t js = rstride * DV;
+    for (int j = 0; j < nsplit; j += 4) {
+      f32x4_t v[4][2];
 #pragma unroll
-      for (int u = 0; u < 8; u++) v[u] = *(const f32x4_t*)(op + (int64_t)(j + u) * DV + dv0);
+      for (int u = 0; u < 4; u++) {
+        const bool ok = j + u < nsplit;
+        v[u][0] = ok ? *(const f32x4_t*)(op + (j + u) * js) : f32x4_t{0.f, 0.f, 0.f, 0.f};
+        v[u][1] = ok ? *(const f32x4_t*)(op + (j + u) * js + 4) : f32x4_t{0.f, 0.f, 0.f, 0.f};
+      }
 #pragma unroll
-      for (int u = 0; u < 8; u++) acc += v[u] * w_s[j + u];
+      for (int u = 0; u < 4; u++) {
+        if (j + u >= nsplit) break;
+        a0 += w_s[j + u] * v[u][0];
+        a1 += w_s[j + u] * v[u][1];
+      }
     }
-    for (; j < nsplit; j++) acc += *(const f32x4_t*)(op + (int64_t)j * DV + dv0) * w_s[j];
-    const int64_t o = rh * DV + dv0;
-    if (out_dtype == SMLA_BF16) {
-      uint32_t w0 = empty ? 0x7fc07fc0u : pack_bf16x2(acc[0] * inv, acc[1] * inv);
-      uint32_t w1 = empty ? 0x7fc07fc0u : pack_bf16x2(acc[2] * inv, acc[3] * inv);
-      *(u32x2_t*)((uint16_t*)out + o) = u32x2_t{w0, w1};
+  }
+  const int64_t o = rh * DV + dv0;
+  if (out_dtype == SMLA_BF16) {
+    u32x4_t w;
+    if (empty) {
+      w = u32x4_t{0x7fc07fc0u, 0x7fc07fc0u, 0x7fc07fc0u, 0x7fc07fc0u};
     } else {
-      const float nan = __builtin_nanf("");
-      *(f32x4_t*)((float*)out + o) = empty ? f32x4_t{nan, nan, nan, nan} : acc * inv;
+      w = u32x4_t{pack_bf16x2(a0[0] * inv, a0[1] * inv), pack_bf16x2(a0[2] * inv, a0[3] * inv),
+                  pack_bf16x2(a1[0] * inv, a1[1] * inv), pack_bf16x2(a1[2] * inv, a1[3] * inv)};
     }
+    *(u32x4_t*)((uint16_t*)out + o) = w;
+  } else {
+    const float nan = __builtin_nanf("");
+    const f32x4_t n4 = {nan, nan, nan, nan};
+    *(f32x4_t*)((float*)out + o) = empty ? n4 : a0 * inv;
+    *(f32x4_t*)((float*)out + o + 4) = empty ? n4 : a1 * inv;
   }
 }
 
@@ -528,6 +540,7 @@ struct Plan {
 int g_target_wgs = 0;  // 0 = default (number of CUs); settable for tuning
 hipEvent_t g_ev_before = nullptr, g_ev_after = nullptr;  // profiling: bracket the main kernel
 bool g_main_only = false;  // profiling: launch the split kernel alone (partials, no merge)
+int g_decode_kernel = 0;   // bf16 rows: 0 = role-split score/value waves, 1 = 64-head lockstep tiles
 
 int num_cus() {
   static int n = 0;
@@ -553,7 +566,9 @@ Plan make_plan(int64_t B, int64_t S, int64_t H, int64_t D, int64_t DV, int64_t T
   if (per < 1) per = 1;
   if ((tiles + per - 1) / per > kMaxSplits) per = (tiles + kMaxSplits - 1) / kMaxSplits;
   if (per > tiles) per = tiles;
-  if (per > smla_attn::kDecodeMaxRowsPerSplit / kTileRows) per = smla_attn::kDecodeMaxRowsPerSplit / kTileRows;
+  const int max_rows = (kv_dtype == SMLA_BF16 && g_decode_kernel == 0) ? smla_attn::kDecodeV6MaxRows
+                                                                       : smla_attn::kDecodeMaxRowsPerSplit;
+  if (per > max_rows / kTileRows) per = max_rows / kTileRows;
   p.rows_per_split = (int)(per * kTileRows);
   p.nsplit = (int)((tiles + per - 1) / per);
   if (p.nsplit > kMaxSplits) p.mfma = false;  // beyond the merge kernel's capacity: generic kernel
@@ -563,7 +578,7 @@ Plan make_plan(int64_t B, int64_t S, int64_t H, int64_t D, int64_t DV, int64_t T
 int launch_merge(const Plan& p, int64_t B, int64_t S, int64_t H, const float* sink, void* out, int out_dtype,
                  void* ws, hipStream_t stream, int part_bf16) {
   if (p.nsplit > 1) {
-    hipLaunchKernelGGL(attn_merge_kernel, dim3((unsigned)(B * S * H)), dim3(128), 0, stream,
+    hipLaunchKernelGGL(attn_merge_kernel, dim3((unsigned)(B * S * H)), dim3(64), 0, stream,
                        (const float*)ws, p.nsplit, B * S, (int)H, 512, sink, out, out_dtype, part_bf16);
     SMLA_HIP_CHECK_LAUNCH();
   }
@@ -575,8 +590,16 @@ int launch_mfma(const Plan& p, const void* q, RowSrc src, const float* sink, con
                 int64_t T, int64_t B, int64_t S, int64_t H, float scale, void* out, int out_dtype,
                 void* ws, hipStream_t stream) {
   if constexpr (!FP8) {
-    int rc = smla_attn::launch_decode_bf16(D, p.nsplit, p.rows_per_split, q, src, sink, idx, T, B, S, H, scale, out,
-                                           out_dtype, (float*)ws, stream, g_ev_before, g_ev_after);
+    int rc;
+    if (g_decode_kernel == 0) {
+      if (g_ev_before) (void)hipEventRecord(g_ev_before, stream);
+      rc = smla_attn::launch_decode_v6(D, p.nsplit, p.rows_per_split, q, src, sink, idx, T, B, S, H, scale, out,
+                                       out_dtype, (float*)ws, stream);
+      if (g_ev_after) (void)hipEventRecord(g_ev_after, stream);
+    } else {
+      rc = smla_attn::launch_decode_bf16(D, p.nsplit, p.rows_per_split, q, src, sink, idx, T, B, S, H, scale, out,
+                                         out_dtype, (float*)ws, stream, g_ev_before, g_ev_after);
+    }
     if (rc != SMLA_OK || g_main_only) return rc;
     return launch_merge(p, B, S, H, sink, out, out_dtype, ws, stream, out_dtype == SMLA_BF16);
   }
@@ -656,6 +679,10 @@ extern "C" void smla_profile_set_attn_events(void* before, void* after) {
   g_ev_before = (hipEvent_t)before;
   g_ev_after = (hipEvent_t)after;
 }
+
+// tuning hook (not part of the public header): bf16-row decode kernel, 0 = role-split score/value
+// waves (default), 1 = 64-head lockstep tiles
+extern "C" void smla_set_attn_decode_kernel(int k) { g_decode_kernel = k; }
 
 // profiling hook (not part of the public header): when on, the MFMA attention path launches only
 // its split kernel (the workspace partials are written, the output is not), so that a sequence of

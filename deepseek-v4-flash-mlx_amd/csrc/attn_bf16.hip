@@ -26,13 +26,6 @@
 namespace smla_attn {
 namespace {
 
-typedef __attribute__((address_space(3))) uint8_t lds_u8_t;
-typedef short v4i16_t __attribute__((ext_vector_type(4)));
-typedef __attribute__((address_space(3))) v4i16_t lds_v4i16_t;
-typedef __attribute__((address_space(3))) u32x4_t lds_u32x4_t;
-typedef __attribute__((address_space(3))) f32x4_t lds_f32x4_t;
-typedef __attribute__((address_space(3))) int lds_i32_t;
-
 template <int D>
 struct Geo {
   static constexpr int ROWB = D * 2;                    // bytes per bf16 row
@@ -55,44 +48,6 @@ struct Geo {
     return qt * (KSTEPS / 4) + (qt < (KSTEPS % 4) ? qt : (KSTEPS % 4));
   }
 };
-
-__device__ inline void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
-
-// wait until at most n vector-memory operations of this wave are outstanding
-__device__ inline void wait_vm(int n) {
-#define SMLA_VM_CASE(N) \
-  case N:               \
-    asm volatile("s_waitcnt vmcnt(" #N ")" ::: "memory"); \
-    break;
-  switch (n) {
-    SMLA_VM_CASE(1) SMLA_VM_CASE(2) SMLA_VM_CASE(3) SMLA_VM_CASE(4) SMLA_VM_CASE(5) SMLA_VM_CASE(6)
-    SMLA_VM_CASE(7) SMLA_VM_CASE(8) SMLA_VM_CASE(9) SMLA_VM_CASE(10) SMLA_VM_CASE(11) SMLA_VM_CASE(12)
-    SMLA_VM_CASE(13) SMLA_VM_CASE(14) SMLA_VM_CASE(15) SMLA_VM_CASE(16) SMLA_VM_CASE(17) SMLA_VM_CASE(18)
-    SMLA_VM_CASE(19) SMLA_VM_CASE(20) SMLA_VM_CASE(21) SMLA_VM_CASE(22) SMLA_VM_CASE(23) SMLA_VM_CASE(24)
-    SMLA_VM_CASE(25) SMLA_VM_CASE(26) SMLA_VM_CASE(27) SMLA_VM_CASE(28) SMLA_VM_CASE(29) SMLA_VM_CASE(30)
-    SMLA_VM_CASE(31) SMLA_VM_CASE(32) SMLA_VM_CASE(33) SMLA_VM_CASE(34) SMLA_VM_CASE(35) SMLA_VM_CASE(36)
-    default:
-      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-      break;
-  }
-#undef SMLA_VM_CASE
-}
-
-// 16-byte HBM -> LDS copy for every lane: lane l's bytes land at lds_dst + 16*l.  Untracked by the
-// compiler (inline asm); callers wait with wait_vm().
-__device__ inline void dma16(const void* gsrc, uint32_t lds_dst_uniform) {
-  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds_dst_uniform), "v"(gsrc)
-               : "memory", "m0");
-}
-
-// 16-byte vector load that the compiler does not track (covered by a later wait_vm)
-__device__ inline u32x4_t load16_untracked(const void* p) {
-  u32x4_t r;
-  asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(r) : "v"(p) : "memory");
-  return r;
-}
-
-__device__ inline bf16x8_t as_bf16x8(u32x4_t v) { return __builtin_bit_cast(bf16x8_t, v); }
 
 template <int D>
 __global__ __launch_bounds__(1024, 1) void attn_decode_bf16_kernel(
@@ -147,21 +102,21 @@ __global__ __launch_bounds__(1024, 1) void attn_decode_bf16_kernel(
     if (rid < n0) return (const uint8_t*)src.kv0 + (b * n0 + rid) * (int64_t)G::ROWB;
     return (const uint8_t*)src.kv1 + (b * n1 + (rid - n0)) * (int64_t)G::ROWB;
   };
-  // DMA of one tile; instructions are dealt round-robin to the waves.  Rows past the split end
-  // are not loaded (their LDS rows are masked).  Returns this wave's instruction count.
+  // DMA of one tile; instructions are dealt round-robin to the waves.  Returns this wave's
+  // instruction count.
   auto issue_tile = [&](int tl) -> int {
     const int rows_in_tile = min(kTileRows, nrows - tl * kTileRows);
     const uint32_t tbase = lds_base + (uint32_t)((tl % G::NBUF) * G::TILE_BYTES);
     int cnt = 0;
     for (int x = wave; x < G::NDMA; x += G::NW) {
+      // rows past the split end load a real row too (masked by the softmax): every LDS value the
+      // MFMAs read must be finite, since 0 * NaN from a stale row would poison the output
       if (x < kTileRows) {
         const int r = x;
-        if (r >= rows_in_tile) continue;
-        const uint8_t* rp = row_ptr(tl * kTileRows + r);
+        const uint8_t* rp = (r < rows_in_tile) ? row_ptr(tl * kTileRows + r) : dummy;
         dma16(rp + 16 * lane, __builtin_amdgcn_readfirstlane(tbase + r * G::MSTRIDE));
       } else {
         const int r0 = (x - kTileRows) * 8;
-        if (r0 >= rows_in_tile) continue;
         const int r = r0 + (lane >> 3);
         const uint8_t* rp = (r < rows_in_tile) ? row_ptr(tl * kTileRows + r) : dummy;
         const int ch = (lane & 7) ^ (r & 7);
@@ -260,7 +215,7 @@ __global__ __launch_bounds__(1024, 1) void attn_decode_bf16_kernel(
 #pragma unroll
     for (int i = 0; i < 8; i++) {
       const float e = (m_ref > -SMLA_INF) ? __expf(x[i] - m_ref) : 0.f;
-      p[i] = bf16_bits_to_f32(f32_to_bf16_bits(e));
+      p[i] = bf16_round(e);
       l_lane += p[i];
     }
     const bf16x8_t pb = as_bf16x8(u32x4_t{pack_bf16x2(p[0], p[1]), pack_bf16x2(p[2], p[3]),
@@ -299,7 +254,7 @@ __global__ __launch_bounds__(1024, 1) void attn_decode_bf16_kernel(
       }
     }
   } else {
-    const int64_t rec = (bs * H + head) * nsplit + split;
+    const int64_t rec = (bs * nsplit + split) * H + head;  // split-major partial records
     if (g == 0 && qt == 0) {
       part[rec * 2] = m_ref;
       part[rec * 2 + 1] = l_tot;

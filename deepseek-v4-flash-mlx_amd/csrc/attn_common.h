@@ -23,7 +23,61 @@ int launch_decode_bf16(int D, int nsplit, int rows_per_split, const void* q, Row
                        const int32_t* idx, int64_t T, int64_t B, int64_t S, int64_t H, float scale, void* out,
                        int out_dtype, float* part, hipStream_t stream, hipEvent_t ev_before, hipEvent_t ev_after);
 
-// largest rows_per_split the bf16 decode kernel accepts (its index table lives in LDS)
+// bf16 rows, D in {576, 512}, DV = 512, H % 16 == 0: 12-wave role-split kernel (4 score waves,
+// 8 value waves, 64 heads per workgroup).  Same partial-state layout as launch_decode_bf16.
+int launch_decode_v6(int D, int nsplit, int rows_per_split, const void* q, RowSrc src, const float* sink,
+                     const int32_t* idx, int64_t T, int64_t B, int64_t S, int64_t H, float scale, void* out,
+                     int out_dtype, float* part, hipStream_t stream);
+constexpr int kDecodeV6MaxRows = 256;  // its index table lives in LDS beside a 4-tile ring
+
+// largest rows_per_split the bf16 decode kernels accept (its index table lives in LDS)
 constexpr int kDecodeMaxRowsPerSplit = 1024;
+
+// ---- device helpers shared by the LDS-DMA decode kernels
+typedef __attribute__((address_space(3))) uint8_t lds_u8_t;
+typedef short v4i16_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) v4i16_t lds_v4i16_t;
+typedef __attribute__((address_space(3))) u32x4_t lds_u32x4_t;
+typedef __attribute__((address_space(3))) f32x4_t lds_f32x4_t;
+typedef __attribute__((address_space(3))) int lds_i32_t;
+
+__device__ inline void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+// wait until at most n vector-memory operations of this wave are outstanding
+__device__ inline void wait_vm(int n) {
+#define SMLA_VM_CASE(N) \
+  case N:               \
+    asm volatile("s_waitcnt vmcnt(" #N ")" ::: "memory"); \
+    break;
+  switch (n) {
+    SMLA_VM_CASE(1) SMLA_VM_CASE(2) SMLA_VM_CASE(3) SMLA_VM_CASE(4) SMLA_VM_CASE(5) SMLA_VM_CASE(6)
+    SMLA_VM_CASE(7) SMLA_VM_CASE(8) SMLA_VM_CASE(9) SMLA_VM_CASE(10) SMLA_VM_CASE(11) SMLA_VM_CASE(12)
+    SMLA_VM_CASE(13) SMLA_VM_CASE(14) SMLA_VM_CASE(15) SMLA_VM_CASE(16) SMLA_VM_CASE(17) SMLA_VM_CASE(18)
+    SMLA_VM_CASE(19) SMLA_VM_CASE(20) SMLA_VM_CASE(21) SMLA_VM_CASE(22) SMLA_VM_CASE(23) SMLA_VM_CASE(24)
+    SMLA_VM_CASE(25) SMLA_VM_CASE(26) SMLA_VM_CASE(27) SMLA_VM_CASE(28) SMLA_VM_CASE(29) SMLA_VM_CASE(30)
+    SMLA_VM_CASE(31) SMLA_VM_CASE(32) SMLA_VM_CASE(33) SMLA_VM_CASE(34) SMLA_VM_CASE(35) SMLA_VM_CASE(36)
+    default:
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      break;
+  }
+#undef SMLA_VM_CASE
+}
+
+// 16-byte HBM -> LDS copy for every lane: lane l's bytes land at lds_dst + 16*l.  Untracked by the
+// compiler (inline asm); callers wait with wait_vm().
+__device__ inline void dma16(const void* gsrc, uint32_t lds_dst_uniform) {
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds_dst_uniform), "v"(gsrc)
+               : "memory", "m0");
+}
+
+// 16-byte vector load that the compiler does not track (covered by a later wait_vm)
+__device__ inline u32x4_t load16_untracked(const void* p) {
+  u32x4_t r;
+  asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(r) : "v"(p) : "memory");
+  return r;
+}
+
+__device__ inline bf16x8_t as_bf16x8(u32x4_t v) { return __builtin_bit_cast(bf16x8_t, v); }
+
 
 }  // namespace smla_attn

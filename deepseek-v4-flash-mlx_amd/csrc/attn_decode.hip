@@ -1,0 +1,387 @@
+// Split-K sparse decode attention over bf16 latent rows (ref_torch/sparse_attn.py:23-34 semantics;
+// absorbed MLA: all heads read the same 576-wide rows, so a row is fetched once for 64 heads).
+//
+// One workgroup of 12 waves per (query row, split of its index list, 64-head group).  Roles:
+//   * 4 score waves, one per 16-head group hg: S^T = K Q^T for a 32-row tile
+//     (2 x 18 v_mfma_f32_16x16x32_bf16, rows as M, heads as N, Q^T in VGPRs), then the online
+//     softmax of those 16 heads (lazy reference max) and P in bf16 to LDS, with the per-head
+//     rescale factor of the tile;
+//   * 8 value waves (head pair hp of 32 heads x value quarter dq of 128 columns):
+//     O^T = alpha * O^T + V^T P^T with v_mfma_f32_32x32x16_bf16 (value columns as M, 32 heads as
+//     N, V^T fragments by ds_read_b64_tr_b16, P^T rows straight from LDS).
+// The two roles are skewed by one tile: iteration i scores tile i while the value waves consume
+// tile i-1, so one workgroup barrier per tile suffices and no fp32 partial scores cross waves.
+//
+// Rows stream HBM -> LDS with global_load_lds_dwordx4 into a ring of 4 tiles (one instruction per
+// row for columns 0..511, one per 8 rows for the 128-byte rope tails, XOR-swizzled by row; the 36
+// instructions of a tile are dealt to the 12 waves).  A tile is requested two iterations before
+// it is scored.  The workgroup's 64 Q rows arrive the same way, laid out as two tiles of head rows
+// in the two ring slots that are free until iteration 0, so their latency overlaps the first
+// tiles' and the score waves read Q^T with the K-read pattern (free of bank conflicts).  Masked ids and rows past
+// the split load row 0, so every LDS value an MFMA reads is finite.
+//
+// Output: final rows (one split) or (m, l, O) partial states in the layout attn_merge_kernel reads.
+#include "attn_common.h"
+
+namespace smla_attn {
+namespace {
+
+typedef int32_t i32x4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) i32x4_t lds_i32x4_t;
+typedef __attribute__((address_space(3))) float lds_f32_t;
+typedef __attribute__((address_space(3))) u32x2_t lds_u32x2_t;
+
+template <int D>
+struct Geo6 {
+  static constexpr int ROWB = D * 2;                    // bytes per bf16 row
+  static constexpr bool TAIL = D > 512;
+  static constexpr int MSTRIDE = 1056;                  // LDS bytes per row, columns 0..511
+  static constexpr int MAIN_BYTES = kTileRows * MSTRIDE;        // 33792
+  static constexpr int TAIL_BYTES = TAIL ? kTileRows * 128 : 0;  // 4096
+  static constexpr int TILE_BYTES = MAIN_BYTES + TAIL_BYTES;
+  static constexpr int NBUF = 4;
+  static constexpr int PSTRIDE = 80;                    // bytes per head in a P buffer (32 rows + pad)
+  static constexpr int PBUF = 64 * PSTRIDE;
+  static constexpr int P_OFF = NBUF * TILE_BYTES;
+  static constexpr int AL_OFF = P_OFF + 2 * PBUF;        // rescale factors: 2 x 64 floats
+  static constexpr int IDS_OFF = AL_OFF + 2 * 64 * 4;
+  static constexpr int MAX_ROWS = 256;                  // rows per split (index table in LDS)
+  static constexpr int LDS_BYTES = IDS_OFF + MAX_ROWS * 4;
+  static constexpr int NW = 12;
+  static constexpr int KSTEPS = D / 32;                 // 18 / 16
+  static constexpr int NDMA = kTileRows + (TAIL ? kTileRows / 8 : 0);   // 36 / 32 per tile
+  static_assert(LDS_BYTES <= 160 * 1024, "LDS budget");
+};
+
+__device__ inline uint32_t pack2(float a, float b) { return pack_bf16x2(a, b); }
+
+// number of a tile's DMA instructions dealt to wave w (instructions w, w+12, w+24, ...)
+template <int D>
+__device__ inline int dma_count(int w) {
+  using G = Geo6<D>;
+  return (G::NDMA - w + G::NW - 1) / G::NW;
+}
+
+template <int D>
+__global__ __launch_bounds__(768) void attn_decode_kernel(
+    const uint16_t* __restrict__ q, RowSrc src, const float* __restrict__ sink, const int32_t* __restrict__ idx,
+    int T, int S, int H, int rows_per_split, float scale, float* __restrict__ part, void* __restrict__ out,
+    int out_dtype) {
+  using G = Geo6<D>;
+  extern __shared__ __align__(16) uint8_t lds_generic[];
+  lds_u8_t* lds = (lds_u8_t*)lds_generic;
+  lds_i32_t* ids_s = (lds_i32_t*)(lds + G::IDS_OFF);
+  lds_f32_t* al_s = (lds_f32_t*)(lds + G::AL_OFF);
+  const uint32_t lds_base = (uint32_t)(uintptr_t)lds;
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int split = blockIdx.x, nsplit = gridDim.x;
+  const int64_t bs = blockIdx.y;
+  const int64_t b = bs / S;
+  const int hb = blockIdx.z * 64;                 // first head of this workgroup
+  const int nh = min(64, H - hb);                 // valid heads here
+  const int t_begin = split * rows_per_split;
+  const int t_end = min(T, t_begin + rows_per_split);
+  const int nrows = max(0, t_end - t_begin);
+  const int ntiles = (nrows + kTileRows - 1) / kTileRows;
+  const int64_t n0 = src.n0, n1 = src.n1, ntot = n0 + n1;
+  const int32_t* ig = idx + bs * (int64_t)T + t_begin;
+
+  const bool scorer = wave < 4;
+  const int g = lane >> 4, c = lane & 15;
+  // ---- row ids -> LDS (-1: masked, out of range or past the split), whole tiles
+  for (int t = tid; t < ntiles * kTileRows; t += G::NW * 64) {
+    int r = -1;
+    if (t < nrows) {
+      r = ig[t];
+      r = (r >= 0 && r < ntot) ? r : -1;
+    }
+    ids_s[t] = r;
+  }
+  __syncthreads();
+
+  const uint8_t* row0 = n0 > 0 ? (const uint8_t*)src.kv0 + b * n0 * (int64_t)G::ROWB
+                               : (const uint8_t*)src.kv1 + b * n1 * (int64_t)G::ROWB;
+  auto row_ptr = [&](int rid) -> const uint8_t* {
+    const uint8_t* p0 = (const uint8_t*)src.kv0 + (b * n0 + rid) * (int64_t)G::ROWB;
+    const uint8_t* p1 = (const uint8_t*)src.kv1 + (b * n1 + (rid - n0)) * (int64_t)G::ROWB;
+    return rid < 0 ? row0 : (rid < n0 ? p0 : p1);
+  };
+  // this wave's share of the copies of one 32-row tile into ring slot `slot` (G::NDMA instructions
+  // per tile, dealt round-robin: one per row for columns 0..511, one per 8 rows for the rope tails)
+  auto issue_rows = [&](int slot, auto&& rowp) {
+    const uint32_t tbase = lds_base + (uint32_t)(slot * G::TILE_BYTES);
+#pragma unroll
+    for (int k = 0; k < 3; k++) {
+      const int x = wave + G::NW * k;
+      if (x < kTileRows) {
+        dma16(rowp(x) + 16 * lane, __builtin_amdgcn_readfirstlane(tbase + x * G::MSTRIDE));
+      } else if (x < G::NDMA) {
+        const int r0 = (x - kTileRows) * 8;
+        const int r = r0 + (lane >> 3);
+        const int ch = (lane & 7) ^ (r & 7);  // rope tails XOR-swizzled by row
+        dma16(rowp(r) + 1024 + 16 * ch, __builtin_amdgcn_readfirstlane(tbase + G::MAIN_BYTES + r0 * 128));
+      }
+    }
+  };
+  auto issue_tile = [&](int tl) {
+    const lds_i32_t* tid_s = ids_s + tl * kTileRows;
+    issue_rows(tl % G::NBUF, [&](int r) { return row_ptr(tid_s[r]); });
+  };
+  const int my_dma = dma_count<D>(wave);
+
+  // ---- prologue copies: the workgroup's 64 Q rows laid out as two tiles of head rows (slots 2-3;
+  // heads past H read head 0), then tiles 0 and 1
+  {
+    const uint8_t* qrow0 = (const uint8_t*)(q + (bs * H + hb) * (int64_t)D);
+    for (int qt = 0; qt < 2; qt++)
+      issue_rows(2 + qt, [&](int r) {
+        const int hl = 32 * qt + r;
+        return qrow0 + (hl < nh ? hl : 0) * (int64_t)G::ROWB;
+      });
+  }
+  if (ntiles > 0) issue_tile(0);
+  if (ntiles > 1) issue_tile(1);
+  wait_vm(ntiles > 1 ? my_dma : 0);  // this wave's copies of Q and of tile 0 have landed
+  lds_barrier();
+
+  // end of iteration it (same schedule in both roles): tile it+1 has landed, barrier, and the slot
+  // of the consumed tile it-1 takes tile it+3
+  auto end_iteration = [&](int it) {
+    if (it + 1 < ntiles) wait_vm(it + 2 < ntiles ? my_dma : 0);
+    lds_barrier();
+    if (it + 3 < ntiles) issue_tile(it + 3);
+  };
+  lds_f32_t* ml_s = al_s;  // (m, l) per head after the loop; the rescale buffers are free then
+  // output staging after the loop (the ring is free then): 64 head rows of 512 values in the output
+  // element type (bf16 for bf16 output or bf16 partials, else fp32), padded against bank conflicts
+  const bool out_bf16 = out_dtype == SMLA_BF16;
+  const int row_bytes = out_bf16 ? 1024 : 2048;
+  const int srow_bytes = row_bytes + 16;
+  // the workgroup's nh x 512 output block is contiguous: final rows [bs][hb..][512] or the split's
+  // partial O records [bs][split][hb..][512] (after the (m, l) records)
+  auto copy_out = [&]() {
+    uint8_t* dst = nsplit == 1
+        ? (uint8_t*)out + (bs * H + hb) * (int64_t)row_bytes
+        : (uint8_t*)(part + (int64_t)gridDim.y * H * nsplit * 2) + ((bs * nsplit + split) * (int64_t)H + hb) * row_bytes;
+    const int chunks_per_row = row_bytes / 16;
+    const int nchunks = nh * chunks_per_row;
+    for (int i = tid; i < nchunks; i += G::NW * 64) {
+      const int hr = i / chunks_per_row, ch = i - hr * chunks_per_row;
+      *(u32x4_t*)(dst + (int64_t)i * 16) = *(const lds_u32x4_t*)(lds + hr * srow_bytes + ch * 16);
+    }
+  };
+
+  if (scorer) {
+    // ---------------- score waves: head group hg = wave
+    const int hg = wave;
+    // Q^T B operand from the Q tiles: head row hg*16 + c, K-step j holds elements 32j + 8g .. +7
+    bf16x8_t qf[G::KSTEPS];
+    {
+      const lds_u8_t* qb = lds + (2 + (hg >> 1)) * G::TILE_BYTES;
+      const int qr = (hg & 1) * 16 + c;
+#pragma unroll
+      for (int j = 0; j < G::KSTEPS; j++) {
+        if (!G::TAIL || j < 16) {
+          qf[j] = as_bf16x8(*(const lds_u32x4_t*)(qb + qr * G::MSTRIDE + 16 * g + 64 * j));
+        } else {
+          const int lch = 4 * (j - 16) + g;
+          qf[j] = as_bf16x8(*(const lds_u32x4_t*)(qb + G::MAIN_BYTES + qr * 128 + 16 * (lch ^ (qr & 7))));
+        }
+      }
+    }
+    lds_barrier();  // Q slots free: they take tiles 2 and 3
+    if (ntiles > 2) issue_tile(2);
+    float m_ref = -SMLA_INF, l_lane = 0.f;
+    const int kq_off = c * G::MSTRIDE + 16 * g;  // A operand, row c (block 0)
+    for (int it = 0; it <= ntiles; it++) {
+      if (it < ntiles) {
+        const lds_u8_t* buf = lds + (it % G::NBUF) * G::TILE_BYTES;
+        // K-operand reads run PF K-steps ahead of the MFMAs
+        auto ldk = [&](int j, int blk) -> u32x4_t {
+          if (!G::TAIL || j < 16) return *(const lds_u32x4_t*)(buf + kq_off + blk * 16 * G::MSTRIDE + 64 * j);
+          const int r = 16 * blk + c, lch = 4 * (j - 16) + g;
+          return *(const lds_u32x4_t*)(buf + G::MAIN_BYTES + r * 128 + 16 * (lch ^ (r & 7)));
+        };
+        constexpr int PF = 6;
+        u32x4_t ka[PF], kb[PF];
+#pragma unroll
+        for (int j = 0; j < PF; j++) {
+          ka[j] = ldk(j, 0);
+          kb[j] = ldk(j, 1);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        f32x4_t s0 = {0.f, 0.f, 0.f, 0.f}, s1 = s0;
+#pragma unroll
+        for (int j = 0; j < G::KSTEPS; j++) {
+          const u32x4_t a0 = ka[j % PF], a1 = kb[j % PF];
+          if (j + PF < G::KSTEPS) {
+            ka[j % PF] = ldk(j + PF, 0);
+            kb[j % PF] = ldk(j + PF, 1);
+          }
+          s0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a0), qf[j], s0, 0, 0, 0);
+          s1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a1), qf[j], s1, 0, 0, 0);
+          __builtin_amdgcn_sched_barrier(0);  // keep the reads PF steps ahead of their MFMAs
+        }
+        // online softmax over rows 4g+i and 16+4g+i for head hg*16 + c
+        const lds_i32_t* tid_s = ids_s + it * kTileRows;
+        const i32x4_t v0 = *(const lds_i32x4_t*)(tid_s + 4 * g);
+        const i32x4_t v1 = *(const lds_i32x4_t*)(tid_s + 16 + 4 * g);
+        float x[8];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          x[i] = v0[i] >= 0 ? s0[i] * scale : -SMLA_INF;
+          x[4 + i] = v1[i] >= 0 ? s1[i] * scale : -SMLA_INF;
+        }
+        float mt = x[0];
+#pragma unroll
+        for (int i = 1; i < 8; i++) mt = fmaxf(mt, x[i]);
+        mt = fmaxf(mt, __shfl_xor(mt, 16, 64));
+        mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
+        float alpha = 1.f;
+        if ((mt > m_ref + kRescaleSlack) || (m_ref == -SMLA_INF && mt > -SMLA_INF)) {
+          alpha = (m_ref > -SMLA_INF) ? __expf(m_ref - mt) : 0.f;
+          l_lane *= alpha;
+          m_ref = mt;
+        }
+        float p[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+          const float e = (m_ref > -SMLA_INF) ? __expf(x[i] - m_ref) : 0.f;
+          p[i] = bf16_round(e);
+          l_lane += p[i];
+        }
+        lds_u8_t* pb = lds + G::P_OFF + (it & 1) * G::PBUF + (hg * 16 + c) * G::PSTRIDE;
+        *(lds_u32x2_t*)(pb + 8 * g) = u32x2_t{pack2(p[0], p[1]), pack2(p[2], p[3])};
+        *(lds_u32x2_t*)(pb + 32 + 8 * g) = u32x2_t{pack2(p[4], p[5]), pack2(p[6], p[7])};
+        if (g == 0) al_s[(it & 1) * 64 + hg * 16 + c] = alpha;
+      }
+      end_iteration(it);
+    }
+    // publish (m, l) per head: to LDS for the value waves' final scaling, and as the partial state
+    float l_tot = l_lane + __shfl_xor(l_lane, 16, 64);
+    l_tot += __shfl_xor(l_tot, 32, 64);
+    const int hl = hg * 16 + c;
+    if (g == 0) {
+      ml_s[hl * 2] = m_ref;
+      ml_s[hl * 2 + 1] = l_tot;
+      if (nsplit > 1 && hl < nh) {
+        const int64_t rec = (bs * nsplit + split) * (int64_t)H + hb + hl;
+        part[rec * 2] = m_ref;
+        part[rec * 2 + 1] = l_tot;
+      }
+    }
+    lds_barrier();  // (m, l) in LDS
+    lds_barrier();  // the value waves' output block is staged
+    copy_out();
+    return;
+  }
+
+  // ---------------- value waves: head pair hp (32 heads) x value quarter dq (128 columns)
+  const int vw = wave - 4;
+  const int hp = vw & 1, dq = vw >> 1;
+  lds_barrier();  // pairs with the score waves' barrier after their Q^T reads
+  if (ntiles > 2) issue_tile(2);
+  f32x16_t o[4];
+#pragma unroll
+  for (int mb = 0; mb < 4; mb++)
+#pragma unroll
+    for (int r = 0; r < 16; r++) o[mb][r] = 0.f;
+  // V^T provider address inside a 16-row K-step: group j = lane>>4 covers value columns
+  // 16*(j&1).. of a 32-column block and rows 8*(j>>1).. ; lane J = lane&15 supplies row J>>2,
+  // columns 4*(J&3)..+3
+  const int vj = lane >> 4, vJ = lane & 15;
+  const int tr_off = (8 * (vj >> 1) + (vJ >> 2)) * G::MSTRIDE + 2 * (128 * dq + 16 * (vj & 1) + 4 * (vJ & 3));
+  const int pr_off = (32 * hp + (lane & 31)) * G::PSTRIDE + 16 * (lane >> 5);  // P^T B operand
+  for (int it = 0; it <= ntiles; it++) {
+    if (it >= 1) {
+      const int tp = it - 1;  // tile consumed this iteration (scored in the previous one)
+      const lds_u8_t* buf = lds + (tp % G::NBUF) * G::TILE_BYTES;
+      const float a = al_s[(tp & 1) * 64 + 32 * hp + (lane & 31)];
+      if (__builtin_amdgcn_ballot_w64(a != 1.f)) {
+#pragma unroll
+        for (int mb = 0; mb < 4; mb++) o[mb] *= a;
+      }
+      const lds_u8_t* pb = lds + G::P_OFF + (tp & 1) * G::PBUF + pr_off;
+#pragma unroll
+      for (int ks = 0; ks < 2; ks++) {
+        const bf16x8_t pf = as_bf16x8(*(const lds_u32x4_t*)(pb + 32 * ks));
+        const lds_u8_t* vb = buf + tr_off + 16 * ks * G::MSTRIDE;
+#pragma unroll
+        for (int mb = 0; mb < 4; mb++) {
+          const v4i16_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t*)(vb + 64 * mb));
+          const v4i16_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t*)(vb + 64 * mb + 4 * G::MSTRIDE));
+          const bf16x8_t va = __builtin_bit_cast(bf16x8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+          o[mb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, pf, o[mb], 0, 0, 0);
+        }
+      }
+    }
+    end_iteration(it);
+  }
+  lds_barrier();  // the score waves' (m, l) are in LDS
+
+  // ---- epilogue: this wave's O^T block (value columns 128dq.. of 32 heads) -> LDS staging rows,
+  // then all waves copy the workgroup's contiguous output block out with 16-byte stores
+  {
+    const int hl = 32 * hp + (lane & 31);  // head within the workgroup
+    const float M = ml_s[hl * 2], L = ml_s[hl * 2 + 1];
+    const bool empty = !(M > -SMLA_INF);
+    float inv = 1.f;
+    if (nsplit == 1) {
+      const float snk = (sink && hl < nh) ? sink[hb + hl] : -SMLA_INF;
+      inv = empty ? 0.f : 1.0f / (L + __expf(snk - M));
+    }
+    const bool nan_out = nsplit == 1 && empty;
+    const int dvb = 128 * dq + 4 * (lane >> 5);  // + 32 mb + 8 qd + (r & 3)
+    lds_u8_t* srow = lds + hl * srow_bytes;
+#pragma unroll
+    for (int mb = 0; mb < 4; mb++)
+#pragma unroll
+      for (int qd = 0; qd < 4; qd++) {
+        const int dv = dvb + 32 * mb + 8 * qd;
+        const f32x4_t v = f32x4_t{o[mb][4 * qd], o[mb][4 * qd + 1], o[mb][4 * qd + 2], o[mb][4 * qd + 3]} * inv;
+        if (out_bf16) {
+          const uint32_t w0 = nan_out ? 0x7fc07fc0u : pack2(v[0], v[1]);
+          const uint32_t w1 = nan_out ? 0x7fc07fc0u : pack2(v[2], v[3]);
+          *(lds_u32x2_t*)(srow + 2 * dv) = u32x2_t{w0, w1};
+        } else {
+          const float nan = __builtin_nanf("");
+          *(lds_f32x4_t*)(srow + 4 * dv) = nan_out ? f32x4_t{nan, nan, nan, nan} : v;
+        }
+      }
+  }
+  lds_barrier();
+  copy_out();
+}
+
+template <int D>
+int launch6(int nsplit, int rows_per_split, const void* q, RowSrc src, const float* sink, const int32_t* idx,
+            int64_t T, int64_t B, int64_t S, int64_t H, float scale, void* out, int out_dtype, float* part,
+            hipStream_t stream) {
+  using G = Geo6<D>;
+  auto kern = attn_decode_kernel<D>;
+  static bool attr_set = false;
+  if (!attr_set) {
+    hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, G::LDS_BYTES);
+    if (e != hipSuccess) return (int)e;
+    attr_set = true;
+  }
+  dim3 grid((unsigned)nsplit, (unsigned)(B * S), (unsigned)((H + 63) / 64));
+  hipLaunchKernelGGL(kern, grid, dim3(G::NW * 64), G::LDS_BYTES, stream, (const uint16_t*)q, src, sink, idx, (int)T,
+                     (int)S, (int)H, rows_per_split, scale, part, out, out_dtype);
+  SMLA_HIP_CHECK_LAUNCH();
+  return SMLA_OK;
+}
+
+}  // namespace
+
+int launch_decode_v6(int D, int nsplit, int rows_per_split, const void* q, RowSrc src, const float* sink,
+                     const int32_t* idx, int64_t T, int64_t B, int64_t S, int64_t H, float scale, void* out,
+                     int out_dtype, float* part, hipStream_t stream) {
+  if (rows_per_split > kDecodeV6MaxRows || rows_per_split % kTileRows != 0 || B * S > 65535) return SMLA_E_UNSUPPORTED;
+  if (D == 576) return launch6<576>(nsplit, rows_per_split, q, src, sink, idx, T, B, S, H, scale, out, out_dtype, part, stream);
+  if (D == 512) return launch6<512>(nsplit, rows_per_split, q, src, sink, idx, T, B, S, H, scale, out, out_dtype, part, stream);
+  return SMLA_E_UNSUPPORTED;
+}
+
+}  // namespace smla_attn

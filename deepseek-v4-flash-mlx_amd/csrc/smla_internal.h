@@ -30,10 +30,18 @@ __host__ __device__ inline uint16_t f32_to_bf16_bits(float f) {
   u += 0x7fffu + ((u >> 16) & 1u);
   return (uint16_t)(u >> 16);
 }
+// device-side fp32 -> bf16, round to nearest even, with the gfx950 conversion instruction
+// (v_cvt_pk_bf16_f32, two values per instruction).  The software form above, whose NaN test
+// becomes divergent control flow, is kept for host code.
+typedef float smla_f32x2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 smla_bf16x2_t __attribute__((ext_vector_type(2)));
 // pack two fp32 into two bf16 (lo in bits 0..15)
 __device__ inline uint32_t pack_bf16x2(float lo, float hi) {
-  return (uint32_t)f32_to_bf16_bits(lo) | ((uint32_t)f32_to_bf16_bits(hi) << 16);
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((smla_f32x2_t){lo, hi}, smla_bf16x2_t));
 }
+__device__ inline uint16_t bf16_rne(float f) { return (uint16_t)(pack_bf16x2(f, 0.f) & 0xffffu); }
+// fp32 rounded to the nearest bf16 value, back in fp32
+__device__ inline float bf16_round(float f) { return __uint_as_float(pack_bf16x2(0.f, f) & 0xffff0000u); }
 
 // ---------------------------------------------------------------------------------------------
 // fp8 e4m3fn (OCP): decode and round-to-nearest-even encode, integer arithmetic only.
@@ -121,7 +129,7 @@ __device__ inline float load_as_f32(const void* p, int64_t i, int dtype) {
 }
 __device__ inline void store_from_f32(void* p, int64_t i, int dtype, float v) {
   if (dtype == SMLA_F32) ((float*)p)[i] = v;
-  else if (dtype == SMLA_BF16) ((uint16_t*)p)[i] = f32_to_bf16_bits(v);
+  else if (dtype == SMLA_BF16) ((uint16_t*)p)[i] = bf16_rne(v);
   else if (dtype == SMLA_F16) ((_Float16*)p)[i] = (_Float16)v;
 }
 

@@ -44,6 +44,7 @@ _TUNING = {
     "smla_set_attn_target_wgs": (None, [_int]),
     "smla_profile_set_attn_events": (None, [_vp, _vp]),
     "smla_profile_set_attn_main_only": (None, [_int]),
+    "smla_set_attn_decode_kernel": (None, [_int]),
     "smla_attn_plan": (None, [_i64, _i64, _i64, _i64, _i64, _i64, _int, _int, ctypes.POINTER(_int),
                               ctypes.POINTER(_int)]),
 }

@@ -38,6 +38,18 @@ def _lib():
     return _lib.lib()
 
 
+@pytest.fixture(params=[0, 1], ids=["role_split", "lockstep64"])
+def decode_kernel(request):
+    """Both bf16-row decode kernels: score/value role-split waves (the default) and the 64-head
+    lockstep-tile kernel."""
+    lib = _lib()
+    lib.smla_set_attn_decode_kernel(request.param)
+    try:
+        yield request.param
+    finally:
+        lib.smla_set_attn_decode_kernel(0)
+
+
 def test_fp32_generic_path_small(dev):
     from smla import sparse_attn as ssa
     g = torch.Generator().manual_seed(0)
@@ -62,9 +74,9 @@ def test_fp32_generic_path_small(dev):
     (3, 1, 32, 96, 256, 0, True, 512, 10.0),
     (1, 1, 48, 1000, 3000, 0, False, 576, 30.0),
 ])
-def test_bf16_mfma_vs_oracle(dev, B, S, H, T, n0, n1, use_sink, D, sharp):
+def test_bf16_mfma_vs_oracle(dev, decode_kernel, B, S, H, T, n0, n1, use_sink, D, sharp):
     from smla import sparse_attn as ssa
-    announce(f"bf16 mfma B={B} S={S} H={H} T={T} n0={n0} n1={n1} D={D} sharp={sharp}")
+    announce(f"bf16 mfma kernel={decode_kernel} B={B} S={S} H={H} T={T} n0={n0} n1={n1} D={D} sharp={sharp}")
     g = torch.Generator().manual_seed(B * 1000 + T)
     q = (torch.randn(B, S, H, D, generator=g) * 0.05 * sharp).to(torch.bfloat16)
     kv0 = (torch.randn(B, n0, D, generator=g) * 0.5).to(torch.bfloat16)
@@ -83,7 +95,7 @@ def test_bf16_mfma_vs_oracle(dev, B, S, H, T, n0, n1, use_sink, D, sharp):
     _check_bf16(out, ref, "bf16 mfma")
 
 
-def test_bf16_split_plans_agree(dev):
+def test_bf16_split_plans_agree(dev, decode_kernel):
     """Every split count (1 = direct epilogue, many = LSE merge) gives the oracle's answer."""
     from smla import sparse_attn as ssa
     g = torch.Generator().manual_seed(7)
@@ -95,7 +107,7 @@ def test_bf16_split_plans_agree(dev):
     lib = _lib()
     try:
         for target in (1, 2, 37, 256, 4096):
-            announce(f"split plan target={target}")
+            announce(f"split plan kernel={decode_kernel} target={target}")
             lib.smla_set_attn_target_wgs(target)
             out = ssa.sparse_attn_batched(q.to(dev), kv.to(dev), None, idx.to(dev), D ** -0.5, dv=512)
             _check_bf16(out, ref, f"target {target}")
