@@ -438,88 +438,102 @@ __global__ __launch_bounds__(kThreads, 1) void attn_mfma_kernel(
 // once into LDS, then every thread streams its float4 of each split's partial output with
 // independent (unrolled) loads.
 constexpr int kMaxSplits = 1024;
-// One wave per (query row, head): the nsplit partial states (m_j, l_j, O_j) of that head, stored
-// split-major ([row][split][head], so each split kernel writes one contiguous block), merge as
+// One workgroup of 8 waves per (query row, head): the nsplit partial states (m_j, l_j, O_j) of that
+// head, stored split-major ([row][split][head], so each split kernel writes one contiguous
+// block), merge as
 //   M = max m_j,  w_j = exp(m_j - M),  O = sum w_j O_j / (sum w_j l_j + exp(sink - M)).
-// Lane l owns value columns 8l .. 8l+7 (DV = 512); the split loads are issued 8 at a time.
-__global__ __launch_bounds__(64) void attn_merge_kernel(const float* __restrict__ part, int nsplit,
-                                                        int64_t BS, int H, int DV,
-                                                        const float* __restrict__ sink,
-                                                        void* __restrict__ out, int out_dtype, int part_bf16) {
-  __shared__ float w_s[kMaxSplits];
-  const int lane = threadIdx.x;
+// Wave w sums the splits w, w+8, ... (lane l owns value columns 8l .. 8l+7, DV = 512), so many
+// waves per CU keep loads in flight; the 8 partial sums meet in LDS.
+constexpr int kMergeWaves = 8;
+__global__ __launch_bounds__(kMergeWaves * 64) void attn_merge_kernel(const float* __restrict__ part, int nsplit,
+                                                                      int64_t BS, int H, int DV,
+                                                                      const float* __restrict__ sink,
+                                                                      void* __restrict__ out, int out_dtype,
+                                                                      int part_bf16) {
+  __shared__ __align__(16) f32x4_t red[kMergeWaves][64][2];
+  __shared__ float lsum[kMergeWaves];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int64_t rh = blockIdx.x;  // bs*H + head
   const int64_t bs = rh / H;
   const int head = (int)(rh % H);
-  const int64_t rstride = H;                              // records between consecutive splits
-  const int64_t rec0 = bs * nsplit * (int64_t)H + head;  // record of split 0
+  const int64_t rec0 = bs * nsplit * (int64_t)H + head;  // record of split 0; splits are H records apart
   const float* ml = part + rec0 * 2;
+  // every wave finds M itself (nsplit values, cached)
   float mx = -SMLA_INF;
-  for (int j = lane; j < nsplit; j += 64) mx = fmaxf(mx, ml[j * rstride * 2]);
+  for (int j = lane; j < nsplit; j += 64) mx = fmaxf(mx, ml[(int64_t)j * H * 2]);
   const float M = wave_max(mx);
   const bool empty = !(M > -SMLA_INF);
-  float ls = 0.f;
-  for (int j = lane; j < nsplit; j += 64) {
-    const float mj = ml[j * rstride * 2];
-    const float w = (mj > -SMLA_INF) ? __expf(mj - M) : 0.f;
-    w_s[j] = w;
-    ls += w * ml[j * rstride * 2 + 1];
-  }
-  float L = wave_sum(ls);
-  __syncthreads();
-  const float snk = sink ? sink[head] : -SMLA_INF;
-  if (!empty) L += __expf(snk - M);
-  const float inv = 1.0f / L;
   const int dv0 = lane * 8;
   const float* obase = part + BS * H * nsplit * 2;
   f32x4_t a0 = {0.f, 0.f, 0.f, 0.f}, a1 = a0;
-  if (part_bf16) {
-    const uint16_t* op = (const uint16_t*)obase + rec0 * DV + dv0;
-    const int64_t js = rstride * DV;
-    int j = 0;
-    for (; j < nsplit; j += 8) {
-      u32x4_t v[8];
+  float ls = 0.f;
+  constexpr int U = 4;
+  for (int j0 = wave; j0 < nsplit; j0 += kMergeWaves * U) {
+    float w[U];
 #pragma unroll
-      for (int u = 0; u < 8; u++) v[u] = (j + u < nsplit) ? *(const u32x4_t*)(op + (j + u) * js) : u32x4_t{0u, 0u, 0u, 0u};
-#pragma unroll
-      for (int u = 0; u < 8; u++) {
-        if (j + u >= nsplit) break;
-        const float w = w_s[j + u];
-        a0 += w * f32x4_t{bf16_bits_to_f32((uint16_t)(v[u][0] & 0xffffu)), bf16_bits_to_f32((uint16_t)(v[u][0] >> 16)),
-                          bf16_bits_to_f32((uint16_t)(v[u][1] & 0xffffu)), bf16_bits_to_f32((uint16_t)(v[u][1] >> 16))};
-        a1 += w * f32x4_t{bf16_bits_to_f32((uint16_t)(v[u][2] & 0xffffu)), bf16_bits_to_f32((uint16_t)(v[u][2] >> 16)),
-                          bf16_bits_to_f32((uint16_t)(v[u][3] & 0xffffu)), bf16_bits_to_f32((uint16_t)(v[u][3] >> 16))};
-      }
+    for (int u = 0; u < U; u++) {
+      const int j = j0 + u * kMergeWaves;
+      const float mj = j < nsplit ? ml[(int64_t)j * H * 2] : -SMLA_INF;
+      w[u] = (mj > -SMLA_INF) ? __expf(mj - M) : 0.f;
+      if (j < nsplit) ls += w[u] * ml[(int64_t)j * H * 2 + 1];
     }
-  } else {
-    const float* op = obase + rec0 * DV + dv0;
-    const int64_t js = rstride * DV;
-    for (int j = 0; j < nsplit; j += 4) {
-      f32x4_t v[4][2];
+    if (part_bf16) {
+      u32x4_t v[U];
 #pragma unroll
-      for (int u = 0; u < 4; u++) {
-        const bool ok = j + u < nsplit;
-        v[u][0] = ok ? *(const f32x4_t*)(op + (j + u) * js) : f32x4_t{0.f, 0.f, 0.f, 0.f};
-        v[u][1] = ok ? *(const f32x4_t*)(op + (j + u) * js + 4) : f32x4_t{0.f, 0.f, 0.f, 0.f};
+      for (int u = 0; u < U; u++) {
+        const int j = j0 + u * kMergeWaves;
+        v[u] = j < nsplit ? *(const u32x4_t*)((const uint16_t*)obase + (rec0 + (int64_t)j * H) * DV + dv0)
+                          : u32x4_t{0u, 0u, 0u, 0u};
       }
 #pragma unroll
-      for (int u = 0; u < 4; u++) {
-        if (j + u >= nsplit) break;
-        a0 += w_s[j + u] * v[u][0];
-        a1 += w_s[j + u] * v[u][1];
+      for (int u = 0; u < U; u++) {
+        a0 += w[u] * f32x4_t{bf16_bits_to_f32((uint16_t)(v[u][0] & 0xffffu)), bf16_bits_to_f32((uint16_t)(v[u][0] >> 16)),
+                             bf16_bits_to_f32((uint16_t)(v[u][1] & 0xffffu)), bf16_bits_to_f32((uint16_t)(v[u][1] >> 16))};
+        a1 += w[u] * f32x4_t{bf16_bits_to_f32((uint16_t)(v[u][2] & 0xffffu)), bf16_bits_to_f32((uint16_t)(v[u][2] >> 16)),
+                             bf16_bits_to_f32((uint16_t)(v[u][3] & 0xffffu)), bf16_bits_to_f32((uint16_t)(v[u][3] >> 16))};
+      }
+    } else {
+      f32x4_t v[U][2];
+#pragma unroll
+      for (int u = 0; u < U; u++) {
+        const int j = j0 + u * kMergeWaves;
+        const float* op = obase + (rec0 + (int64_t)j * H) * DV + dv0;
+        v[u][0] = j < nsplit ? *(const f32x4_t*)op : f32x4_t{0.f, 0.f, 0.f, 0.f};
+        v[u][1] = j < nsplit ? *(const f32x4_t*)(op + 4) : f32x4_t{0.f, 0.f, 0.f, 0.f};
+      }
+#pragma unroll
+      for (int u = 0; u < U; u++) {
+        a0 += w[u] * v[u][0];
+        a1 += w[u] * v[u][1];
       }
     }
   }
+  red[wave][lane][0] = a0;
+  red[wave][lane][1] = a1;
+  // ls: this wave's share of sum w_j l_j (identical in every lane: all lanes walk the same splits)
+  if (lane == 0) lsum[wave] = ls;
+  __syncthreads();
+  if (wave != 0) return;
+  float L = 0.f;
+#pragma unroll
+  for (int w = 0; w < kMergeWaves; w++) {
+    a0 = w == 0 ? red[0][lane][0] : a0 + red[w][lane][0];
+    a1 = w == 0 ? red[0][lane][1] : a1 + red[w][lane][1];
+    L += lsum[w];
+  }
+  const float snk = sink ? sink[head] : -SMLA_INF;
+  if (!empty) L += __expf(snk - M);
+  const float inv = 1.0f / L;
   const int64_t o = rh * DV + dv0;
   if (out_dtype == SMLA_BF16) {
-    u32x4_t w;
+    u32x4_t wv;
     if (empty) {
-      w = u32x4_t{0x7fc07fc0u, 0x7fc07fc0u, 0x7fc07fc0u, 0x7fc07fc0u};
+      wv = u32x4_t{0x7fc07fc0u, 0x7fc07fc0u, 0x7fc07fc0u, 0x7fc07fc0u};
     } else {
-      w = u32x4_t{pack_bf16x2(a0[0] * inv, a0[1] * inv), pack_bf16x2(a0[2] * inv, a0[3] * inv),
-                  pack_bf16x2(a1[0] * inv, a1[1] * inv), pack_bf16x2(a1[2] * inv, a1[3] * inv)};
+      wv = u32x4_t{pack_bf16x2(a0[0] * inv, a0[1] * inv), pack_bf16x2(a0[2] * inv, a0[3] * inv),
+                   pack_bf16x2(a1[0] * inv, a1[1] * inv), pack_bf16x2(a1[2] * inv, a1[3] * inv)};
     }
-    *(u32x4_t*)((uint16_t*)out + o) = w;
+    *(u32x4_t*)((uint16_t*)out + o) = wv;
   } else {
     const float nan = __builtin_nanf("");
     const f32x4_t n4 = {nan, nan, nan, nan};
@@ -578,7 +592,7 @@ Plan make_plan(int64_t B, int64_t S, int64_t H, int64_t D, int64_t DV, int64_t T
 int launch_merge(const Plan& p, int64_t B, int64_t S, int64_t H, const float* sink, void* out, int out_dtype,
                  void* ws, hipStream_t stream, int part_bf16) {
   if (p.nsplit > 1) {
-    hipLaunchKernelGGL(attn_merge_kernel, dim3((unsigned)(B * S * H)), dim3(64), 0, stream,
+    hipLaunchKernelGGL(attn_merge_kernel, dim3((unsigned)(B * S * H)), dim3(kMergeWaves * 64), 0, stream,
                        (const float*)ws, p.nsplit, B * S, (int)H, 512, sink, out, out_dtype, part_bf16);
     SMLA_HIP_CHECK_LAUNCH();
   }

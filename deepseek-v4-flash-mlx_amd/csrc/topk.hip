@@ -31,27 +31,17 @@ __device__ inline uint32_t desc_key(float f) {
 // block total.  `tmp` holds kWaves + 1 ints.
 __device__ inline int block_excl_scan(int v, int* tmp, int* total) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  int x = v;
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    int y = __shfl_up(x, o, 64);
-    if (lane >= o) x += y;
-  }
+  const int x = wave_incl_scan(v);
   if (lane == 63) tmp[wave] = x;
   __syncthreads();
   if (wave == 0) {
-    int t = lane < kWaves ? tmp[lane] : 0;
-    int s = t;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-      int y = __shfl_up(s, o, 64);
-      if (lane >= o) s += y;
-    }
+    const int t = lane < kWaves ? tmp[lane] : 0;
+    const int s = wave_incl_scan(t);
     if (lane < kWaves) tmp[lane] = s - t;  // exclusive wave offsets
     if (lane == kWaves - 1) tmp[kWaves] = s;
   }
   __syncthreads();
-  int res = tmp[wave] + x - v;
+  const int res = tmp[wave] + x - v;
   *total = tmp[kWaves];
   __syncthreads();
   return res;
@@ -92,6 +82,7 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(const float* __restr
   __shared__ uint32_t cand_key[kMaxCand];
   __shared__ int cand_idx[kMaxCand];
   __shared__ int s_int[4];
+  __shared__ int s_nan[kWaves];
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int64_t r = blockIdx.x;
@@ -118,10 +109,26 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(const float* __restr
   uint32_t key[PER];
   float lmin = SMLA_INF, lmax = -SMLA_INF;
   bool nan_seen = false;
+  // this thread's PER contiguous scores: 16-byte loads when the run lies inside the row and is
+  // 16-byte aligned (rows of N floats: N % 4 == 0), element loads otherwise
+  float fv[PER];
+  if (PER % 4 == 0 && (N & 3) == 0 && base + PER <= N) {
+#pragma unroll
+    for (int j = 0; j < PER; j += 4) {
+      const f32x4_t v4 = *(const f32x4_t*)(sr + base + j);
+      fv[j] = v4[0];
+      fv[j + 1] = v4[1];
+      fv[j + 2] = v4[2];
+      fv[j + 3] = v4[3];
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < PER; j++) fv[j] = base + j < N ? sr[base + j] : 0.f;
+  }
 #pragma unroll
   for (int j = 0; j < PER; j++) {
     const int64_t n = base + j;
-    const float f = n < nv ? sr[n] : 0.f;
+    const float f = fv[j];
     key[j] = n < nv ? desc_key(f) : 0xffffffffu;
     if (n < nv) {
       lmin = fminf(lmin, f);
@@ -129,27 +136,22 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(const float* __restr
       nan_seen |= f != f;
     }
   }
-  nan_seen = __syncthreads_or(nan_seen);
-  // ---- row min / max
+  // ---- row min / max (and whether a NaN is visible)
   {
-    float a = lmin, bmx = lmax;
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) {
-      a = fminf(a, __shfl_xor(a, o, 64));
-      bmx = fmaxf(bmx, __shfl_xor(bmx, o, 64));
-    }
+    const float a = wave_min_dpp(lmin), bmx = wave_max_dpp(lmax);
+    const bool wnan = __builtin_amdgcn_ballot_w64(nan_seen) != 0;
     if (lane == 0) {
       redf[wave] = a;
       redf[kWaves + wave] = bmx;
+      s_nan[wave] = wnan;
     }
     for (int i = tid; i < kBuckets; i += kTopkThreads) bhist[i] = 0;
     __syncthreads();
-    lmin = redf[0];
-    lmax = redf[kWaves];
-    for (int w = 1; w < kWaves; w++) {
-      lmin = fminf(lmin, redf[w]);
-      lmax = fmaxf(lmax, redf[kWaves + w]);
-    }
+    // every wave reduces the kWaves per-wave results itself (one LDS read per lane)
+    const int wl = lane < kWaves ? lane : 0;
+    lmin = wave_min_dpp(redf[wl]);
+    lmax = wave_max_dpp(redf[kWaves + wl]);
+    nan_seen = __builtin_amdgcn_ballot_w64(lane < kWaves && s_nan[wl] != 0) != 0;
   }
   uint32_t Kt = 0;
   int It = -1;
@@ -184,12 +186,24 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(const float* __restr
     const int cb = bhist[bb];
     if (cb <= kMaxCand) {
       // gather the boundary bucket's entries and rank them exactly
+      // candidates of the boundary bucket: per-thread count, wave offsets by scan, one LDS
+      // atomic per wave
+      int mine = 0;
+#pragma unroll
+      for (int j = 0; j < PER; j++) mine += (base + j < nv && bucket_of(key[j], lmax, bscale) == bb);
+      const int incl = wave_incl_scan(mine);
+      int wbase = 0;
+      if (lane == 63 && incl > 0) wbase = atomicAdd(&s_int[3], incl);
+      wbase = __builtin_amdgcn_readlane(wbase, 63);
+      int slot = wbase + incl - mine;
 #pragma unroll
       for (int j = 0; j < PER; j++) {
         if (base + j < nv && bucket_of(key[j], lmax, bscale) == bb) {
-          const int slot = atomicAdd(&s_int[3], 1);
-          cand_key[slot] = key[j];
-          cand_idx[slot] = (int)(base + j);
+          if (slot < kMaxCand) {
+            cand_key[slot] = key[j];
+            cand_idx[slot] = (int)(base + j);
+          }
+          slot++;
         }
       }
       __syncthreads();
@@ -238,12 +252,7 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(const float* __restr
           cc[i] = sacc;
           t4 += sacc;
         }
-        int incl = t4;
-#pragma unroll
-        for (int o = 1; o < 64; o <<= 1) {
-          const int y = __shfl_up(incl, o, 64);
-          if (lane >= o) incl += y;
-        }
+        const int incl = wave_incl_scan(t4);
         const int bef = incl - t4;
         if (bef < remaining && remaining <= incl) {
           int cum = bef;
@@ -295,7 +304,10 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(const float* __restr
 #pragma unroll
   for (int j = 0; j < PER; j++) {
     const int64_t n = base + j;
-    if ((n < nv) && (key[j] < Kt || (key[j] == Kt && n <= It))) orow[pos++] = (int32_t)n + id_offset;
+    if ((n < nv) && (key[j] < Kt || (key[j] == Kt && n <= It))) {
+      if (pos < take) orow[pos] = (int32_t)n + id_offset;
+      pos++;
+    }
   }
   for (int64_t j = take + tid; j < k; j += kTopkThreads) orow[j] = -1;
 }
