@@ -37,6 +37,8 @@ def algorithmic_attention_bytes(B, H, T, D=576, DV=512, row_bytes=1152):
     return B * T * row_bytes + B * H * D * 2 + B * H * DV * 2 + B * T * 4
 
 
+BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
+
 KERNEL_NAMES = {0: "attn_decode_kernel<576>", 1: "attn_decode_bf16_kernel<576>"}
 
 
@@ -67,6 +69,8 @@ def parse():
                     help="bf16-row decode kernel: 0 = role-split score/value waves (default), 1 = 64-head lockstep tiles")
     ap.add_argument("--target-wgs", type=int, default=0,
                     help="attention split plan: target workgroups (0 = one per CU)")
+    ap.add_argument("--no-prefill", action="store_true", help="skip the prefill MFMA-utilisation leg")
+    ap.add_argument("--prefill-reps", type=int, default=5)
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="only run a plain device copy of this many MiB, 8 times (HBM counter calibration)")
     return ap.parse_args()
@@ -83,6 +87,40 @@ def copy_calibration(mib):
         dst.copy_(src)
     torch.cuda.synchronize()
     print(json.dumps({"copy_bytes_per_launch": mib << 20, "launches": 8}), flush=True)
+
+
+def prefill_measure(dev, reps):
+    """Prefill (S=4096 queries, H=64, 576-wide bf16 rows): each query attends its 128-row raw
+    window and every causally visible block-4 compressed row.  One attention launch per pass
+    (one split per query); MFMA utilisation = algorithmic flops / time / dense bf16 peak."""
+    import torch
+    from smla import compressor as scomp
+    from smla import sparse_attn as ssa
+    from smla import workloads as wl
+    w = wl.prefill_4k()
+    H = w["q"].shape[2]
+    q = w["q"].to(dev)
+    raw = w["raw"].to(dev)
+    comp = scomp.block_mean_pool(raw, 4)
+    idx = wl.prefill_indices(4096, ratio=4, window=128, n_raw=4096)
+    pairs = int((idx >= 0).sum())                  # (query, row) pairs
+    flops = 2.0 * pairs * H * (576 + 512)
+    idx = idx[None].to(dev)
+    for _ in range(2):
+        ssa.sparse_attn_two_source(q, raw, comp, None, idx, w["scale"], dv=512)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        ssa.sparse_attn_two_source(q, raw, comp, None, idx, w["scale"], dv=512)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / reps
+    tflops = flops / (ms * 1e-3) / 1e12
+    return {"workload": "prefill_4k: S=4096 queries, H=64, raw [4096,576] + mean-pooled [1024,576] bf16, "
+                        "window 128 + causal compressed rows",
+            "ms": round(ms, 4), "flops": flops, "query_row_pairs": pairs, "tflops": round(tflops, 1),
+            "mfma_peak_tflops": BF16_PEAK_TFLOPS, "mfma_util": round(tflops / BF16_PEAK_TFLOPS, 4)}
 
 
 def cpu_baseline(w, nthreads, reps):
@@ -277,6 +315,11 @@ def main():
                 "kernel": KERNEL_NAMES[args.decode_kernel], "kernel_us": round(k_us, 3),
                 "algorithmic_bytes": alg_bytes, "nsplit": ns.value, "rows_per_split": rps.value}
 
+    prefill = None
+    if not args.no_prefill:
+        print("[bench] prefill leg", file=sys.stderr, flush=True)
+        prefill = prefill_measure(dev, args.prefill_reps)
+
     cpu = None
     if not args.no_cpu_baseline:
         ncores = len(os.sched_getaffinity(0))
@@ -305,6 +348,7 @@ def main():
                    "global_batch": B, "seq_len": 32768, "parallelism": "single GPU"},
         "roofline": roofline,
         "cpu_baseline": cpu,
+        "prefill": prefill,
         "attention_op_us": round(attn_op_us, 3),
         "rotated_copies": args.rot,
     }

@@ -580,8 +580,11 @@ Plan make_plan(int64_t B, int64_t S, int64_t H, int64_t D, int64_t DV, int64_t T
   if (per < 1) per = 1;
   if ((tiles + per - 1) / per > kMaxSplits) per = (tiles + kMaxSplits - 1) / kMaxSplits;
   if (per > tiles) per = tiles;
-  const int max_rows = (kv_dtype == SMLA_BF16 && g_decode_kernel == 0) ? smla_attn::kDecodeV6MaxRows
-                                                                       : smla_attn::kDecodeMaxRowsPerSplit;
+  // role-split kernel: short splits (<= 256 rows, 4-tile ring) unless there are enough (row,
+  // head group) items to fill the GPU without splitting, then one split of up to 8192 rows
+  const bool v6 = kv_dtype == SMLA_BF16 && g_decode_kernel == 0;
+  const int max_rows = !v6 ? smla_attn::kDecodeMaxRowsPerSplit
+                           : (rows >= target ? smla_attn::kDecodeV6MaxRows : smla_attn::kDecodeV6ShortRows);
   if (per > max_rows / kTileRows) per = max_rows / kTileRows;
   p.rows_per_split = (int)(per * kTileRows);
   p.nsplit = (int)((tiles + per - 1) / per);

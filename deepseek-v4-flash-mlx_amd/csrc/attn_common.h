@@ -28,7 +28,8 @@ int launch_decode_bf16(int D, int nsplit, int rows_per_split, const void* q, Row
 int launch_decode_v6(int D, int nsplit, int rows_per_split, const void* q, RowSrc src, const float* sink,
                      const int32_t* idx, int64_t T, int64_t B, int64_t S, int64_t H, float scale, void* out,
                      int out_dtype, float* part, hipStream_t stream);
-constexpr int kDecodeV6MaxRows = 256;  // its index table lives in LDS beside a 4-tile ring
+constexpr int kDecodeV6ShortRows = 256;  // up to here: 4-tile ring; its index table lives in LDS
+constexpr int kDecodeV6MaxRows = 8192;   // beyond: 3-tile ring and a larger index table
 
 // largest rows_per_split the bf16 decode kernels accept (its index table lives in LDS)
 constexpr int kDecodeMaxRowsPerSplit = 1024;

@@ -31,7 +31,7 @@ typedef __attribute__((address_space(3))) i32x4_t lds_i32x4_t;
 typedef __attribute__((address_space(3))) float lds_f32_t;
 typedef __attribute__((address_space(3))) u32x2_t lds_u32x2_t;
 
-template <int D>
+template <int D, int NBUF_, int MAXROWS_>
 struct Geo6 {
   static constexpr int ROWB = D * 2;                    // bytes per bf16 row
   static constexpr bool TAIL = D > 512;
@@ -39,35 +39,40 @@ struct Geo6 {
   static constexpr int MAIN_BYTES = kTileRows * MSTRIDE;        // 33792
   static constexpr int TAIL_BYTES = TAIL ? kTileRows * 128 : 0;  // 4096
   static constexpr int TILE_BYTES = MAIN_BYTES + TAIL_BYTES;
-  static constexpr int NBUF = 4;
+  static constexpr int NBUF = NBUF_;                    // ring slots (the last two stage Q first)
   static constexpr int PSTRIDE = 80;                    // bytes per head in a P buffer (32 rows + pad)
   static constexpr int PBUF = 64 * PSTRIDE;
   static constexpr int P_OFF = NBUF * TILE_BYTES;
   static constexpr int AL_OFF = P_OFF + 2 * PBUF;        // rescale factors: 2 x 64 floats
   static constexpr int IDS_OFF = AL_OFF + 2 * 64 * 4;
-  static constexpr int MAX_ROWS = 256;                  // rows per split (index table in LDS)
-  static constexpr int LDS_BYTES = IDS_OFF + MAX_ROWS * 4;
+  static constexpr int MAX_ROWS = MAXROWS_;             // rows per split (index table in LDS)
+  static constexpr int ML_OFF = IDS_OFF + MAX_ROWS * 4;  // (m, l) per head after the loop
+  static constexpr int LDS_BYTES = ML_OFF + 64 * 2 * 4;
   static constexpr int NW = 12;
   static constexpr int KSTEPS = D / 32;                 // 18 / 16
   static constexpr int NDMA = kTileRows + (TAIL ? kTileRows / 8 : 0);   // 36 / 32 per tile
+  static constexpr int STAGE_BF16 = 64 * (1024 + 16);   // output staging after the loop
+  static constexpr int STAGE_F32 = 64 * (2048 + 16);
   static_assert(LDS_BYTES <= 160 * 1024, "LDS budget");
+  static_assert(NBUF >= 3, "Q takes the last two slots; tile 0 needs one more");
+  static_assert(STAGE_BF16 <= ML_OFF, "bf16 staging below the (m, l) table");
+  static constexpr bool STAGE_F32_FITS = STAGE_F32 <= ML_OFF;
 };
 
 __device__ inline uint32_t pack2(float a, float b) { return pack_bf16x2(a, b); }
 
 // number of a tile's DMA instructions dealt to wave w (instructions w, w+12, w+24, ...)
-template <int D>
+template <class G>
 __device__ inline int dma_count(int w) {
-  using G = Geo6<D>;
   return (G::NDMA - w + G::NW - 1) / G::NW;
 }
 
-template <int D>
+template <int D, int NBUF, int MAXROWS>
 __global__ __launch_bounds__(768) void attn_decode_kernel(
     const uint16_t* __restrict__ q, RowSrc src, const float* __restrict__ sink, const int32_t* __restrict__ idx,
     int T, int S, int H, int rows_per_split, float scale, float* __restrict__ part, void* __restrict__ out,
     int out_dtype) {
-  using G = Geo6<D>;
+  using G = Geo6<D, NBUF, MAXROWS>;
   extern __shared__ __align__(16) uint8_t lds_generic[];
   lds_u8_t* lds = (lds_u8_t*)lds_generic;
   lds_i32_t* ids_s = (lds_i32_t*)(lds + G::IDS_OFF);
@@ -83,22 +88,32 @@ __global__ __launch_bounds__(768) void attn_decode_kernel(
   const int t_begin = split * rows_per_split;
   const int t_end = min(T, t_begin + rows_per_split);
   const int nrows = max(0, t_end - t_begin);
-  const int ntiles = (nrows + kTileRows - 1) / kTileRows;
+  const int ntiles_all = (nrows + kTileRows - 1) / kTileRows;
   const int64_t n0 = src.n0, n1 = src.n1, ntot = n0 + n1;
   const int32_t* ig = idx + bs * (int64_t)T + t_begin;
-
   const bool scorer = wave < 4;
   const int g = lane >> 4, c = lane & 15;
-  // ---- row ids -> LDS (-1: masked, out of range or past the split), whole tiles
-  for (int t = tid; t < ntiles * kTileRows; t += G::NW * 64) {
+
+  // ---- row ids -> LDS (-1: masked, out of range or past the split), whole tiles; the tiles
+  // past the last live id are dropped (index lists padded with -1 at the end cost nothing)
+  int last = -1;
+  for (int t = tid; t < ntiles_all * kTileRows; t += G::NW * 64) {
     int r = -1;
     if (t < nrows) {
       r = ig[t];
       r = (r >= 0 && r < ntot) ? r : -1;
     }
     ids_s[t] = r;
+    if (r >= 0) last = t;
+  }
+  {
+    const float wl = wave_max_dpp((float)last);
+    if (lane == 0) al_s[wave] = wl;  // (the rescale buffer is free until iteration 0)
   }
   __syncthreads();
+  const int last_live = (int)wave_max_dpp(lane < G::NW ? al_s[lane] : -1.f);
+  const int ntiles = (last_live + kTileRows) / kTileRows;
+  __syncthreads();  // al_s reads done before any later use
 
   const uint8_t* row0 = n0 > 0 ? (const uint8_t*)src.kv0 + b * n0 * (int64_t)G::ROWB
                                : (const uint8_t*)src.kv1 + b * n1 * (int64_t)G::ROWB;
@@ -128,31 +143,32 @@ __global__ __launch_bounds__(768) void attn_decode_kernel(
     const lds_i32_t* tid_s = ids_s + tl * kTileRows;
     issue_rows(tl % G::NBUF, [&](int r) { return row_ptr(tid_s[r]); });
   };
-  const int my_dma = dma_count<D>(wave);
+  const int my_dma = dma_count<G>(wave);
 
-  // ---- prologue copies: the workgroup's 64 Q rows laid out as two tiles of head rows (slots 2-3;
-  // heads past H read head 0), then tiles 0 and 1
+  // ---- prologue copies: the workgroup's 64 Q rows laid out as two tiles of head rows in the last
+  // two ring slots (heads past H read head 0), then tiles 0 .. NBUF-3
+  constexpr int QS = G::NBUF - 2;  // first Q slot
   {
     const uint8_t* qrow0 = (const uint8_t*)(q + (bs * H + hb) * (int64_t)D);
     for (int qt = 0; qt < 2; qt++)
-      issue_rows(2 + qt, [&](int r) {
+      issue_rows(QS + qt, [&](int r) {
         const int hl = 32 * qt + r;
         return qrow0 + (hl < nh ? hl : 0) * (int64_t)G::ROWB;
       });
   }
-  if (ntiles > 0) issue_tile(0);
-  if (ntiles > 1) issue_tile(1);
-  wait_vm(ntiles > 1 ? my_dma : 0);  // this wave's copies of Q and of tile 0 have landed
+  for (int tl = 0; tl < min(ntiles, QS); tl++) issue_tile(tl);
+  // this wave's copies of Q and of tile 0 have landed (tiles 1 .. QS-1 may still fly)
+  wait_vm(max(0, min(QS, ntiles) - 1) * my_dma);
   lds_barrier();
 
   // end of iteration it (same schedule in both roles): tile it+1 has landed, barrier, and the slot
-  // of the consumed tile it-1 takes tile it+3
+  // of the consumed tile it-1 takes tile it+NBUF-1
   auto end_iteration = [&](int it) {
-    if (it + 1 < ntiles) wait_vm(it + 2 < ntiles ? my_dma : 0);
+    if (it + 1 < ntiles) wait_vm(max(0, min(it + G::NBUF - 2, ntiles - 1) - (it + 1)) * my_dma);
     lds_barrier();
-    if (it + 3 < ntiles) issue_tile(it + 3);
+    if (it + G::NBUF - 1 < ntiles) issue_tile(it + G::NBUF - 1);
   };
-  lds_f32_t* ml_s = al_s;  // (m, l) per head after the loop; the rescale buffers are free then
+  lds_f32_t* ml_s = (lds_f32_t*)(lds + G::ML_OFF);  // (m, l) per head after the loop
   // output staging after the loop (the ring is free then): 64 head rows of 512 values in the output
   // element type (bf16 for bf16 output or bf16 partials, else fp32), padded against bank conflicts
   const bool out_bf16 = out_dtype == SMLA_BF16;
@@ -178,7 +194,7 @@ __global__ __launch_bounds__(768) void attn_decode_kernel(
     // Q^T B operand from the Q tiles: head row hg*16 + c, K-step j holds elements 32j + 8g .. +7
     bf16x8_t qf[G::KSTEPS];
     {
-      const lds_u8_t* qb = lds + (2 + (hg >> 1)) * G::TILE_BYTES;
+      const lds_u8_t* qb = lds + (QS + (hg >> 1)) * G::TILE_BYTES;
       const int qr = (hg & 1) * 16 + c;
 #pragma unroll
       for (int j = 0; j < G::KSTEPS; j++) {
@@ -190,8 +206,8 @@ __global__ __launch_bounds__(768) void attn_decode_kernel(
         }
       }
     }
-    lds_barrier();  // Q slots free: they take tiles 2 and 3
-    if (ntiles > 2) issue_tile(2);
+    lds_barrier();  // Q slots free: they take tiles QS and QS+1 in turn
+    if (ntiles > QS) issue_tile(QS);
     float m_ref = -SMLA_INF, l_lane = 0.f;
     const int kq_off = c * G::MSTRIDE + 16 * g;  // A operand, row c (block 0)
     for (int it = 0; it <= ntiles; it++) {
@@ -281,7 +297,7 @@ __global__ __launch_bounds__(768) void attn_decode_kernel(
   const int vw = wave - 4;
   const int hp = vw & 1, dq = vw >> 1;
   lds_barrier();  // pairs with the score waves' barrier after their Q^T reads
-  if (ntiles > 2) issue_tile(2);
+  if (ntiles > QS) issue_tile(QS);
   f32x16_t o[4];
 #pragma unroll
   for (int mb = 0; mb < 4; mb++)
@@ -354,12 +370,12 @@ __global__ __launch_bounds__(768) void attn_decode_kernel(
   copy_out();
 }
 
-template <int D>
+template <int D, int NBUF, int MAXROWS>
 int launch6(int nsplit, int rows_per_split, const void* q, RowSrc src, const float* sink, const int32_t* idx,
             int64_t T, int64_t B, int64_t S, int64_t H, float scale, void* out, int out_dtype, float* part,
             hipStream_t stream) {
-  using G = Geo6<D>;
-  auto kern = attn_decode_kernel<D>;
+  using G = Geo6<D, NBUF, MAXROWS>;
+  auto kern = attn_decode_kernel<D, NBUF, MAXROWS>;
   static bool attr_set = false;
   if (!attr_set) {
     hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, G::LDS_BYTES);
@@ -375,12 +391,24 @@ int launch6(int nsplit, int rows_per_split, const void* q, RowSrc src, const flo
 
 }  // namespace
 
+// rows_per_split <= 256: 4-slot ring (deeper prefetch, for the short splits of decode);
+// otherwise a 3-slot ring and an index table of up to 8192 rows (one split per query: prefill,
+// long single-sequence lists)
 int launch_decode_v6(int D, int nsplit, int rows_per_split, const void* q, RowSrc src, const float* sink,
                      const int32_t* idx, int64_t T, int64_t B, int64_t S, int64_t H, float scale, void* out,
                      int out_dtype, float* part, hipStream_t stream) {
   if (rows_per_split > kDecodeV6MaxRows || rows_per_split % kTileRows != 0 || B * S > 65535) return SMLA_E_UNSUPPORTED;
-  if (D == 576) return launch6<576>(nsplit, rows_per_split, q, src, sink, idx, T, B, S, H, scale, out, out_dtype, part, stream);
-  if (D == 512) return launch6<512>(nsplit, rows_per_split, q, src, sink, idx, T, B, S, H, scale, out, out_dtype, part, stream);
+  const bool short_split = rows_per_split <= kDecodeV6ShortRows;
+  if (D == 576)
+    return short_split ? launch6<576, 4, kDecodeV6ShortRows>(nsplit, rows_per_split, q, src, sink, idx, T, B, S, H, scale,
+                                                             out, out_dtype, part, stream)
+                       : launch6<576, 3, kDecodeV6MaxRows>(nsplit, rows_per_split, q, src, sink, idx, T, B, S, H, scale,
+                                                           out, out_dtype, part, stream);
+  if (D == 512)
+    return short_split ? launch6<512, 4, kDecodeV6ShortRows>(nsplit, rows_per_split, q, src, sink, idx, T, B, S, H, scale,
+                                                             out, out_dtype, part, stream)
+                       : launch6<512, 3, kDecodeV6MaxRows>(nsplit, rows_per_split, q, src, sink, idx, T, B, S, H, scale,
+                                                           out, out_dtype, part, stream);
   return SMLA_E_UNSUPPORTED;
 }
 
