@@ -71,6 +71,7 @@ def parse():
                     help="attention split plan: target workgroups (0 = one per CU)")
     ap.add_argument("--no-prefill", action="store_true", help="skip the prefill MFMA-utilisation leg")
     ap.add_argument("--prefill-reps", type=int, default=5)
+    ap.add_argument("--no-others", action="store_true", help="skip the other workloads and kernels")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="only run a plain device copy of this many MiB, 8 times (HBM counter calibration)")
     return ap.parse_args()
@@ -121,6 +122,109 @@ def prefill_measure(dev, reps):
                         "window 128 + causal compressed rows",
             "ms": round(ms, 4), "flops": flops, "query_row_pairs": pairs, "tflops": round(tflops, 1),
             "mfma_peak_tflops": BF16_PEAK_TFLOPS, "mfma_util": round(tflops / BF16_PEAK_TFLOPS, 4)}
+
+
+def _time_ms(fn, reps):
+    import torch
+    for _ in range(2):
+        fn()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        fn()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / reps
+
+
+def other_workloads(dev, reps):
+    """The other decode workloads and the path's remaining kernels, each timed with HIP events
+    over `reps` eager passes on resident inputs (inputs smaller than the 256 MB MALL may be served
+    from it on repeats; the block-mean pool's 377 MB are not)."""
+    import torch
+    from smla import compressor as scomp
+    from smla import indexer as sidx
+    from smla import norm_rope as snr
+    from smla import ops
+    from smla import sparse_attn as ssa
+    from smla import workloads as wl
+    res = {}
+
+    # ---- decode_64k: one sequence, 20 consecutive positions 65516..65535; per step: indexer over
+    # the (p+1)//4 visible compressed keys, window + top-2048 ids, attention, merge
+    w = wl.decode_64k()
+    raw = w["raw"].to(dev)
+    comp = scomp.block_mean_pool(raw, 4)
+    keys, ks = w["k_codes"].to(dev), w["kscale"].to(dev)
+    qi, wt, q = w["q_idx"].to(dev), w["w"].to(dev), w["q"].to(dev)
+    n_raw, k, win = raw.shape[1], w["k"], w["window"]
+    poss = [w["pos0"] + i for i in range(w["steps"])]
+    nvis = [torch.tensor([[(p + 1) // 4]], dtype=torch.int32, device=dev) for p in poss]
+    posd = [torch.tensor([p], dtype=torch.int32, device=dev) for p in poss]
+
+    def run64():
+        for i in range(w["steps"]):
+            sc = sidx.indexer_score(qi[i][None, None], keys, ks, wt[i][None, None], nvis[i])
+            idx = sidx.select_decode_indices(sc[:, 0], k, posd[i], win, n_raw)
+            ssa.sparse_attn_two_source(q[i][None], raw, comp, None, idx[:, None, :], w["scale"], dv=512)
+    ms = _time_ms(run64, max(1, reps // 4))
+    per = ms / w["steps"]
+    step_bytes = algorithmic_attention_bytes(1, 64, win + k)
+    res["decode_64k"] = {"workload": "decode_64k: B=1 H=64, raw [65536,576] + mean-pooled [16384,576] bf16, fp8 keys "
+                                     "[16384,64], 20 steps at positions 65516..65535, top-k 2048 + window 128",
+                         "tok_s": round(w["steps"] / (ms * 1e-3), 1), "ms_per_step": round(per, 4),
+                         "attention_bytes_per_step": step_bytes}
+
+    # ---- batched_fp8: 64 sequences, e4m3 rows with pow2 scales, 2048 ids each (attention + merge)
+    w = wl.batched_fp8()
+    qb, codes, scl, idxb = w["q"].to(dev), w["codes"].to(dev), w["scales"].to(dev), w["idx"].to(dev)
+    ms = _time_ms(lambda: ssa.sparse_attn_batched(qb, codes, None, idxb, w["scale"], dv=512, kv_scale=scl), reps)
+    nsel = int((w["idx"] >= 0).sum())
+    fb = nsel * 612 + 64 * 64 * 576 * 2 + 64 * 64 * 512 * 2 + nsel * 4
+    res["batched_fp8"] = {"workload": "batched_fp8: B=64 H=64, e4m3 rows (612 B with 9 fp32 pow2 scales), lengths "
+                                      "U{2048..16384}, 2048 ids per sequence",
+                          "tok_s": round(64 / (ms * 1e-3), 1), "ms": round(ms, 4), "algorithmic_bytes": fb,
+                          "achieved_gbs": round(fb / (ms * 1e-3) / 1e9, 1)}
+    del qb, codes, scl, idxb
+
+    # ---- kernels of the decode_32k step, at its shapes
+    w = wl.decode_32k()
+    raw = w["raw"].to(dev)
+    qi, keys, ks, wt = w["q_idx"].to(dev), w["k_codes"].to(dev), w["kscale"].to(dev), w["w"].to(dev)
+    B, N, Hi, Di = 8, keys.shape[1], qi.shape[2], qi.shape[3]
+    ms = _time_ms(lambda: sidx.indexer_score(qi, keys, ks, wt), reps)
+    flops = 2.0 * B * N * Hi * Di
+    res["indexer_score"] = {"shape": "B=8 Hi=64 Di=64 N=8192, bf16 q x e4m3 keys, fixed-order fp32 fma chains",
+                            "us": round(ms * 1e3, 3), "bound": "valu fp32",
+                            "achieved_tflops": round(flops / (ms * 1e-3) / 1e12, 2), "peak_tflops": 157.3,
+                            "hbm_bytes": B * N * (Di + 4) + B * N * 4}
+    sc = sidx.indexer_score(qi, keys, ks, wt)
+    pos = torch.full((B,), w["pos"], dtype=torch.int32, device=dev)
+    ms = _time_ms(lambda: sidx.select_decode_indices(sc[:, 0], w["k"], pos, w["window"], raw.shape[1]), reps)
+    res["select_decode"] = {"shape": "8 rows x 8192 scores, k=2048, window 128 (one launch)",
+                            "us": round(ms * 1e3, 3), "bound": "latency (one workgroup per row)"}
+    ms = _time_ms(lambda: scomp.block_mean_pool(raw, 4), max(2, reps // 2))
+    mb = raw.numel() * 2 + raw.numel() // 4 * 2
+    res["block_mean_pool"] = {"shape": "[8,32768,576] bf16 -> [8,8192,576]", "us": round(ms * 1e3, 3),
+                              "bytes": mb, "achieved_gbs": round(mb / (ms * 1e-3) / 1e9, 1), "peak_gbs": HBM_PEAK_GBS}
+    del raw
+    g = torch.Generator().manual_seed(7)
+    kvp = torch.randn(1, 4096, 1024, generator=g).to(dev)
+    scp = torch.randn(1, 4096, 1024, generator=g).to(dev)
+    ape = torch.randn(4, 1024, generator=g).to(dev)
+    nw = torch.rand(512, generator=g).to(dev)
+    cos_t, sin_t = snr.rope_tables(64, 65536, device=dev)
+    ms = _time_ms(lambda: ops.gated_pool_op(kvp, scp, ape, nw, cos_t, sin_t, 4, 64, 1e-6, True), reps)
+    gb = 2 * kvp.numel() * 4 + 1024 * 512 * 4 + 1024 * 32 * 4 * 2
+    res["gated_pool"] = {"shape": "kv, score [1,4096,1024] fp32 -> [1,1024,512] (overlap softmax + RMSNorm + RoPE + fp8 sim)",
+                         "us": round(ms * 1e3, 3), "bytes": gb, "achieved_gbs": round(gb / (ms * 1e-3) / 1e9, 1)}
+    x = torch.randn(8192, 576, generator=g).to(dev)
+    ms = _time_ms(lambda: ops.quant_fp8_pow2_op(x), reps)
+    qbytes = x.numel() * 4 + x.numel() + x.numel() // 64 * 4
+    res["quant_fp8_pow2"] = {"shape": "[8192,576] fp32 -> e4m3 codes + per-64 pow2 scales", "us": round(ms * 1e3, 3),
+                             "bytes": qbytes, "achieved_gbs": round(qbytes / (ms * 1e-3) / 1e9, 1)}
+    return res
 
 
 def cpu_baseline(w, nthreads, reps):
@@ -320,6 +424,11 @@ def main():
         print("[bench] prefill leg", file=sys.stderr, flush=True)
         prefill = prefill_measure(dev, args.prefill_reps)
 
+    others = None
+    if not args.no_others:
+        print("[bench] other workloads and kernels", file=sys.stderr, flush=True)
+        others = other_workloads(dev, 10)
+
     cpu = None
     if not args.no_cpu_baseline:
         ncores = len(os.sched_getaffinity(0))
@@ -349,6 +458,7 @@ def main():
         "roofline": roofline,
         "cpu_baseline": cpu,
         "prefill": prefill,
+        "other": others,
         "attention_op_us": round(attn_op_us, 3),
         "rotated_copies": args.rot,
     }

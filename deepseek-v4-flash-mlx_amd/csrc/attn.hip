@@ -458,68 +458,94 @@ __global__ __launch_bounds__(kMergeWaves * 64) void attn_merge_kernel(const floa
   const int head = (int)(rh % H);
   const int64_t rec0 = bs * nsplit * (int64_t)H + head;  // record of split 0; splits are H records apart
   const float* ml = part + rec0 * 2;
-  // every wave finds M itself (nsplit values, cached)
-  float mx = -SMLA_INF;
-  for (int j = lane; j < nsplit; j += 64) mx = fmaxf(mx, ml[(int64_t)j * H * 2]);
-  const float M = wave_max(mx);
-  const bool empty = !(M > -SMLA_INF);
   const int dv0 = lane * 8;
   const float* obase = part + BS * H * nsplit * 2;
   f32x4_t a0 = {0.f, 0.f, 0.f, 0.f}, a1 = a0;
-  float ls = 0.f;
-  constexpr int U = 4;
-  for (int j0 = wave; j0 < nsplit; j0 += kMergeWaves * U) {
-    float w[U];
+  float ls = 0.f, M = -SMLA_INF;
+  bool empty = true;
+  constexpr int U = 4;  // splits per wave per pass: wave w takes w, w+8, w+16, w+24
+  // split weights: lane j holds (m_j, l_j) when nsplit <= 64 (one round trip together with the
+  // O loads below; w_j reaches the summing wave by readlane); larger counts reread them
+  const bool reg_ml = nsplit <= 64;
+  float mj_l = -SMLA_INF, lj_l = 0.f, wl = 0.f;  // wl: weight of split `lane` (kept for all passes)
+  for (int j0 = wave, pass = 0; pass == 0 || j0 < nsplit; j0 += kMergeWaves * U, pass++) {
+    // the partial O loads go out first: they do not depend on the weights
+    u32x4_t vb[U];
+    f32x4_t vf[U][2];
 #pragma unroll
     for (int u = 0; u < U; u++) {
       const int j = j0 + u * kMergeWaves;
-      const float mj = j < nsplit ? ml[(int64_t)j * H * 2] : -SMLA_INF;
-      w[u] = (mj > -SMLA_INF) ? __expf(mj - M) : 0.f;
-      if (j < nsplit) ls += w[u] * ml[(int64_t)j * H * 2 + 1];
-    }
-    if (part_bf16) {
-      u32x4_t v[U];
-#pragma unroll
-      for (int u = 0; u < U; u++) {
-        const int j = j0 + u * kMergeWaves;
-        v[u] = j < nsplit ? *(const u32x4_t*)((const uint16_t*)obase + (rec0 + (int64_t)j * H) * DV + dv0)
-                          : u32x4_t{0u, 0u, 0u, 0u};
-      }
-#pragma unroll
-      for (int u = 0; u < U; u++) {
-        a0 += w[u] * f32x4_t{bf16_bits_to_f32((uint16_t)(v[u][0] & 0xffffu)), bf16_bits_to_f32((uint16_t)(v[u][0] >> 16)),
-                             bf16_bits_to_f32((uint16_t)(v[u][1] & 0xffffu)), bf16_bits_to_f32((uint16_t)(v[u][1] >> 16))};
-        a1 += w[u] * f32x4_t{bf16_bits_to_f32((uint16_t)(v[u][2] & 0xffffu)), bf16_bits_to_f32((uint16_t)(v[u][2] >> 16)),
-                             bf16_bits_to_f32((uint16_t)(v[u][3] & 0xffffu)), bf16_bits_to_f32((uint16_t)(v[u][3] >> 16))};
-      }
-    } else {
-      f32x4_t v[U][2];
-#pragma unroll
-      for (int u = 0; u < U; u++) {
-        const int j = j0 + u * kMergeWaves;
+      const bool ok = j < nsplit;
+      if (part_bf16) {
+        vb[u] = ok ? *(const u32x4_t*)((const uint16_t*)obase + (rec0 + (int64_t)j * H) * DV + dv0)
+                   : u32x4_t{0u, 0u, 0u, 0u};
+      } else {
         const float* op = obase + (rec0 + (int64_t)j * H) * DV + dv0;
-        v[u][0] = j < nsplit ? *(const f32x4_t*)op : f32x4_t{0.f, 0.f, 0.f, 0.f};
-        v[u][1] = j < nsplit ? *(const f32x4_t*)(op + 4) : f32x4_t{0.f, 0.f, 0.f, 0.f};
+        vf[u][0] = ok ? *(const f32x4_t*)op : f32x4_t{0.f, 0.f, 0.f, 0.f};
+        vf[u][1] = ok ? *(const f32x4_t*)(op + 4) : f32x4_t{0.f, 0.f, 0.f, 0.f};
       }
+    }
+    if (pass == 0) {
+      float mx = -SMLA_INF;
+      if (reg_ml) {
+        if (lane < nsplit) {
+          mj_l = ml[(int64_t)lane * H * 2];
+          lj_l = ml[(int64_t)lane * H * 2 + 1];
+        }
+        mx = mj_l;
+      } else {
+        for (int j = lane; j < nsplit; j += 64) mx = fmaxf(mx, ml[(int64_t)j * H * 2]);
+      }
+      M = wave_max_dpp(mx);
+      empty = !(M > -SMLA_INF);
+      if (reg_ml) {
+        wl = (mj_l > -SMLA_INF) ? __expf(mj_l - M) : 0.f;
+        // every wave forms the whole denominator itself (all lanes; identical in every wave)
+        float t = wl * lj_l;
+        t += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(t), 0xB1, 0xf, 0xf, false));
+        t += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(t), 0x4E, 0xf, 0xf, false));
+        t += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(t), 0x141, 0xf, 0xf, false));
+        t += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(t), 0x140, 0xf, 0xf, false));
+        ls = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(t), 0)) +
+             __int_as_float(__builtin_amdgcn_readlane(__float_as_int(t), 16)) +
+             __int_as_float(__builtin_amdgcn_readlane(__float_as_int(t), 32)) +
+             __int_as_float(__builtin_amdgcn_readlane(__float_as_int(t), 48));
+      }
+    }
 #pragma unroll
-      for (int u = 0; u < U; u++) {
-        a0 += w[u] * v[u][0];
-        a1 += w[u] * v[u][1];
+    for (int u = 0; u < U; u++) {
+      const int j = j0 + u * kMergeWaves;
+      float w;
+      if (reg_ml) {
+        w = j < nsplit ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wl), j)) : 0.f;
+      } else {
+        const float mj = j < nsplit ? ml[(int64_t)j * H * 2] : -SMLA_INF;
+        w = (mj > -SMLA_INF) ? __expf(mj - M) : 0.f;
+        if (j < nsplit) ls += w * ml[(int64_t)j * H * 2 + 1];
+      }
+      if (part_bf16) {
+        a0 += w * f32x4_t{bf16_bits_to_f32((uint16_t)(vb[u][0] & 0xffffu)), bf16_bits_to_f32((uint16_t)(vb[u][0] >> 16)),
+                          bf16_bits_to_f32((uint16_t)(vb[u][1] & 0xffffu)), bf16_bits_to_f32((uint16_t)(vb[u][1] >> 16))};
+        a1 += w * f32x4_t{bf16_bits_to_f32((uint16_t)(vb[u][2] & 0xffffu)), bf16_bits_to_f32((uint16_t)(vb[u][2] >> 16)),
+                          bf16_bits_to_f32((uint16_t)(vb[u][3] & 0xffffu)), bf16_bits_to_f32((uint16_t)(vb[u][3] >> 16))};
+      } else {
+        a0 += w * vf[u][0];
+        a1 += w * vf[u][1];
       }
     }
   }
+  // ls: the denominator sum w_j l_j (reg_ml: complete in every wave; else this wave's share)
   red[wave][lane][0] = a0;
   red[wave][lane][1] = a1;
-  // ls: this wave's share of sum w_j l_j (identical in every lane: all lanes walk the same splits)
   if (lane == 0) lsum[wave] = ls;
   __syncthreads();
   if (wave != 0) return;
-  float L = 0.f;
+  float L = reg_ml ? ls : 0.f;
 #pragma unroll
   for (int w = 0; w < kMergeWaves; w++) {
     a0 = w == 0 ? red[0][lane][0] : a0 + red[w][lane][0];
     a1 = w == 0 ? red[0][lane][1] : a1 + red[w][lane][1];
-    L += lsum[w];
+    if (!reg_ml) L += lsum[w];
   }
   const float snk = sink ? sink[head] : -SMLA_INF;
   if (!empty) L += __expf(snk - M);
