@@ -438,90 +438,87 @@ __global__ __launch_bounds__(kThreads, 1) void attn_mfma_kernel(
 // once into LDS, then every thread streams its float4 of each split's partial output with
 // independent (unrolled) loads.
 constexpr int kMaxSplits = 1024;
-// One workgroup of 8 waves per (query row, head): the nsplit partial states (m_j, l_j, O_j) of that
-// head, stored split-major ([row][split][head], so each split kernel writes one contiguous
-// block), merge as
+// One wave per (query row, head) and workgroup: the nsplit partial states (m_j, l_j,
+// O_j) of that head, stored split-major ([row][split][head], so each split kernel writes one
+// contiguous block), merge as
 //   M = max m_j,  w_j = exp(m_j - M),  O = sum w_j O_j / (sum w_j l_j + exp(sink - M)).
-// Wave w sums the splits w, w+8, ... (lane l owns value columns 8l .. 8l+7, DV = 512), so many
-// waves per CU keep loads in flight; the 8 partial sums meet in LDS.
-constexpr int kMergeWaves = 8;
-__global__ __launch_bounds__(kMergeWaves * 64) void attn_merge_kernel(const float* __restrict__ part, int nsplit,
+// Lane l owns value columns 8l .. 8l+7 (DV = 512).  The split loads of a wave are issued 8 at a
+// time together with the (m, l) loads, so one memory round trip covers a row's whole merge.
+constexpr int kMergeHeads = 1;  // heads (waves) per workgroup: one, so the rows spread over every CU
+__global__ __launch_bounds__(kMergeHeads * 64) void attn_merge_kernel(const float* __restrict__ part, int nsplit,
                                                                       int64_t BS, int H, int DV,
                                                                       const float* __restrict__ sink,
                                                                       void* __restrict__ out, int out_dtype,
                                                                       int part_bf16) {
-  __shared__ __align__(16) f32x4_t red[kMergeWaves][64][2];
-  __shared__ float lsum[kMergeWaves];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int64_t rh = blockIdx.x;  // bs*H + head
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t rh = (int64_t)blockIdx.x * kMergeHeads + wave;  // bs*H + head
+  if (rh >= BS * H) return;
   const int64_t bs = rh / H;
   const int head = (int)(rh % H);
   const int64_t rec0 = bs * nsplit * (int64_t)H + head;  // record of split 0; splits are H records apart
   const float* ml = part + rec0 * 2;
   const int dv0 = lane * 8;
   const float* obase = part + BS * H * nsplit * 2;
-  f32x4_t a0 = {0.f, 0.f, 0.f, 0.f}, a1 = a0;
-  float ls = 0.f, M = -SMLA_INF;
-  bool empty = true;
-  constexpr int U = 4;  // splits per wave per pass: wave w takes w, w+8, w+16, w+24
-  // split weights: lane j holds (m_j, l_j) when nsplit <= 64 (one round trip together with the
-  // O loads below; w_j reaches the summing wave by readlane); larger counts reread them
+  const int64_t jstride = (int64_t)H * DV;                 // elements between consecutive splits
   const bool reg_ml = nsplit <= 64;
-  float mj_l = -SMLA_INF, lj_l = 0.f, wl = 0.f;  // wl: weight of split `lane` (kept for all passes)
-  for (int j0 = wave, pass = 0; pass == 0 || j0 < nsplit; j0 += kMergeWaves * U, pass++) {
-    // the partial O loads go out first: they do not depend on the weights
-    u32x4_t vb[U];
-    f32x4_t vf[U][2];
+  constexpr int U = 8;
+  // batch 0 of the O loads, then the (m, l) loads (lane j: split j)
+  u32x4_t vb[U];
+  f32x4_t vf[U][2];
+  auto load_batch = [&](int j0) {
 #pragma unroll
     for (int u = 0; u < U; u++) {
-      const int j = j0 + u * kMergeWaves;
+      const int j = j0 + u;
       const bool ok = j < nsplit;
       if (part_bf16) {
-        vb[u] = ok ? *(const u32x4_t*)((const uint16_t*)obase + (rec0 + (int64_t)j * H) * DV + dv0)
-                   : u32x4_t{0u, 0u, 0u, 0u};
+        vb[u] = ok ? *(const u32x4_t*)((const uint16_t*)obase + rec0 * DV + j * jstride + dv0) : u32x4_t{0u, 0u, 0u, 0u};
       } else {
-        const float* op = obase + (rec0 + (int64_t)j * H) * DV + dv0;
+        const float* op = obase + rec0 * DV + j * jstride + dv0;
         vf[u][0] = ok ? *(const f32x4_t*)op : f32x4_t{0.f, 0.f, 0.f, 0.f};
         vf[u][1] = ok ? *(const f32x4_t*)(op + 4) : f32x4_t{0.f, 0.f, 0.f, 0.f};
       }
     }
-    if (pass == 0) {
-      float mx = -SMLA_INF;
-      if (reg_ml) {
-        if (lane < nsplit) {
-          mj_l = ml[(int64_t)lane * H * 2];
-          lj_l = ml[(int64_t)lane * H * 2 + 1];
-        }
-        mx = mj_l;
-      } else {
-        for (int j = lane; j < nsplit; j += 64) mx = fmaxf(mx, ml[(int64_t)j * H * 2]);
-      }
-      M = wave_max_dpp(mx);
-      empty = !(M > -SMLA_INF);
-      if (reg_ml) {
-        wl = (mj_l > -SMLA_INF) ? __expf(mj_l - M) : 0.f;
-        // every wave forms the whole denominator itself (all lanes; identical in every wave)
-        float t = wl * lj_l;
-        t += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(t), 0xB1, 0xf, 0xf, false));
-        t += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(t), 0x4E, 0xf, 0xf, false));
-        t += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(t), 0x141, 0xf, 0xf, false));
-        t += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(t), 0x140, 0xf, 0xf, false));
-        ls = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(t), 0)) +
-             __int_as_float(__builtin_amdgcn_readlane(__float_as_int(t), 16)) +
-             __int_as_float(__builtin_amdgcn_readlane(__float_as_int(t), 32)) +
-             __int_as_float(__builtin_amdgcn_readlane(__float_as_int(t), 48));
-      }
+  };
+  load_batch(0);
+  float mj_l = -SMLA_INF, lj_l = 0.f, mx = -SMLA_INF;
+  if (reg_ml) {
+    if (lane < nsplit) {
+      mj_l = ml[(int64_t)lane * H * 2];
+      lj_l = ml[(int64_t)lane * H * 2 + 1];
     }
+    mx = mj_l;
+  } else {
+    for (int j = lane; j < nsplit; j += 64) mx = fmaxf(mx, ml[(int64_t)j * H * 2]);
+  }
+  const float M = wave_max_dpp(mx);
+  const bool empty = !(M > -SMLA_INF);
+  float L = 0.f, wl = 0.f;
+  if (reg_ml) {
+    wl = (mj_l > -SMLA_INF) ? __expf(mj_l - M) : 0.f;
+    float t = wl * lj_l;
+    t += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(t), 0xB1, 0xf, 0xf, false));
+    t += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(t), 0x4E, 0xf, 0xf, false));
+    t += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(t), 0x141, 0xf, 0xf, false));
+    t += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(t), 0x140, 0xf, 0xf, false));
+    L = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(t), 0)) +
+        __int_as_float(__builtin_amdgcn_readlane(__float_as_int(t), 16)) +
+        __int_as_float(__builtin_amdgcn_readlane(__float_as_int(t), 32)) +
+        __int_as_float(__builtin_amdgcn_readlane(__float_as_int(t), 48));
+  }
+  f32x4_t a0 = {0.f, 0.f, 0.f, 0.f}, a1 = a0;
+  for (int j0 = 0; j0 < nsplit; j0 += U) {
+    if (j0 > 0) load_batch(j0);
 #pragma unroll
     for (int u = 0; u < U; u++) {
-      const int j = j0 + u * kMergeWaves;
+      const int j = j0 + u;
+      if (j >= nsplit) break;
       float w;
       if (reg_ml) {
-        w = j < nsplit ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wl), j)) : 0.f;
+        w = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wl), j));
       } else {
-        const float mj = j < nsplit ? ml[(int64_t)j * H * 2] : -SMLA_INF;
+        const float mj = ml[(int64_t)j * H * 2];
         w = (mj > -SMLA_INF) ? __expf(mj - M) : 0.f;
-        if (j < nsplit) ls += w * ml[(int64_t)j * H * 2 + 1];
+        L += w * ml[(int64_t)j * H * 2 + 1];
       }
       if (part_bf16) {
         a0 += w * f32x4_t{bf16_bits_to_f32((uint16_t)(vb[u][0] & 0xffffu)), bf16_bits_to_f32((uint16_t)(vb[u][0] >> 16)),
@@ -533,19 +530,6 @@ __global__ __launch_bounds__(kMergeWaves * 64) void attn_merge_kernel(const floa
         a1 += w * vf[u][1];
       }
     }
-  }
-  // ls: the denominator sum w_j l_j (reg_ml: complete in every wave; else this wave's share)
-  red[wave][lane][0] = a0;
-  red[wave][lane][1] = a1;
-  if (lane == 0) lsum[wave] = ls;
-  __syncthreads();
-  if (wave != 0) return;
-  float L = reg_ml ? ls : 0.f;
-#pragma unroll
-  for (int w = 0; w < kMergeWaves; w++) {
-    a0 = w == 0 ? red[0][lane][0] : a0 + red[w][lane][0];
-    a1 = w == 0 ? red[0][lane][1] : a1 + red[w][lane][1];
-    if (!reg_ml) L += lsum[w];
   }
   const float snk = sink ? sink[head] : -SMLA_INF;
   if (!empty) L += __expf(snk - M);
@@ -606,11 +590,10 @@ Plan make_plan(int64_t B, int64_t S, int64_t H, int64_t D, int64_t DV, int64_t T
   if (per < 1) per = 1;
   if ((tiles + per - 1) / per > kMaxSplits) per = (tiles + kMaxSplits - 1) / kMaxSplits;
   if (per > tiles) per = tiles;
-  // role-split kernel: short splits (<= 256 rows, 4-tile ring) unless there are enough (row,
-  // head group) items to fill the GPU without splitting, then one split of up to 8192 rows
-  const bool v6 = kv_dtype == SMLA_BF16 && g_decode_kernel == 0;
-  const int max_rows = !v6 ? smla_attn::kDecodeMaxRowsPerSplit
-                           : (rows >= target ? smla_attn::kDecodeV6MaxRows : smla_attn::kDecodeV6ShortRows);
+  // role-split kernel: splits of up to 8192 rows (the launcher picks the 4-tile ring for splits of
+  // at most 256 rows, a 3-tile ring with a larger index table beyond)
+  const bool v6 = (kv_dtype == SMLA_BF16 || kv_dtype == SMLA_FP8_E4M3) && g_decode_kernel == 0;
+  const int max_rows = v6 ? smla_attn::kDecodeV6MaxRows : smla_attn::kDecodeMaxRowsPerSplit;
   if (per > max_rows / kTileRows) per = max_rows / kTileRows;
   p.rows_per_split = (int)(per * kTileRows);
   p.nsplit = (int)((tiles + per - 1) / per);
@@ -621,7 +604,8 @@ Plan make_plan(int64_t B, int64_t S, int64_t H, int64_t D, int64_t DV, int64_t T
 int launch_merge(const Plan& p, int64_t B, int64_t S, int64_t H, const float* sink, void* out, int out_dtype,
                  void* ws, hipStream_t stream, int part_bf16) {
   if (p.nsplit > 1) {
-    hipLaunchKernelGGL(attn_merge_kernel, dim3((unsigned)(B * S * H)), dim3(kMergeWaves * 64), 0, stream,
+    hipLaunchKernelGGL(attn_merge_kernel, dim3((unsigned)((B * S * H + kMergeHeads - 1) / kMergeHeads)),
+                       dim3(kMergeHeads * 64), 0, stream,
                        (const float*)ws, p.nsplit, B * S, (int)H, 512, sink, out, out_dtype, part_bf16);
     SMLA_HIP_CHECK_LAUNCH();
   }
@@ -636,13 +620,19 @@ int launch_mfma(const Plan& p, const void* q, RowSrc src, const float* sink, con
     int rc;
     if (g_decode_kernel == 0) {
       if (g_ev_before) (void)hipEventRecord(g_ev_before, stream);
-      rc = smla_attn::launch_decode_v6(D, p.nsplit, p.rows_per_split, q, src, sink, idx, T, B, S, H, scale, out,
-                                       out_dtype, (float*)ws, stream);
+      rc = smla_attn::launch_decode_v6(D, false, p.nsplit, p.rows_per_split, q, src, sink, idx, T, B, S, H, scale,
+                                       out, out_dtype, (float*)ws, stream);
       if (g_ev_after) (void)hipEventRecord(g_ev_after, stream);
     } else {
       rc = smla_attn::launch_decode_bf16(D, p.nsplit, p.rows_per_split, q, src, sink, idx, T, B, S, H, scale, out,
                                          out_dtype, (float*)ws, stream, g_ev_before, g_ev_after);
     }
+    if (rc != SMLA_OK || g_main_only) return rc;
+    return launch_merge(p, B, S, H, sink, out, out_dtype, ws, stream, out_dtype == SMLA_BF16);
+  }
+  if (g_decode_kernel == 0) {  // fp8 rows on the role-split kernel
+    int rc = smla_attn::launch_decode_v6(D, true, p.nsplit, p.rows_per_split, q, src, sink, idx, T, B, S, H, scale,
+                                         out, out_dtype, (float*)ws, stream);
     if (rc != SMLA_OK || g_main_only) return rc;
     return launch_merge(p, B, S, H, sink, out, out_dtype, ws, stream, out_dtype == SMLA_BF16);
   }

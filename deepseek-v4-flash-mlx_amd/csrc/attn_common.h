@@ -23,11 +23,12 @@ int launch_decode_bf16(int D, int nsplit, int rows_per_split, const void* q, Row
                        const int32_t* idx, int64_t T, int64_t B, int64_t S, int64_t H, float scale, void* out,
                        int out_dtype, float* part, hipStream_t stream, hipEvent_t ev_before, hipEvent_t ev_after);
 
-// bf16 rows, D in {576, 512}, DV = 512, H % 16 == 0: 12-wave role-split kernel (4 score waves,
-// 8 value waves, 64 heads per workgroup).  Same partial-state layout as launch_decode_bf16.
-int launch_decode_v6(int D, int nsplit, int rows_per_split, const void* q, RowSrc src, const float* sink,
-                     const int32_t* idx, int64_t T, int64_t B, int64_t S, int64_t H, float scale, void* out,
-                     int out_dtype, float* part, hipStream_t stream);
+// bf16 or fp8 (e4m3 + per-64 pow2 scales) rows, D in {576, 512}, DV = 512, H % 16 == 0: 12-wave
+// role-split kernel (4 score waves, 8 value waves, 64 heads per workgroup).  Same partial-state
+// layout as launch_decode_bf16.
+int launch_decode_v6(int D, bool kv_fp8, int nsplit, int rows_per_split, const void* q, RowSrc src,
+                     const float* sink, const int32_t* idx, int64_t T, int64_t B, int64_t S, int64_t H, float scale,
+                     void* out, int out_dtype, float* part, hipStream_t stream);
 constexpr int kDecodeV6ShortRows = 256;  // up to here: 4-tile ring; its index table lives in LDS
 constexpr int kDecodeV6MaxRows = 8192;   // beyond: 3-tile ring and a larger index table
 

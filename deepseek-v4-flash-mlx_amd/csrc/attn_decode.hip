@@ -67,7 +67,7 @@ __device__ inline int dma_count(int w) {
   return (G::NDMA - w + G::NW - 1) / G::NW;
 }
 
-template <int D, int NBUF, int MAXROWS>
+template <int D, int NBUF, int MAXROWS, bool FP8>
 __global__ __launch_bounds__(768) void attn_decode_kernel(
     const uint16_t* __restrict__ q, RowSrc src, const float* __restrict__ sink, const int32_t* __restrict__ idx,
     int T, int S, int H, int rows_per_split, float scale, float* __restrict__ part, void* __restrict__ out,
@@ -140,10 +140,69 @@ __global__ __launch_bounds__(768) void attn_decode_kernel(
     }
   };
   auto issue_tile = [&](int tl) {
-    const lds_i32_t* tid_s = ids_s + tl * kTileRows;
-    issue_rows(tl % G::NBUF, [&](int r) { return row_ptr(tid_s[r]); });
+    if constexpr (!FP8) {
+      const lds_i32_t* tid_s = ids_s + tl * kTileRows;
+      issue_rows(tl % G::NBUF, [&](int r) { return row_ptr(tid_s[r]); });
+    }
   };
-  const int my_dma = dma_count<G>(wave);
+  const int my_dma = FP8 ? 0 : dma_count<G>(wave);  // a data tile's DMA instructions of this wave
+
+  // ---- fp8 rows (e4m3 codes + one fp32 power-of-two scale per 64 columns): the value waves load
+  // a tile's 32 x D codes into registers (16 codes per lane-chunk, chunks dealt over the 512
+  // value lanes) and write them to the ring slot as bf16 (exact: 4 significant bits times a power
+  // of two), in the layout the DMA gives bf16 rows
+  constexpr int F8_CH = D / 16;                       // 16-code chunks per row (36 / 32)
+  constexpr int F8_K = (kTileRows * F8_CH + 511) / 512;  // chunks per value lane (3 / 2)
+  struct F8Regs {
+    u32x4_t v[F8_K];
+    float s[F8_K];
+  };
+  auto f8_load = [&](int tl, F8Regs& fr) {
+    const lds_i32_t* tid_s = ids_s + tl * kTileRows;
+    const int vl = (wave - 4) * 64 + lane;
+#pragma unroll
+    for (int k = 0; k < F8_K; k++) {
+      const int ci = vl + 512 * k;
+      const int r = ci / F8_CH, cc = ci - r * F8_CH;
+      if (ci < kTileRows * F8_CH) {
+        const int rid = tid_s[r];
+        const int64_t row = rid < 0 ? (n0 > 0 ? b * n0 : b * n1) : (rid < n0 ? b * n0 + rid : b * n1 + (rid - n0));
+        const bool in0 = rid < 0 ? n0 > 0 : rid < n0;
+        const uint8_t* cp = (const uint8_t*)(in0 ? src.kv0 : src.kv1) + row * D + 16 * cc;
+        const float* sp = (in0 ? src.sc0 : src.sc1) + row * (D / 64) + (cc >> 2);
+        fr.v[k] = *(const u32x4_t*)cp;
+        fr.s[k] = *sp;
+      }
+    }
+  };
+  auto f8_store = [&](int tl, const F8Regs& fr) {
+    lds_u8_t* slot = lds + (tl % G::NBUF) * G::TILE_BYTES;
+    const int vl = (wave - 4) * 64 + lane;
+#pragma unroll
+    for (int k = 0; k < F8_K; k++) {
+      const int ci = vl + 512 * k;
+      const int r = ci / F8_CH, cc = ci - r * F8_CH;
+      if (ci < kTileRows * F8_CH) {
+        uint32_t w[8];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+          const f32x2_t lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)fr.v[k][j], false);
+          const f32x2_t hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)fr.v[k][j], true);
+          w[2 * j] = pack_bf16x2(lo.x * fr.s[k], lo.y * fr.s[k]);
+          w[2 * j + 1] = pack_bf16x2(hi.x * fr.s[k], hi.y * fr.s[k]);
+        }
+        const u32x4_t w0 = {w[0], w[1], w[2], w[3]}, w1 = {w[4], w[5], w[6], w[7]};
+        if (cc < 32) {
+          *(lds_u32x4_t*)(slot + r * G::MSTRIDE + 32 * cc) = w0;
+          *(lds_u32x4_t*)(slot + r * G::MSTRIDE + 32 * cc + 16) = w1;
+        } else {  // rope dims: 16-byte chunks 2(cc-32), 2(cc-32)+1 of the row's tail, swizzled
+          const int l0 = 2 * (cc - 32);
+          *(lds_u32x4_t*)(slot + G::MAIN_BYTES + r * 128 + 16 * (l0 ^ (r & 7))) = w0;
+          *(lds_u32x4_t*)(slot + G::MAIN_BYTES + r * 128 + 16 * ((l0 + 1) ^ (r & 7))) = w1;
+        }
+      }
+    }
+  };
 
   // ---- prologue copies: the workgroup's 64 Q rows laid out as two tiles of head rows in the last
   // two ring slots (heads past H read head 0), then tiles 0 .. NBUF-3
@@ -157,6 +216,16 @@ __global__ __launch_bounds__(768) void attn_decode_kernel(
       });
   }
   for (int tl = 0; tl < min(ntiles, QS); tl++) issue_tile(tl);
+  F8Regs f8r;  // fp8: the value waves' registers of the next tile to write
+  if constexpr (FP8) {
+    if (!scorer) {
+      for (int tl = 0; tl < min(ntiles, QS); tl++) {
+        f8_load(tl, f8r);
+        f8_store(tl, f8r);
+      }
+      if (QS < ntiles) f8_load(QS, f8r);
+    }
+  }
   // this wave's copies of Q and of tile 0 have landed (tiles 1 .. QS-1 may still fly)
   wait_vm(max(0, min(QS, ntiles) - 1) * my_dma);
   lds_barrier();
@@ -164,7 +233,9 @@ __global__ __launch_bounds__(768) void attn_decode_kernel(
   // end of iteration it (same schedule in both roles): tile it+1 has landed, barrier, and the slot
   // of the consumed tile it-1 takes tile it+NBUF-1
   auto end_iteration = [&](int it) {
-    if (it + 1 < ntiles) wait_vm(max(0, min(it + G::NBUF - 2, ntiles - 1) - (it + 1)) * my_dma);
+    if constexpr (!FP8) {
+      if (it + 1 < ntiles) wait_vm(max(0, min(it + G::NBUF - 2, ntiles - 1) - (it + 1)) * my_dma);
+    }
     lds_barrier();
     if (it + G::NBUF - 1 < ntiles) issue_tile(it + G::NBUF - 1);
   };
@@ -310,6 +381,14 @@ __global__ __launch_bounds__(768) void attn_decode_kernel(
   const int tr_off = (8 * (vj >> 1) + (vJ >> 2)) * G::MSTRIDE + 2 * (128 * dq + 16 * (vj & 1) + 4 * (vJ & 3));
   const int pr_off = (32 * hp + (lane & 31)) * G::PSTRIDE + 16 * (lane >> 5);  // P^T B operand
   for (int it = 0; it <= ntiles; it++) {
+    if constexpr (FP8) {
+      // tile it+NBUF-2 goes to the slot of tile it-2 (consumed before the last barrier); it is
+      // scored NBUF-2 iterations later.  Then the next tile's codes are requested.
+      if (it + G::NBUF - 2 < ntiles) {
+        f8_store(it + G::NBUF - 2, f8r);
+        if (it + G::NBUF - 1 < ntiles) f8_load(it + G::NBUF - 1, f8r);
+      }
+    }
     if (it >= 1) {
       const int tp = it - 1;  // tile consumed this iteration (scored in the previous one)
       const lds_u8_t* buf = lds + (tp % G::NBUF) * G::TILE_BYTES;
@@ -370,12 +449,12 @@ __global__ __launch_bounds__(768) void attn_decode_kernel(
   copy_out();
 }
 
-template <int D, int NBUF, int MAXROWS>
+template <int D, int NBUF, int MAXROWS, bool FP8>
 int launch6(int nsplit, int rows_per_split, const void* q, RowSrc src, const float* sink, const int32_t* idx,
             int64_t T, int64_t B, int64_t S, int64_t H, float scale, void* out, int out_dtype, float* part,
             hipStream_t stream) {
   using G = Geo6<D, NBUF, MAXROWS>;
-  auto kern = attn_decode_kernel<D, NBUF, MAXROWS>;
+  auto kern = attn_decode_kernel<D, NBUF, MAXROWS, FP8>;
   static bool attr_set = false;
   if (!attr_set) {
     hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, G::LDS_BYTES);
@@ -394,21 +473,23 @@ int launch6(int nsplit, int rows_per_split, const void* q, RowSrc src, const flo
 // rows_per_split <= 256: 4-slot ring (deeper prefetch, for the short splits of decode);
 // otherwise a 3-slot ring and an index table of up to 8192 rows (one split per query: prefill,
 // long single-sequence lists)
-int launch_decode_v6(int D, int nsplit, int rows_per_split, const void* q, RowSrc src, const float* sink,
-                     const int32_t* idx, int64_t T, int64_t B, int64_t S, int64_t H, float scale, void* out,
-                     int out_dtype, float* part, hipStream_t stream) {
+int launch_decode_v6(int D, bool kv_fp8, int nsplit, int rows_per_split, const void* q, RowSrc src,
+                     const float* sink, const int32_t* idx, int64_t T, int64_t B, int64_t S, int64_t H, float scale,
+                     void* out, int out_dtype, float* part, hipStream_t stream) {
   if (rows_per_split > kDecodeV6MaxRows || rows_per_split % kTileRows != 0 || B * S > 65535) return SMLA_E_UNSUPPORTED;
-  const bool short_split = rows_per_split <= kDecodeV6ShortRows;
-  if (D == 576)
-    return short_split ? launch6<576, 4, kDecodeV6ShortRows>(nsplit, rows_per_split, q, src, sink, idx, T, B, S, H, scale,
-                                                             out, out_dtype, part, stream)
-                       : launch6<576, 3, kDecodeV6MaxRows>(nsplit, rows_per_split, q, src, sink, idx, T, B, S, H, scale,
-                                                           out, out_dtype, part, stream);
-  if (D == 512)
-    return short_split ? launch6<512, 4, kDecodeV6ShortRows>(nsplit, rows_per_split, q, src, sink, idx, T, B, S, H, scale,
-                                                             out, out_dtype, part, stream)
-                       : launch6<512, 3, kDecodeV6MaxRows>(nsplit, rows_per_split, q, src, sink, idx, T, B, S, H, scale,
-                                                           out, out_dtype, part, stream);
+  const bool sh = rows_per_split <= kDecodeV6ShortRows;
+#define SMLA_V6(DD, F8)                                                                                           \
+  return sh ? launch6<DD, 4, kDecodeV6ShortRows, F8>(nsplit, rows_per_split, q, src, sink, idx, T, B, S, H, scale, \
+                                                     out, out_dtype, part, stream)                                 \
+            : launch6<DD, 3, kDecodeV6MaxRows, F8>(nsplit, rows_per_split, q, src, sink, idx, T, B, S, H, scale,   \
+                                                   out, out_dtype, part, stream);
+  if (D == 576) {
+    if (kv_fp8) SMLA_V6(576, true) else SMLA_V6(576, false)
+  }
+  if (D == 512) {
+    if (kv_fp8) SMLA_V6(512, true) else SMLA_V6(512, false)
+  }
+#undef SMLA_V6
   return SMLA_E_UNSUPPORTED;
 }
 

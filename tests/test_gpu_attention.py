@@ -131,21 +131,24 @@ def test_all_masked_rows_are_nan(dev):
     assert torch.isnan(out32[1]).all() and not torch.isnan(out32[0]).any()
 
 
-@pytest.mark.parametrize("B,T,n,sharp", [(1, 64, 200, 1.0), (3, 700, 2000, 40.0), (2, 2048, 2048, 1.0)])
-def test_fp8_rows_vs_oracle(dev, B, T, n, sharp):
+@pytest.mark.parametrize("B,T,n,sharp,H,D", [(1, 64, 200, 1.0, 64, 576), (3, 700, 2000, 40.0, 64, 576),
+                                           (2, 2048, 2048, 1.0, 64, 576), (2, 333, 900, 10.0, 48, 576),
+                                           (2, 300, 500, 5.0, 64, 512)])
+def test_fp8_rows_vs_oracle(dev, decode_kernel, B, T, n, sharp, H, D):
     from smla import sparse_attn as ssa
     from smla import workloads as wl
-    announce(f"fp8 rows B={B} T={T} n={n}")
+    announce(f"fp8 rows kernel={decode_kernel} B={B} T={T} n={n} H={H} D={D}")
     g = torch.Generator().manual_seed(T)
-    q = (torch.randn(B, 1, 64, 576, generator=g) * 0.05 * sharp).to(torch.bfloat16)
-    x = torch.randn(B, n, 576, generator=g) * 0.05
+    q = (torch.randn(B, 1, H, D, generator=g) * 0.05 * sharp).to(torch.bfloat16)
+    x = torch.randn(B, n, D, generator=g) * 0.05
     codes, scales = wl.quant_e4m3_pow2(x)
     idx = torch.randint(0, n, (B, 1, T), generator=g, dtype=torch.int32)
     idx[..., :3] = -1
-    out = ssa.sparse_attn_batched(q.to(dev), codes.to(dev), None, idx.to(dev), 576 ** -0.5, dv=512,
+    idx[..., -2:] = -1
+    out = ssa.sparse_attn_batched(q.to(dev), codes.to(dev), None, idx.to(dev), D ** -0.5, dv=512,
                                   kv_scale=scales.to(dev))
     rows = wl.dequant_e4m3(codes, scales)
-    ref = _oracle_two_source(q, rows, None, None, idx, 576 ** -0.5, 512)
+    ref = _oracle_two_source(q, rows, None, None, idx, D ** -0.5, 512)
     _check_bf16(out, ref, "fp8 rows")
 
 
