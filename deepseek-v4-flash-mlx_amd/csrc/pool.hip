@@ -13,7 +13,7 @@
 //                        epilogue, RoPE position pos+1-r), append it to the compressed cache and
 //                        shift the ring.  One workgroup per sequence; no host synchronisation.
 //  * quant_kernel      : act_quant_sim's stored form (v4mlx/compressor.py:11-20): per 64-block pow2
-//                        scale and e4m3 codes, one wave per block-row.
+//                        scale and e4m3 codes, 16 lanes per block.
 #include "smla_internal.h"
 
 namespace {
@@ -230,37 +230,50 @@ __global__ __launch_bounds__(kPoolThreads) void ring_step_kernel(
   }
 }
 
-// one thread per 64-element block
-__global__ void quant_kernel(const void* __restrict__ x, int x_dtype, int64_t nblocks, uint8_t* __restrict__ codes,
-                             float* __restrict__ scales) {
-  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= nblocks) return;
-  float v[64];
-  float a = 0.f;
-#pragma unroll
-  for (int j = 0; j < 64; j++) {
-    v[j] = load_as_f32(x, i * 64 + j, x_dtype);
-    a = fmaxf(a, fabsf(v[j]));
-  }
-  a = fmaxf(a, 1e-4f);
-  float s = pow2_ceil(a / 448.0f);
-  scales[i] = s;
-  u32x4_t* dst = (u32x4_t*)(codes + i * 64);
-#pragma unroll
-  for (int q = 0; q < 4; q++) {
-    u32x4_t w;
-#pragma unroll
-    for (int k = 0; k < 4; k++) {
-      uint32_t word = 0;
-#pragma unroll
-      for (int by = 0; by < 4; by++) {
-        float z = fminf(fmaxf(v[16 * q + 4 * k + by] / s, -448.f), 448.f);
-        word |= f32_to_e4m3(z) << (8 * by);
-      }
-      w[k] = word;
+// 16 lanes per 64-element block (one DPP row), 4 elements per lane: vector loads, the block's
+// abs-max by row reduction, x * (1/s) (exact: s is a power of two, so the product equals x / s),
+// clamp to +-448, e4m3 round-to-nearest-even in integer arithmetic
+template <int XDT>
+__global__ __launch_bounds__(256) void quant_kernel(const void* __restrict__ x, int64_t nblocks,
+                                                    uint8_t* __restrict__ codes, float* __restrict__ scales) {
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t blk = t >> 4;
+  const int sub = (int)(t & 15);
+  const bool ok = blk < nblocks;
+  const int64_t e0 = blk * 64 + sub * 4;
+  float v[4] = {0.f, 0.f, 0.f, 0.f};
+  if (ok) {
+    if constexpr (XDT == SMLA_F32) {
+      const f32x4_t w = *(const f32x4_t*)((const float*)x + e0);
+      v[0] = w[0];
+      v[1] = w[1];
+      v[2] = w[2];
+      v[3] = w[3];
+    } else {
+      const u32x2_t w = *(const u32x2_t*)((const uint16_t*)x + e0);
+      v[0] = bf16_bits_to_f32((uint16_t)(w[0] & 0xffffu));
+      v[1] = bf16_bits_to_f32((uint16_t)(w[0] >> 16));
+      v[2] = bf16_bits_to_f32((uint16_t)(w[1] & 0xffffu));
+      v[3] = bf16_bits_to_f32((uint16_t)(w[1] >> 16));
     }
-    dst[q] = w;
   }
+  float a = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+  a = fmaxf(a, dpp_f<0xB1>(a));
+  a = fmaxf(a, dpp_f<0x4E>(a));
+  a = fmaxf(a, dpp_f<0x141>(a));
+  a = fmaxf(a, dpp_f<0x140>(a));  // every lane of the 16-lane row: the block's abs-max
+  a = fmaxf(a, 1e-4f);
+  const float s = pow2_ceil(a / 448.0f);
+  const float inv = 1.0f / s;
+  if (!ok) return;
+  uint32_t word = 0;
+#pragma unroll
+  for (int by = 0; by < 4; by++) {
+    const float z = fminf(fmaxf(v[by] * inv, -448.f), 448.f);
+    word |= f32_to_e4m3(z) << (8 * by);
+  }
+  *(uint32_t*)(codes + e0) = word;
+  if (sub == 0) scales[blk] = s;
 }
 
 }  // namespace
@@ -330,9 +343,14 @@ extern "C" int smla_quant_fp8_pow2(const void* x, int x_dtype, int64_t rows, int
   if (!x || !codes || !scales) return SMLA_E_NULL;
   if (rows <= 0 || D <= 0 || D % 64 != 0) return SMLA_E_SHAPE;
   if (x_dtype != SMLA_F32 && x_dtype != SMLA_BF16) return SMLA_E_DTYPE;
-  int64_t nb = rows * (D / 64);
-  hipLaunchKernelGGL(quant_kernel, dim3((unsigned)((nb + 127) / 128)), dim3(128), 0, (hipStream_t)stream, x, x_dtype,
-                     nb, codes, scales);
+  const int64_t nb = rows * (D / 64);
+  const int64_t nthreads = nb * 16;
+  if ((nthreads + 255) / 256 > 0x7fffffff) return SMLA_E_UNSUPPORTED;
+  const dim3 grid((unsigned)((nthreads + 255) / 256));
+  if (x_dtype == SMLA_F32)
+    hipLaunchKernelGGL(quant_kernel<SMLA_F32>, grid, dim3(256), 0, (hipStream_t)stream, x, nb, codes, scales);
+  else
+    hipLaunchKernelGGL(quant_kernel<SMLA_BF16>, grid, dim3(256), 0, (hipStream_t)stream, x, nb, codes, scales);
   SMLA_HIP_CHECK_LAUNCH();
   return SMLA_OK;
 }
