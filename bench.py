@@ -204,6 +204,12 @@ def other_workloads(dev, reps):
     ms = _time_ms(lambda: sidx.select_decode_indices(sc[:, 0], w["k"], pos, w["window"], raw.shape[1]), reps)
     res["select_decode"] = {"shape": "8 rows x 8192 scores, k=2048, window 128 (one launch)",
                             "us": round(ms * 1e3, 3), "bound": "latency (one workgroup per row)"}
+    ws = torch.empty(ops.index_decode_workspace(B, 1, N), dtype=torch.uint8, device=dev)
+    ms = _time_ms(lambda: sidx.index_decode(qi, keys, ks, wt, None, w["k"], pos, w["window"], raw.shape[1],
+                                            workspace=ws), reps)
+    res["index_decode"] = {"shape": "B=8 Hi=64 Di=64 N=8192 -> window 128 + top-2048 ids: MFMA scores with a "
+                                    "certified bound, band rescoring, exact selection (two launches)",
+                           "us": round(ms * 1e3, 3)}
     ms = _time_ms(lambda: scomp.block_mean_pool(raw, 4), max(2, reps // 2))
     mb = raw.numel() * 2 + raw.numel() // 4 * 2
     res["block_mean_pool"] = {"shape": "[8,32768,576] bf16 -> [8,8192,576]", "us": round(ms * 1e3, 3),
@@ -284,6 +290,7 @@ def main():
     from smla import _lib
     from smla import compressor as scomp
     from smla import indexer as sidx
+    from smla import ops
     from smla import sparse_attn as ssa
     from smla import workloads as wl
 
@@ -312,6 +319,8 @@ def main():
     pos = torch.full((B,), w["pos"], dtype=torch.int32, device=dev)
     print(f"[bench] {args.rot} cache copies resident ({args.rot * sum(t.numel() * t.element_size() for t in copies[0]) / 2**30:.1f} GiB)",
           file=sys.stderr, flush=True)
+
+    ws = torch.empty(ops.index_decode_workspace(B, 1, keys0.shape[1]), dtype=torch.uint8, device=dev)
 
     def step(r):
         raw, comp, keys, ks = copies[r]
@@ -377,8 +386,7 @@ def main():
     idx_all = []
     for r in range(args.rot):
         raw, comp, keys, ks = copies[r]
-        sc = sidx.indexer_score(qi, keys, ks, wt)
-        idx_all.append(sidx.select_decode_indices(sc[:, 0], k, pos, win, n_raw))
+        idx_all.append(sidx.index_decode(qi, keys, ks, wt, None, k, pos, win, n_raw, workspace=ws))
     torch.cuda.synchronize()
     # the split kernel alone: a graph of `rot` launches (one per cache copy, main kernel only), replayed
     # back to back between two events on the replay stream

@@ -434,100 +434,126 @@ __global__ __launch_bounds__(kThreads, 1) void attn_mfma_kernel(
   }
 }
 
-// one workgroup (128 threads, 4 dv each) per (query row, head): split weights w_j = exp(m_j - M)
-// once into LDS, then every thread streams its float4 of each split's partial output with
-// independent (unrolled) loads.
-constexpr int kMaxSplits = 1024;
-// One wave per (query row, head) and workgroup: the nsplit partial states (m_j, l_j,
-// O_j) of that head, stored split-major ([row][split][head], so each split kernel writes one
-// contiguous block), merge as
+// Merge of split partial states.  The nsplit states (m_j, l_j, O_j) of one (query row, head) are
+// stored split-major ([row][split][head], so each split workgroup writes one contiguous block) and
+// merge as
 //   M = max m_j,  w_j = exp(m_j - M),  O = sum w_j O_j / (sum w_j l_j + exp(sink - M)).
-// Lane l owns value columns 8l .. 8l+7 (DV = 512).  The split loads of a wave are issued 8 at a
-// time together with the (m, l) loads, so one memory round trip covers a row's whole merge.
-constexpr int kMergeHeads = 1;  // heads (waves) per workgroup: one, so the rows spread over every CU
-__global__ __launch_bounds__(kMergeHeads * 64) void attn_merge_kernel(const float* __restrict__ part, int nsplit,
-                                                                      int64_t BS, int H, int DV,
-                                                                      const float* __restrict__ sink,
-                                                                      void* __restrict__ out, int out_dtype,
-                                                                      int part_bf16) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int64_t rh = (int64_t)blockIdx.x * kMergeHeads + wave;  // bs*H + head
-  if (rh >= BS * H) return;
+// One workgroup of WAVES waves per (query row, head); thread t owns value columns
+// CPL*t .. CPL*t+CPL-1 (CPL = 512 / (64 WAVES)).  The O loads of the first CHUNK splits (16 to 64)
+// are issued before the (m, l) loads, so for up to CHUNK splits one memory round trip covers the
+// whole merge;
+// (m, l) and the weights pass through LDS, so any split count up to kMaxSplits takes the same path.
+constexpr int kMaxSplits = 1024;
+
+template <int WAVES, bool BF16P, int CH>
+__global__ __launch_bounds__(WAVES * 64) void attn_merge_kernel(const float* __restrict__ part, int nsplit,
+                                                                int64_t BS, int H, const float* __restrict__ sink,
+                                                                void* __restrict__ out, int out_dtype) {
+  constexpr int NT = WAVES * 64;
+  constexpr int DV = 512;
+  constexpr int CPL = DV / NT;                        // value columns per thread: 4, 2 or 1
+  constexpr int LW = BF16P ? (CPL + 1) / 2 : CPL;     // 32-bit words loaded per split
+  constexpr int CHUNK = CH < 64 / LW ? CH : 64 / LW;  // splits in flight: at most 64 words per thread
+  static_assert(CPL >= 1 && CPL <= 4 && NT * CPL == DV, "merge thread layout");
+  static_assert(kMaxSplits % CHUNK == 0, "padded weights fit the table");
+  __shared__ __align__(16) float m_s[kMaxSplits];
+  __shared__ float l_s[kMaxSplits];
+  __shared__ float red[2][WAVES];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t rh = blockIdx.x;  // bs*H + head
   const int64_t bs = rh / H;
   const int head = (int)(rh % H);
   const int64_t rec0 = bs * nsplit * (int64_t)H + head;  // record of split 0; splits are H records apart
   const float* ml = part + rec0 * 2;
-  const int dv0 = lane * 8;
+  const int dv0 = tid * CPL;
+  const int64_t jstride = (int64_t)H * DV;  // elements between consecutive splits
   const float* obase = part + BS * H * nsplit * 2;
-  const int64_t jstride = (int64_t)H * DV;                 // elements between consecutive splits
-  const bool reg_ml = nsplit <= 64;
-  constexpr int U = 8;
-  // batch 0 of the O loads, then the (m, l) loads (lane j: split j)
-  u32x4_t vb[U];
-  f32x4_t vf[U][2];
-  auto load_batch = [&](int j0) {
+
+  uint32_t v[CHUNK][LW];
+  // unconditional loads (an index past the last split re-reads the last one, whose weight in the
+  // padded table is zero): a guarded load would become a branch with a full wait behind it
+  auto load_chunk = [&](int j0) {
 #pragma unroll
-    for (int u = 0; u < U; u++) {
-      const int j = j0 + u;
-      const bool ok = j < nsplit;
-      if (part_bf16) {
-        vb[u] = ok ? *(const u32x4_t*)((const uint16_t*)obase + rec0 * DV + j * jstride + dv0) : u32x4_t{0u, 0u, 0u, 0u};
+    for (int u = 0; u < CHUNK; u++) {
+      const int j = min(j0 + u, nsplit - 1);
+      if constexpr (BF16P) {
+        const uint16_t* p = (const uint16_t*)obase + rec0 * DV + j * jstride + dv0;
+        if constexpr (CPL == 4) {
+          const u32x2_t t = *(const u32x2_t*)p;
+          v[u][0] = t[0];
+          v[u][1] = t[1];
+        } else if constexpr (CPL == 2) {
+          v[u][0] = *(const uint32_t*)p;
+        } else {
+          v[u][0] = (uint32_t)*p;
+        }
       } else {
-        const float* op = obase + rec0 * DV + j * jstride + dv0;
-        vf[u][0] = ok ? *(const f32x4_t*)op : f32x4_t{0.f, 0.f, 0.f, 0.f};
-        vf[u][1] = ok ? *(const f32x4_t*)(op + 4) : f32x4_t{0.f, 0.f, 0.f, 0.f};
+        const float* p = obase + rec0 * DV + j * jstride + dv0;
+        if constexpr (CPL == 4) {
+          const f32x4_t t = *(const f32x4_t*)p;
+#pragma unroll
+          for (int c = 0; c < 4; c++) v[u][c] = __float_as_uint(t[c]);
+        } else if constexpr (CPL == 2) {
+          const u32x2_t t = *(const u32x2_t*)p;
+          v[u][0] = t[0];
+          v[u][1] = t[1];
+        } else {
+          v[u][0] = __float_as_uint(*p);
+        }
       }
     }
   };
-  load_batch(0);
-  float mj_l = -SMLA_INF, lj_l = 0.f, mx = -SMLA_INF;
-  if (reg_ml) {
-    if (lane < nsplit) {
-      mj_l = ml[(int64_t)lane * H * 2];
-      lj_l = ml[(int64_t)lane * H * 2 + 1];
-    }
-    mx = mj_l;
-  } else {
-    for (int j = lane; j < nsplit; j += 64) mx = fmaxf(mx, ml[(int64_t)j * H * 2]);
+  load_chunk(0);
+
+  // (m, l) of every split to LDS; row max M
+  float mx = -SMLA_INF;
+  for (int j = tid; j < nsplit; j += NT) {
+    const float m = ml[(int64_t)j * H * 2], l = ml[(int64_t)j * H * 2 + 1];
+    m_s[j] = m;
+    l_s[j] = l;
+    mx = fmaxf(mx, m);
   }
-  const float M = wave_max_dpp(mx);
-  const bool empty = !(M > -SMLA_INF);
-  float L = 0.f, wl = 0.f;
-  if (reg_ml) {
-    wl = (mj_l > -SMLA_INF) ? __expf(mj_l - M) : 0.f;
-    float t = wl * lj_l;
-    t += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(t), 0xB1, 0xf, 0xf, false));
-    t += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(t), 0x4E, 0xf, 0xf, false));
-    t += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(t), 0x141, 0xf, 0xf, false));
-    t += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(t), 0x140, 0xf, 0xf, false));
-    L = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(t), 0)) +
-        __int_as_float(__builtin_amdgcn_readlane(__float_as_int(t), 16)) +
-        __int_as_float(__builtin_amdgcn_readlane(__float_as_int(t), 32)) +
-        __int_as_float(__builtin_amdgcn_readlane(__float_as_int(t), 48));
-  }
-  f32x4_t a0 = {0.f, 0.f, 0.f, 0.f}, a1 = a0;
-  for (int j0 = 0; j0 < nsplit; j0 += U) {
-    if (j0 > 0) load_batch(j0);
+  mx = wave_max_dpp(mx);
+  if (lane == 0) red[0][wave] = mx;
+  __syncthreads();
+  float M = red[0][0];
 #pragma unroll
-    for (int u = 0; u < U; u++) {
-      const int j = j0 + u;
-      if (j >= nsplit) break;
-      float w;
-      if (reg_ml) {
-        w = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wl), j));
+  for (int w = 1; w < WAVES; w++) M = fmaxf(M, red[0][w]);
+  const bool empty = !(M > -SMLA_INF);
+  // weights w_j (in place of m_j) and the denominator L
+  // (zero weights pad the last chunk, so the accumulation below runs whole chunks)
+  float lsum = 0.f;
+  const int npad = (nsplit + CHUNK - 1) / CHUNK * CHUNK;
+  for (int j = tid; j < npad; j += NT) {
+    const float m = j < nsplit ? m_s[j] : -SMLA_INF;
+    const float w = m > -SMLA_INF ? __expf(m - M) : 0.f;
+    m_s[j] = w;
+    if (j < nsplit) lsum += w * l_s[j];
+  }
+  lsum = wave_sum_dpp(lsum);
+  if (lane == 0) red[1][wave] = lsum;
+  __syncthreads();
+  float L = 0.f;
+#pragma unroll
+  for (int w = 0; w < WAVES; w++) L += red[1][w];
+
+  float acc[CPL];
+#pragma unroll
+  for (int c = 0; c < CPL; c++) acc[c] = 0.f;
+  for (int j0 = 0; j0 < nsplit; j0 += CHUNK) {
+    if (j0 > 0) load_chunk(j0);
+#pragma unroll
+    for (int u = 0; u < CHUNK; u++) {
+      const float w = m_s[j0 + u];
+      if constexpr (BF16P) {
+#pragma unroll
+        for (int c = 0; c < CPL; c++) {
+          const uint32_t x = v[u][c >> 1];
+          acc[c] += w * __uint_as_float((c & 1) ? (x & 0xffff0000u) : (x << 16));
+        }
       } else {
-        const float mj = ml[(int64_t)j * H * 2];
-        w = (mj > -SMLA_INF) ? __expf(mj - M) : 0.f;
-        L += w * ml[(int64_t)j * H * 2 + 1];
-      }
-      if (part_bf16) {
-        a0 += w * f32x4_t{bf16_bits_to_f32((uint16_t)(vb[u][0] & 0xffffu)), bf16_bits_to_f32((uint16_t)(vb[u][0] >> 16)),
-                          bf16_bits_to_f32((uint16_t)(vb[u][1] & 0xffffu)), bf16_bits_to_f32((uint16_t)(vb[u][1] >> 16))};
-        a1 += w * f32x4_t{bf16_bits_to_f32((uint16_t)(vb[u][2] & 0xffffu)), bf16_bits_to_f32((uint16_t)(vb[u][2] >> 16)),
-                          bf16_bits_to_f32((uint16_t)(vb[u][3] & 0xffffu)), bf16_bits_to_f32((uint16_t)(vb[u][3] >> 16))};
-      } else {
-        a0 += w * vf[u][0];
-        a1 += w * vf[u][1];
+#pragma unroll
+        for (int c = 0; c < CPL; c++) acc[c] += w * __uint_as_float(v[u][c]);
       }
     }
   }
@@ -535,20 +561,21 @@ __global__ __launch_bounds__(kMergeHeads * 64) void attn_merge_kernel(const floa
   if (!empty) L += __expf(snk - M);
   const float inv = 1.0f / L;
   const int64_t o = rh * DV + dv0;
+  const float nan = __builtin_nanf("");
   if (out_dtype == SMLA_BF16) {
-    u32x4_t wv;
-    if (empty) {
-      wv = u32x4_t{0x7fc07fc0u, 0x7fc07fc0u, 0x7fc07fc0u, 0x7fc07fc0u};
+    uint16_t* po = (uint16_t*)out + o;
+    if constexpr (CPL == 4) {
+      *(u32x2_t*)po = empty ? u32x2_t{0x7fc07fc0u, 0x7fc07fc0u}
+                            : u32x2_t{pack_bf16x2(acc[0] * inv, acc[1] * inv), pack_bf16x2(acc[2] * inv, acc[3] * inv)};
+    } else if constexpr (CPL == 2) {
+      *(uint32_t*)po = empty ? 0x7fc07fc0u : pack_bf16x2(acc[0] * inv, acc[1] * inv);
     } else {
-      wv = u32x4_t{pack_bf16x2(a0[0] * inv, a0[1] * inv), pack_bf16x2(a0[2] * inv, a0[3] * inv),
-                   pack_bf16x2(a1[0] * inv, a1[1] * inv), pack_bf16x2(a1[2] * inv, a1[3] * inv)};
+      *po = empty ? (uint16_t)0x7fc0u : bf16_rne(acc[0] * inv);
     }
-    *(u32x4_t*)((uint16_t*)out + o) = wv;
   } else {
-    const float nan = __builtin_nanf("");
-    const f32x4_t n4 = {nan, nan, nan, nan};
-    *(f32x4_t*)((float*)out + o) = empty ? n4 : a0 * inv;
-    *(f32x4_t*)((float*)out + o + 4) = empty ? n4 : a1 * inv;
+    float* po = (float*)out + o;
+#pragma unroll
+    for (int c = 0; c < CPL; c++) po[c] = empty ? nan : acc[c] * inv;
   }
 }
 
@@ -603,12 +630,37 @@ Plan make_plan(int64_t B, int64_t S, int64_t H, int64_t D, int64_t DV, int64_t T
 
 int launch_merge(const Plan& p, int64_t B, int64_t S, int64_t H, const float* sink, void* out, int out_dtype,
                  void* ws, hipStream_t stream, int part_bf16) {
-  if (p.nsplit > 1) {
-    hipLaunchKernelGGL(attn_merge_kernel, dim3((unsigned)((B * S * H + kMergeHeads - 1) / kMergeHeads)),
-                       dim3(kMergeHeads * 64), 0, stream,
-                       (const float*)ws, p.nsplit, B * S, (int)H, 512, sink, out, out_dtype, part_bf16);
-    SMLA_HIP_CHECK_LAUNCH();
+  if (p.nsplit <= 1) return SMLA_OK;
+  const int64_t rows = B * S * H;
+  // waves per (row, head): enough workgroups in flight to cover the partials' latency
+  const int waves = rows >= 1024 ? 2 : rows >= 256 ? 4 : 8;
+  const dim3 grid((unsigned)rows), block(waves * 64);
+  // splits in flight per chunk: the smallest of 16 / 32 / 64 that covers nsplit
+  const int ch = p.nsplit <= 16 ? 16 : p.nsplit <= 32 ? 32 : 64;
+#define SMLA_MERGE(W, BP, C) hipLaunchKernelGGL((attn_merge_kernel<W, BP, C>), grid, block, 0, stream, \
+                                                (const float*)ws, p.nsplit, B * S, (int)H, sink, out, out_dtype)
+#define SMLA_MERGE_CH(W, BP) \
+  if (ch == 16) SMLA_MERGE(W, BP, 16); else if (ch == 32) SMLA_MERGE(W, BP, 32); else SMLA_MERGE(W, BP, 64)
+  if (part_bf16) {
+    if (waves == 2) {
+      SMLA_MERGE_CH(2, true);
+    } else if (waves == 4) {
+      SMLA_MERGE_CH(4, true);
+    } else {
+      SMLA_MERGE_CH(8, true);
+    }
+  } else {
+    if (waves == 2) {
+      SMLA_MERGE_CH(2, false);
+    } else if (waves == 4) {
+      SMLA_MERGE_CH(4, false);
+    } else {
+      SMLA_MERGE_CH(8, false);
+    }
   }
+#undef SMLA_MERGE_CH
+#undef SMLA_MERGE
+  SMLA_HIP_CHECK_LAUNCH();
   return SMLA_OK;
 }
 

@@ -79,7 +79,6 @@ __device__ inline u32x4_t load16_untracked(const void* p) {
   return r;
 }
 
-__device__ inline bf16x8_t as_bf16x8(u32x4_t v) { return __builtin_bit_cast(bf16x8_t, v); }
 
 
 }  // namespace smla_attn

@@ -12,6 +12,7 @@ typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+__device__ inline bf16x8_t as_bf16x8(u32x4_t v) { return __builtin_bit_cast(bf16x8_t, v); }
 
 #define SMLA_INF __builtin_inff()
 
@@ -141,6 +142,18 @@ __device__ inline float wave_max_dpp(float v) {
   return fmaxf(fmaxf(a, b), fmaxf(c, d));
 }
 __device__ inline float wave_min_dpp(float v) { return -wave_max_dpp(-v); }
+// wave-wide sum (every lane gets the same result, summed in a fixed order)
+__device__ inline float wave_sum_dpp(float v) {
+  v += dpp_f<0xB1>(v);
+  v += dpp_f<0x4E>(v);
+  v += dpp_f<0x141>(v);
+  v += dpp_f<0x140>(v);
+  const float a = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+  const float b = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+  const float c = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+  const float d = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+  return (a + b) + (c + d);
+}
 // inclusive prefix sum over the 64 lanes (lane order)
 __device__ inline int wave_incl_scan(int x) {
   x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xf, 0xf, false);  // row_shr:1
@@ -168,6 +181,12 @@ __device__ inline void store_from_f32(void* p, int64_t i, int dtype, float v) {
   else if (dtype == SMLA_BF16) ((uint16_t*)p)[i] = bf16_rne(v);
   else if (dtype == SMLA_F16) ((_Float16*)p)[i] = (_Float16)v;
 }
+
+// certified MFMA indexer scores (indexer.hip): approx [B*S, N] and per-chunk bounds
+// ebound [B*S, ceil(N / 256)]; q [B, S, 64, 64] bf16, keys [B, N, 64] e4m3
+int launch_indexer_cert(const uint16_t* q, const uint8_t* keys, const float* kscale, const float* weights,
+                        const int32_t* nvis, int64_t B, int64_t S, int64_t N, float* approx, float* ebound,
+                        hipStream_t st);
 
 #define SMLA_HIP_CHECK_LAUNCH()                         \
   do {                                                  \

@@ -56,10 +56,32 @@ __device__ inline float key_score(uint32_t key) {
   return __uint_as_float((asc & 0x80000000u) ? (asc ^ 0x80000000u) : ~asc);
 }
 
+// Context of a certified selection (smla_index_decode).  The scores are the approximations a_n of
+// indexer_cert_kernel, ebound holds their per-chunk bounds (|a_n - s_n| <= bound, s_n the
+// fixed-order score), and q / keys / kscale / w let the kernel recompute s_n for any key.
+struct CertCtx {
+  const float* ebound;  // [R, nchunk]
+  int nchunk;
+  const uint16_t* q;    // [R, 64, 64] bf16
+  const uint8_t* keys;  // [B, N, 64] e4m3
+  const float* kscale;  // [B, N] or null
+  const float* w;       // [R, 64]
+  int64_t S;            // query rows per batch entry: key rows of row r are batch r / S
+  int force_exact;      // 1: skip certification, rescore every visible key (the slow path)
+  float* rescored;      // [R, N]: the slow path's exact scores (the approximations' buffer itself)
+};
+
+constexpr int kQS = 68;  // LDS row stride (floats) of the staged q rows: 16-byte per-head reads hit all banks
+constexpr int kRescoreBatch = 4;  // keys a wave rescores together (independent chains interleaved)
+constexpr int kStageIds = 4096;   // selections up to this size are staged in LDS for coalesced stores
+
+__device__ inline int bucket_of_score(float s, float lmax, float bscale) {
+  const float t = (lmax - s) * bscale;
+  return t < 1.f ? 0 : (t >= (float)kBuckets ? kBuckets - 1 : (int)t);
+}
 // monotone bucket of a finite score: 0 holds the largest scores
 __device__ inline int bucket_of(uint32_t key, float lmax, float bscale) {
-  int bb = (int)((lmax - key_score(key)) * bscale);
-  return bb < 0 ? 0 : (bb >= kBuckets ? kBuckets - 1 : bb);
+  return bucket_of_score(key_score(key), lmax, bscale);
 }
 
 // Row selection.  Produces the threshold pair (Kt, It) of the k-th best entry in the order
@@ -68,26 +90,40 @@ __device__ inline int bucket_of(uint32_t key, float lmax, float bscale) {
 //    entry is found from a histogram + scan, and its (few) candidates are ranked exactly;
 //  * fallback (degenerate spreads, > 256 candidates in the boundary bucket): 4 radix passes of 8
 //    bits over the keys, then the tie rank among entries equal to the k-th key.
+// Certified mode (CERT): the scores are approximations a_n with |a_n - s_n| <= E for the exact
+// scores s_n.  With bb the bucket of the k-th largest a, an entry with bucket(a_n - 2E) < bb
+// is certainly selected, one with bucket(a_n + 2E) > bb certainly not; the entries in between
+// (the band: bucket bb and whatever lies within 2E of it) are rescored exactly and ranked.  The
+// k-th largest s lies within E of the k-th largest a, which makes this the exact selection.  A
+// row that cannot be certified (a bound that is not finite, a degenerate spread, more than 256
+// band entries) is rescored in full and selected exactly.
 // Output: window ids (optional), then the selected ids ascending (+ id_offset), then -1.
-template <int PER>
-__global__ __launch_bounds__(kTopkThreads) void topk_kernel(const float* __restrict__ scores, int64_t N,
+template <int PER, bool CERT>
+__global__ __launch_bounds__(kTopkThreads) void topk_kernel(const float* scores, int64_t N,
                                                             const int32_t* __restrict__ nvis, int k,
                                                             int32_t* __restrict__ out, int64_t out_stride,
                                                             int32_t id_offset, const int32_t* __restrict__ wpos,
-                                                            int window) {
+                                                            int window, CertCtx cc) {
   __shared__ int hist[kWaves][256];
-  __shared__ int bhist[kBuckets];
+  __shared__ int bhist[kBuckets + 1];  // + a slot that absorbs the counts of entries past nvis
   __shared__ int tmp[kWaves + 1];
-  __shared__ float redf[2 * kWaves];
-  __shared__ uint32_t cand_key[kMaxCand];
+  __shared__ float redf[3 * kWaves];
+  __shared__ uint64_t cand_pair[kMaxCand];  // (key << 32) | index: the selection order is the integer order
   __shared__ int cand_idx[kMaxCand];
-  __shared__ int s_int[4];
+  __shared__ int out_s[kStageIds];           // the selected ids in output order, stored coalesced at the end
+  __shared__ int s_int[5];
   __shared__ int s_nan[kWaves];
+  __shared__ float q_s[CERT ? 64 * kQS : 1];
+  __shared__ float w_s[CERT ? 64 : 1];
+  __shared__ u32x4_t ck_s[CERT ? kMaxCand * 4 : 1];  // key rows being rescored (64 e4m3 codes each)
+  __shared__ float cks_s[CERT ? kMaxCand : 1];       // their kscale
+  __shared__ float r_s[CERT ? kWaves * kRescoreBatch * 64 : 1];  // per wave: ReLU(dot_h) of its keys
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int64_t r = blockIdx.x;
-  int64_t nv = nvis ? (int64_t)nvis[r] : N;
-  if (nv > N) nv = N;
+  // N <= 65536 (PER * kTopkThreads): every index of the row fits 32 bits
+  int nv = nvis ? nvis[r] : (int)N;
+  if (nv > (int)N) nv = (int)N;
   if (nv < 0) nv = 0;
   const float* sr = scores + r * N;
   int32_t* orow = out + r * out_stride;
@@ -101,215 +137,442 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(const float* __restr
   }
   const int take = (int)(nv < k ? nv : k);
 
-  const int64_t base = (int64_t)tid * PER;
+  const int base = tid * PER;
+  // this thread's entries j < nloc are visible (index base + j < nvis)
+  const int nloc = nv - base < 0 ? 0 : (nv - base > PER ? PER : nv - base);
   if (nv <= k) {
-    for (int64_t j = tid; j < k; j += kTopkThreads) orow[j] = j < nv ? (int32_t)j + id_offset : -1;
+    for (int j = tid; j < k; j += kTopkThreads) orow[j] = j < nv ? j + id_offset : -1;
     return;
   }
-  uint32_t key[PER];
-  float lmin = SMLA_INF, lmax = -SMLA_INF;
-  bool nan_seen = false;
+  const int64_t bkey = CERT ? r / cc.S : 0;  // batch entry of the key rows
+  // the q row (4 bf16 per thread) and weights: loaded now, staged in LDS after the first barrier
+  u32x2_t qraw = {0u, 0u};
+  float wraw = 0.f;
+  if constexpr (CERT) {
+    qraw = *(const u32x2_t*)(cc.q + r * 4096 + 4 * tid);
+    if (tid < 64) wraw = cc.w[r * 64 + tid];
+  }
+  // fixed-order scores of kRescoreBatch keys (rows rows[b] of ck_s, 64 codes each), one batch per
+  // wave: lane h runs head h's chain over d for every key of the batch (independent chains, one q
+  // read for all), the ReLU values go to LDS, and every lane runs each key's chain over the heads
+  // in head order (the arithmetic of indexer_kernel).  Returns acc (before the kscale product).
+  auto exact_batch = [&](const int (&rows)[kRescoreBatch], float (&acc)[kRescoreBatch]) {
+    static_assert(kRescoreBatch == 4, "ReLU values are exchanged as one 16-byte vector per head");
+    float dot[kRescoreBatch];
+#pragma unroll
+    for (int b = 0; b < kRescoreBatch; b++) dot[b] = 0.f;
+#pragma unroll 1
+    for (int v = 0; v < 4; v++) {
+      u32x4_t kw[kRescoreBatch];
+#pragma unroll
+      for (int b = 0; b < kRescoreBatch; b++) kw[b] = ck_s[4 * rows[b] + v];
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const f32x4_t q4 = *(const f32x4_t*)&q_s[lane * kQS + 16 * v + 4 * j];
+#pragma unroll
+        for (int b = 0; b < kRescoreBatch; b++) {
+          const f32x2_t lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)kw[b][j], false);
+          const f32x2_t hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)kw[b][j], true);
+          dot[b] = __builtin_fmaf(q4[0], lo.x, dot[b]);
+          dot[b] = __builtin_fmaf(q4[1], lo.y, dot[b]);
+          dot[b] = __builtin_fmaf(q4[2], hi.x, dot[b]);
+          dot[b] = __builtin_fmaf(q4[3], hi.y, dot[b]);
+        }
+      }
+    }
+    // ReLU values as [head][key]: one 16-byte read per head serves the whole batch
+    float* rw = r_s + wave * kRescoreBatch * 64;
+    *(f32x4_t*)&rw[4 * lane] = f32x4_t{dot[0] > 0.f ? dot[0] : 0.f, dot[1] > 0.f ? dot[1] : 0.f,
+                                       dot[2] > 0.f ? dot[2] : 0.f, dot[3] > 0.f ? dot[3] : 0.f};
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's LDS writes are done
+#pragma unroll
+    for (int b = 0; b < kRescoreBatch; b++) acc[b] = 0.f;
+#pragma unroll 1
+    for (int h4 = 0; h4 < 64; h4 += 4) {
+      const f32x4_t w4 = *(const f32x4_t*)&w_s[h4];
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const f32x4_t r4 = *(const f32x4_t*)&rw[4 * (h4 + i)];
+#pragma unroll
+        for (int b = 0; b < kRescoreBatch; b++) acc[b] = __builtin_fmaf(w4[i], r4[b], acc[b]);
+      }
+    }
+  };
+  // rank of candidate c among the first `total` in the order (key asc, index asc)
+  auto rank_of = [&](int c, int total) -> int {
+    const uint64_t me = cand_pair[c];
+    int rank = 0;
+#pragma unroll 16
+    for (int j = 0; j < total; j++) rank += cand_pair[j] < me;
+    return rank;
+  };
+
   // this thread's PER contiguous scores: 16-byte loads when the run lies inside the row and is
   // 16-byte aligned (rows of N floats: N % 4 == 0), element loads otherwise
   float fv[PER];
-  if (PER % 4 == 0 && (N & 3) == 0 && base + PER <= N) {
+  auto load_scores = [&](const float* row) {
+    if (PER % 4 == 0 && (N & 3) == 0 && base + PER <= N) {
 #pragma unroll
-    for (int j = 0; j < PER; j += 4) {
-      const f32x4_t v4 = *(const f32x4_t*)(sr + base + j);
-      fv[j] = v4[0];
-      fv[j + 1] = v4[1];
-      fv[j + 2] = v4[2];
-      fv[j + 3] = v4[3];
-    }
-  } else {
+      for (int j = 0; j < PER; j += 4) {
+        const f32x4_t v4 = *(const f32x4_t*)(row + base + j);
+        fv[j] = v4[0];
+        fv[j + 1] = v4[1];
+        fv[j + 2] = v4[2];
+        fv[j + 3] = v4[3];
+      }
+    } else {
 #pragma unroll
-    for (int j = 0; j < PER; j++) fv[j] = base + j < N ? sr[base + j] : 0.f;
-  }
-#pragma unroll
-  for (int j = 0; j < PER; j++) {
-    const int64_t n = base + j;
-    const float f = fv[j];
-    key[j] = n < nv ? desc_key(f) : 0xffffffffu;
-    if (n < nv) {
-      lmin = fminf(lmin, f);
-      lmax = fmaxf(lmax, f);
-      nan_seen |= f != f;
+      for (int j = 0; j < PER; j++) fv[j] = base + j < N ? row[base + j] : 0.f;
+    }
+  };
+  load_scores(sr);
+  float emax = 0.f;
+  if constexpr (CERT) {
+    for (int c = tid; c < cc.nchunk; c += kTopkThreads) {
+      const float e = cc.ebound[r * cc.nchunk + c];
+      emax = fmaxf(emax, e == e ? e : SMLA_INF);
     }
   }
-  // ---- row min / max (and whether a NaN is visible)
-  {
-    const float a = wave_min_dpp(lmin), bmx = wave_max_dpp(lmax);
-    const bool wnan = __builtin_amdgcn_ballot_w64(nan_seen) != 0;
-    if (lane == 0) {
-      redf[wave] = a;
-      redf[kWaves + wave] = bmx;
-      s_nan[wave] = wnan;
-    }
-    for (int i = tid; i < kBuckets; i += kTopkThreads) bhist[i] = 0;
-    __syncthreads();
-    // every wave reduces the kWaves per-wave results itself (one LDS read per lane)
-    const int wl = lane < kWaves ? lane : 0;
-    lmin = wave_min_dpp(redf[wl]);
-    lmax = wave_max_dpp(redf[kWaves + wl]);
-    nan_seen = __builtin_amdgcn_ballot_w64(lane < kWaves && s_nan[wl] != 0) != 0;
-  }
+  uint32_t key[PER];
   uint32_t Kt = 0;
   int It = -1;
-  bool done = false;
-  if (lmax == lmin && !nan_seen) {
-    // every visible score equal: the k lowest indices
-    Kt = desc_key(lmax);
-    It = k - 1;
-    done = true;
-  }
-  const float bscale = (float)kBuckets / (lmax - lmin);
-  if (!done && !nan_seen && bscale < SMLA_INF && bscale > 0.f && lmin > -SMLA_INF && lmax < SMLA_INF) {
-    // ---- bucket histogram (bucket 0 holds the largest scores)
+  // certified selection state (used by the emit when band_mode)
+  bool band_mode = false;
+  uint64_t in_mask = 0, band_mask = 0;
+  int slot0 = 0;
+  bool certified = CERT;
+#pragma unroll 1
+  for (int pass = 0; pass < 2; pass++) {
+    if (pass > 0) __syncthreads();  // the previous pass's readers of redf / bhist are done
+    float lmin = SMLA_INF, lmax = -SMLA_INF;
+    bool nan_seen = false;
 #pragma unroll
-    for (int j = 0; j < PER; j++)
-      if (base + j < nv) atomicAdd(&bhist[bucket_of(key[j], lmax, bscale)], 1);
-    __syncthreads();
-    // thread t owns buckets 2t, 2t+1
-    const int c0 = bhist[2 * tid], c1 = bhist[2 * tid + 1];
-    int tot;
-    const int before = block_excl_scan(c0 + c1, tmp, &tot);
-    if (tid == 0) s_int[3] = 0;  // candidate counter
-    if (before < k && k <= before + c0) {
-      s_int[0] = 2 * tid;
-      s_int[1] = k - before;
-    } else if (before + c0 < k && k <= before + c0 + c1) {
-      s_int[0] = 2 * tid + 1;
-      s_int[1] = k - before - c0;
+    for (int j = 0; j < PER; j++) {
+      const bool vis = j < nloc;
+      const float f = fv[j];
+      key[j] = vis ? desc_key(f) : 0xffffffffu;
+      lmin = fminf(lmin, vis ? f : SMLA_INF);
+      lmax = fmaxf(lmax, vis ? f : -SMLA_INF);
+      nan_seen |= vis && f != f;
     }
-    __syncthreads();
-    const int bb = s_int[0], need = s_int[1];
-    const int cb = bhist[bb];
-    if (cb <= kMaxCand) {
-      // gather the boundary bucket's entries and rank them exactly
-      // candidates of the boundary bucket: per-thread count, wave offsets by scan, one LDS
-      // atomic per wave
-      int mine = 0;
+    // ---- row min / max (and whether a NaN is visible; the bound max on a certified pass)
+    {
+      const float a = wave_min_dpp(lmin), bmx = wave_max_dpp(lmax);
+      const float em = CERT ? wave_max_dpp(emax) : 0.f;
+      const bool wnan = __builtin_amdgcn_ballot_w64(nan_seen) != 0;
+      if (lane == 0) {
+        redf[wave] = a;
+        redf[kWaves + wave] = bmx;
+        redf[2 * kWaves + wave] = em;
+        s_nan[wave] = wnan;
+      }
+      for (int i = tid; i <= kBuckets; i += kTopkThreads) bhist[i] = 0;
+      if (CERT && pass == 0) {
+        const int h = (4 * tid) >> 6, d0 = (4 * tid) & 63;
+        *(f32x4_t*)&q_s[h * kQS + d0] = f32x4_t{__uint_as_float(qraw[0] << 16), __uint_as_float(qraw[0] & 0xffff0000u),
+                                                __uint_as_float(qraw[1] << 16), __uint_as_float(qraw[1] & 0xffff0000u)};
+        if (tid < 64) w_s[tid] = wraw;
+      }
+      __syncthreads();
+      // every wave reduces the kWaves per-wave results itself (one LDS read per lane)
+      const int wl = lane < kWaves ? lane : 0;
+      lmin = wave_min_dpp(redf[wl]);
+      lmax = wave_max_dpp(redf[kWaves + wl]);
+      if (CERT) emax = wave_max_dpp(redf[2 * kWaves + wl]);
+      nan_seen = __builtin_amdgcn_ballot_w64(lane < kWaves && s_nan[wl] != 0) != 0;
+    }
+    const float bscale = (float)kBuckets / (lmax - lmin);
+    const bool spread_ok = !nan_seen && bscale < SMLA_INF && bscale > 0.f && lmin > -SMLA_INF && lmax < SMLA_INF;
+    if (CERT && certified) {
+      // band half-width: twice the row bound, plus room for the rounding of a -+ E2
+      const float E2 = 2.f * emax * (1.f + 0x1p-8f) + 0x1p-20f * fmaxf(fabsf(lmin), fabsf(lmax));
+      if (cc.force_exact == 0 && spread_ok && E2 < SMLA_INF) {
+        // ---- bucket histogram of the approximate scores
 #pragma unroll
-      for (int j = 0; j < PER; j++) mine += (base + j < nv && bucket_of(key[j], lmax, bscale) == bb);
-      const int incl = wave_incl_scan(mine);
-      int wbase = 0;
-      if (lane == 63 && incl > 0) wbase = atomicAdd(&s_int[3], incl);
-      wbase = __builtin_amdgcn_readlane(wbase, 63);
-      int slot = wbase + incl - mine;
+        for (int j = 0; j < PER; j++) atomicAdd(&bhist[j < nloc ? bucket_of(key[j], lmax, bscale) : kBuckets], 1);
+        __syncthreads();
+        const int c0 = bhist[2 * tid], c1 = bhist[2 * tid + 1];
+        int tot;
+        const int before = block_excl_scan(c0 + c1, tmp, &tot);
+        if (tid == 0) {
+          s_int[3] = 0;
+          s_int[4] = 0;
+        }
+        if (before < k && k <= before + c0) {
+          s_int[0] = 2 * tid;
+          s_int[1] = k - before;
+        } else if (before + c0 < k && k <= before + c0 + c1) {
+          s_int[0] = 2 * tid + 1;
+          s_int[1] = k - before - c0;
+        }
+        __syncthreads();
+        const int bb = s_int[0], need = s_int[1];
+        // ---- band: in (certainly selected), band (rescored), the rest certainly not selected
+        int mine = 0, mine_u = 0;
 #pragma unroll
-      for (int j = 0; j < PER; j++) {
-        if (base + j < nv && bucket_of(key[j], lmax, bscale) == bb) {
-          if (slot < kMaxCand) {
-            cand_key[slot] = key[j];
-            cand_idx[slot] = (int)(base + j);
+        for (int j = 0; j < PER; j++) {
+          const float a = key_score(key[j]);
+          const bool in = j < nloc && bucket_of_score(a - E2, lmax, bscale) < bb;
+          const bool band = j < nloc && !in && bucket_of_score(a + E2, lmax, bscale) <= bb;
+          in_mask |= (uint64_t)in << j;
+          band_mask |= (uint64_t)band << j;
+          mine += band;
+          mine_u += band && bucket_of(key[j], lmax, bscale) < bb;
+        }
+        const int incl = wave_incl_scan(mine);
+        const int incl_u = wave_incl_scan(mine_u);
+        int wbase = 0;
+        if (lane == 63) {
+          if (incl > 0) wbase = atomicAdd(&s_int[3], incl);
+          if (incl_u > 0) atomicAdd(&s_int[4], incl_u);
+        }
+        wbase = __builtin_amdgcn_readlane(wbase, 63);
+        slot0 = wbase + incl - mine;
+        int slot = slot0;
+#pragma unroll
+        for (int j = 0; j < PER; j++) {
+          if ((band_mask >> j) & 1u) {
+            if (slot < kMaxCand) cand_idx[slot] = (int)(base + j);
+            slot++;
           }
-          slot++;
+        }
+        __syncthreads();
+        const int total = s_int[3], ucnt = s_int[4];
+        if (total <= kMaxCand) {
+          // exact scores of the band: its key rows and scales to LDS in one round trip, then one
+          // wave per entry
+          for (int t = tid; t < total * 4; t += kTopkThreads)
+            ck_s[t] = *(const u32x4_t*)(cc.keys + (bkey * N + cand_idx[t >> 2]) * 64 + 16 * (t & 3));
+          if (cc.kscale)
+            for (int c = tid; c < total; c += kTopkThreads) cks_s[c] = cc.kscale[bkey * N + cand_idx[c]];
+          __syncthreads();
+          // kRescoreBatch entries per wave at a time: c0 + b * kWaves (past the end: entry c0 again)
+#pragma unroll 1
+          for (int c0 = wave; c0 < total; c0 += kRescoreBatch * kWaves) {
+            int rows[kRescoreBatch];
+#pragma unroll
+            for (int b = 0; b < kRescoreBatch; b++) rows[b] = c0 + b * kWaves < total ? c0 + b * kWaves : c0;
+            float acc[kRescoreBatch];
+            exact_batch(rows, acc);
+            if (lane == 0) {
+#pragma unroll
+              for (int b = 0; b < kRescoreBatch; b++) {
+                const int c = c0 + b * kWaves;
+                if (c < total) {
+                  const float sx = cc.kscale ? acc[b] * cks_s[c] : acc[b];
+                  cand_pair[c] = ((uint64_t)desc_key(sx) << 32) | (uint32_t)cand_idx[c];
+                }
+              }
+            }
+          }
+          __syncthreads();
+          // the band supplies need + (its entries above bucket bb) of the selection
+          const int need_b = need + ucnt;
+          if (tid < total && rank_of(tid, total) == need_b - 1) {
+            const uint64_t pr = cand_pair[tid];
+            s_int[0] = (int)(uint32_t)(pr >> 32);
+            s_int[1] = (int)(uint32_t)pr;
+          }
+          __syncthreads();
+          Kt = (uint32_t)s_int[0];
+          It = s_int[1];
+          band_mode = true;
+          break;
+        }
+        in_mask = band_mask = 0;
+      }
+      // not certifiable: every visible key's exact score (one wave per key, written over the
+      // approximations), then the exact selection below
+      float* resc = cc.rescored + r * N;
+      // kRescoreBatch keys per wave at a time: n0 + b * kWaves; their rows go to the wave's own
+      // ck_s rows (lanes 0 .. 4 kRescoreBatch - 1 load 16 bytes each)
+#pragma unroll 1
+      for (int n0 = wave; n0 < nv; n0 += kRescoreBatch * kWaves) {
+        const int bl = (lane >> 2) & (kRescoreBatch - 1);
+        const int nl = n0 + bl * kWaves < nv ? n0 + bl * kWaves : n0;
+        if (lane < 4 * kRescoreBatch)
+          ck_s[4 * (wave * kRescoreBatch + bl) + (lane & 3)] =
+              *(const u32x4_t*)(cc.keys + (bkey * N + nl) * 64 + 16 * (lane & 3));
+        __builtin_amdgcn_s_waitcnt(0xc07f);
+        int rows[kRescoreBatch];
+#pragma unroll
+        for (int b = 0; b < kRescoreBatch; b++) rows[b] = wave * kRescoreBatch + b;
+        float acc[kRescoreBatch];
+        exact_batch(rows, acc);
+        if (lane == 0) {
+#pragma unroll
+          for (int b = 0; b < kRescoreBatch; b++) {
+            const int n = n0 + b * kWaves;
+            if (n < nv) resc[n] = cc.kscale ? acc[b] * cc.kscale[bkey * N + n] : acc[b];
+          }
         }
       }
+      __threadfence_block();
       __syncthreads();
-      if (tid < cb) {
-        const uint32_t kk = cand_key[tid];
-        const int ii = cand_idx[tid];
-        int rank = 0;
-#pragma unroll 4
-        for (int j = 0; j < cb; j++) {
-          const uint32_t k2 = cand_key[j];
-          rank += (k2 < kk) || (k2 == kk && cand_idx[j] < ii);
-        }
-        if (rank == need - 1) {
-          s_int[0] = (int)kk;
-          s_int[1] = ii;
-        }
-      }
-      __syncthreads();
-      Kt = (uint32_t)s_int[0];
-      It = s_int[1];
+      load_scores(resc);
+      certified = false;
+      continue;
+    }
+    bool done = false;
+    if (lmax == lmin && !nan_seen) {
+      // every visible score equal: the k lowest indices
+      Kt = desc_key(lmax);
+      It = k - 1;
       done = true;
     }
-    __syncthreads();
-  }
-  if (!done) {
-    // ---- radix select over the 32-bit keys
-    uint32_t prefix = 0, pmask = 0;
-    int remaining = k;
-#pragma unroll 1
-    for (int shift = 24; shift >= 0; shift -= 8) {
-      for (int i = lane; i < 256; i += 64) hist[wave][i] = 0;
-      __syncthreads();
+    if (!done && spread_ok) {
+      // ---- bucket histogram (bucket 0 holds the largest scores)
 #pragma unroll
-      for (int j = 0; j < PER; j++) {
-        if (base + j < nv && (key[j] & pmask) == prefix) atomicAdd(&hist[wave][(key[j] >> shift) & 255u], 1);
+      for (int j = 0; j < PER; j++) atomicAdd(&bhist[j < nloc ? bucket_of(key[j], lmax, bscale) : kBuckets], 1);
+      __syncthreads();
+      // thread t owns buckets 2t, 2t+1
+      const int c0 = bhist[2 * tid], c1 = bhist[2 * tid + 1];
+      int tot;
+      const int before = block_excl_scan(c0 + c1, tmp, &tot);
+      if (tid == 0) s_int[3] = 0;  // candidate counter
+      if (before < k && k <= before + c0) {
+        s_int[0] = 2 * tid;
+        s_int[1] = k - before;
+      } else if (before + c0 < k && k <= before + c0 + c1) {
+        s_int[0] = 2 * tid + 1;
+        s_int[1] = k - before - c0;
       }
       __syncthreads();
-      if (wave == 0) {
-        int cc[4];
-        int t4 = 0;
-#pragma unroll 1
-        for (int i = 0; i < 4; i++) {
-          int sacc = 0;
-#pragma unroll 4
-          for (int w = 0; w < kWaves; w++) sacc += hist[w][lane * 4 + i];
-          cc[i] = sacc;
-          t4 += sacc;
+      const int bb = s_int[0], need = s_int[1];
+      const int cb = bhist[bb];
+      if (cb <= kMaxCand) {
+        // candidates of the boundary bucket: per-thread count, wave offsets by scan, one LDS
+        // atomic per wave
+        int mine = 0;
+#pragma unroll
+        for (int j = 0; j < PER; j++) mine += (j < nloc && bucket_of(key[j], lmax, bscale) == bb);
+        const int incl = wave_incl_scan(mine);
+        int wbase = 0;
+        if (lane == 63 && incl > 0) wbase = atomicAdd(&s_int[3], incl);
+        wbase = __builtin_amdgcn_readlane(wbase, 63);
+        int slot = wbase + incl - mine;
+#pragma unroll
+        for (int j = 0; j < PER; j++) {
+          if (j < nloc && bucket_of(key[j], lmax, bscale) == bb) {
+            if (slot < kMaxCand) cand_pair[slot] = ((uint64_t)key[j] << 32) | (uint32_t)(base + j);
+            slot++;
+          }
         }
-        const int incl = wave_incl_scan(t4);
-        const int bef = incl - t4;
-        if (bef < remaining && remaining <= incl) {
-          int cum = bef;
+        __syncthreads();
+        if (tid < cb && rank_of(tid, cb) == need - 1) {
+          const uint64_t pr = cand_pair[tid];
+          s_int[0] = (int)(uint32_t)(pr >> 32);
+          s_int[1] = (int)(uint32_t)pr;
+        }
+        __syncthreads();
+        Kt = (uint32_t)s_int[0];
+        It = s_int[1];
+        done = true;
+      }
+      __syncthreads();
+    }
+    if (!done) {
+      // ---- radix select over the 32-bit keys
+      uint32_t prefix = 0, pmask = 0;
+      int remaining = k;
+#pragma unroll 1
+      for (int shift = 24; shift >= 0; shift -= 8) {
+        for (int i = lane; i < 256; i += 64) hist[wave][i] = 0;
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < PER; j++) {
+          if (j < nloc && (key[j] & pmask) == prefix) atomicAdd(&hist[wave][(key[j] >> shift) & 255u], 1);
+        }
+        __syncthreads();
+        if (wave == 0) {
+          int cc4[4];
+          int t4 = 0;
+#pragma unroll 1
           for (int i = 0; i < 4; i++) {
-            if (remaining <= cum + cc[i]) {
-              s_int[0] = lane * 4 + i;
-              s_int[1] = cum;
-              break;
+            int sacc = 0;
+#pragma unroll 4
+            for (int w = 0; w < kWaves; w++) sacc += hist[w][lane * 4 + i];
+            cc4[i] = sacc;
+            t4 += sacc;
+          }
+          const int incl = wave_incl_scan(t4);
+          const int bef = incl - t4;
+          if (bef < remaining && remaining <= incl) {
+            int cum = bef;
+            for (int i = 0; i < 4; i++) {
+              if (remaining <= cum + cc4[i]) {
+                s_int[0] = lane * 4 + i;
+                s_int[1] = cum;
+                break;
+              }
+              cum += cc4[i];
             }
-            cum += cc[i];
+          }
+        }
+        __syncthreads();
+        prefix |= (uint32_t)s_int[0] << shift;
+        pmask |= 255u << shift;
+        remaining -= s_int[1];
+        __syncthreads();
+      }
+      // index of the `remaining`-th entry equal to the k-th key (index order)
+      int nt = 0;
+#pragma unroll
+      for (int j = 0; j < PER; j++) nt += (j < nloc && key[j] == prefix);
+      int tot_ties;
+      const int trank = block_excl_scan(nt, tmp, &tot_ties);
+      if (trank < remaining && remaining <= trank + nt) {
+        int cnt = trank;
+#pragma unroll
+        for (int j = 0; j < PER; j++) {
+          if (j < nloc && key[j] == prefix) {
+            cnt++;
+            if (cnt == remaining) s_int[2] = (int)(base + j);
           }
         }
       }
       __syncthreads();
-      prefix |= (uint32_t)s_int[0] << shift;
-      pmask |= 255u << shift;
-      remaining -= s_int[1];
-      __syncthreads();
+      Kt = prefix;
+      It = s_int[2];
     }
-    // index of the `remaining`-th entry equal to the k-th key (index order)
-    int nt = 0;
-#pragma unroll
-    for (int j = 0; j < PER; j++) nt += (base + j < nv && key[j] == prefix);
-    int tot_ties;
-    const int trank = block_excl_scan(nt, tmp, &tot_ties);
-    if (trank < remaining && remaining <= trank + nt) {
-      int cnt = trank;
-#pragma unroll
-      for (int j = 0; j < PER; j++) {
-        if (base + j < nv && key[j] == prefix) {
-          cnt++;
-          if (cnt == remaining) s_int[2] = (int)(base + j);
-        }
-      }
-    }
-    __syncthreads();
-    Kt = prefix;
-    It = s_int[2];
+    break;
   }
   // ---- emit the selected ids in ascending order
+  auto selected = [&](int j, int& slot) -> bool {
+    const int n = base + j;
+    if (j >= nloc) return false;
+    if (CERT && band_mode) {
+      if ((in_mask >> j) & 1u) return true;
+      if (!((band_mask >> j) & 1u)) return false;
+      const uint32_t ck = (uint32_t)(cand_pair[slot++] >> 32);
+      return ck < Kt || (ck == Kt && n <= It);
+    }
+    return key[j] < Kt || (key[j] == Kt && n <= It);
+  };
   int nsel = 0;
+  int slot = slot0;
 #pragma unroll
-  for (int j = 0; j < PER; j++) {
-    const int64_t n = base + j;
-    nsel += (n < nv) && (key[j] < Kt || (key[j] == Kt && n <= It));
-  }
+  for (int j = 0; j < PER; j++) nsel += selected(j, slot);
   int tot_sel;
   int pos = block_excl_scan(nsel, tmp, &tot_sel);
+  const bool stage = take <= kStageIds;
+  slot = slot0;
 #pragma unroll
   for (int j = 0; j < PER; j++) {
-    const int64_t n = base + j;
-    if ((n < nv) && (key[j] < Kt || (key[j] == Kt && n <= It))) {
-      if (pos < take) orow[pos] = (int32_t)n + id_offset;
+    if (selected(j, slot)) {
+      if (pos < take) {
+        if (stage) out_s[pos] = (int32_t)(base + j) + id_offset;
+        else orow[pos] = (int32_t)(base + j) + id_offset;
+      }
       pos++;
     }
   }
-  for (int64_t j = take + tid; j < k; j += kTopkThreads) orow[j] = -1;
+  if (stage) {
+    __syncthreads();
+    for (int j = tid; j < k; j += kTopkThreads) orow[j] = j < take ? out_s[j] : -1;
+  } else {
+    for (int j = take + tid; j < k; j += kTopkThreads) orow[j] = -1;
+  }
 }
 
 __global__ void window_idx_kernel(int64_t w, int64_t seqlen, int64_t start_pos, int64_t cols, int64_t total_per_b,
@@ -346,7 +609,8 @@ __global__ void decode_window_kernel(const int32_t* __restrict__ pos, int64_t R,
 }  // namespace
 
 static int launch_select(const float* scores, int64_t R, int64_t N, const int32_t* nvis, int64_t k, int32_t* out,
-                         int64_t out_stride, int32_t id_offset, const int32_t* wpos, int window, hipStream_t st);
+                         int64_t out_stride, int32_t id_offset, const int32_t* wpos, int window, hipStream_t st,
+                         const CertCtx* cert = nullptr);
 
 extern "C" int smla_topk(const float* scores, int64_t R, int64_t N, const int32_t* nvis, int64_t k, int32_t* out,
                          int64_t out_stride, int32_t id_offset, void* stream) {
@@ -358,15 +622,21 @@ extern "C" int smla_topk(const float* scores, int64_t R, int64_t N, const int32_
 }
 
 static int launch_select(const float* scores, int64_t R, int64_t N, const int32_t* nvis, int64_t k, int32_t* out,
-                         int64_t out_stride, int32_t id_offset, const int32_t* wpos, int window, hipStream_t st) {
+                         int64_t out_stride, int32_t id_offset, const int32_t* wpos, int window, hipStream_t st,
+                         const CertCtx* cert) {
   int64_t per = (N + kTopkThreads - 1) / kTopkThreads;
   dim3 grid((unsigned)R), blk(kTopkThreads);
-#define SMLA_TOPK_CASE(P)                                                                          \
-  if (per <= P) {                                                                                  \
-    hipLaunchKernelGGL(topk_kernel<P>, grid, blk, 0, st, scores, N, nvis, (int)k, out, out_stride, id_offset, \
-                       wpos, window);                                                              \
-    SMLA_HIP_CHECK_LAUNCH();                                                                       \
-    return SMLA_OK;                                                                                \
+  const CertCtx cc = cert ? *cert : CertCtx{};
+#define SMLA_TOPK_CASE(P)                                                                                  \
+  if (per <= P) {                                                                                          \
+    if (cert)                                                                                              \
+      hipLaunchKernelGGL((topk_kernel<P, true>), grid, blk, 0, st, scores, N, nvis, (int)k, out, out_stride, \
+                         id_offset, wpos, window, cc);                                                     \
+    else                                                                                                   \
+      hipLaunchKernelGGL((topk_kernel<P, false>), grid, blk, 0, st, scores, N, nvis, (int)k, out,          \
+                         out_stride, id_offset, wpos, window, cc);                                         \
+    SMLA_HIP_CHECK_LAUNCH();                                                                               \
+    return SMLA_OK;                                                                                        \
   }
   SMLA_TOPK_CASE(2)
   SMLA_TOPK_CASE(4)
@@ -386,6 +656,48 @@ extern "C" int smla_select_decode(const float* scores, int64_t R, int64_t N, con
   if (R > 0x7fffffff || k > 0x7fffffff || window > 0x7fffffff) return SMLA_E_UNSUPPORTED;
   if ((N + kTopkThreads - 1) / kTopkThreads > 64) return SMLA_E_UNSUPPORTED;
   return launch_select(scores, R, N, nvis, k, out, out_stride, id_offset, pos, (int)window, (hipStream_t)stream);
+}
+
+static int g_cert_force_exact = 0;  // tests: 1 = rescore every visible key (the uncertified path)
+
+extern "C" void smla_set_index_cert_force_exact(int on) { g_cert_force_exact = on ? 1 : 0; }
+
+extern "C" size_t smla_index_decode_workspace(int64_t B, int64_t S, int64_t N) {
+  if (B <= 0 || S <= 0 || N <= 0) return 0;
+  const int64_t R = B * S, nchunk = (N + 255) / 256;
+  return (size_t)(R * N + R * nchunk) * sizeof(float);
+}
+
+extern "C" int smla_index_decode(const void* q, int q_dtype, const void* keys, int k_dtype, const float* kscale,
+                                 const float* weights, const int32_t* nvis, int64_t B, int64_t S, int64_t Hi,
+                                 int64_t Di, int64_t N, int64_t k, const int32_t* pos, int64_t window,
+                                 int32_t* out, int64_t out_stride, int32_t id_offset, void* workspace,
+                                 size_t workspace_bytes, void* stream) {
+  if (!q || !keys || !weights || !out) return SMLA_E_NULL;
+  if (window > 0 && !pos) return SMLA_E_NULL;
+  if (B <= 0 || S <= 0 || Hi <= 0 || Di <= 0 || N <= 0 || k <= 0 || window < 0 || out_stride < k + window)
+    return SMLA_E_SHAPE;
+  if (!workspace || workspace_bytes < smla_index_decode_workspace(B, S, N)) return SMLA_E_WORKSPACE;
+  const int64_t R = B * S;
+  if (R > 65535 || k > 0x7fffffff || window > 0x7fffffff || (N + kTopkThreads - 1) / kTopkThreads > 64)
+    return SMLA_E_UNSUPPORTED;
+  hipStream_t st = (hipStream_t)stream;
+  float* approx = (float*)workspace;
+  float* ebound = approx + R * N;
+  const int32_t* wpos = window > 0 ? pos : nullptr;
+  if (!(q_dtype == SMLA_BF16 && k_dtype == SMLA_FP8_E4M3 && Hi == 64 && Di == 64)) {
+    // other shapes: the fixed-order scores themselves, then the exact selection
+    const int rc = smla_indexer_score(q, q_dtype, keys, k_dtype, kscale, weights, nvis, B, S, Hi, Di, N, approx,
+                                      stream);
+    if (rc != SMLA_OK) return rc;
+    return launch_select(approx, R, N, nvis, k, out, out_stride, id_offset, wpos, (int)window, st);
+  }
+  int rc = launch_indexer_cert((const uint16_t*)q, (const uint8_t*)keys, kscale, weights, nvis, B, S, N, approx,
+                               ebound, st);
+  if (rc != SMLA_OK) return rc;
+  const CertCtx cc{ebound, (int)((N + 255) / 256), (const uint16_t*)q, (const uint8_t*)keys, kscale, weights, S,
+                   g_cert_force_exact, approx};
+  return launch_select(approx, R, N, nvis, k, out, out_stride, id_offset, wpos, (int)window, st, &cc);
 }
 
 extern "C" int smla_window_topk_idxs(int64_t window_size, int64_t bsz, int64_t seqlen, int64_t start_pos,

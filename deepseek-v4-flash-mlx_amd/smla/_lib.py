@@ -31,6 +31,9 @@ _SIGNATURES = {
                                   _vp, _vp]),
     "smla_topk": (_int, [_vp, _i64, _i64, _vp, _i64, _vp, _i64, _i32, _vp]),
     "smla_select_decode": (_int, [_vp, _i64, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _i32, _vp]),
+    "smla_index_decode": (_int, [_vp, _int, _vp, _int, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64,
+                                 _vp, _i64, _vp, _i64, _i32, _vp, _sz, _vp]),
+    "smla_index_decode_workspace": (_sz, [_i64, _i64, _i64]),
     "smla_block_mean_pool": (_int, [_vp, _int, _i64, _i64, _i64, _i64, _vp, _int, _vp]),
     "smla_gated_pool": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _f32,
                                _int, _vp, _vp]),
@@ -45,6 +48,7 @@ _TUNING = {
     "smla_profile_set_attn_events": (None, [_vp, _vp]),
     "smla_profile_set_attn_main_only": (None, [_int]),
     "smla_set_attn_decode_kernel": (None, [_int]),
+    "smla_set_index_cert_force_exact": (None, [_int]),
     "smla_attn_plan": (None, [_i64, _i64, _i64, _i64, _i64, _i64, _int, _int, ctypes.POINTER(_int),
                               ctypes.POINTER(_int)]),
 }

@@ -32,3 +32,21 @@ def select_decode_indices(scores, k, pos, window, n_raw, out=None):
         out = torch.empty(B, window + k, dtype=torch.int32, device=scores.device)
     ops.select_decode_into(scores.contiguous(), k, pos, window, out, id_offset=n_raw)
     return out
+
+
+def index_decode(q_idx, keys, kscale, weights, nvis, k, pos, window, n_raw, out=None, workspace=None):
+    """Indexer scores and the decode index list in one call: the same list as ``indexer_score``
+    followed by ``select_decode_indices`` (bit-exact), with the scores of bf16 q x e4m3 keys
+    (64 heads x 64 dims) taken on MFMA under a certified error bound and only the keys near the
+    top-k boundary rescored in the fixed order.
+    q_idx [B,1,Hi,Di], keys [B,N,Di], kscale [B,N] or None, weights [B,1,Hi], nvis [B,1] or None,
+    pos [B] int32 -> out [B, window + k] int32."""
+    B, S = q_idx.shape[:2]
+    N = keys.shape[1]
+    if out is None:
+        out = torch.empty(B * S, window + k, dtype=torch.int32, device=q_idx.device)
+    if workspace is None:
+        workspace = torch.empty(ops.index_decode_workspace(B, S, N), dtype=torch.uint8, device=q_idx.device)
+    ops.index_decode_into(q_idx, keys, kscale, weights, nvis, k, pos if window > 0 else None, window, out,
+                          workspace, id_offset=n_raw)
+    return out

@@ -254,6 +254,37 @@ def select_decode_into(scores, k, pos, window, out, id_offset=0, nvis=None):
     return out
 
 
+def index_decode_workspace(B, S, N):
+    """Bytes of workspace smla_index_decode needs for B*S query rows over N keys."""
+    return int(_lib.lib().smla_index_decode_workspace(B, S, N))
+
+
+def index_decode_into(q, keys, kscale, weights, nvis, k, pos, window, out, workspace, id_offset=0):
+    """Indexer scores and the decode index build in one call (smla_index_decode): q [B,S,Hi,Di],
+    keys [B,N,Di], kscale [B,N]|None, weights [B,S,Hi], nvis [B,S]|None, pos [B*S] int32 (None
+    when window == 0), out int32 [B*S, >= window + k] (row stride out.stride(0)), workspace a
+    uint8 tensor of at least index_decode_workspace(B, S, N) bytes."""
+    _on_gpu(q, keys, kscale, weights, nvis, pos, out, workspace)
+    if out.dtype != torch.int32 or out.stride(-1) != 1:
+        raise ValueError("out must be an int32 view with unit inner stride")
+    B, S, Hi, Di = q.shape
+    N = keys.shape[1]
+    need = index_decode_workspace(B, S, N)
+    if workspace.numel() * workspace.element_size() < need:
+        raise ValueError(f"workspace holds {workspace.numel() * workspace.element_size()} bytes, needs {need}")
+    if nvis is not None:
+        nvis = nvis.to(torch.int32).contiguous()
+    if pos is not None:
+        pos = pos.to(torch.int32).contiguous()
+    if kscale is not None:
+        kscale = kscale.float().contiguous()
+    q, keys, weights = q.contiguous(), keys.contiguous(), weights.float().contiguous()
+    _lib.call("smla_index_decode", _p(q), dtype_code(q), _p(keys), dtype_code(keys), _p(kscale), _p(weights),
+              _p(nvis), B, S, Hi, Di, N, k, _p(pos), window, _p(out), out.stride(0), int(id_offset),
+              _p(workspace), need, _stream(q))
+    return out
+
+
 def topk_into(scores, k, out, id_offset=0, nvis=None):
     """Write the top-k selection of scores [R, N] into the int32 view out [R, >=k] (row stride
     out.stride(0)); no allocation."""

@@ -17,6 +17,7 @@
  *                              oracle/decode_engine.py:112-114; the indexer is the build's)
  *   smla_topk                 oracle/decode_engine.py:112-114  cidx selection (take-all when nvis <= k)
  *   smla_select_decode        oracle/decode_engine.py:110-114  widx + cidx in one launch
+ *   smla_index_decode         oracle/decode_engine.py:110-114  indexer scores + widx + cidx (fused)
  *   smla_block_mean_pool      (none: block mean of the 32K decode workload)
  *   smla_gated_pool           ref_torch/compressor.py:41-49    pooling + RMSNorm + RoPE of compressor_prefill
  *   smla_ring_step            oracle/decode_engine.py:96-105   decode compressor ring step and cache append
@@ -138,6 +139,24 @@ int smla_topk(const float* scores, int64_t R, int64_t N, const int32_t* nvis, in
 int smla_select_decode(const float* scores, int64_t R, int64_t N, const int32_t* nvis, int64_t k,
                        const int32_t* pos, int64_t window, int32_t* out, int64_t out_stride,
                        int32_t id_offset, void* stream);
+
+/* Indexer score and decode index build fused: the same output as smla_indexer_score into scores
+ * followed by smla_select_decode (or smla_topk when window == 0; pos may then be NULL), for
+ * R = B*S query rows.  Bit-exact to that pair (the selected sets are the fixed-order scores'
+ * top-k).  For bf16 q, e4m3 keys and Hi == Di == 64 the scores are first computed on MFMA
+ * together with a certified error bound; only keys whose rank the bound leaves open are
+ * rescored in the fixed order (rows that cannot be certified are rescored in full).  Other
+ * shapes and types run the two-step path.  Replaces the compressed index selection of
+ * oracle/decode_engine.py:110-114 with an indexer-ranked one.
+ * workspace: smla_index_decode_workspace(B, S, N) bytes.  Requires ceil(N / 1024) <= 64 and
+ * B*S <= 65535.
+ */
+int smla_index_decode(const void* q, int q_dtype, const void* keys, int k_dtype, const float* kscale,
+                      const float* weights, const int32_t* nvis, int64_t B, int64_t S, int64_t Hi,
+                      int64_t Di, int64_t N, int64_t k, const int32_t* pos, int64_t window,
+                      int32_t* out, int64_t out_stride, int32_t id_offset, void* workspace,
+                      size_t workspace_bytes, void* stream);
+size_t smla_index_decode_workspace(int64_t B, int64_t S, int64_t N);
 
 /* ---------------------------------------------------------------------------------------------
  * Compressor.

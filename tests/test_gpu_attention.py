@@ -2,6 +2,8 @@
 
 Tolerances: fp32 path 1e-5 max-abs; bf16 path max-abs <= 2e-2 and max-abs / max|ref| <= 1e-2
 (the oracle runs in fp32 on the exact bf16 / dequantised-fp8 input values)."""
+import ctypes
+
 import numpy as np
 import pytest
 import torch
@@ -113,6 +115,31 @@ def test_bf16_split_plans_agree(dev, decode_kernel):
             _check_bf16(out, ref, f"target {target}")
     finally:
         lib.smla_set_attn_target_wgs(0)
+
+
+def test_many_splits_merge(dev):
+    """141 splits of 32 rows per query row (more than one load chunk and more splits than merge
+    threads), 16 sequences, a sink and scattered -1 ids: the merge gives the oracle's answer."""
+    from smla import sparse_attn as ssa
+    g = torch.Generator().manual_seed(11)
+    B, H, D, n, T = 16, 64, 576, 5000, 4500
+    announce(f"many splits B={B} T={T}")
+    q = (torch.randn(B, 1, H, D, generator=g) * 0.3).to(torch.bfloat16)
+    kv = (torch.randn(B, n, D, generator=g) * 0.5).to(torch.bfloat16)
+    idx = torch.randint(0, n, (B, 1, T), generator=g, dtype=torch.int32)
+    idx[:, :, ::7] = -1
+    sink = torch.randn(H, generator=g)
+    ref = _oracle_two_source(q, kv, None, sink, idx, D ** -0.5, 512)
+    lib = _lib()
+    ns, rps = ctypes.c_int(0), ctypes.c_int(0)
+    try:
+        lib.smla_set_attn_target_wgs(4096)
+        lib.smla_attn_plan(B, 1, H, D, 512, T, 1, 1, ctypes.byref(ns), ctypes.byref(rps))
+        assert ns.value > 128, ns.value
+        out = ssa.sparse_attn_batched(q.to(dev), kv.to(dev), sink.to(dev), idx.to(dev), D ** -0.5, dv=512)
+    finally:
+        lib.smla_set_attn_target_wgs(0)
+    _check_bf16(out, ref, "many splits")
 
 
 def test_all_masked_rows_are_nan(dev):
