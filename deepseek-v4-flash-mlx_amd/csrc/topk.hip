@@ -17,8 +17,7 @@
 
 namespace {
 
-constexpr int kTopkThreads = 1024;
-constexpr int kWaves = kTopkThreads / 64;
+constexpr int kTopkThreads = 1024;  // the largest workgroup (sizes the per-thread run PER)
 
 __device__ inline uint32_t desc_key(float f) {
   if (f == 0.f) f = 0.f;  // -0 -> +0
@@ -27,22 +26,23 @@ __device__ inline uint32_t desc_key(float f) {
   return ~asc;
 }
 
-// exclusive scan of one value per thread over the block; returns the exclusive prefix and the
-// block total.  `tmp` holds kWaves + 1 ints.
+// exclusive scan of one value per thread over a block of NW waves; returns the exclusive prefix
+// and the block total.  `tmp` holds NW + 1 ints.
+template <int NW>
 __device__ inline int block_excl_scan(int v, int* tmp, int* total) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int x = wave_incl_scan(v);
   if (lane == 63) tmp[wave] = x;
   __syncthreads();
   if (wave == 0) {
-    const int t = lane < kWaves ? tmp[lane] : 0;
+    const int t = lane < NW ? tmp[lane] : 0;
     const int s = wave_incl_scan(t);
-    if (lane < kWaves) tmp[lane] = s - t;  // exclusive wave offsets
-    if (lane == kWaves - 1) tmp[kWaves] = s;
+    if (lane < NW) tmp[lane] = s - t;  // exclusive wave offsets
+    if (lane == NW - 1) tmp[NW] = s;
   }
   __syncthreads();
   const int res = tmp[wave] + x - v;
-  *total = tmp[kWaves];
+  *total = tmp[NW];
   __syncthreads();
   return res;
 }
@@ -98,12 +98,15 @@ __device__ inline int bucket_of(uint32_t key, float lmax, float bscale) {
 // row that cannot be certified (a bound that is not finite, a degenerate spread, more than 256
 // band entries) is rescored in full and selected exactly.
 // Output: window ids (optional), then the selected ids ascending (+ id_offset), then -1.
-template <int PER, bool CERT>
-__global__ __launch_bounds__(kTopkThreads) void topk_kernel(const float* scores, int64_t N,
+template <int PER, bool CERT, int NT>
+__global__ __launch_bounds__(NT) void topk_kernel(const float* scores, int64_t N,
                                                             const int32_t* __restrict__ nvis, int k,
                                                             int32_t* __restrict__ out, int64_t out_stride,
                                                             int32_t id_offset, const int32_t* __restrict__ wpos,
                                                             int window, CertCtx cc) {
+  constexpr int kWaves = NT / 64;
+  constexpr int kBPT = kBuckets / NT;  // histogram buckets owned by each thread in the scan
+  static_assert(kBPT * NT == kBuckets, "buckets per thread");
   __shared__ int hist[kWaves][256];
   __shared__ int bhist[kBuckets + 1];  // + a slot that absorbs the counts of entries past nvis
   __shared__ int tmp[kWaves + 1];
@@ -121,7 +124,7 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(const float* scores,
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int64_t r = blockIdx.x;
-  // N <= 65536 (PER * kTopkThreads): every index of the row fits 32 bits
+  // N <= 65536 (PER * NT): every index of the row fits 32 bits
   int nv = nvis ? nvis[r] : (int)N;
   if (nv > (int)N) nv = (int)N;
   if (nv < 0) nv = 0;
@@ -129,7 +132,7 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(const float* scores,
   int32_t* orow = out + r * out_stride;
   if (wpos) {
     const int64_t p = wpos[r];
-    for (int j = tid; j < window; j += kTopkThreads) {
+    for (int j = tid; j < window; j += NT) {
       const int64_t v = p - window + 1 + j;
       orow[j] = v < 0 ? -1 : (int32_t)v;
     }
@@ -141,7 +144,7 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(const float* scores,
   // this thread's entries j < nloc are visible (index base + j < nvis)
   const int nloc = nv - base < 0 ? 0 : (nv - base > PER ? PER : nv - base);
   if (nv <= k) {
-    for (int j = tid; j < k; j += kTopkThreads) orow[j] = j < nv ? j + id_offset : -1;
+    for (int j = tid; j < k; j += NT) orow[j] = j < nv ? j + id_offset : -1;
     return;
   }
   const int64_t bkey = CERT ? r / cc.S : 0;  // batch entry of the key rows
@@ -198,6 +201,26 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(const float* scores,
       }
     }
   };
+  // the bucket holding the k-th entry (bucket 0 = largest scores) and how many of its entries the
+  // selection takes: s_int[0], s_int[1].  Thread t owns buckets kBPT t .. kBPT t + kBPT - 1.
+  auto find_boundary = [&](int t) {
+    int c[kBPT], sum = 0;
+#pragma unroll
+    for (int i = 0; i < kBPT; i++) {
+      c[i] = bhist[kBPT * t + i];
+      sum += c[i];
+    }
+    int tot;
+    int before = block_excl_scan<kWaves>(sum, tmp, &tot);
+#pragma unroll
+    for (int i = 0; i < kBPT; i++) {
+      if (before < k && k <= before + c[i]) {
+        s_int[0] = kBPT * t + i;
+        s_int[1] = k - before;
+      }
+      before += c[i];
+    }
+  };
   // rank of candidate c among the first `total` in the order (key asc, index asc)
   auto rank_of = [&](int c, int total) -> int {
     const uint64_t me = cand_pair[c];
@@ -228,7 +251,7 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(const float* scores,
   load_scores(sr);
   float emax = 0.f;
   if constexpr (CERT) {
-    for (int c = tid; c < cc.nchunk; c += kTopkThreads) {
+    for (int c = tid; c < cc.nchunk; c += NT) {
       const float e = cc.ebound[r * cc.nchunk + c];
       emax = fmaxf(emax, e == e ? e : SMLA_INF);
     }
@@ -266,7 +289,7 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(const float* scores,
         redf[2 * kWaves + wave] = em;
         s_nan[wave] = wnan;
       }
-      for (int i = tid; i <= kBuckets; i += kTopkThreads) bhist[i] = 0;
+      for (int i = tid; i <= kBuckets; i += NT) bhist[i] = 0;
       if (CERT && pass == 0) {
         const int h = (4 * tid) >> 6, d0 = (4 * tid) & 63;
         *(f32x4_t*)&q_s[h * kQS + d0] = f32x4_t{__uint_as_float(qraw[0] << 16), __uint_as_float(qraw[0] & 0xffff0000u),
@@ -291,19 +314,10 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(const float* scores,
 #pragma unroll
         for (int j = 0; j < PER; j++) atomicAdd(&bhist[j < nloc ? bucket_of(key[j], lmax, bscale) : kBuckets], 1);
         __syncthreads();
-        const int c0 = bhist[2 * tid], c1 = bhist[2 * tid + 1];
-        int tot;
-        const int before = block_excl_scan(c0 + c1, tmp, &tot);
+        find_boundary(tid);
         if (tid == 0) {
           s_int[3] = 0;
           s_int[4] = 0;
-        }
-        if (before < k && k <= before + c0) {
-          s_int[0] = 2 * tid;
-          s_int[1] = k - before;
-        } else if (before + c0 < k && k <= before + c0 + c1) {
-          s_int[0] = 2 * tid + 1;
-          s_int[1] = k - before - c0;
         }
         __syncthreads();
         const int bb = s_int[0], need = s_int[1];
@@ -341,10 +355,10 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(const float* scores,
         if (total <= kMaxCand) {
           // exact scores of the band: its key rows and scales to LDS in one round trip, then one
           // wave per entry
-          for (int t = tid; t < total * 4; t += kTopkThreads)
+          for (int t = tid; t < total * 4; t += NT)
             ck_s[t] = *(const u32x4_t*)(cc.keys + (bkey * N + cand_idx[t >> 2]) * 64 + 16 * (t & 3));
           if (cc.kscale)
-            for (int c = tid; c < total; c += kTopkThreads) cks_s[c] = cc.kscale[bkey * N + cand_idx[c]];
+            for (int c = tid; c < total; c += NT) cks_s[c] = cc.kscale[bkey * N + cand_idx[c]];
           __syncthreads();
           // kRescoreBatch entries per wave at a time: c0 + b * kWaves (past the end: entry c0 again)
 #pragma unroll 1
@@ -425,18 +439,8 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(const float* scores,
 #pragma unroll
       for (int j = 0; j < PER; j++) atomicAdd(&bhist[j < nloc ? bucket_of(key[j], lmax, bscale) : kBuckets], 1);
       __syncthreads();
-      // thread t owns buckets 2t, 2t+1
-      const int c0 = bhist[2 * tid], c1 = bhist[2 * tid + 1];
-      int tot;
-      const int before = block_excl_scan(c0 + c1, tmp, &tot);
+      find_boundary(tid);
       if (tid == 0) s_int[3] = 0;  // candidate counter
-      if (before < k && k <= before + c0) {
-        s_int[0] = 2 * tid;
-        s_int[1] = k - before;
-      } else if (before + c0 < k && k <= before + c0 + c1) {
-        s_int[0] = 2 * tid + 1;
-        s_int[1] = k - before - c0;
-      }
       __syncthreads();
       const int bb = s_int[0], need = s_int[1];
       const int cb = bhist[bb];
@@ -520,7 +524,7 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(const float* scores,
 #pragma unroll
       for (int j = 0; j < PER; j++) nt += (j < nloc && key[j] == prefix);
       int tot_ties;
-      const int trank = block_excl_scan(nt, tmp, &tot_ties);
+      const int trank = block_excl_scan<kWaves>(nt, tmp, &tot_ties);
       if (trank < remaining && remaining <= trank + nt) {
         int cnt = trank;
 #pragma unroll
@@ -554,7 +558,7 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(const float* scores,
 #pragma unroll
   for (int j = 0; j < PER; j++) nsel += selected(j, slot);
   int tot_sel;
-  int pos = block_excl_scan(nsel, tmp, &tot_sel);
+  int pos = block_excl_scan<kWaves>(nsel, tmp, &tot_sel);
   const bool stage = take <= kStageIds;
   slot = slot0;
 #pragma unroll
@@ -569,9 +573,9 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(const float* scores,
   }
   if (stage) {
     __syncthreads();
-    for (int j = tid; j < k; j += kTopkThreads) orow[j] = j < take ? out_s[j] : -1;
+    for (int j = tid; j < k; j += NT) orow[j] = j < take ? out_s[j] : -1;
   } else {
-    for (int j = take + tid; j < k; j += kTopkThreads) orow[j] = -1;
+    for (int j = take + tid; j < k; j += NT) orow[j] = -1;
   }
 }
 
@@ -624,27 +628,28 @@ extern "C" int smla_topk(const float* scores, int64_t R, int64_t N, const int32_
 static int launch_select(const float* scores, int64_t R, int64_t N, const int32_t* nvis, int64_t k, int32_t* out,
                          int64_t out_stride, int32_t id_offset, const int32_t* wpos, int window, hipStream_t st,
                          const CertCtx* cert) {
-  int64_t per = (N + kTopkThreads - 1) / kTopkThreads;
-  dim3 grid((unsigned)R), blk(kTopkThreads);
   const CertCtx cc = cert ? *cert : CertCtx{};
-#define SMLA_TOPK_CASE(P)                                                                                  \
-  if (per <= P) {                                                                                          \
-    if (cert)                                                                                              \
-      hipLaunchKernelGGL((topk_kernel<P, true>), grid, blk, 0, st, scores, N, nvis, (int)k, out, out_stride, \
-                         id_offset, wpos, window, cc);                                                     \
-    else                                                                                                   \
-      hipLaunchKernelGGL((topk_kernel<P, false>), grid, blk, 0, st, scores, N, nvis, (int)k, out,          \
-                         out_stride, id_offset, wpos, window, cc);                                         \
-    SMLA_HIP_CHECK_LAUNCH();                                                                               \
-    return SMLA_OK;                                                                                        \
+  const dim3 grid((unsigned)R);
+  // 1024 threads (16 waves: the per-entry phases are VALU-bound and need the waves to hide latency)
+#define SMLA_TOPK_LAUNCH(P, T)                                                                              \
+  {                                                                                                      \
+    if (cert)                                                                                            \
+      hipLaunchKernelGGL((topk_kernel<P, true, T>), grid, dim3(T), 0, st, scores, N, nvis, (int)k, out,  \
+                         out_stride, id_offset, wpos, window, cc);                                       \
+    else                                                                                                 \
+      hipLaunchKernelGGL((topk_kernel<P, false, T>), grid, dim3(T), 0, st, scores, N, nvis, (int)k, out, \
+                         out_stride, id_offset, wpos, window, cc);                                       \
+    SMLA_HIP_CHECK_LAUNCH();                                                                             \
+    return SMLA_OK;                                                                                      \
   }
-  SMLA_TOPK_CASE(2)
-  SMLA_TOPK_CASE(4)
-  SMLA_TOPK_CASE(8)
-  SMLA_TOPK_CASE(16)
-  SMLA_TOPK_CASE(32)
-  SMLA_TOPK_CASE(64)
-#undef SMLA_TOPK_CASE
+  const int64_t per = (N + kTopkThreads - 1) / kTopkThreads;
+  if (per <= 2) SMLA_TOPK_LAUNCH(2, kTopkThreads)
+  if (per <= 4) SMLA_TOPK_LAUNCH(4, kTopkThreads)
+  if (per <= 8) SMLA_TOPK_LAUNCH(8, kTopkThreads)
+  if (per <= 16) SMLA_TOPK_LAUNCH(16, kTopkThreads)
+  if (per <= 32) SMLA_TOPK_LAUNCH(32, kTopkThreads)
+  if (per <= 64) SMLA_TOPK_LAUNCH(64, kTopkThreads)
+#undef SMLA_TOPK_LAUNCH
   return SMLA_E_UNSUPPORTED;  // N > 65536
 }
 
