@@ -156,6 +156,135 @@ __global__ __launch_bounds__(256) void indexer_kernel(const void* __restrict__ q
   if (n < N) scores[bs * N + n] = live ? (kscale ? acc * kscale[row] : acc) : -SMLA_INF;
 }
 
+// Hi = Di = 64: each lane scores two keys (n and n + 64 of a 128-key workgroup) over its wave's 16
+// heads, walking d in four blocks of 16 in order, so every q read from LDS serves both keys' fma
+// chains (the LDS reads of q bound the one-key form).  Same arithmetic order as indexer_kernel:
+// per (head, key) one fma chain over d = 0..63, then the chain over the heads.
+constexpr int kKeys2 = 128;
+template <int KDT, int QDT>
+__global__ __launch_bounds__(256) void indexer2_kernel(const void* __restrict__ q, const void* __restrict__ keys,
+                                                       const float* __restrict__ kscale,
+                                                       const float* __restrict__ weights,
+                                                       const int32_t* __restrict__ nvis, int64_t S, int64_t N,
+                                                       float* __restrict__ scores) {
+  constexpr int DI = 64;
+  __shared__ __align__(16) float sq[64 * DI];
+  __shared__ float sw[64];
+  __shared__ float sr[kKeys2][65];  // r[key][head]
+  const int64_t bs = blockIdx.y;
+  const int64_t b = bs / S;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t nA = (int64_t)blockIdx.x * kKeys2 + lane, nB = nA + 64;
+  const int64_t nv = nvis ? (int64_t)nvis[bs] : N;
+  const int64_t rowA = b * N + (nA < N ? nA : N - 1), rowB = b * N + (nB < N ? nB : N - 1);
+
+  // both key rows in registers, in their storage type (converted one 16-wide block at a time)
+  constexpr int KW = KDT == SMLA_FP8_E4M3 ? 4 : (KDT == SMLA_BF16 ? 8 : 16);  // 16-byte words per row
+  u32x4_t ka[KW], kb[KW];
+  {
+    const u32x4_t* pa = (const u32x4_t*)((const uint8_t*)keys + rowA * DI * (KW / 4));
+    const u32x4_t* pb = (const u32x4_t*)((const uint8_t*)keys + rowB * DI * (KW / 4));
+#pragma unroll
+    for (int v = 0; v < KW; v++) {
+      ka[v] = pa[v];
+      kb[v] = pb[v];
+    }
+  }
+  // 16 values of a key row starting at d0 = 16 db, as fp32
+  auto block16 = [&](const u32x4_t (&kr)[KW], int db, float (&o)[16]) {
+    if constexpr (KDT == SMLA_FP8_E4M3) {
+      const u32x4_t w = kr[db];
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const f32x2_t lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)w[j], false);
+        const f32x2_t hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)w[j], true);
+        o[4 * j] = lo.x;
+        o[4 * j + 1] = lo.y;
+        o[4 * j + 2] = hi.x;
+        o[4 * j + 3] = hi.y;
+      }
+    } else if constexpr (KDT == SMLA_BF16) {
+#pragma unroll
+      for (int v = 0; v < 2; v++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+          const uint32_t w = kr[2 * db + v][j];
+          o[8 * v + 2 * j] = __uint_as_float(w << 16);
+          o[8 * v + 2 * j + 1] = __uint_as_float(w & 0xffff0000u);
+        }
+    } else {
+#pragma unroll
+      for (int v = 0; v < 4; v++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) o[4 * v + j] = __uint_as_float(kr[4 * db + v][j]);
+    }
+  };
+  // q rows -> LDS as fp32, weights
+  {
+    if constexpr (QDT == SMLA_BF16) {
+      const u32x4_t* qp = (const u32x4_t*)((const uint16_t*)q + bs * 64 * DI);
+      for (int i = tid; i < 64 * DI / 8; i += 256) {
+        const u32x4_t v = qp[i];
+        f32x4_t lo, hi;
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+          lo[2 * j] = __uint_as_float(v[j] << 16);
+          lo[2 * j + 1] = __uint_as_float(v[j] & 0xffff0000u);
+          hi[2 * j] = __uint_as_float(v[j + 2] << 16);
+          hi[2 * j + 1] = __uint_as_float(v[j + 2] & 0xffff0000u);
+        }
+        *(f32x4_t*)(sq + 8 * i) = lo;
+        *(f32x4_t*)(sq + 8 * i + 4) = hi;
+      }
+    } else {
+      const f32x4_t* qp = (const f32x4_t*)((const float*)q + bs * 64 * DI);
+      for (int i = tid; i < 64 * DI / 4; i += 256) *(f32x4_t*)(sq + 4 * i) = qp[i];
+    }
+    if (tid < 64) sw[tid] = weights[bs * 64 + tid];
+  }
+  __syncthreads();
+  float dA[16], dB[16];
+#pragma unroll
+  for (int hh = 0; hh < 16; hh++) {
+    dA[hh] = 0.f;
+    dB[hh] = 0.f;
+  }
+  const int h0 = wave * 16;
+#pragma unroll
+  for (int db = 0; db < 4; db++) {
+    float xa[16], xb[16];
+    block16(ka, db, xa);
+    block16(kb, db, xb);
+#pragma unroll
+    for (int hh = 0; hh < 16; hh++) {
+      const f32x4_t* qh = (const f32x4_t*)(sq + (h0 + hh) * DI + 16 * db);
+#pragma unroll
+      for (int v = 0; v < 4; v++) {
+        const f32x4_t qq = qh[v];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+          dA[hh] = __builtin_fmaf(qq[j], xa[4 * v + j], dA[hh]);
+          dB[hh] = __builtin_fmaf(qq[j], xb[4 * v + j], dB[hh]);
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int hh = 0; hh < 16; hh++) {
+    sr[lane][h0 + hh] = dA[hh] > 0.f ? dA[hh] : 0.f;
+    sr[64 + lane][h0 + hh] = dB[hh] > 0.f ? dB[hh] : 0.f;
+  }
+  __syncthreads();
+  if (wave >= 2) return;
+  // chain over the heads: wave 0 for the first 64 keys, wave 1 for the next 64
+  const int kl = wave * 64 + lane;
+  const int64_t n = (int64_t)blockIdx.x * kKeys2 + kl;
+  float acc = 0.f;
+#pragma unroll 8
+  for (int h = 0; h < 64; h++) acc = __builtin_fmaf(sw[h], sr[kl][h], acc);
+  if (n < N) scores[bs * N + n] = n < nv ? (kscale ? acc * kscale[b * N + n] : acc) : -SMLA_INF;
+}
+
 // Hi > 64: one thread per key, sequential over all heads (same arithmetic order)
 template <int DI, int KDT>
 __global__ __launch_bounds__(256) void indexer_wide_kernel(const void* __restrict__ q, int q_dtype,
@@ -187,7 +316,15 @@ __global__ __launch_bounds__(256) void indexer_wide_kernel(const void* __restric
 template <int DI, int KDT>
 int launch_k(const void* q, int q_dtype, const void* keys, const float* kscale, const float* w,
              const int32_t* nvis, int64_t B, int64_t S, int64_t Hi, int64_t N, float* scores, hipStream_t st) {
-  if (Hi <= 64) {
+  if (Hi == 64 && DI == 64) {
+    const dim3 grid((unsigned)((N + kKeys2 - 1) / kKeys2), (unsigned)(B * S));
+    if (q_dtype == SMLA_BF16)
+      hipLaunchKernelGGL((indexer2_kernel<KDT, SMLA_BF16>), grid, dim3(256), 0, st, q, keys, kscale, w, nvis, S, N,
+                         scores);
+    else
+      hipLaunchKernelGGL((indexer2_kernel<KDT, SMLA_F32>), grid, dim3(256), 0, st, q, keys, kscale, w, nvis, S, N,
+                         scores);
+  } else if (Hi <= 64) {
     dim3 grid((unsigned)((N + kKeys - 1) / kKeys), (unsigned)(B * S));
     const int threads = (int)(((Hi + kHG - 1) / kHG) * 64);
     if (q_dtype == SMLA_BF16)

@@ -21,6 +21,8 @@ def _bits(a):
     ("bf16", "bf16", False, 8, 128, 1000),
     ("f32", "fp8", True, 3, 32, 333),
     ("bf16", "f32", True, 64, 64, 257),
+    ("f32", "bf16", False, 64, 64, 1000),
+    ("f32", "fp8", True, 64, 64, 130),
 ])
 def test_indexer_bit_exact(dev, qdt, kdt, use_scale, Hi, Di, N):
     from smla import indexer as sidx
