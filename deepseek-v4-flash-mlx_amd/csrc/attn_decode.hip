@@ -94,27 +94,6 @@ __global__ __launch_bounds__(768) void attn_decode_kernel(
   const bool scorer = wave < 4;
   const int g = lane >> 4, c = lane & 15;
 
-  // ---- row ids -> LDS (-1: masked, out of range or past the split), whole tiles; the tiles
-  // past the last live id are dropped (index lists padded with -1 at the end cost nothing)
-  int last = -1;
-  for (int t = tid; t < ntiles_all * kTileRows; t += G::NW * 64) {
-    int r = -1;
-    if (t < nrows) {
-      r = ig[t];
-      r = (r >= 0 && r < ntot) ? r : -1;
-    }
-    ids_s[t] = r;
-    if (r >= 0) last = t;
-  }
-  {
-    const float wl = wave_max_dpp((float)last);
-    if (lane == 0) al_s[wave] = wl;  // (the rescale buffer is free until iteration 0)
-  }
-  __syncthreads();
-  const int last_live = (int)wave_max_dpp(lane < G::NW ? al_s[lane] : -1.f);
-  const int ntiles = (last_live + kTileRows) / kTileRows;
-  __syncthreads();  // al_s reads done before any later use
-
   const uint8_t* row0 = n0 > 0 ? (const uint8_t*)src.kv0 + b * n0 * (int64_t)G::ROWB
                                : (const uint8_t*)src.kv1 + b * n1 * (int64_t)G::ROWB;
   auto row_ptr = [&](int rid) -> const uint8_t* {
@@ -139,6 +118,40 @@ __global__ __launch_bounds__(768) void attn_decode_kernel(
       }
     }
   };
+  // ---- the workgroup's 64 Q rows first (they do not depend on the index list, so their copies
+  // overlap the id loads): two tiles of head rows in the last two ring slots, heads past H read
+  // head 0
+  constexpr int QS = G::NBUF - 2;  // first Q slot
+  {
+    const uint8_t* qrow0 = (const uint8_t*)(q + (bs * H + hb) * (int64_t)D);
+    for (int qt = 0; qt < 2; qt++)
+      issue_rows(QS + qt, [&](int r) {
+        const int hl = 32 * qt + r;
+        return qrow0 + (hl < nh ? hl : 0) * (int64_t)G::ROWB;
+      });
+  }
+
+  // ---- row ids -> LDS (-1: masked, out of range or past the split), whole tiles; the tiles
+  // past the last live id are dropped (index lists padded with -1 at the end cost nothing)
+  int last = -1;
+  for (int t = tid; t < ntiles_all * kTileRows; t += G::NW * 64) {
+    int r = -1;
+    if (t < nrows) {
+      r = ig[t];
+      r = (r >= 0 && r < ntot) ? r : -1;
+    }
+    ids_s[t] = r;
+    if (r >= 0) last = t;
+  }
+  {
+    const float wl = wave_max_dpp((float)last);
+    if (lane == 0) al_s[wave] = wl;  // (the rescale buffer is free until iteration 0)
+  }
+  __syncthreads();
+  const int last_live = (int)wave_max_dpp(lane < G::NW ? al_s[lane] : -1.f);
+  const int ntiles = (last_live + kTileRows) / kTileRows;
+  __syncthreads();  // al_s reads done before any later use
+
   auto issue_tile = [&](int tl) {
     if constexpr (!FP8) {
       const lds_i32_t* tid_s = ids_s + tl * kTileRows;
@@ -204,17 +217,7 @@ __global__ __launch_bounds__(768) void attn_decode_kernel(
     }
   };
 
-  // ---- prologue copies: the workgroup's 64 Q rows laid out as two tiles of head rows in the last
-  // two ring slots (heads past H read head 0), then tiles 0 .. NBUF-3
-  constexpr int QS = G::NBUF - 2;  // first Q slot
-  {
-    const uint8_t* qrow0 = (const uint8_t*)(q + (bs * H + hb) * (int64_t)D);
-    for (int qt = 0; qt < 2; qt++)
-      issue_rows(QS + qt, [&](int r) {
-        const int hl = 32 * qt + r;
-        return qrow0 + (hl < nh ? hl : 0) * (int64_t)G::ROWB;
-      });
-  }
+  // ---- prologue copies: tiles 0 .. NBUF-3 (the Q rows are already on their way)
   for (int tl = 0; tl < min(ntiles, QS); tl++) issue_tile(tl);
   F8Regs f8r;  // fp8: the value waves' registers of the next tile to write
   if constexpr (FP8) {
