@@ -27,24 +27,18 @@ __device__ inline uint32_t desc_key(float f) {
 }
 
 // exclusive scan of one value per thread over a block of NW waves; returns the exclusive prefix
-// and the block total.  `tmp` holds NW + 1 ints.
+// and the block total.  `tmp` holds NW ints.  One barrier: every wave scans the per-wave totals
+// itself.  The caller separates two scans on the same `tmp` by a barrier.
 template <int NW>
 __device__ inline int block_excl_scan(int v, int* tmp, int* total) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int x = wave_incl_scan(v);
   if (lane == 63) tmp[wave] = x;
   __syncthreads();
-  if (wave == 0) {
-    const int t = lane < NW ? tmp[lane] : 0;
-    const int s = wave_incl_scan(t);
-    if (lane < NW) tmp[lane] = s - t;  // exclusive wave offsets
-    if (lane == NW - 1) tmp[NW] = s;
-  }
-  __syncthreads();
-  const int res = tmp[wave] + x - v;
-  *total = tmp[NW];
-  __syncthreads();
-  return res;
+  const int wi = wave_incl_scan(lane < NW ? tmp[lane] : 0);
+  const int before = wave > 0 ? __builtin_amdgcn_readlane(wi, wave - 1) : 0;
+  *total = __builtin_amdgcn_readlane(wi, NW - 1);
+  return before + x - v;
 }
 
 constexpr int kBuckets = 2048;
