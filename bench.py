@@ -221,7 +221,7 @@ def other_workloads(dev, reps):
     ape = torch.randn(4, 1024, generator=g).to(dev)
     nw = torch.rand(512, generator=g).to(dev)
     cos_t, sin_t = snr.rope_tables(64, 65536, device=dev)
-    ms = _time_ms(lambda: ops.gated_pool_op(kvp, scp, ape, nw, cos_t, sin_t, 4, 64, 1e-6, True), reps)
+    ms = _time_ms(lambda: ops.gated_pool_op(kvp, scp, ape, nw, cos_t, sin_t, 4, 64, 1e-6, 1), reps)
     gb = 2 * kvp.numel() * 4 + 1024 * 512 * 4 + 1024 * 32 * 4 * 2
     res["gated_pool"] = {"shape": "kv, score [1,4096,1024] fp32 -> [1,1024,512] (overlap softmax + RMSNorm + RoPE + fp8 sim)",
                          "us": round(ms * 1e3, 3), "bytes": gb, "achieved_gbs": round(gb / (ms * 1e-3) / 1e9, 1)}
@@ -230,6 +230,14 @@ def other_workloads(dev, reps):
     qbytes = x.numel() * 4 + x.numel() + x.numel() // 64 * 4
     res["quant_fp8_pow2"] = {"shape": "[8192,576] fp32 -> e4m3 codes + per-64 pow2 scales", "us": round(ms * 1e3, 3),
                              "bytes": qbytes, "achieved_gbs": round(qbytes / (ms * 1e-3) / 1e9, 1)}
+    del x
+    # indexer keys: 1M rows of 128 (512 MB of fp32, larger than the 256 MB MALL) -> stored fp4 form
+    xk = torch.randn(1 << 20, 128, device=dev)
+    ms = _time_ms(lambda: ops.rotate_fp4_op(xk, True, True, False, True), max(2, reps // 2))
+    kb = xk.numel() * 4 + xk.numel() // 2 + xk.numel() // 32
+    res["rotate_fp4"] = {"shape": "[1048576,128] fp32 -> Hadamard + fp4 e2m1 (packed codes + ue8m0 per 32)",
+                         "us": round(ms * 1e3, 3), "bytes": kb, "achieved_gbs": round(kb / (ms * 1e-3) / 1e9, 1),
+                         "peak_gbs": HBM_PEAK_GBS}
     return res
 
 

@@ -6,8 +6,10 @@
 //                        per-channel softmax over 2r slots (slots 0..r-1: previous group's first
 //                        half channels, r..2r-1: own group's second half, ref_torch/compressor.py:
 //                        12-18; group 0 has no previous slots), weighted sum, RMSNorm, RoPE of the
-//                        last rd channels at position g*r, optional fp8 round trip of the first
-//                        d-rd channels (v4mlx/compressor.py:60-62).  One workgroup per output row.
+//                        last rd channels at position g*r, then optionally the fp8 round trip of
+//                        the first d-rd channels (v4mlx/compressor.py:60-62) or, for the indexer
+//                        compressor, the Hadamard rotation and fp4 round trip of all d channels
+//                        (v4mlx/compressor.py:57-59).  One workgroup of d/2 threads per output row.
 //  * ring_step_kernel  : oracle/decode_engine.py:96-105 — write the token into ring slot
 //                        r + pos%r, and on a group boundary pool the ring into one row (same
 //                        epilogue, RoPE position pos+1-r), append it to the compressed cache and
@@ -86,12 +88,13 @@ __device__ inline float block_sum(float v, float* red) {
 }
 
 // Epilogue shared by the prefill pool and the ring step: RMSNorm(norm_w), RoPE of the last rd
-// channels at position `pos`, optional fp8 round trip of channels [0, d-rd).  Thread t owns
-// channels 2t and 2t+1 (d == 2*blockDim.x).  `v0,v1` are the pooled values; the result is written
-// to dst[2t], dst[2t+1].
-__device__ inline void pool_epilogue(float v0, float v1, int d, int rd, float eps, int fp8_sim,
+// channels at position `pos`, then the `sim` quantisation (SMLA_SIM_*).  Thread t owns channels 2t
+// and 2t+1 (d == 2*blockDim.x).  `v0,v1` are the pooled values; the result is written to dst[2t],
+// dst[2t+1].  `xch` (d floats of LDS) carries the rotation stages that cross waves.
+__device__ inline void pool_epilogue(float v0, float v1, int d, int rd, float eps, int sim,
                                      const float* __restrict__ norm_w, const float* __restrict__ cos_t,
-                                     const float* __restrict__ sin_t, int64_t pos, float* red, float* dst) {
+                                     const float* __restrict__ sin_t, int64_t pos, float* red, float* xch,
+                                     float* dst) {
   const int t = threadIdx.x;
   const int c0 = 2 * t;
   float ss = block_sum(v0 * v0 + v1 * v1, red);
@@ -106,7 +109,8 @@ __device__ inline void pool_epilogue(float v0, float v1, int d, int rd, float ep
     float r1 = y0 * sn + y1 * cs;
     y0 = r0;
     y1 = r1;
-  } else if (fp8_sim) {
+  }
+  if (sim == SMLA_SIM_FP8 && c0 < nope) {
     // 64-channel blocks = 32 consecutive threads (half a wave)
     float a = fmaxf(fabsf(y0), fabsf(y1));
 #pragma unroll
@@ -117,6 +121,43 @@ __device__ inline void pool_epilogue(float v0, float v1, int d, int rd, float ep
     float z1 = fminf(fmaxf(y1 / s, -448.f), 448.f);
     y0 = e4m3_to_f32(f32_to_e4m3(z0)) * s;
     y1 = e4m3_to_f32(f32_to_e4m3(z1)) * s;
+  } else if (sim == SMLA_SIM_ROTATE_FP4) {
+    // Hadamard butterfly over the d channels (v4mlx/qat.py:8-20): stage h pairs channels c and
+    // c + h.  h = 1 is inside the thread; h = 2m pairs thread t with t ^ m, in the same wave for
+    // m < 64, through LDS beyond.
+    float a = y0 + y1, b = y0 - y1;
+    y0 = a;
+    y1 = b;
+    for (int m = 1; m <= 32 && 4 * m <= d; m *= 2) {
+      const float o0 = __shfl_xor(y0, m, 64), o1 = __shfl_xor(y1, m, 64);
+      const bool up = t & m;
+      y0 = up ? o0 - y0 : y0 + o0;
+      y1 = up ? o1 - y1 : y1 + o1;
+    }
+    for (int m = 64; 4 * m <= d; m *= 2) {
+      xch[c0] = y0;
+      xch[c0 + 1] = y1;
+      __syncthreads();
+      const int pc = 2 * (t ^ m);
+      const float o0 = xch[pc], o1 = xch[pc + 1];
+      __syncthreads();
+      const bool up = t & m;
+      y0 = up ? o0 - y0 : y0 + o0;
+      y1 = up ? o1 - y1 : y1 + o1;
+    }
+    const float hs = hadamard_scale(__builtin_ctz((unsigned)d));
+    y0 *= hs;
+    y1 *= hs;
+    // fp4 round trip per 32-channel block = 16 threads (one DPP row), v4mlx/qat.py:23-31
+    float am = fmaxf(fabsf(y0), fabsf(y1));
+    am = fmaxf(am, dpp_f<0xB1>(am));
+    am = fmaxf(am, dpp_f<0x4E>(am));
+    am = fmaxf(am, dpp_f<0x141>(am));
+    am = fmaxf(am, dpp_f<0x140>(am));
+    const int k = fp4_scale_exp(am);
+    const float si = exp2i_f32(-k), s = exp2i_f32(k);
+    y0 = e2m1_to_f32(f32_to_e2m1(fminf(fmaxf(y0 * si, -6.f), 6.f))) * s;
+    y1 = e2m1_to_f32(f32_to_e2m1(fminf(fmaxf(y1 * si, -6.f), 6.f))) * s;
   }
   dst[c0] = y0;
   dst[c0 + 1] = y1;
@@ -141,8 +182,9 @@ constexpr int kMaxRatio = 8;
 __global__ __launch_bounds__(kPoolThreads) void gated_pool_kernel(
     const float* __restrict__ kv, const float* __restrict__ score, const float* __restrict__ ape,
     const float* __restrict__ norm_w, const float* __restrict__ cos_t, const float* __restrict__ sin_t, int64_t N,
-    int d, int ratio, int rd, float eps, int fp8_sim, float* __restrict__ out) {
+    int d, int ratio, int rd, float eps, int sim, float* __restrict__ out) {
   __shared__ float red[kPoolThreads / 64];
+  __shared__ float xch[2 * kPoolThreads];
   const int64_t G = N / ratio;
   const int64_t bg = blockIdx.x;
   const int64_t b = bg / G, g = bg % G;
@@ -169,7 +211,7 @@ __global__ __launch_bounds__(kPoolThreads) void gated_pool_kernel(
     }
     pooled[k] = softmax_pool<2 * kMaxRatio>(v, s, ns);
   }
-  pool_epilogue(pooled[0], pooled[1], d, rd, eps, fp8_sim, norm_w, cos_t, sin_t, g * ratio, red,
+  pool_epilogue(pooled[0], pooled[1], d, rd, eps, sim, norm_w, cos_t, sin_t, g * ratio, red, xch,
                 out + bg * (int64_t)d);
 }
 
@@ -177,8 +219,9 @@ __global__ __launch_bounds__(kPoolThreads) void ring_step_kernel(
     float* __restrict__ ring_kv, float* __restrict__ ring_sc, const float* __restrict__ kv_p,
     const float* __restrict__ score_p, const int32_t* __restrict__ pos_arr, const float* __restrict__ ape,
     const float* __restrict__ norm_w, const float* __restrict__ cos_t, const float* __restrict__ sin_t,
-    int64_t n_pos, int d, int ratio, int rd, float eps, int fp8_sim, float* __restrict__ comp, int64_t comp_cap) {
+    int64_t n_pos, int d, int ratio, int rd, float eps, int sim, float* __restrict__ comp, int64_t comp_cap) {
   __shared__ float red[kPoolThreads / 64];
+  __shared__ float xch[2 * kPoolThreads];
   const int64_t b = blockIdx.x;
   const int t = threadIdx.x;
   const int64_t two_d = 2 * (int64_t)d;
@@ -211,7 +254,7 @@ __global__ __launch_bounds__(kPoolThreads) void ring_step_kernel(
   }
   const int64_t grp = (pos + 1) / ratio - 1;
   __shared__ float rowbuf[2 * kPoolThreads];
-  pool_epilogue(pooled[0], pooled[1], d, rd, eps, fp8_sim, norm_w, cos_t, sin_t, pos + 1 - ratio, red, rowbuf);
+  pool_epilogue(pooled[0], pooled[1], d, rd, eps, sim, norm_w, cos_t, sin_t, pos + 1 - ratio, red, xch, rowbuf);
   if (grp < comp_cap) {
     float* dst = comp + (b * comp_cap + grp) * (int64_t)d;
     dst[2 * t] = rowbuf[2 * t];
@@ -300,24 +343,26 @@ extern "C" int smla_block_mean_pool(const void* x, int x_dtype, int64_t B, int64
   return SMLA_OK;
 }
 
-static int check_pool_dims(int64_t d, int64_t ratio, int64_t rd) {
+// d = 2 * threads with whole waves and at most kPoolThreads threads: 128, 256 or 512
+static int check_pool_dims(int64_t d, int64_t ratio, int64_t rd, int sim) {
   if (d <= 0 || ratio <= 0 || rd <= 0 || rd > d || rd % 2 != 0) return SMLA_E_SHAPE;
-  if (d != 2 * kPoolThreads || ratio > kMaxRatio || (d - rd) % 64 != 0) return SMLA_E_UNSUPPORTED;
+  if ((d != 128 && d != 256 && d != 512) || ratio > kMaxRatio || (d - rd) % 64 != 0) return SMLA_E_UNSUPPORTED;
+  if (sim != SMLA_SIM_NONE && sim != SMLA_SIM_FP8 && sim != SMLA_SIM_ROTATE_FP4) return SMLA_E_RANGE;
   return SMLA_OK;
 }
 
 extern "C" int smla_gated_pool(const float* kv, const float* score, const float* ape, const float* norm_w,
                                const float* cos_t, const float* sin_t, int64_t B, int64_t N, int64_t d, int64_t ratio,
-                               int64_t rd, float eps, int fp8_sim, float* out, void* stream) {
+                               int64_t rd, float eps, int sim, float* out, void* stream) {
   if (!kv || !score || !ape || !norm_w || !cos_t || !sin_t || !out) return SMLA_E_NULL;
   if (B <= 0 || N <= 0) return SMLA_E_SHAPE;
-  int rc = check_pool_dims(d, ratio, rd);
+  int rc = check_pool_dims(d, ratio, rd, sim);
   if (rc) return rc;
   if (N % ratio != 0) return SMLA_E_SHAPE;
   int64_t rows = B * (N / ratio);
   if (rows <= 0) return SMLA_OK;
-  hipLaunchKernelGGL(gated_pool_kernel, dim3((unsigned)rows), dim3(kPoolThreads), 0, (hipStream_t)stream, kv, score,
-                     ape, norm_w, cos_t, sin_t, N, (int)d, (int)ratio, (int)rd, eps, fp8_sim, out);
+  hipLaunchKernelGGL(gated_pool_kernel, dim3((unsigned)rows), dim3((unsigned)(d / 2)), 0, (hipStream_t)stream, kv,
+                     score, ape, norm_w, cos_t, sin_t, N, (int)d, (int)ratio, (int)rd, eps, sim, out);
   SMLA_HIP_CHECK_LAUNCH();
   return SMLA_OK;
 }
@@ -325,15 +370,15 @@ extern "C" int smla_gated_pool(const float* kv, const float* score, const float*
 extern "C" int smla_ring_step(float* ring_kv, float* ring_sc, const float* kv_p, const float* score_p,
                               const int32_t* pos, const float* ape, const float* norm_w, const float* cos_t,
                               const float* sin_t, int64_t n_pos, int64_t B, int64_t d, int64_t ratio, int64_t rd,
-                              float eps, int fp8_sim, float* comp_cache, int64_t comp_cap, void* stream) {
+                              float eps, int sim, float* comp_cache, int64_t comp_cap, void* stream) {
   if (!ring_kv || !ring_sc || !kv_p || !score_p || !pos || !ape || !norm_w || !cos_t || !sin_t || !comp_cache)
     return SMLA_E_NULL;
   if (B <= 0 || comp_cap < 0 || n_pos <= 0) return SMLA_E_SHAPE;
-  int rc = check_pool_dims(d, ratio, rd);
+  int rc = check_pool_dims(d, ratio, rd, sim);
   if (rc) return rc;
-  hipLaunchKernelGGL(ring_step_kernel, dim3((unsigned)B), dim3(kPoolThreads), 0, (hipStream_t)stream, ring_kv,
+  hipLaunchKernelGGL(ring_step_kernel, dim3((unsigned)B), dim3((unsigned)(d / 2)), 0, (hipStream_t)stream, ring_kv,
                      ring_sc, kv_p, score_p, pos, ape, norm_w, cos_t, sin_t, n_pos, (int)d, (int)ratio, (int)rd,
-                     eps, fp8_sim, comp_cache, comp_cap);
+                     eps, sim, comp_cache, comp_cap);
   SMLA_HIP_CHECK_LAUNCH();
   return SMLA_OK;
 }

@@ -105,6 +105,47 @@ __host__ __device__ inline float pow2_ceil(float v) {
 }
 
 // ---------------------------------------------------------------------------------------------
+// fp4 e2m1 (grid 0, 0.5, 1, 1.5, 2, 3, 4, 6; bit 3 the sign) with power-of-two block scales.
+// Round to nearest, ties to the even code: the magnitude code counts the decision points passed,
+// strict between an even code and the next, inclusive between an odd code and the next.
+// |z| <= 6 expected (callers clip).
+__host__ __device__ inline uint32_t f32_to_e2m1(float z) {
+  const float a = fabsf(z);
+  uint32_t m = (uint32_t)(a > 0.25f) + (uint32_t)(a >= 0.75f) + (uint32_t)(a > 1.25f) + (uint32_t)(a >= 1.75f) +
+               (uint32_t)(a > 2.5f) + (uint32_t)(a >= 3.5f) + (uint32_t)(a > 5.0f);
+  uint32_t u;
+  __builtin_memcpy(&u, &z, 4);
+  return m | ((u >> 28) & 8u);
+}
+__host__ __device__ inline float e2m1_to_f32(uint32_t code) {
+  // magnitudes 0, 0.5, 1, 1.5, 2, 3, 4, 6 = (code < 2 ? code / 2 : (2 + (code & 1)) * 2^((code >> 1) - 1) / 2)
+  const uint32_t c = code & 7u;
+  const float m = c < 2u ? 0.5f * (float)c : (float)(2u + (c & 1u)) * (float)(1u << ((c >> 1) - 1u)) * 0.5f;
+  return (code & 8u) ? -m : m;
+}
+// exponent k of the fp4 block scale s = 2^k = 2^ceil(log2(max(amax, 6*2^-126) / 6)); the division
+// is the float32 one of the definition (rounded), the ceiling is exact on its bits
+__host__ __device__ inline int fp4_scale_exp(float amax) {
+  const float a = fmaxf(amax, 6.0f * 0x1p-126f);
+  const float v = a / 6.0f;  // >= 2^-126: a normal number
+  uint32_t u;
+  __builtin_memcpy(&u, &v, 4);
+  return (int)((u >> 23) & 0xffu) - 127 + ((u & 0x7fffffu) ? 1 : 0);
+}
+// 2^k as float32 for -126 <= k <= 127
+__host__ __device__ inline float exp2i_f32(int k) {
+  const uint32_t u = (uint32_t)(k + 127) << 23;
+  float f;
+  __builtin_memcpy(&f, &u, 4);
+  return f;
+}
+// float32(n^-0.5) for n = 2^lg: 2^-(lg/2), times float32(sqrt(0.5)) = 0x3F3504F3 when lg is odd
+__host__ __device__ inline float hadamard_scale(int lg) {
+  const float p = exp2i_f32(-(lg >> 1));
+  return (lg & 1) ? p * 0.707106769084930419921875f : p;
+}
+
+// ---------------------------------------------------------------------------------------------
 // wave64 reductions
 __device__ inline float wave_max(float v) {
 #pragma unroll

@@ -40,7 +40,12 @@ _SIGNATURES = {
     "smla_ring_step": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64,
                               _f32, _int, _vp, _i64, _vp]),
     "smla_quant_fp8_pow2": (_int, [_vp, _int, _i64, _i64, _vp, _vp, _vp]),
+    "smla_rotate_fp4": (_int, [_vp, _int, _i64, _i64, _int, _vp, _vp, _vp, _vp]),
 }
+
+# sim modes of smla_gated_pool / smla_ring_step, flags of smla_rotate_fp4
+SIM_NONE, SIM_FP8, SIM_ROTATE_FP4 = 0, 1, 2
+QAT_ROTATE, QAT_FP4 = 1, 2
 
 # symbols exported for tuning only (not part of the public header)
 _TUNING = {

@@ -4,7 +4,9 @@
   done with torch indexing on the device).
 * ``compressor_prefill(x, wkv, wgate, ape, norm_w, ...)`` — ``ref_torch/compressor.py:21-50``:
   projections with torch.matmul (fp32), pooling + RMSNorm + RoPE in the HIP ``gated_pool``
-  kernel; returns (kv, state) like the reference.
+  kernel; returns (kv, state) like the reference.  ``fp8_sim`` adds the fp8 round trip of the
+  non-rope channels (``v4mlx/compressor.py:60-62``); ``rotate`` the indexer compressor's
+  Hadamard + fp4 round trip of all channels (``v4mlx/compressor.py:57-59``), in the same kernel.
 * ``block_mean_pool(kv, ratio)`` — plain block mean, HIP.
 * ``Ring`` — the decode-time compressor ring of ``oracle/decode_engine.py:90-105`` kept on the
   device: ``Ring.step`` writes the token, emits a row every ``ratio`` tokens straight into the
@@ -12,8 +14,12 @@
 """
 import torch
 
-from . import ops
+from . import _lib, ops
 from .norm_rope import rope_tables
+
+
+def _sim(fp8_sim, rotate):
+    return _lib.SIM_ROTATE_FP4 if rotate else _lib.SIM_FP8 if fp8_sim else _lib.SIM_NONE
 
 
 def overlap_transform(tensor, ratio, d, value):
@@ -25,7 +31,8 @@ def overlap_transform(tensor, ratio, d, value):
 
 
 def compressor_prefill(x, wkv, wgate, ape, norm_w, head_dim=512, ratio=4, rope_head_dim=64, base=160000.0,
-                       original_seq_len=65536, factor=16, beta_fast=32, beta_slow=1, fp8_sim=False):
+                       original_seq_len=65536, factor=16, beta_fast=32, beta_slow=1, fp8_sim=False,
+                       rotate=False):
     """x:[b,s,dim] -> (kv:[b, s//ratio, head_dim] fp32 post-RoPE, state dict)."""
     b, s, _ = x.shape
     xf = x.float()
@@ -44,7 +51,7 @@ def compressor_prefill(x, wkv, wgate, ape, norm_w, head_dim=512, ratio=4, rope_h
     cos_t, sin_t = rope_tables(rope_head_dim, s, original_seq_len, base, factor, beta_fast, beta_slow,
                                device=x.device)
     out = ops.gated_pool_op(kv[:, :cut], score[:, :cut], ape, norm_w, cos_t, sin_t, ratio, rope_head_dim,
-                            1e-6, fp8_sim)
+                            1e-6, _sim(fp8_sim, rotate))
     return out, state
 
 
@@ -61,8 +68,8 @@ class Ring:
     """
 
     def __init__(self, B, head_dim, ape, norm_w, ratio=4, rope_head_dim=64, max_pos=65536, fp8_sim=True,
-                 device="cuda", rope_args=(65536, 160000.0, 16, 32, 1)):
-        self.ratio, self.rd, self.fp8_sim = ratio, rope_head_dim, fp8_sim
+                 device="cuda", rope_args=(65536, 160000.0, 16, 32, 1), rotate=False):
+        self.ratio, self.rd, self.sim = ratio, rope_head_dim, _sim(fp8_sim, rotate)
         self.ring_kv = torch.zeros(B, 2 * ratio, 2 * head_dim, device=device)
         self.ring_sc = torch.full((B, 2 * ratio, 2 * head_dim), float("-inf"), device=device)
         self.ape = ape.float().contiguous().to(device)
@@ -89,4 +96,4 @@ class Ring:
     def step(self, kv_p, score_p, pos, comp_cache):
         """kv_p/score_p: [B, 2d] projections of the token at positions pos [B] (int32, device)."""
         ops.ring_step_op(self.ring_kv, self.ring_sc, kv_p, score_p, pos, self.ape, self.norm_w, self.cos_t,
-                         self.sin_t, self.ratio, self.rd, 1e-6, self.fp8_sim, comp_cache)
+                         self.sin_t, self.ratio, self.rd, 1e-6, self.sim, comp_cache)

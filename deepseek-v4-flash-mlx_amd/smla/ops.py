@@ -144,8 +144,9 @@ def _(x, ratio):
 @torch.library.custom_op("smla::gated_pool", mutates_args=(), device_types="cuda")
 def gated_pool_op(kv: torch.Tensor, score: torch.Tensor, ape: torch.Tensor, norm_w: torch.Tensor,
                   cos_t: torch.Tensor, sin_t: torch.Tensor, ratio: int, rope_head_dim: int, eps: float,
-                  fp8_sim: bool) -> torch.Tensor:
-    """kv, score [B,N,2d] fp32 (N % ratio == 0) -> [B,N//ratio,d] fp32."""
+                  sim: int) -> torch.Tensor:
+    """kv, score [B,N,2d] fp32 (N % ratio == 0) -> [B,N//ratio,d] fp32.  sim: 0 none, 1 fp8 of the
+    non-rope channels, 2 Hadamard + fp4 of all channels (``_lib.SIM_*``)."""
     _on_gpu(kv, score, ape, norm_w, cos_t, sin_t)
     kv, score = kv.float().contiguous(), score.float().contiguous()
     ape, norm_w = ape.float().contiguous(), norm_w.float().contiguous()
@@ -156,12 +157,12 @@ def gated_pool_op(kv: torch.Tensor, score: torch.Tensor, ape: torch.Tensor, norm
         raise ValueError("rotation tables must cover every token position")
     out = torch.empty(B, N // ratio, d, dtype=torch.float32, device=kv.device)
     _lib.call("smla_gated_pool", _p(kv), _p(score), _p(ape), _p(norm_w), _p(cos_t), _p(sin_t), B, N, d,
-              ratio, rope_head_dim, float(eps), int(bool(fp8_sim)), _p(out), _stream(kv))
+              ratio, rope_head_dim, float(eps), int(sim), _p(out), _stream(kv))
     return out
 
 
 @gated_pool_op.register_fake
-def _(kv, score, ape, norm_w, cos_t, sin_t, ratio, rope_head_dim, eps, fp8_sim):
+def _(kv, score, ape, norm_w, cos_t, sin_t, ratio, rope_head_dim, eps, sim):
     return kv.new_empty(kv.shape[0], kv.shape[1] // ratio, kv.shape[2] // 2, dtype=torch.float32)
 
 
@@ -170,7 +171,7 @@ def _(kv, score, ape, norm_w, cos_t, sin_t, ratio, rope_head_dim, eps, fp8_sim):
                          device_types="cuda")
 def ring_step_op(ring_kv: torch.Tensor, ring_sc: torch.Tensor, kv_p: torch.Tensor, score_p: torch.Tensor,
                  pos: torch.Tensor, ape: torch.Tensor, norm_w: torch.Tensor, cos_t: torch.Tensor,
-                 sin_t: torch.Tensor, ratio: int, rope_head_dim: int, eps: float, fp8_sim: bool,
+                 sin_t: torch.Tensor, ratio: int, rope_head_dim: int, eps: float, sim: int,
                  comp_cache: torch.Tensor) -> None:
     """In-place decode ring update for B sequences; appends emitted rows to comp_cache [B,cap,d]."""
     _on_gpu(ring_kv, ring_sc, kv_p, score_p, pos, ape, norm_w, cos_t, sin_t, comp_cache)
@@ -184,11 +185,11 @@ def ring_step_op(ring_kv: torch.Tensor, ring_sc: torch.Tensor, kv_p: torch.Tenso
     _lib.call("smla_ring_step", _p(ring_kv), _p(ring_sc), _p(kv_p), _p(score_p), _p(pos),
               _p(ape.float().contiguous()), _p(norm_w.float().contiguous()), _p(cos_t.float().contiguous()),
               _p(sin_t.float().contiguous()), cos_t.shape[0], B, d, ratio, rope_head_dim, float(eps),
-              int(bool(fp8_sim)), _p(comp_cache), comp_cache.shape[1], _stream(ring_kv))
+              int(sim), _p(comp_cache), comp_cache.shape[1], _stream(ring_kv))
 
 
 @ring_step_op.register_fake
-def _(ring_kv, ring_sc, kv_p, score_p, pos, ape, norm_w, cos_t, sin_t, ratio, rope_head_dim, eps, fp8_sim,
+def _(ring_kv, ring_sc, kv_p, score_p, pos, ape, norm_w, cos_t, sin_t, ratio, rope_head_dim, eps, sim,
       comp_cache):
     return None
 
@@ -211,6 +212,37 @@ def quant_fp8_pow2_op(x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
 def _(x):
     return (x.new_empty(x.shape, dtype=torch.uint8),
             x.new_empty(*x.shape[:-1], x.shape[-1] // 64, dtype=torch.float32))
+
+
+# ----------------------------------------------------------------------------------------------
+@torch.library.custom_op("smla::rotate_fp4", mutates_args=(), device_types="cuda")
+def rotate_fp4_op(x: torch.Tensor, rotate: bool, fp4: bool, want_out: bool,
+                  want_codes: bool) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """x [..., n] fp32/bf16 (n a power of two, 32..1024) -> (out fp32 [..., n], packed e2m1 codes
+    uint8 [..., n/2], ue8m0 scales uint8 [..., n/32]); outputs not asked for come back empty."""
+    _on_gpu(x)
+    if x.dtype not in (torch.float32, torch.bfloat16):
+        raise TypeError("rotate_fp4 takes fp32 or bf16")
+    if want_codes and not fp4:
+        raise ValueError("the stored form is the fp4 one")
+    x = x.contiguous()
+    n = x.shape[-1]
+    rows = x.numel() // n if n else 0
+    out = torch.empty(x.shape if want_out else (0,), dtype=torch.float32, device=x.device)
+    codes = torch.empty((*x.shape[:-1], n // 2) if want_codes else (0,), dtype=torch.uint8, device=x.device)
+    scales = torch.empty((*x.shape[:-1], n // 32) if want_codes else (0,), dtype=torch.uint8, device=x.device)
+    flags = (_lib.QAT_ROTATE if rotate else 0) | (_lib.QAT_FP4 if fp4 else 0)
+    _lib.call("smla_rotate_fp4", _p(x), dtype_code(x), rows, n, flags, _p(out) if want_out else None,
+              _p(codes) if want_codes else None, _p(scales) if want_codes else None, _stream(x))
+    return out, codes, scales
+
+
+@rotate_fp4_op.register_fake
+def _(x, rotate, fp4, want_out, want_codes):
+    n = x.shape[-1]
+    return (x.new_empty(x.shape if want_out else (0,), dtype=torch.float32),
+            x.new_empty((*x.shape[:-1], n // 2) if want_codes else (0,), dtype=torch.uint8),
+            x.new_empty((*x.shape[:-1], n // 32) if want_codes else (0,), dtype=torch.uint8))
 
 
 # ----------------------------------------------------------------------------------------------

@@ -22,6 +22,8 @@
  *   smla_gated_pool           ref_torch/compressor.py:41-49    pooling + RMSNorm + RoPE of compressor_prefill
  *   smla_ring_step            oracle/decode_engine.py:96-105   decode compressor ring step and cache append
  *   smla_quant_fp8_pow2       v4mlx/compressor.py:11-20        act_quant_sim (stored form: codes + pow2 scales)
+ *   smla_rotate_fp4           v4mlx/qat.py:8-31                hadamard_rotate, fp4_act_quant (and stored form)
+ *                             v4mlx/compressor.py:57-59        the indexer compressor's key transform
  */
 #ifndef SMLA_H
 #define SMLA_H
@@ -167,29 +169,39 @@ size_t smla_index_decode_workspace(int64_t B, int64_t S, int64_t N);
 int smla_block_mean_pool(const void* x, int x_dtype, int64_t B, int64_t N, int64_t D,
                          int64_t ratio, void* out, int out_dtype, void* stream);
 
+/* Quantisation applied to a compressed row after its RoPE (the `sim` argument of smla_gated_pool
+ * and smla_ring_step):
+ *   SMLA_SIM_NONE        none (ref_torch/compressor.py:21-50);
+ *   SMLA_SIM_FP8         the d-rd non-rope channels fp8 round-tripped with pow2 block-64 scales
+ *                        (v4mlx/compressor.py:60-62, apply_sim=True);
+ *   SMLA_SIM_ROTATE_FP4  all d channels Hadamard-rotated, then fp4 round-tripped with pow2
+ *                        block-32 scales (v4mlx/compressor.py:57-59, rotate=True: the indexer
+ *                        compressor). */
+enum { SMLA_SIM_NONE = 0, SMLA_SIM_FP8 = 1, SMLA_SIM_ROTATE_FP4 = 2 };
+
 /* smla_gated_pool: the pooling half of ref_torch/compressor.py:21-50 (compressor_prefill), from
  * the projections kv = x@wkv^T and score = x@wgate^T:
  *   kv, score [B,N,2d] fp32 (N a multiple of ratio);  ape [ratio,2d];  norm_w [d];
  *   cos, sin [>= N, rd/2] fp32 rotation tables indexed by token position (row g uses position
- *   g*ratio);  out [B, N/ratio, d] fp32 (or, with fp8_sim != 0, the d-rd non-rope channels
- *   fp8 round-tripped with pow2 block-64 scales as v4mlx/compressor.py:60-62).
+ *   g*ratio);  out [B, N/ratio, d] fp32, quantised as `sim` says (SMLA_SIM_*).
+ *   d is 128, 256 or 512; (d - rd) % 64 == 0; ratio <= 8.
  */
 int smla_gated_pool(const float* kv, const float* score, const float* ape, const float* norm_w,
                     const float* cos_t, const float* sin_t, int64_t B, int64_t N, int64_t d,
-                    int64_t ratio, int64_t rd, float eps, int fp8_sim, float* out, void* stream);
+                    int64_t ratio, int64_t rd, float eps, int sim, float* out, void* stream);
 
 /* smla_ring_step: one decode token of the compressor ring (oracle/decode_engine.py:96-105) for
  * B sequences at positions pos[b]:
  *   ring_kv, ring_sc [B, 2*ratio, 2d] fp32 (updated);  kv_p, score_p [B, 2d] fp32 projections;
  *   when (pos+1) % ratio == 0 the ring emits a row (softmax pool, RMSNorm(norm_w), RoPE with
- *   cos/sin [n_pos, rd/2] at position pos+1-ratio, optional fp8 round trip of the non-rope
- *   channels) written to comp_cache[b, (pos+1)/ratio - 1, :] ([B, comp_cap, d] fp32), then
+ *   cos/sin [n_pos, rd/2] at position pos+1-ratio, then the `sim` quantisation, SMLA_SIM_*)
+ *   written to comp_cache[b, (pos+1)/ratio - 1, :] ([B, comp_cap, d] fp32), then
  *   shifts.  Rows that would land at or past comp_cap are not written.  A sequence whose pos is
  *   negative or whose RoPE position is not below n_pos is left untouched. */
 int smla_ring_step(float* ring_kv, float* ring_sc, const float* kv_p, const float* score_p,
                    const int32_t* pos, const float* ape, const float* norm_w,
                    const float* cos_t, const float* sin_t, int64_t n_pos, int64_t B, int64_t d,
-                   int64_t ratio, int64_t rd, float eps, int fp8_sim, float* comp_cache,
+                   int64_t ratio, int64_t rd, float eps, int sim, float* comp_cache,
                    int64_t comp_cap, void* stream);
 
 /* smla_quant_fp8_pow2: per 64-element block, s = 2^ceil(log2(max(|x|,1e-4)/448)),
@@ -198,6 +210,26 @@ int smla_ring_step(float* ring_kv, float* ring_sc, const float* kv_p, const floa
  * v4mlx/compressor.py:11-20. */
 int smla_quant_fp8_pow2(const void* x, int x_dtype, int64_t rows, int64_t D, uint8_t* codes,
                         float* scales, void* stream);
+
+/* ---------------------------------------------------------------------------------------------
+ * Indexer-key transform.  Replaces v4mlx/qat.py:8-31 (hadamard_rotate, fp4_act_quant) as the
+ * indexer compressor applies them (v4mlx/compressor.py:57-59).
+ *
+ *   x       [rows, n] F32 or BF16, n a power of two in 32..1024, 16-byte aligned
+ *   flags   SMLA_QAT_ROTATE: y = H_n x * float32(n^-0.5), the butterfly with stages
+ *           h = 1, 2, ..., n/2 in float32 (pairs (y[i], y[i+h]) -> (sum, difference));
+ *           SMLA_QAT_FP4: per block of 32, s = 2^ceil(log2(max(amax, 6*2^-126) / 6)),
+ *           q = e2m1(clip(y / s, +-6)) (round to nearest even, grid 0..6);
+ *           both: rotation first (the indexer key path)
+ *   out     [rows, n] fp32 or NULL: the result (with FP4, the round trip q * s)
+ *   codes   [rows, n/2] uint8 or NULL: packed e2m1 codes, element 2i in the low nibble of byte
+ *           i, bit 3 the sign (needs SMLA_QAT_FP4);
+ *   scales  [rows, n/32] uint8 ue8m0 (log2(s) + 127), given exactly when codes is.
+ * At least one of out / codes.  Bit-exact with the reference's float32 arithmetic; the scale
+ * exponent is the exact ceiling of log2 of the float32 quotient amax / 6. */
+enum { SMLA_QAT_ROTATE = 1, SMLA_QAT_FP4 = 2 };
+int smla_rotate_fp4(const void* x, int x_dtype, int64_t rows, int64_t n, int flags, float* out,
+                    uint8_t* codes, uint8_t* scales, void* stream);
 
 #ifdef __cplusplus
 }

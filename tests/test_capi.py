@@ -67,7 +67,18 @@ def test_host_validation_rejects_bad_arguments():
     assert lib.smla_indexer_score(fake, 1, fake, 2, None, fake, None, 1, 1, 4, 48, 10, fake, None) == -4
     assert lib.smla_block_mean_pool(fake, 1, 1, 8, 12, 4, fake, 1, None) == -4   # D % 8
     assert lib.smla_gated_pool(fake, fake, fake, fake, fake, fake, 1, 8, 512, 4, 63, 1e-6, 0, fake, None) == -2
-    assert lib.smla_gated_pool(fake, fake, fake, fake, fake, fake, 1, 8, 256, 4, 64, 1e-6, 0, fake, None) == -4
+    assert lib.smla_gated_pool(fake, fake, fake, fake, fake, fake, 1, 8, 192, 4, 64, 1e-6, 0, fake, None) == -4
+    assert lib.smla_gated_pool(fake, fake, fake, fake, fake, fake, 1, 8, 256, 4, 64, 1e-6, 3, fake, None) == -6
+    # rotate_fp4: row length, flags, codes without scales, dtype, alignment
+    assert lib.smla_rotate_fp4(fake, 0, 4, 48, 3, fake, None, None, None) == -4
+    assert lib.smla_rotate_fp4(fake, 0, 4, 2048, 3, fake, None, None, None) == -4
+    assert lib.smla_rotate_fp4(fake, 0, 4, 64, 4, fake, None, None, None) == -4
+    assert lib.smla_rotate_fp4(fake, 0, 4, 64, 3, None, fake, None, None) == -1
+    assert lib.smla_rotate_fp4(fake, 0, 4, 64, 1, None, fake, fake, None) == -4     # codes need FP4
+    assert lib.smla_rotate_fp4(fake, 0, 4, 64, 3, None, None, None, None) == -1     # no output
+    assert lib.smla_rotate_fp4(fake, 2, 4, 64, 3, fake, None, None, None) == -3
+    assert lib.smla_rotate_fp4(ctypes.c_void_p(24), 0, 4, 64, 3, fake, None, None, None) == -4
+    assert lib.smla_rotate_fp4(fake, 0, 0, 64, 3, fake, None, None, None) == 0       # no rows
     assert lib.smla_quant_fp8_pow2(fake, 1, 4, 100, fake, fake, None) == -2
     assert lib.smla_window_topk_idxs(0, 1, 1, 0, fake, None) == -2
     assert lib.smla_decode_window_idxs(fake, 2, 128, fake, 64, None) == -2
@@ -97,6 +108,14 @@ def codec(tmp_path_factory):
     lib.host_pow2_ceil.argtypes = [ctypes.c_float]
     lib.host_f32_to_bf16.restype = ctypes.c_uint16
     lib.host_f32_to_bf16.argtypes = [ctypes.c_float]
+    lib.host_f32_to_e2m1.restype = ctypes.c_uint32
+    lib.host_f32_to_e2m1.argtypes = [ctypes.c_float]
+    lib.host_e2m1_to_f32.restype = ctypes.c_float
+    lib.host_e2m1_to_f32.argtypes = [ctypes.c_uint32]
+    lib.host_fp4_scale_exp.restype = ctypes.c_int
+    lib.host_fp4_scale_exp.argtypes = [ctypes.c_float]
+    lib.host_hadamard_scale.restype = ctypes.c_float
+    lib.host_hadamard_scale.argtypes = [ctypes.c_int]
     return lib
 
 
@@ -128,3 +147,24 @@ def test_device_pow2_and_bf16_match_oracle(codec):
     ref = torch.from_numpy(x).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
     got = np.array([codec.host_f32_to_bf16(float(v)) for v in x], dtype=np.uint16)
     np.testing.assert_array_equal(got, ref)
+
+
+def test_device_fp4_codec_matches_oracle(codec):
+    from oracle import qat
+    for c in range(16):
+        v = codec.host_e2m1_to_f32(c)
+        assert v == qat.e2m1_value(c) and np.signbit(v) == bool(c & 8), c
+    grid = qat.FP4_GRID.astype(np.float64)
+    mids = ((grid[1:] + grid[:-1]) / 2).astype(np.float32)
+    rng = np.random.default_rng(5)
+    x = np.concatenate([qat.FP4_GRID, mids, np.nextafter(mids, 0), np.nextafter(mids, 7),
+                        rng.uniform(-6, 6, 3000).astype(np.float32)])
+    x = np.concatenate([x, -x, np.float32([-0.0, 1e-30, -1e-30])]).astype(np.float32)
+    got = np.array([codec.host_f32_to_e2m1(float(v)) for v in x], dtype=np.uint8)
+    np.testing.assert_array_equal(got, qat.e2m1_code(x))
+    amax = np.concatenate([(rng.uniform(0.5, 1, 2000) * np.exp2(rng.integers(-140, 120, 2000))),
+                           6.0 * np.exp2(np.arange(-126.0, 126.0)), [0.0, 3.4e38]]).astype(np.float32)
+    got = np.array([codec.host_fp4_scale_exp(float(a)) for a in amax])
+    np.testing.assert_array_equal(got, qat.fp4_scale_exponent(amax))
+    for lg in range(5, 11):
+        assert codec.host_hadamard_scale(lg) == qat.rotate_scale(2 ** lg)

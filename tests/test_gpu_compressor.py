@@ -51,7 +51,7 @@ def test_gated_pool_vs_oracle(dev, fp8_sim):
     cis = onr.precompute_freqs_cis(rd, N, 65536, 160000.0, 16, 32, 1)
     cos_t, sin_t = cis.real.contiguous(), cis.imag.contiguous()
     got = ops.gated_pool_op(kv.to(dev), sc_.to(dev), ape.to(dev), nw.to(dev), cos_t.to(dev), sin_t.to(dev), r, rd,
-                            1e-6, fp8_sim).cpu()
+                            1e-6, int(fp8_sim)).cpu()
     ref = oc.gated_pool(kv, sc_, ape, nw, cis, r, rd)
     if not fp8_sim:
         np.testing.assert_allclose(got.numpy(), ref.numpy(), rtol=1e-4, atol=2e-5)
