@@ -238,6 +238,31 @@ def other_workloads(dev, reps):
     res["rotate_fp4"] = {"shape": "[1048576,128] fp32 -> Hadamard + fp4 e2m1 (packed codes + ue8m0 per 32)",
                          "us": round(ms * 1e3, 3), "bytes": kb, "achieved_gbs": round(kb / (ms * 1e-3) / 1e9, 1),
                          "peak_gbs": HBM_PEAK_GBS}
+    del xk
+    # attention output path of one decode step: 8 tokens, inverse RoPE + o_grouped (wo_a 8x[1024,4096],
+    # wo_b [4096,8192], bf16).  Three weight copies (384 MB) rotate so the MALL cannot hold them.
+    T, ncopy = 8, 3
+    wts = [((torch.randn(8192, 4096, device=dev) * 0.02).to(torch.bfloat16),
+            (torch.randn(4096, 8192, device=dev) * 0.02).to(torch.bfloat16)) for _ in range(ncopy)]
+    o = torch.randn(T, 64, 512, device=dev).to(torch.bfloat16)
+    opos = torch.arange(30000, 30000 + T, dtype=torch.int32, device=dev)
+    ct, st_ = snr.rope_tables(64, 65536, device=dev)
+    calls = [lambda i=i: ops.o_proj_op(o, opos, ct, st_, wts[i][0], wts[i][1], 8, torch.bfloat16)
+             for i in range(ncopy)]
+    for c in calls:
+        c()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for c in calls:
+            c()
+    ms = _time_ms(graph.replay, max(2, reps // 4)) / ncopy
+    ob = 2 * 8192 * 4096 * 2 + o.numel() * 2 + T * 8192 * 2 * 2 + T * 4096 * 2
+    res["o_proj"] = {"shape": "T=8 tokens: inverse RoPE + o_grouped, wo_a [8192,4096] + wo_b [4096,8192] bf16 "
+                              "(two launches; a graph of 3 calls over rotating weight copies, per call)",
+                     "us": round(ms * 1e3, 3), "bytes": ob, "achieved_gbs": round(ob / (ms * 1e-3) / 1e9, 1),
+                     "peak_gbs": HBM_PEAK_GBS}
+    del graph, wts
     return res
 
 

@@ -8,7 +8,7 @@ from concurrent.futures import ThreadPoolExecutor
 _HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(os.path.dirname(_HERE), "csrc")
 SOURCES = ["attn.hip", "attn_bf16.hip", "attn_decode.hip", "prefill.hip", "indexer.hip", "topk.hip", "pool.hip",
-           "qat.hip", "capi.hip"]
+           "qat.hip", "linear.hip", "capi.hip"]
 OUT = os.path.join(_HERE, "libsmla.so")
 
 FLAGS = ["-O3", "--offload-arch=gfx950", "-std=c++17", "-fPIC",

@@ -41,6 +41,10 @@ _SIGNATURES = {
                               _f32, _int, _vp, _i64, _vp]),
     "smla_quant_fp8_pow2": (_int, [_vp, _int, _i64, _i64, _vp, _vp, _vp]),
     "smla_rotate_fp4": (_int, [_vp, _int, _i64, _i64, _int, _vp, _vp, _vp, _vp]),
+    "smla_rope": (_int, [_vp, _int, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _i64, _int, _vp]),
+    "smla_linear": (_int, [_vp, _int, _vp, _int, _i64, _i64, _i64, _i64, _vp, _int, _vp]),
+    "smla_o_proj": (_int, [_vp, _int, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _int,
+                           _i64, _vp, _vp, _int, _vp]),
 }
 
 # sim modes of smla_gated_pool / smla_ring_step, flags of smla_rotate_fp4
@@ -54,6 +58,7 @@ _TUNING = {
     "smla_profile_set_attn_main_only": (None, [_int]),
     "smla_set_attn_decode_kernel": (None, [_int]),
     "smla_set_index_cert_force_exact": (None, [_int]),
+    "smla_set_linear_form": (None, [_int]),
     "smla_attn_plan": (None, [_i64, _i64, _i64, _i64, _i64, _i64, _int, _int, ctypes.POINTER(_int),
                               ctypes.POINTER(_int)]),
 }

@@ -1,9 +1,21 @@
-"""MLA projections with the signatures of ``v4mlx/mla.py`` (torch on the GPU).
+"""MLA projections with the signatures of ``v4mlx/mla.py``, on the GPU.
 
-These dense GEMMs surround the sparse-attention core; they run as torch.matmul (hipBLASLt) with
-the reference's shapes: H=64 heads, head_dim 512, rope 64, 8 output groups of rank 1024.
+These dense GEMMs surround the sparse-attention core, with the reference's shapes: H=64 heads,
+head_dim 512, rope 64, 8 output groups of rank 1024.  Decode shapes (at most 32 token rows, bf16)
+run the HIP projection kernel (``smla_linear`` / ``smla_o_proj``: MFMA, bound by streaming the
+weights once); larger batches (prefill) run torch.matmul (hipBLASLt).
 """
 import torch
+
+from . import ops
+
+_MAX_DECODE_ROWS = 32
+
+
+def _decode_shape(x, *ws, k_mult=512):
+    rows = x.numel() // x.shape[-1] if x.dim() else 0
+    return (x.is_cuda and 0 < rows <= _MAX_DECODE_ROWS and x.dtype == torch.bfloat16
+            and all(w.dtype == torch.bfloat16 for w in ws) and x.shape[-1] % k_mult == 0)
 
 N_HEADS, HEAD_DIM, ROPE_HD = 64, 512, 64
 N_GROUPS, O_LORA = 8, 1024
@@ -11,6 +23,9 @@ N_GROUPS, O_LORA = 8, 1024
 
 def linear(x, W):
     """``v4mlx/mla.py:16-18``: y = x @ W^T, W [out, in]."""
+    if _decode_shape(x, W) and W.shape[0] % 16 == 0:
+        lead = x.shape[:-1]
+        return ops.linear_op(x.reshape(-1, x.shape[-1]), W, 1, torch.bfloat16).reshape(*lead, W.shape[0])
     return x @ W.t()
 
 
@@ -39,8 +54,25 @@ def o_grouped(o, wo_a, wo_b):
     """``v4mlx/mla.py:42-56``: grouped low-rank output projection.
     o [..., N_HEADS*HEAD_DIM] -> [..., dim];  wo_a [N_GROUPS*O_LORA, N_HEADS*HEAD_DIM/N_GROUPS]."""
     lead = o.shape[:-1]
+    if _decode_shape(o, wo_a, wo_b, k_mult=512 * N_GROUPS):
+        o3 = o.reshape(-1, N_GROUPS, o.shape[-1] // N_GROUPS)          # heads of a group as one slice
+        y = ops.o_proj_op(o3, None, None, None, wo_a, wo_b, N_GROUPS, torch.bfloat16)
+        return y.reshape(*lead, wo_b.shape[0])
     og = o.reshape(-1, N_GROUPS, o.shape[-1] // N_GROUPS).transpose(0, 1).contiguous()   # [G, M, 4096]
     wa = wo_a.reshape(N_GROUPS, O_LORA, -1).transpose(1, 2).contiguous()                 # [G, 4096, 1024]
     ob = torch.bmm(og, wa)                                                              # [G, M, 1024]
     ob = ob.transpose(0, 1).reshape(*lead, N_GROUPS * O_LORA)
     return linear(ob, wo_b)
+
+
+def o_project(o, pos, cos_t, sin_t, wo_a, wo_b):
+    """``oracle/decode_engine.py:118-119`` (up to the hc_post call): o [T, N_HEADS, HEAD_DIM] has the
+    last ROPE_HD dims of every head rotated back to position 0 (inverse RoPE at pos [T], cos/sin
+    tables [n_pos, ROPE_HD/2]), then goes through ``o_grouped``.  One fused HIP path for decode
+    shapes; an in-place HIP rotation of a copy plus the GEMMs otherwise."""
+    T = o.shape[0]
+    if _decode_shape(o.reshape(T, -1), wo_a, wo_b, k_mult=512 * N_GROUPS):
+        return ops.o_proj_op(o, pos, cos_t, sin_t, wo_a, wo_b, N_GROUPS, torch.bfloat16)
+    r = o.contiguous().clone()
+    ops.rope_op_(r, pos, cos_t, sin_t, True)
+    return o_grouped(r.reshape(T, -1), wo_a, wo_b)

@@ -246,6 +246,78 @@ def _(x, rotate, fp4, want_out, want_codes):
 
 
 # ----------------------------------------------------------------------------------------------
+_YDT = {torch.float32: _lib.F32, torch.bfloat16: _lib.BF16}
+
+
+@torch.library.custom_op("smla::linear", mutates_args=(), device_types="cuda")
+def linear_op(x: torch.Tensor, w: torch.Tensor, groups: int, out_dtype: torch.dtype) -> torch.Tensor:
+    """x [T, G*K] bf16, w [G*N, K] bf16 -> y [T, G*N] (T <= 32): y[:, gN:(g+1)N] = x[:, gK:(g+1)K] @ w_g^T."""
+    _on_gpu(x, w)
+    x, w = x.contiguous(), w.contiguous()
+    T = x.shape[0]
+    K = w.shape[1]
+    N = w.shape[0] // groups
+    if x.shape[1] != groups * K or w.shape[0] != groups * N:
+        raise ValueError("linear: x [T, G*K] and w [G*N, K] do not agree")
+    y = torch.empty(T, groups * N, dtype=out_dtype, device=x.device)
+    _lib.call("smla_linear", _p(x), dtype_code(x), _p(w), dtype_code(w), T, groups, N, K, _p(y), _YDT[out_dtype],
+              _stream(x))
+    return y
+
+
+@linear_op.register_fake
+def _(x, w, groups, out_dtype):
+    return x.new_empty(x.shape[0], w.shape[0], dtype=out_dtype)
+
+
+@torch.library.custom_op("smla::rope_", mutates_args=("x",), device_types="cuda")
+def rope_op_(x: torch.Tensor, pos: torch.Tensor, cos_t: torch.Tensor, sin_t: torch.Tensor, inverse: bool) -> None:
+    """In place: the last rd = 2 * cos_t.shape[1] dims of every head of x [T, heads, head_dim]."""
+    _on_gpu(x, pos, cos_t, sin_t)
+    if not x.is_contiguous() or x.dim() != 3:
+        raise ValueError("rope_: x must be a contiguous [T, heads, head_dim] tensor")
+    pos = pos.to(torch.int32).contiguous()
+    cos_t, sin_t = cos_t.float().contiguous(), sin_t.float().contiguous()
+    T, H, D = x.shape
+    _lib.call("smla_rope", _p(x), dtype_code(x), T, H, D, 2 * cos_t.shape[1], _p(pos), _p(cos_t), _p(sin_t),
+              cos_t.shape[0], int(bool(inverse)), _stream(x))
+
+
+@rope_op_.register_fake
+def _(x, pos, cos_t, sin_t, inverse):
+    return None
+
+
+@torch.library.custom_op("smla::o_proj", mutates_args=(), device_types="cuda")
+def o_proj_op(o: torch.Tensor, pos: Optional[torch.Tensor], cos_t: Optional[torch.Tensor],
+              sin_t: Optional[torch.Tensor], wo_a: torch.Tensor, wo_b: torch.Tensor, groups: int,
+              out_dtype: torch.dtype) -> torch.Tensor:
+    """o [T, heads, head_dim] bf16 -> [T, dim]: inverse RoPE of the rope dims at pos (when given),
+    grouped projection by wo_a [G*R, heads*head_dim/G], then wo_b [dim, G*R] (T <= 32)."""
+    tensors = [o, wo_a, wo_b] + ([pos, cos_t, sin_t] if pos is not None else [])
+    _on_gpu(*tensors)
+    o, wo_a, wo_b = o.contiguous(), wo_a.contiguous(), wo_b.contiguous()
+    T, H, D = o.shape
+    R = wo_a.shape[0] // groups
+    dim = wo_b.shape[0]
+    mid = torch.empty(T, groups * R, dtype=torch.bfloat16, device=o.device)
+    y = torch.empty(T, dim, dtype=out_dtype, device=o.device)
+    rd = n_pos = 0
+    if pos is not None:
+        pos = pos.to(torch.int32).contiguous()
+        cos_t, sin_t = cos_t.float().contiguous(), sin_t.float().contiguous()
+        rd, n_pos = 2 * cos_t.shape[1], cos_t.shape[0]
+    _lib.call("smla_o_proj", _p(o), dtype_code(o), _p(pos), _p(cos_t), _p(sin_t), n_pos, T, H, D, rd, groups, R,
+              _p(wo_a), _p(wo_b), dtype_code(wo_a), dim, _p(mid), _p(y), _YDT[out_dtype], _stream(o))
+    return y
+
+
+@o_proj_op.register_fake
+def _(o, pos, cos_t, sin_t, wo_a, wo_b, groups, out_dtype):
+    return o.new_empty(o.shape[0], wo_b.shape[0], dtype=out_dtype)
+
+
+# ----------------------------------------------------------------------------------------------
 def window_topk_idxs(window_size, bsz, seqlen, start_pos, device="cuda"):
     """Device-built window index matrix (int32); see sparse_attn.get_window_topk_idxs."""
     if start_pos > 0:

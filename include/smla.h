@@ -24,6 +24,11 @@
  *   smla_quant_fp8_pow2       v4mlx/compressor.py:11-20        act_quant_sim (stored form: codes + pow2 scales)
  *   smla_rotate_fp4           v4mlx/qat.py:8-31                hadamard_rotate, fp4_act_quant (and stored form)
  *                             v4mlx/compressor.py:57-59        the indexer compressor's key transform
+ *   smla_rope                 ref_torch/norm_rope.py:53-62     apply_rotary_emb(x, freqs_cis, inverse) in place
+ *                             v4mlx/norm_rope.py:46-62         (MLX twin, cos/sin tables)
+ *   smla_linear               v4mlx/mla.py:16-18               linear(x, W) for T <= 32 tokens (decode)
+ *   smla_o_proj               oracle/decode_engine.py:118-119  inverse RoPE of o's rope dims + o_grouped
+ *                             v4mlx/mla.py:42-56               o_grouped(o, wo_a, wo_b)
  */
 #ifndef SMLA_H
 #define SMLA_H
@@ -230,6 +235,39 @@ int smla_quant_fp8_pow2(const void* x, int x_dtype, int64_t rows, int64_t D, uin
 enum { SMLA_QAT_ROTATE = 1, SMLA_QAT_FP4 = 2 };
 int smla_rotate_fp4(const void* x, int x_dtype, int64_t rows, int64_t n, int flags, float* out,
                     uint8_t* codes, uint8_t* scales, void* stream);
+
+/* ---------------------------------------------------------------------------------------------
+ * RoPE and the projections around the attention core.
+ *
+ * smla_rope: in place on x [T, heads, head_dim] (F32 or BF16, 8-byte aligned): the last rd dims
+ * of every head, as interleaved pairs (x0, x1), become (x0 c - x1 s, x0 s + x1 c) with
+ * c = cos_t[pos[t], j], s = sin_t[pos[t], j] (negated when `inverse`), every product and sum
+ * rounded in float32, then the result rounded to x's type.  cos_t, sin_t [n_pos, rd/2] fp32;
+ * pos [T] int32 in [0, n_pos).  Replaces ref_torch/norm_rope.py:53-62 and v4mlx/norm_rope.py:46-62. */
+int smla_rope(void* x, int x_dtype, int64_t T, int64_t heads, int64_t head_dim, int64_t rd,
+              const int32_t* pos, const float* cos_t, const float* sin_t, int64_t n_pos, int inverse,
+              void* stream);
+
+/* smla_linear: y[t, g*N + n] = sum_k x[t, g*K + k] * w[g*N + n, k] for G groups of N rows (G = 1
+ * is v4mlx/mla.py:16-18, y = x @ W^T; G > 1 is the grouped product of v4mlx/mla.py:49-53).
+ *   x [T, G*K] BF16, w [G*N, K] BF16, y [T, G*N] BF16 or F32; float32 accumulation.
+ *   T <= 32 (the decode step's tokens), N % 16 == 0, K % 512 == 0, 16-byte aligned pointers.
+ *   Bound by streaming w from HBM once. */
+int smla_linear(const void* x, int x_dtype, const void* w, int w_dtype, int64_t T, int64_t G,
+                int64_t N, int64_t K, void* y, int y_dtype, void* stream);
+
+/* smla_o_proj: the attention output path of oracle/decode_engine.py:118-119 for T tokens:
+ *   o [T, heads, head_dim] BF16; when pos != NULL the last rd dims of every head are rotated back
+ *   (inverse RoPE at pos[t], cos_t/sin_t [n_pos, rd/2] fp32) on the fly, rounded to bf16;
+ *   mid [T, G*R] BF16 (caller workspace) = grouped projection with wo_a [G*R, heads*head_dim/G];
+ *   y [T, dim] BF16 or F32 = mid @ wo_b^T with wo_b [dim, G*R].  w_dtype: BF16.
+ *   Same limits as smla_linear; with RoPE head_dim % 64 == 0, rd % 64 == 0 and each group's
+ *   slice a whole number of heads.  Replaces v4mlx/mla.py:42-56 (o_grouped) after the inverse
+ *   rotary call. */
+int smla_o_proj(const void* o, int o_dtype, const int32_t* pos, const float* cos_t,
+                const float* sin_t, int64_t n_pos, int64_t T, int64_t heads, int64_t head_dim,
+                int64_t rd, int64_t G, int64_t R, const void* wo_a, const void* wo_b, int w_dtype,
+                int64_t dim, void* mid, void* y, int y_dtype, void* stream);
 
 #ifdef __cplusplus
 }

@@ -34,6 +34,10 @@ def _inputs(n, rows, seed):
     return x
 
 
+def _bits(a):
+    return np.ascontiguousarray(a, dtype=np.float32).view(np.uint32)
+
+
 @pytest.mark.parametrize("n", NS)
 @pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16])
 def test_rotate_fp4_bit_exact(dev, n, dt):
@@ -44,9 +48,10 @@ def test_rotate_fp4_bit_exact(dev, n, dt):
     xf = x.float().numpy()
     xd = x.to(dev)
     rot = oqat.hadamard_rotate(xf)
-    np.testing.assert_array_equal(sq.hadamard_rotate(xd).cpu().numpy(), rot)
-    np.testing.assert_array_equal(sq.fp4_act_quant(xd).cpu().numpy(), oqat.fp4_act_quant(xf))
-    np.testing.assert_array_equal(sq.rotate_fp4(xd).cpu().numpy(), oqat.rotate_fp4(xf))
+    # bit patterns: signs of zero included
+    np.testing.assert_array_equal(_bits(sq.hadamard_rotate(xd).cpu().numpy()), _bits(rot))
+    np.testing.assert_array_equal(_bits(sq.fp4_act_quant(xd).cpu().numpy()), _bits(oqat.fp4_act_quant(xf)))
+    np.testing.assert_array_equal(_bits(sq.rotate_fp4(xd).cpu().numpy()), _bits(oqat.rotate_fp4(xf)))
     codes, scales = sq.fp4_pack(xd)
     rc, rs = oqat.fp4_quantize(rot)
     np.testing.assert_array_equal(codes.cpu().numpy(), rc)
@@ -65,7 +70,7 @@ def test_rotate_fp4_large_batch(dev):
     x = torch.randn(65536, 128, generator=g)
     out, codes, scales = ops.rotate_fp4_op(x.to(dev), True, True, True, True)
     ref = oqat.rotate_fp4(x.numpy())
-    np.testing.assert_array_equal(out.cpu().numpy(), ref)
+    np.testing.assert_array_equal(_bits(out.cpu().numpy()), _bits(ref))
     rc, rs = oqat.fp4_quantize(oqat.hadamard_rotate(x.numpy()))
     np.testing.assert_array_equal(codes.cpu().numpy(), rc)
     np.testing.assert_array_equal(scales.cpu().numpy(), rs)

@@ -1,10 +1,10 @@
 """The lane layout of the fp4 key kernel (csrc/qat.hip rotate_fp4_kernel), modelled on the CPU.
 
-A row of n values spans L = n / E lanes with E consecutive values per lane (E = 8, or 16 for
-n = 1024).  Butterfly stages shorter than E run inside a lane; stage h >= E pairs lane l with
-lane l ^ (h / E) at the same register, the lane with bit h / E clear keeping the sum.  The model
-runs that schedule with float32 arithmetic and must reproduce the oracle bit for bit; it also
-checks that a block of 32 is the aligned group of 32 / E lanes the kernel reduces over."""
+A row of n values spans L = n / 32 lanes with E = 32 consecutive values per lane (one fp4 block
+per lane).  Butterfly stages shorter than E run inside a lane; stage h >= E pairs lane l with
+lane l ^ (h / E) at the same register: the lane with bit h / E clear keeps v + o, the other
+o - v (the kernel's fma(+-1, v, o)).  The model runs that schedule with float32 arithmetic and
+must reproduce the oracle bit for bit, signs of zero included."""
 import numpy as np
 import pytest
 
@@ -13,7 +13,7 @@ from oracle import qat
 
 def _kernel_model(x):
     n = x.shape[-1]
-    E = 8 if n <= 512 else 16
+    E = 32
     L = n // E
     v = x.astype(np.float32).reshape(-1, L, E).copy()        # [row, lane, register]
     h = 1
@@ -38,6 +38,8 @@ def _kernel_model(x):
 def test_lane_schedule_reproduces_oracle(n):
     rng = np.random.default_rng(n)
     x = (rng.standard_normal((6, n)) * np.exp2(rng.integers(-10, 10, (6, n)))).astype(np.float32)
-    np.testing.assert_array_equal(_kernel_model(x), qat.hadamard_rotate(x))
-    E = 8 if n <= 512 else 16
-    assert 32 % E == 0 and (n // E) % (32 // E) == 0          # blocks never straddle a row
+    x[0] = 0.0
+    x[1] = 1.5                        # equal values: differences are +0
+    got, ref = _kernel_model(x), qat.hadamard_rotate(x)
+    np.testing.assert_array_equal(got, ref)
+    np.testing.assert_array_equal(np.signbit(got), np.signbit(ref))
