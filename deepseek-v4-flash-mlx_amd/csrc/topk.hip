@@ -101,6 +101,7 @@ __global__ __launch_bounds__(NT) void topk_kernel(const float* scores, int64_t N
   constexpr int kWaves = NT / 64;
   constexpr int kBPT = kBuckets / NT;  // histogram buckets owned by each thread in the scan
   static_assert(kBPT * NT == kBuckets, "buckets per thread");
+  static_assert(PER <= 64, "per-thread selection masks are 64 bits");
   __shared__ int hist[kWaves][256];
   __shared__ int bhist[kBuckets + 1];  // + a slot that absorbs the counts of entries past nvis
   __shared__ int tmp[kWaves + 1];
@@ -429,9 +430,14 @@ __global__ __launch_bounds__(NT) void topk_kernel(const float* scores, int64_t N
       done = true;
     }
     if (!done && spread_ok) {
-      // ---- bucket histogram (bucket 0 holds the largest scores)
+      // ---- bucket histogram (bucket 0 holds the largest scores).  Each entry's bucket is
+      // computed once, from the score itself (key_score(key) only folds -0 to +0, which the
+      // subtraction from lmax does not see); entries past nvis go to the absorbing slot.
+      int bk[PER];
 #pragma unroll
-      for (int j = 0; j < PER; j++) atomicAdd(&bhist[j < nloc ? bucket_of(key[j], lmax, bscale) : kBuckets], 1);
+      for (int j = 0; j < PER; j++) bk[j] = j < nloc ? bucket_of_score(fv[j], lmax, bscale) : kBuckets;
+#pragma unroll
+      for (int j = 0; j < PER; j++) atomicAdd(&bhist[bk[j]], 1);
       __syncthreads();
       find_boundary(tid);
       if (tid == 0) s_int[3] = 0;  // candidate counter
@@ -443,7 +449,7 @@ __global__ __launch_bounds__(NT) void topk_kernel(const float* scores, int64_t N
         // atomic per wave
         int mine = 0;
 #pragma unroll
-        for (int j = 0; j < PER; j++) mine += (j < nloc && bucket_of(key[j], lmax, bscale) == bb);
+        for (int j = 0; j < PER; j++) mine += bk[j] == bb;
         const int incl = wave_incl_scan(mine);
         int wbase = 0;
         if (lane == 63 && incl > 0) wbase = atomicAdd(&s_int[3], incl);
@@ -451,7 +457,7 @@ __global__ __launch_bounds__(NT) void topk_kernel(const float* scores, int64_t N
         int slot = wbase + incl - mine;
 #pragma unroll
         for (int j = 0; j < PER; j++) {
-          if (j < nloc && bucket_of(key[j], lmax, bscale) == bb) {
+          if (bk[j] == bb) {
             if (slot < kMaxCand) cand_pair[slot] = ((uint64_t)key[j] << 32) | (uint32_t)(base + j);
             slot++;
           }
@@ -547,17 +553,18 @@ __global__ __launch_bounds__(NT) void topk_kernel(const float* scores, int64_t N
     }
     return key[j] < Kt || (key[j] == Kt && n <= It);
   };
-  int nsel = 0;
+  // the selection as a bit mask, evaluated once for the count and the placement
+  uint64_t selm = 0;  // PER <= 64
   int slot = slot0;
 #pragma unroll
-  for (int j = 0; j < PER; j++) nsel += selected(j, slot);
+  for (int j = 0; j < PER; j++) selm |= (uint64_t)selected(j, slot) << j;
+  const int nsel = __builtin_popcountll(selm);
   int tot_sel;
   int pos = block_excl_scan<kWaves>(nsel, tmp, &tot_sel);
   const bool stage = take <= kStageIds;
-  slot = slot0;
 #pragma unroll
   for (int j = 0; j < PER; j++) {
-    if (selected(j, slot)) {
+    if ((selm >> j) & 1ull) {
       if (pos < take) {
         if (stage) out_s[pos] = (int32_t)(base + j) + id_offset;
         else orow[pos] = (int32_t)(base + j) + id_offset;
