@@ -156,44 +156,47 @@ __global__ __launch_bounds__(256) void indexer_kernel(const void* __restrict__ q
   if (n < N) scores[bs * N + n] = live ? (kscale ? acc * kscale[row] : acc) : -SMLA_INF;
 }
 
-// Hi = Di = 64: each lane scores two keys (n and n + 64 of a 128-key workgroup) over its wave's 16
-// heads, walking d in four blocks of 16 in order, so every q read from LDS serves both keys' fma
-// chains (the LDS reads of q bound the one-key form).  Same arithmetic order as indexer_kernel:
-// per (head, key) one fma chain over d = 0..63, then the chain over the heads.
-constexpr int kKeys2 = 128;
-template <int KDT, int QDT>
-__global__ __launch_bounds__(256) void indexer2_kernel(const void* __restrict__ q, const void* __restrict__ keys,
-                                                       const float* __restrict__ kscale,
-                                                       const float* __restrict__ weights,
-                                                       const int32_t* __restrict__ nvis, int64_t S, int64_t N,
-                                                       float* __restrict__ scores) {
+// Hi = Di = 64: each lane scores KPL keys (n, n + 64, ... of a 64*KPL-key workgroup) over its
+// wave's HPW heads (64 / HPW waves), walking d in four blocks of 16 in order, so every q read from
+// LDS serves KPL keys' fma chains.  Launched as KPL = 2, HPW = 16 (4 waves, 128 keys): measured
+// against 4 x 8, 2 x 8, 4 x 4 and q through scalar loads, it is the fastest; the 2048 fmas per lane
+// at two waves per SIMD are the bound.  Same arithmetic order as indexer_kernel: per (head, key)
+// one fma chain over d = 0..63, then the chain over the heads.
+template <int KDT, int QDT, int KPL, int HPW>
+__global__ __launch_bounds__(64 * (64 / HPW)) void indexer2_kernel(const void* __restrict__ q,
+                                                                  const void* __restrict__ keys,
+                                                                  const float* __restrict__ kscale,
+                                                                  const float* __restrict__ weights,
+                                                                  const int32_t* __restrict__ nvis, int64_t S,
+                                                                  int64_t N, float* __restrict__ scores) {
   constexpr int DI = 64;
+  constexpr int NWV = 64 / HPW;    // waves
+  constexpr int KEYS = 64 * KPL;   // keys per workgroup
+  constexpr int NT = 64 * NWV;
+  static_assert(KPL <= NWV, "the head chain takes one key per lane on the first KPL waves");
   __shared__ __align__(16) float sq[64 * DI];
   __shared__ float sw[64];
-  __shared__ float sr[kKeys2][65];  // r[key][head]
+  __shared__ float sr[KEYS][65];  // r[key][head]
   const int64_t bs = blockIdx.y;
   const int64_t b = bs / S;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int64_t nA = (int64_t)blockIdx.x * kKeys2 + lane, nB = nA + 64;
+  const int64_t n0 = (int64_t)blockIdx.x * KEYS + lane;
   const int64_t nv = nvis ? (int64_t)nvis[bs] : N;
-  const int64_t rowA = b * N + (nA < N ? nA : N - 1), rowB = b * N + (nB < N ? nB : N - 1);
 
-  // both key rows in registers, in their storage type (converted one 16-wide block at a time)
+  // the lane's key rows in registers, in their storage type (converted one 16-wide block at a time)
   constexpr int KW = KDT == SMLA_FP8_E4M3 ? 4 : (KDT == SMLA_BF16 ? 8 : 16);  // 16-byte words per row
-  u32x4_t ka[KW], kb[KW];
-  {
-    const u32x4_t* pa = (const u32x4_t*)((const uint8_t*)keys + rowA * DI * (KW / 4));
-    const u32x4_t* pb = (const u32x4_t*)((const uint8_t*)keys + rowB * DI * (KW / 4));
+  u32x4_t kr[KPL][KW];
 #pragma unroll
-    for (int v = 0; v < KW; v++) {
-      ka[v] = pa[v];
-      kb[v] = pb[v];
-    }
+  for (int i = 0; i < KPL; i++) {
+    const int64_t n = n0 + 64 * i;
+    const u32x4_t* pk = (const u32x4_t*)((const uint8_t*)keys + (b * N + (n < N ? n : N - 1)) * DI * (KW / 4));
+#pragma unroll
+    for (int v = 0; v < KW; v++) kr[i][v] = pk[v];
   }
   // 16 values of a key row starting at d0 = 16 db, as fp32
-  auto block16 = [&](const u32x4_t (&kr)[KW], int db, float (&o)[16]) {
+  auto block16 = [&](const u32x4_t (&row)[KW], int db, float (&o)[16]) {
     if constexpr (KDT == SMLA_FP8_E4M3) {
-      const u32x4_t w = kr[db];
+      const u32x4_t w = row[db];
 #pragma unroll
       for (int j = 0; j < 4; j++) {
         const f32x2_t lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)w[j], false);
@@ -208,7 +211,7 @@ __global__ __launch_bounds__(256) void indexer2_kernel(const void* __restrict__ 
       for (int v = 0; v < 2; v++)
 #pragma unroll
         for (int j = 0; j < 4; j++) {
-          const uint32_t w = kr[2 * db + v][j];
+          const uint32_t w = row[2 * db + v][j];
           o[8 * v + 2 * j] = __uint_as_float(w << 16);
           o[8 * v + 2 * j + 1] = __uint_as_float(w & 0xffff0000u);
         }
@@ -216,14 +219,14 @@ __global__ __launch_bounds__(256) void indexer2_kernel(const void* __restrict__ 
 #pragma unroll
       for (int v = 0; v < 4; v++)
 #pragma unroll
-        for (int j = 0; j < 4; j++) o[4 * v + j] = __uint_as_float(kr[4 * db + v][j]);
+        for (int j = 0; j < 4; j++) o[4 * v + j] = __uint_as_float(row[4 * db + v][j]);
     }
   };
   // q rows -> LDS as fp32, weights
   {
     if constexpr (QDT == SMLA_BF16) {
       const u32x4_t* qp = (const u32x4_t*)((const uint16_t*)q + bs * 64 * DI);
-      for (int i = tid; i < 64 * DI / 8; i += 256) {
+      for (int i = tid; i < 64 * DI / 8; i += NT) {
         const u32x4_t v = qp[i];
         f32x4_t lo, hi;
 #pragma unroll
@@ -238,47 +241,52 @@ __global__ __launch_bounds__(256) void indexer2_kernel(const void* __restrict__ 
       }
     } else {
       const f32x4_t* qp = (const f32x4_t*)((const float*)q + bs * 64 * DI);
-      for (int i = tid; i < 64 * DI / 4; i += 256) *(f32x4_t*)(sq + 4 * i) = qp[i];
+      for (int i = tid; i < 64 * DI / 4; i += NT) *(f32x4_t*)(sq + 4 * i) = qp[i];
     }
     if (tid < 64) sw[tid] = weights[bs * 64 + tid];
   }
   __syncthreads();
-  float dA[16], dB[16];
+  float dot[KPL][HPW];
 #pragma unroll
-  for (int hh = 0; hh < 16; hh++) {
-    dA[hh] = 0.f;
-    dB[hh] = 0.f;
-  }
-  const int h0 = wave * 16;
+  for (int i = 0; i < KPL; i++)
+#pragma unroll
+    for (int hh = 0; hh < HPW; hh++) dot[i][hh] = 0.f;
+  const int h0 = wave * HPW;
 #pragma unroll
   for (int db = 0; db < 4; db++) {
-    float xa[16], xb[16];
-    block16(ka, db, xa);
-    block16(kb, db, xb);
+    float x[KPL][16];
 #pragma unroll
-    for (int hh = 0; hh < 16; hh++) {
-      const f32x4_t* qh = (const f32x4_t*)(sq + (h0 + hh) * DI + 16 * db);
+    for (int i = 0; i < KPL; i++) block16(kr[i], db, x[i]);
+    // the next head's 16 q values are read before this head's fmas (one head of lookahead)
+    f32x4_t qn[4];
 #pragma unroll
-      for (int v = 0; v < 4; v++) {
-        const f32x4_t qq = qh[v];
+    for (int v = 0; v < 4; v++) qn[v] = ((const f32x4_t*)(sq + h0 * DI + 16 * db))[v];
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-          dA[hh] = __builtin_fmaf(qq[j], xa[4 * v + j], dA[hh]);
-          dB[hh] = __builtin_fmaf(qq[j], xb[4 * v + j], dB[hh]);
-        }
+    for (int hh = 0; hh < HPW; hh++) {
+      f32x4_t qc[4];
+#pragma unroll
+      for (int v = 0; v < 4; v++) qc[v] = qn[v];
+      if (hh + 1 < HPW) {
+#pragma unroll
+        for (int v = 0; v < 4; v++) qn[v] = ((const f32x4_t*)(sq + (h0 + hh + 1) * DI + 16 * db))[v];
       }
+#pragma unroll
+      for (int v = 0; v < 4; v++)
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+#pragma unroll
+          for (int i = 0; i < KPL; i++) dot[i][hh] = __builtin_fmaf(qc[v][j], x[i][4 * v + j], dot[i][hh]);
     }
   }
 #pragma unroll
-  for (int hh = 0; hh < 16; hh++) {
-    sr[lane][h0 + hh] = dA[hh] > 0.f ? dA[hh] : 0.f;
-    sr[64 + lane][h0 + hh] = dB[hh] > 0.f ? dB[hh] : 0.f;
-  }
+  for (int i = 0; i < KPL; i++)
+#pragma unroll
+    for (int hh = 0; hh < HPW; hh++) sr[64 * i + lane][h0 + hh] = dot[i][hh] > 0.f ? dot[i][hh] : 0.f;
   __syncthreads();
-  if (wave >= 2) return;
-  // chain over the heads: wave 0 for the first 64 keys, wave 1 for the next 64
+  if (wave >= KPL) return;
+  // chain over the heads: wave i for keys 64 i .. 64 i + 63
   const int kl = wave * 64 + lane;
-  const int64_t n = (int64_t)blockIdx.x * kKeys2 + kl;
+  const int64_t n = (int64_t)blockIdx.x * KEYS + kl;
   float acc = 0.f;
 #pragma unroll 8
   for (int h = 0; h < 64; h++) acc = __builtin_fmaf(sw[h], sr[kl][h], acc);
@@ -317,13 +325,13 @@ template <int DI, int KDT>
 int launch_k(const void* q, int q_dtype, const void* keys, const float* kscale, const float* w,
              const int32_t* nvis, int64_t B, int64_t S, int64_t Hi, int64_t N, float* scores, hipStream_t st) {
   if (Hi == 64 && DI == 64) {
-    const dim3 grid((unsigned)((N + kKeys2 - 1) / kKeys2), (unsigned)(B * S));
+    const dim3 grid((unsigned)((N + 127) / 128), (unsigned)(B * S));
     if (q_dtype == SMLA_BF16)
-      hipLaunchKernelGGL((indexer2_kernel<KDT, SMLA_BF16>), grid, dim3(256), 0, st, q, keys, kscale, w, nvis, S, N,
-                         scores);
+      hipLaunchKernelGGL((indexer2_kernel<KDT, SMLA_BF16, 2, 16>), grid, dim3(256), 0, st, q, keys, kscale, w, nvis, S,
+                         N, scores);
     else
-      hipLaunchKernelGGL((indexer2_kernel<KDT, SMLA_F32>), grid, dim3(256), 0, st, q, keys, kscale, w, nvis, S, N,
-                         scores);
+      hipLaunchKernelGGL((indexer2_kernel<KDT, SMLA_F32, 2, 16>), grid, dim3(256), 0, st, q, keys, kscale, w, nvis, S,
+                         N, scores);
   } else if (Hi <= 64) {
     dim3 grid((unsigned)((N + kKeys - 1) / kKeys), (unsigned)(B * S));
     const int threads = (int)(((Hi + kHG - 1) / kHG) * 64);
