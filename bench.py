@@ -138,10 +138,29 @@ def _time_ms(fn, reps):
     return e0.elapsed_time(e1) / reps
 
 
+def _time_graph_ms(fn, reps, inner=20):
+    """GPU time of one call of `fn`: `inner` calls captured in one HIP graph after two eager
+    warm-ups, the graph replayed `reps` times between HIP events; host dispatch and the graph
+    launch are amortised over inner * reps calls."""
+    import torch
+    for _ in range(2):
+        fn()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for _ in range(inner):
+            fn()
+    ms = _time_ms(graph.replay, max(3, reps // inner) if inner > 1 else reps) / inner
+    del graph
+    torch.cuda.synchronize()
+    return ms
+
+
 def other_workloads(dev, reps):
-    """The other decode workloads and the path's remaining kernels, each timed with HIP events
-    over `reps` eager passes on resident inputs (inputs smaller than the 256 MB MALL may be served
-    from it on repeats; the block-mean pool's 377 MB are not)."""
+    """The other decode workloads and the path's remaining kernels, each captured in a HIP graph
+    and timed with HIP events over `reps` replays on resident inputs (inputs smaller than the
+    256 MB MALL may be served from it on repeats; the block-mean pool's 377 MB, the fp4 keys'
+    512 MB and the rotating o_proj weights are not)."""
     import torch
     from smla import compressor as scomp
     from smla import indexer as sidx
@@ -168,7 +187,7 @@ def other_workloads(dev, reps):
             sc = sidx.indexer_score(qi[i][None, None], keys, ks, wt[i][None, None], nvis[i])
             idx = sidx.select_decode_indices(sc[:, 0], k, posd[i], win, n_raw)
             ssa.sparse_attn_two_source(q[i][None], raw, comp, None, idx[:, None, :], w["scale"], dv=512)
-    ms = _time_ms(run64, max(1, reps // 4))
+    ms = _time_graph_ms(run64, max(1, reps // 4), inner=1)
     per = ms / w["steps"]
     step_bytes = algorithmic_attention_bytes(1, 64, win + k)
     res["decode_64k"] = {"workload": "decode_64k: B=1 H=64, raw [65536,576] + mean-pooled [16384,576] bf16, fp8 keys "
@@ -179,7 +198,7 @@ def other_workloads(dev, reps):
     # ---- batched_fp8: 64 sequences, e4m3 rows with pow2 scales, 2048 ids each (attention + merge)
     w = wl.batched_fp8()
     qb, codes, scl, idxb = w["q"].to(dev), w["codes"].to(dev), w["scales"].to(dev), w["idx"].to(dev)
-    ms = _time_ms(lambda: ssa.sparse_attn_batched(qb, codes, None, idxb, w["scale"], dv=512, kv_scale=scl), reps)
+    ms = _time_graph_ms(lambda: ssa.sparse_attn_batched(qb, codes, None, idxb, w["scale"], dv=512, kv_scale=scl), reps)
     nsel = int((w["idx"] >= 0).sum())
     fb = nsel * 612 + 64 * 64 * 576 * 2 + 64 * 64 * 512 * 2 + nsel * 4
     res["batched_fp8"] = {"workload": "batched_fp8: B=64 H=64, e4m3 rows (612 B with 9 fp32 pow2 scales), lengths "
@@ -193,7 +212,7 @@ def other_workloads(dev, reps):
     raw = w["raw"].to(dev)
     qi, keys, ks, wt = w["q_idx"].to(dev), w["k_codes"].to(dev), w["kscale"].to(dev), w["w"].to(dev)
     B, N, Hi, Di = 8, keys.shape[1], qi.shape[2], qi.shape[3]
-    ms = _time_ms(lambda: sidx.indexer_score(qi, keys, ks, wt), reps)
+    ms = _time_graph_ms(lambda: sidx.indexer_score(qi, keys, ks, wt), reps)
     flops = 2.0 * B * N * Hi * Di
     res["indexer_score"] = {"shape": "B=8 Hi=64 Di=64 N=8192, bf16 q x e4m3 keys, fixed-order fp32 fma chains",
                             "us": round(ms * 1e3, 3), "bound": "valu fp32",
@@ -201,16 +220,16 @@ def other_workloads(dev, reps):
                             "hbm_bytes": B * N * (Di + 4) + B * N * 4}
     sc = sidx.indexer_score(qi, keys, ks, wt)
     pos = torch.full((B,), w["pos"], dtype=torch.int32, device=dev)
-    ms = _time_ms(lambda: sidx.select_decode_indices(sc[:, 0], w["k"], pos, w["window"], raw.shape[1]), reps)
+    ms = _time_graph_ms(lambda: sidx.select_decode_indices(sc[:, 0], w["k"], pos, w["window"], raw.shape[1]), reps)
     res["select_decode"] = {"shape": "8 rows x 8192 scores, k=2048, window 128 (one launch)",
                             "us": round(ms * 1e3, 3), "bound": "latency (one workgroup per row)"}
     ws = torch.empty(ops.index_decode_workspace(B, 1, N), dtype=torch.uint8, device=dev)
-    ms = _time_ms(lambda: sidx.index_decode(qi, keys, ks, wt, None, w["k"], pos, w["window"], raw.shape[1],
+    ms = _time_graph_ms(lambda: sidx.index_decode(qi, keys, ks, wt, None, w["k"], pos, w["window"], raw.shape[1],
                                             workspace=ws), reps)
     res["index_decode"] = {"shape": "B=8 Hi=64 Di=64 N=8192 -> window 128 + top-2048 ids: MFMA scores with a "
                                     "certified bound, band rescoring, exact selection (two launches)",
                            "us": round(ms * 1e3, 3)}
-    ms = _time_ms(lambda: scomp.block_mean_pool(raw, 4), max(2, reps // 2))
+    ms = _time_graph_ms(lambda: scomp.block_mean_pool(raw, 4), max(2, reps // 2))
     mb = raw.numel() * 2 + raw.numel() // 4 * 2
     res["block_mean_pool"] = {"shape": "[8,32768,576] bf16 -> [8,8192,576]", "us": round(ms * 1e3, 3),
                               "bytes": mb, "achieved_gbs": round(mb / (ms * 1e-3) / 1e9, 1), "peak_gbs": HBM_PEAK_GBS}
@@ -221,19 +240,19 @@ def other_workloads(dev, reps):
     ape = torch.randn(4, 1024, generator=g).to(dev)
     nw = torch.rand(512, generator=g).to(dev)
     cos_t, sin_t = snr.rope_tables(64, 65536, device=dev)
-    ms = _time_ms(lambda: ops.gated_pool_op(kvp, scp, ape, nw, cos_t, sin_t, 4, 64, 1e-6, 1), reps)
+    ms = _time_graph_ms(lambda: ops.gated_pool_op(kvp, scp, ape, nw, cos_t, sin_t, 4, 64, 1e-6, 1), reps)
     gb = 2 * kvp.numel() * 4 + 1024 * 512 * 4 + 1024 * 32 * 4 * 2
     res["gated_pool"] = {"shape": "kv, score [1,4096,1024] fp32 -> [1,1024,512] (overlap softmax + RMSNorm + RoPE + fp8 sim)",
                          "us": round(ms * 1e3, 3), "bytes": gb, "achieved_gbs": round(gb / (ms * 1e-3) / 1e9, 1)}
     x = torch.randn(8192, 576, generator=g).to(dev)
-    ms = _time_ms(lambda: ops.quant_fp8_pow2_op(x), reps)
+    ms = _time_graph_ms(lambda: ops.quant_fp8_pow2_op(x), reps)
     qbytes = x.numel() * 4 + x.numel() + x.numel() // 64 * 4
     res["quant_fp8_pow2"] = {"shape": "[8192,576] fp32 -> e4m3 codes + per-64 pow2 scales", "us": round(ms * 1e3, 3),
                              "bytes": qbytes, "achieved_gbs": round(qbytes / (ms * 1e-3) / 1e9, 1)}
     del x
     # indexer keys: 1M rows of 128 (512 MB of fp32, larger than the 256 MB MALL) -> stored fp4 form
     xk = torch.randn(1 << 20, 128, device=dev)
-    ms = _time_ms(lambda: ops.rotate_fp4_op(xk, True, True, False, True), max(2, reps // 2))
+    ms = _time_graph_ms(lambda: ops.rotate_fp4_op(xk, True, True, False, True), max(2, reps // 2))
     kb = xk.numel() * 4 + xk.numel() // 2 + xk.numel() // 32
     res["rotate_fp4"] = {"shape": "[1048576,128] fp32 -> Hadamard + fp4 e2m1 (packed codes + ue8m0 per 32)",
                          "us": round(ms * 1e3, 3), "bytes": kb, "achieved_gbs": round(kb / (ms * 1e-3) / 1e9, 1),
