@@ -23,6 +23,7 @@ def _sim(fp8_sim, rotate):
 
 
 def overlap_transform(tensor, ratio, d, value):
+    ops._on_gpu(tensor)
     b, s = tensor.shape[0], tensor.shape[1]
     new = tensor.new_full((b, s, 2 * ratio, d), value)
     new[:, :, ratio:] = tensor[:, :, :, d:]
@@ -34,6 +35,7 @@ def compressor_prefill(x, wkv, wgate, ape, norm_w, head_dim=512, ratio=4, rope_h
                        original_seq_len=65536, factor=16, beta_fast=32, beta_slow=1, fp8_sim=False,
                        rotate=False):
     """x:[b,s,dim] -> (kv:[b, s//ratio, head_dim] fp32 post-RoPE, state dict)."""
+    ops._on_gpu(x, wkv, wgate, ape, norm_w)
     b, s, _ = x.shape
     xf = x.float()
     kv = xf @ wkv.float().t()

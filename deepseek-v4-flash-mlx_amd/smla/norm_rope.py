@@ -2,17 +2,21 @@
 
 The rotation tables are host-side constants, computed once on the CPU in fp32 exactly as the
 reference does (``torch.polar`` of ``outer(positions, freqs)``, ``ref_torch/norm_rope.py:46-50``)
-and uploaded; the HIP kernels (compressor pooling, ring step) consume them as cos/sin arrays.
-``rmsnorm``/``apply_rotary_emb`` are plain torch on the GPU for callers around the hot path.
+and uploaded; the HIP kernels (compressor pooling, ring step, ``smla_rope``) consume them as cos/sin
+arrays.  ``apply_rotary_emb`` runs ``smla_rope``; ``rmsnorm`` is plain torch on the GPU for callers
+around the hot path.  Both refuse tensors that are not on the GPU.
 """
 import functools
 import math
 
 import torch
 
+from . import ops
+
 
 def rmsnorm(x, weight, eps=1e-6):
     """``ref_torch/norm_rope.py:10-16``."""
+    ops._on_gpu(x, weight)
     xf = x.float()
     return (weight * (xf * torch.rsqrt(xf.square().mean(-1, keepdim=True) + eps))).to(x.dtype)
 
@@ -60,11 +64,18 @@ def rope_tables(dim, seqlen, original_seq_len=65536, base=160000.0, factor=16, b
 
 
 def apply_rotary_emb(x, freqs_cis, inverse=False):
-    """``ref_torch/norm_rope.py:53-62``: rotate interleaved pairs by complex freqs."""
-    xc = torch.view_as_complex(x.float().unflatten(-1, (-1, 2)))
-    fc = freqs_cis.conj() if inverse else freqs_cis
-    if xc.ndim == 3:
-        fc = fc.view(1, xc.size(1), xc.size(-1))
-    else:
-        fc = fc.view(1, xc.size(1), 1, xc.size(-1))
-    return torch.view_as_real(xc * fc).flatten(-2).to(x.dtype)
+    """``ref_torch/norm_rope.py:53-62``: rotate the interleaved pairs of x [b, s, dim] or
+    [b, s, heads, dim] by freqs_cis [s, dim/2] (row i for sequence position i), conjugated when
+    ``inverse``; returns a new tensor of x's dtype.  Runs ``smla_rope`` (each product and sum
+    rounded in float32, then rounded to x's dtype) on a copy of x."""
+    ops._on_gpu(x, freqs_cis)
+    if x.dtype not in (torch.float32, torch.bfloat16):
+        raise TypeError("apply_rotary_emb takes fp32 or bf16")
+    b, s = x.shape[0], x.shape[1]
+    d = x.shape[-1]
+    heads = x.shape[2] if x.dim() == 4 else 1
+    y = x.contiguous().clone().reshape(b * s, heads, d)
+    cos_t, sin_t = freqs_cis.real.float().contiguous(), freqs_cis.imag.float().contiguous()
+    pos = torch.arange(s, dtype=torch.int32, device=x.device).repeat(b)
+    ops.rope_op_(y, pos, cos_t, sin_t, bool(inverse))
+    return y.reshape(x.shape)

@@ -85,12 +85,33 @@ def test_host_validation_rejects_bad_arguments():
 
 
 def test_python_ops_refuse_cpu_tensors():
+    from smla import compressor as sc
+    from smla import mla
+    from smla import norm_rope as snr
+    from smla import qat as sq
     from smla import sparse_attn as ssa
     q = torch.zeros(1, 16, 576)
     kv = torch.zeros(8, 576)
     idx = torch.zeros(1, 4, dtype=torch.int32)
     with pytest.raises(Exception):
         ssa.sparse_attn(q, kv, None, idx, 1.0)
+    # every mirror of the reference's functions refuses CPU tensors instead of running torch on them
+    x = torch.zeros(2, 4096, dtype=torch.bfloat16)
+    w = torch.zeros(1024, 4096, dtype=torch.bfloat16)
+    cases = [
+        lambda: mla.linear(x, w),
+        lambda: mla.perhead_norm(torch.zeros(2, 64, 512)),
+        lambda: mla.o_grouped(torch.zeros(2, 32768, dtype=torch.bfloat16), torch.zeros(8192, 4096), torch.zeros(4096, 8192)),
+        lambda: snr.rmsnorm(torch.zeros(2, 8), torch.ones(8)),
+        lambda: snr.apply_rotary_emb(torch.zeros(1, 4, 64), snr.precompute_freqs_cis(64, 4, 0, 1e4, 1, 32, 1)),
+        lambda: sc.overlap_transform(torch.zeros(1, 2, 4, 16), 4, 8, 0.0),
+        lambda: sc.compressor_prefill(torch.zeros(1, 8, 16), torch.zeros(256, 16), torch.zeros(256, 16),
+                                      torch.zeros(4, 256), torch.ones(128), head_dim=128),
+        lambda: sq.rotate_fp4(torch.zeros(4, 128)),
+    ]
+    for c in cases:
+        with pytest.raises(RuntimeError):
+            c()
 
 
 @pytest.fixture(scope="module")

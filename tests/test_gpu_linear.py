@@ -153,3 +153,19 @@ def test_o_proj_graph_replays(dev):
         assert torch.equal(out, eager), f"replay {r}"
         ops.o_proj_op(o, pos, cos_t, sin_t, wa, wb, G, torch.bfloat16)     # eager work between replays
         torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("shape,dt", [((2, 5, 64), torch.float32), ((2, 5, 8, 64), torch.bfloat16),
+                                      ((1, 7, 64, 64), torch.float32)])
+@pytest.mark.parametrize("inverse", [False, True])
+def test_apply_rotary_emb_mirror(dev, shape, dt, inverse):
+    """smla.norm_rope.apply_rotary_emb (ref_torch/norm_rope.py:53-62 signature, on smla_rope) equals
+    the oracle's rotation bit for bit."""
+    from smla import norm_rope as snr
+    announce(f"apply_rotary_emb {shape} {dt} inverse={inverse}")
+    g = torch.Generator().manual_seed(sum(shape))
+    x = torch.randn(*shape, generator=g).to(dt)
+    cis = onr.precompute_freqs_cis(shape[-1], shape[1], 65536, 160000.0, 16, 32, 1)
+    got = snr.apply_rotary_emb(x.to(dev), cis.to(dev), inverse=inverse).cpu()
+    ref = onr.apply_rotary_emb(x, cis, inverse=inverse)
+    assert got.dtype == x.dtype and torch.equal(got, ref)
