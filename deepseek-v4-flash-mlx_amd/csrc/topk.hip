@@ -105,7 +105,7 @@ __global__ __launch_bounds__(NT) void topk_kernel(const float* scores, int64_t N
   __shared__ int hist[kWaves][256];
   __shared__ int bhist[kBuckets + 1];  // + a slot that absorbs the counts of entries past nvis
   __shared__ int tmp[kWaves + 1];
-  __shared__ float redf[3 * kWaves];
+  __shared__ float redf[5 * kWaves];
   __shared__ uint64_t cand_pair[kMaxCand];  // (key << 32) | index: the selection order is the integer order
   __shared__ int cand_idx[kMaxCand];
   __shared__ int out_s[kStageIds];           // the selected ids in output order, stored coalesced at the end
@@ -120,10 +120,30 @@ __global__ __launch_bounds__(NT) void topk_kernel(const float* scores, int64_t N
   const int lane = tid & 63, wave = tid >> 6;
   const int64_t r = blockIdx.x;
   // N <= 65536 (PER * NT): every index of the row fits 32 bits
+  const int base = tid * PER;
+  // this thread's PER contiguous scores: 16-byte loads when the run lies inside the row and is
+  // 16-byte aligned (rows of N floats: N % 4 == 0), element loads otherwise.  Issued first: the
+  // window-id stores below may alias the scores, so loads placed after them would wait for them.
+  float fv[PER];
+  auto load_scores = [&](const float* row) {
+    if (PER % 4 == 0 && (N & 3) == 0 && base + PER <= N) {
+#pragma unroll
+      for (int j = 0; j < PER; j += 4) {
+        const f32x4_t v4 = *(const f32x4_t*)(row + base + j);
+        fv[j] = v4[0];
+        fv[j + 1] = v4[1];
+        fv[j + 2] = v4[2];
+        fv[j + 3] = v4[3];
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < PER; j++) fv[j] = base + j < N ? row[base + j] : 0.f;
+    }
+  };
+  load_scores(scores + r * N);
   int nv = nvis ? nvis[r] : (int)N;
   if (nv > (int)N) nv = (int)N;
   if (nv < 0) nv = 0;
-  const float* sr = scores + r * N;
   int32_t* orow = out + r * out_stride;
   if (wpos) {
     const int64_t p = wpos[r];
@@ -135,7 +155,6 @@ __global__ __launch_bounds__(NT) void topk_kernel(const float* scores, int64_t N
   }
   const int take = (int)(nv < k ? nv : k);
 
-  const int base = tid * PER;
   // this thread's entries j < nloc are visible (index base + j < nvis)
   const int nloc = nv - base < 0 ? 0 : (nv - base > PER ? PER : nv - base);
   if (nv <= k) {
@@ -225,25 +244,6 @@ __global__ __launch_bounds__(NT) void topk_kernel(const float* scores, int64_t N
     return rank;
   };
 
-  // this thread's PER contiguous scores: 16-byte loads when the run lies inside the row and is
-  // 16-byte aligned (rows of N floats: N % 4 == 0), element loads otherwise
-  float fv[PER];
-  auto load_scores = [&](const float* row) {
-    if (PER % 4 == 0 && (N & 3) == 0 && base + PER <= N) {
-#pragma unroll
-      for (int j = 0; j < PER; j += 4) {
-        const f32x4_t v4 = *(const f32x4_t*)(row + base + j);
-        fv[j] = v4[0];
-        fv[j + 1] = v4[1];
-        fv[j + 2] = v4[2];
-        fv[j + 3] = v4[3];
-      }
-    } else {
-#pragma unroll
-      for (int j = 0; j < PER; j++) fv[j] = base + j < N ? row[base + j] : 0.f;
-    }
-  };
-  load_scores(sr);
   float emax = 0.f;
   if constexpr (CERT) {
     for (int c = tid; c < cc.nchunk; c += NT) {
@@ -299,8 +299,37 @@ __global__ __launch_bounds__(NT) void topk_kernel(const float* scores, int64_t N
       if (CERT) emax = wave_max_dpp(redf[2 * kWaves + wl]);
       nan_seen = __builtin_amdgcn_ballot_w64(lane < kWaves && s_nan[wl] != 0) != 0;
     }
-    const float bscale = (float)kBuckets / (lmax - lmin);
-    const bool spread_ok = !nan_seen && bscale < SMLA_INF && bscale > 0.f && lmin > -SMLA_INF && lmax < SMLA_INF;
+    // The plain selection buckets the finite scores: -inf scores (the indexer's mark of masked
+    // keys) go to the absorbing slot and are never selected as long as k finite scores are visible
+    // (with fewer, the radix fallback ranks them).  The finite minimum and the -inf count are only
+    // reduced when the row minimum is -inf (a block-uniform condition).  The certified pass keeps
+    // the full range.
+    const bool plain = !(CERT && certified);
+    float lminf = lmin, ninf = 0.f;
+    if (plain && lmin == -SMLA_INF && !nan_seen && lmax > -SMLA_INF) {
+      float mf = SMLA_INF, ni = 0.f;
+#pragma unroll
+      for (int j = 0; j < PER; j++) {
+        const bool vis = j < nloc;
+        mf = fminf(mf, vis && fv[j] > -SMLA_INF ? fv[j] : SMLA_INF);
+        ni += (vis && fv[j] == -SMLA_INF) ? 1.f : 0.f;
+      }
+      mf = wave_min_dpp(mf);
+      ni = wave_sum_dpp(ni);
+      if (lane == 0) {
+        redf[3 * kWaves + wave] = mf;
+        redf[4 * kWaves + wave] = ni;
+      }
+      __syncthreads();
+      const int wl = lane < kWaves ? lane : 0;
+      lminf = wave_min_dpp(redf[3 * kWaves + wl]);
+      ninf = wave_sum_dpp(lane < kWaves ? redf[4 * kWaves + wl] : 0.f);  // exact: an integer <= 65536
+    }
+    const bool ninf_ok = !plain || (float)nv - ninf >= (float)k;
+    const float lo = plain ? lminf : lmin;
+    const float bscale = (float)kBuckets / (lmax - lo);
+    const bool spread_ok = !nan_seen && ninf_ok && bscale < SMLA_INF && bscale > 0.f && lo > -SMLA_INF &&
+                           lmax < SMLA_INF;
     if (CERT && certified) {
       // band half-width: twice the row bound, plus room for the rounding of a -+ E2
       const float E2 = 2.f * emax * (1.f + 0x1p-8f) + 0x1p-20f * fmaxf(fabsf(lmin), fabsf(lmax));
@@ -435,7 +464,7 @@ __global__ __launch_bounds__(NT) void topk_kernel(const float* scores, int64_t N
       // subtraction from lmax does not see); entries past nvis go to the absorbing slot.
       int bk[PER];
 #pragma unroll
-      for (int j = 0; j < PER; j++) bk[j] = j < nloc ? bucket_of_score(fv[j], lmax, bscale) : kBuckets;
+      for (int j = 0; j < PER; j++) bk[j] = (j < nloc && fv[j] > -SMLA_INF) ? bucket_of_score(fv[j], lmax, bscale) : kBuckets;
 #pragma unroll
       for (int j = 0; j < PER; j++) atomicAdd(&bhist[bk[j]], 1);
       __syncthreads();

@@ -135,6 +135,31 @@ def test_topk_fallback_spreads(dev, case):
     np.testing.assert_array_equal(got, oidx.topk(s, k, nvis))
 
 
+@pytest.mark.parametrize("case", ["tail", "scattered", "few_finite", "all_neg_inf"])
+def test_topk_negative_infinity_scores(dev, case):
+    """-inf is the indexer's mark of masked keys: rows that hold -inf scores as visible entries keep
+    the bucket pass when k finite scores remain (the -inf entries are never selected), and take the
+    exact fallback when fewer remain (the -inf entries are then taken lowest index first)."""
+    from smla import indexer as sidx
+    announce(f"topk -inf {case}")
+    rng = np.random.default_rng(11)
+    R, N, k = 3, 16384, 2048
+    s = (rng.standard_normal((R, N)) * 40).astype(np.float32)
+    if case == "tail":
+        s[:, N - 5:] = -np.inf
+    elif case == "scattered":
+        s[:, ::7] = -np.inf
+    elif case == "few_finite":
+        s[:, 1500:] = -np.inf              # 1500 finite scores: every one selected, then -inf by index
+    else:
+        s[:] = -np.inf
+    got = sidx.topk(torch.from_numpy(s).to(dev), k).cpu().numpy()
+    np.testing.assert_array_equal(got, oidx.topk(s, k))
+    nvis = np.array([N, N - 3, 9000], np.int32)
+    got = sidx.topk(torch.from_numpy(s).to(dev), k, torch.from_numpy(nvis).to(dev)).cpu().numpy()
+    np.testing.assert_array_equal(got, oidx.topk(s, k, nvis))
+
+
 @pytest.mark.parametrize("R,N,k,window", [(8, 8192, 2048, 128), (3, 100, 512, 128), (2, 4096, 64, 7)])
 def test_select_decode_fused(dev, R, N, k, window):
     """One launch writes the decode window ids then the top-k ids (offset into the raw cache)."""
