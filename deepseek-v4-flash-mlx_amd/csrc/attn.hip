@@ -445,16 +445,18 @@ __global__ __launch_bounds__(kThreads, 1) void attn_mfma_kernel(
 // (m, l) and the weights pass through LDS, so any split count up to kMaxSplits takes the same path.
 constexpr int kMaxSplits = 1024;
 
-template <int WAVES, bool BF16P, int CH>
+template <int WAVES, bool BF16P, int CH, int DVS = 1>
 __global__ __launch_bounds__(WAVES * 64) void attn_merge_kernel(const float* __restrict__ part, int nsplit,
                                                                 int64_t BS, int H, const float* __restrict__ sink,
                                                                 void* __restrict__ out, int out_dtype) {
   constexpr int NT = WAVES * 64;
   constexpr int DV = 512;
-  constexpr int CPL = DV / NT;                        // value columns per thread: 4, 2 or 1
+  constexpr int CPL = DV / (DVS * NT);                // value columns per thread: 4, 2 or 1
+  // DVS > 1: the row's columns are split over DVS workgroups (blockIdx.y), for row counts too small
+  // to spread over the CUs otherwise
   constexpr int LW = BF16P ? (CPL + 1) / 2 : CPL;     // 32-bit words loaded per split
   constexpr int CHUNK = CH < 64 / LW ? CH : 64 / LW;  // splits in flight: at most 64 words per thread
-  static_assert(CPL >= 1 && CPL <= 4 && NT * CPL == DV, "merge thread layout");
+  static_assert(CPL >= 1 && CPL <= 4 && DVS * NT * CPL == DV, "merge thread layout");
   static_assert(kMaxSplits % CHUNK == 0, "padded weights fit the table");
   __shared__ __align__(16) float m_s[kMaxSplits];
   __shared__ float l_s[kMaxSplits];
@@ -465,7 +467,7 @@ __global__ __launch_bounds__(WAVES * 64) void attn_merge_kernel(const float* __r
   const int head = (int)(rh % H);
   const int64_t rec0 = bs * nsplit * (int64_t)H + head;  // record of split 0; splits are H records apart
   const float* ml = part + rec0 * 2;
-  const int dv0 = tid * CPL;
+  const int dv0 = (int)blockIdx.y * (DV / DVS) + tid * CPL;
   const int64_t jstride = (int64_t)H * DV;  // elements between consecutive splits
   const float* obase = part + BS * H * nsplit * 2;
 
@@ -632,13 +634,14 @@ int launch_merge(const Plan& p, int64_t B, int64_t S, int64_t H, const float* si
                  void* ws, hipStream_t stream, int part_bf16) {
   if (p.nsplit <= 1) return SMLA_OK;
   const int64_t rows = B * S * H;
-  // waves per (row, head): enough workgroups in flight to cover the partials' latency
-  const int waves = rows >= 1024 ? 2 : rows >= 256 ? 4 : 8;
-  const dim3 grid((unsigned)rows), block(waves * 64);
+  // waves per (row, head): enough workgroups in flight to cover the partials' latency; below 256
+  // rows, one wave per quarter of the row's columns (4-byte loads, 4 workgroups per row)
+  const int waves = rows >= 1024 ? 2 : rows >= 256 ? 4 : 1;
+  const dim3 grid((unsigned)rows, waves == 1 ? 4u : 1u), block(waves * 64);
   // splits in flight per chunk: the smallest of 16 / 32 / 64 that covers nsplit
   const int ch = p.nsplit <= 16 ? 16 : p.nsplit <= 32 ? 32 : 64;
-#define SMLA_MERGE(W, BP, C) hipLaunchKernelGGL((attn_merge_kernel<W, BP, C>), grid, block, 0, stream, \
-                                                (const float*)ws, p.nsplit, B * S, (int)H, sink, out, out_dtype)
+#define SMLA_MERGE(W, BP, C) hipLaunchKernelGGL((attn_merge_kernel<W, BP, C, (W == 1 ? 4 : 1)>), grid, block, 0, \
+                                                stream, (const float*)ws, p.nsplit, B * S, (int)H, sink, out, out_dtype)
 #define SMLA_MERGE_CH(W, BP) \
   if (ch == 16) SMLA_MERGE(W, BP, 16); else if (ch == 32) SMLA_MERGE(W, BP, 32); else SMLA_MERGE(W, BP, 64)
   if (part_bf16) {
@@ -647,7 +650,7 @@ int launch_merge(const Plan& p, int64_t B, int64_t S, int64_t H, const float* si
     } else if (waves == 4) {
       SMLA_MERGE_CH(4, true);
     } else {
-      SMLA_MERGE_CH(8, true);
+      SMLA_MERGE_CH(1, true);
     }
   } else {
     if (waves == 2) {
@@ -655,7 +658,7 @@ int launch_merge(const Plan& p, int64_t B, int64_t S, int64_t H, const float* si
     } else if (waves == 4) {
       SMLA_MERGE_CH(4, false);
     } else {
-      SMLA_MERGE_CH(8, false);
+      SMLA_MERGE_CH(1, false);
     }
   }
 #undef SMLA_MERGE_CH
