@@ -18,7 +18,7 @@ HEADER = os.path.join(ROOT, "include", "smla.h")
 
 def _declared():
     text = open(HEADER).read()
-    return sorted(set(re.findall(r"^\s*(?:int|size_t|const char\*)\s+(smla_\w+)\s*\(", text, re.M)))
+    return sorted(set(re.findall(r"^\s*(?:int|int64_t|size_t|const char\*)\s+(smla_\w+)\s*\(", text, re.M)))
 
 
 def test_library_exports_every_declared_symbol():
