@@ -14,7 +14,7 @@
 //
 // Rows stream HBM -> LDS with global_load_lds_dwordx4 into a ring of 4 tiles (one instruction per
 // row for columns 0..511, one per 8 rows for the 128-byte rope tails, XOR-swizzled by row; the 36
-// instructions of a tile are dealt to the 12 waves).  A tile is requested two iterations before
+// instructions of a tile are dealt to the 8 value waves).  A tile is requested two iterations before
 // it is scored.  The workgroup's 64 Q rows arrive the same way, laid out as two tiles of head rows
 // in the two ring slots that are free until iteration 0, so their latency overlaps the first
 // tiles' and the score waves read Q^T with the K-read pattern (free of bank conflicts).  Masked ids and rows past
@@ -61,10 +61,13 @@ struct Geo6 {
 
 __device__ inline uint32_t pack2(float a, float b) { return pack_bf16x2(a, b); }
 
-// number of a tile's DMA instructions dealt to wave w (instructions w, w+12, w+24, ...)
+// The copies are dealt to the value waves only (wave 4 + v issues instructions v, v+8, v+16, ...):
+// a wave whose copy waits at issue for the memory pipeline stalls with it, and the score waves
+// carry the tile loop's critical path while the value waves have slack.
+constexpr int kDmaWaves = 8;
 template <class G>
 __device__ inline int dma_count(int w) {
-  return (G::NDMA - w + G::NW - 1) / G::NW;
+  return w < 4 ? 0 : (G::NDMA - (w - 4) + kDmaWaves - 1) / kDmaWaves;
 }
 
 template <int D, int NBUF, int MAXROWS, bool FP8>
@@ -102,12 +105,14 @@ __global__ __launch_bounds__(768) void attn_decode_kernel(
     return rid < 0 ? row0 : (rid < n0 ? p0 : p1);
   };
   // this wave's share of the copies of one 32-row tile into ring slot `slot` (G::NDMA instructions
-  // per tile, dealt round-robin: one per row for columns 0..511, one per 8 rows for the rope tails)
+  // per tile, dealt round-robin over the value waves: one per row for columns 0..511, one per 8 rows
+  // for the rope tails)
   auto issue_rows = [&](int slot, auto&& rowp) {
     const uint32_t tbase = lds_base + (uint32_t)(slot * G::TILE_BYTES);
+    if (wave < 4) return;
 #pragma unroll
-    for (int k = 0; k < 3; k++) {
-      const int x = wave + G::NW * k;
+    for (int k = 0; k < (G::NDMA + kDmaWaves - 1) / kDmaWaves; k++) {
+      const int x = wave - 4 + kDmaWaves * k;
       if (x < kTileRows) {
         dma16(rowp(x) + 16 * lane, __builtin_amdgcn_readfirstlane(tbase + x * G::MSTRIDE));
       } else if (x < G::NDMA) {
