@@ -71,6 +71,12 @@ __device__ inline void dma16(const void* gsrc, uint32_t lds_dst_uniform) {
   asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds_dst_uniform), "v"(gsrc)
                : "memory", "m0");
 }
+// the same copy with the non-temporal hint: data read once (a query's own Q rows) should not push
+// reused rows out of the L2
+__device__ inline void dma16_nt(const void* gsrc, uint32_t lds_dst_uniform) {
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off nt" ::"s"(lds_dst_uniform), "v"(gsrc)
+               : "memory", "m0");
+}
 
 // 16-byte vector load that the compiler does not track (covered by a later wait_vm)
 __device__ inline u32x4_t load16_untracked(const void* p) {

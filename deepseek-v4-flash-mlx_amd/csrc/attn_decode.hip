@@ -70,6 +70,20 @@ __device__ inline int dma_count(int w) {
   return w < 4 ? 0 : (G::NDMA - (w - 4) + kDmaWaves - 1) / kDmaWaves;
 }
 
+// Workgroups are dealt to the 8 XCDs round-robin (workgroup L runs on XCD L mod 8), and each XCD
+// has its own L2.  With one workgroup per query row (prefill), neighbouring rows share most of their
+// window rows, so XCD x takes chunks of 128 consecutive rows: chunk position x in even rounds and
+// 7 - x in odd rounds, because a row's work grows with its position and the snake keeps the XCDs
+// even.  Other row counts keep the plain order.
+__device__ inline int64_t query_row_of(int64_t L, int64_t n) {
+  constexpr int64_t kX = 8, kC = 128;
+  if (n % (kX * kC) != 0) return L;
+  const int64_t x = L % kX, i = L / kX;
+  const int64_t r = i / kC, j = i % kC;
+  const int64_t pos = (r & 1) ? kX - 1 - x : x;
+  return r * kX * kC + pos * kC + j;
+}
+
 template <int D, int NBUF, int MAXROWS, bool FP8>
 __global__ __launch_bounds__(768) void attn_decode_kernel(
     const uint16_t* __restrict__ q, RowSrc src, const float* __restrict__ sink, const int32_t* __restrict__ idx,
@@ -84,7 +98,7 @@ __global__ __launch_bounds__(768) void attn_decode_kernel(
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int split = blockIdx.x, nsplit = gridDim.x;
-  const int64_t bs = blockIdx.y;
+  const int64_t bs = (nsplit == 1 && gridDim.z == 1) ? query_row_of(blockIdx.y, gridDim.y) : (int64_t)blockIdx.y;
   const int64_t b = bs / S;
   const int hb = blockIdx.z * 64;                 // first head of this workgroup
   const int nh = min(64, H - hb);                 // valid heads here
@@ -107,19 +121,27 @@ __global__ __launch_bounds__(768) void attn_decode_kernel(
   // this wave's share of the copies of one 32-row tile into ring slot `slot` (G::NDMA instructions
   // per tile, dealt round-robin over the value waves: one per row for columns 0..511, one per 8 rows
   // for the rope tails)
-  auto issue_rows = [&](int slot, auto&& rowp) {
+  auto issue_rows = [&](int slot, auto&& rowp, bool nt) {
     const uint32_t tbase = lds_base + (uint32_t)(slot * G::TILE_BYTES);
     if (wave < 4) return;
 #pragma unroll
     for (int k = 0; k < (G::NDMA + kDmaWaves - 1) / kDmaWaves; k++) {
       const int x = wave - 4 + kDmaWaves * k;
       if (x < kTileRows) {
-        dma16(rowp(x) + 16 * lane, __builtin_amdgcn_readfirstlane(tbase + x * G::MSTRIDE));
+        const uint32_t ld = __builtin_amdgcn_readfirstlane(tbase + x * G::MSTRIDE);
+        if (nt)
+          dma16_nt(rowp(x) + 16 * lane, ld);
+        else
+          dma16(rowp(x) + 16 * lane, ld);
       } else if (x < G::NDMA) {
         const int r0 = (x - kTileRows) * 8;
         const int r = r0 + (lane >> 3);
         const int ch = (lane & 7) ^ (r & 7);  // rope tails XOR-swizzled by row
-        dma16(rowp(r) + 1024 + 16 * ch, __builtin_amdgcn_readfirstlane(tbase + G::MAIN_BYTES + r0 * 128));
+        const uint32_t ld = __builtin_amdgcn_readfirstlane(tbase + G::MAIN_BYTES + r0 * 128);
+        if (nt)
+          dma16_nt(rowp(r) + 1024 + 16 * ch, ld);
+        else
+          dma16(rowp(r) + 1024 + 16 * ch, ld);
       }
     }
   };
@@ -130,10 +152,13 @@ __global__ __launch_bounds__(768) void attn_decode_kernel(
   {
     const uint8_t* qrow0 = (const uint8_t*)(q + (bs * H + hb) * (int64_t)D);
     for (int qt = 0; qt < 2; qt++)
-      issue_rows(QS + qt, [&](int r) {
-        const int hl = 32 * qt + r;
-        return qrow0 + (hl < nh ? hl : 0) * (int64_t)G::ROWB;
-      });
+      issue_rows(
+          QS + qt,
+          [&](int r) {
+            const int hl = 32 * qt + r;
+            return qrow0 + (hl < nh ? hl : 0) * (int64_t)G::ROWB;
+          },
+          nsplit == 1);  // one workgroup per query row: its Q rows are read once
   }
 
   // ---- row ids -> LDS (-1: masked, out of range or past the split), whole tiles; the tiles
@@ -160,7 +185,7 @@ __global__ __launch_bounds__(768) void attn_decode_kernel(
   auto issue_tile = [&](int tl) {
     if constexpr (!FP8) {
       const lds_i32_t* tid_s = ids_s + tl * kTileRows;
-      issue_rows(tl % G::NBUF, [&](int r) { return row_ptr(tid_s[r]); });
+      issue_rows(tl % G::NBUF, [&](int r) { return row_ptr(tid_s[r]); }, false);
     }
   };
   const int my_dma = FP8 ? 0 : dma_count<G>(wave);  // a data tile's DMA instructions of this wave
@@ -261,9 +286,17 @@ __global__ __launch_bounds__(768) void attn_decode_kernel(
         : (uint8_t*)(part + (int64_t)gridDim.y * H * nsplit * 2) + ((bs * nsplit + split) * (int64_t)H + hb) * row_bytes;
     const int chunks_per_row = row_bytes / 16;
     const int nchunks = nh * chunks_per_row;
-    for (int i = tid; i < nchunks; i += G::NW * 64) {
-      const int hr = i / chunks_per_row, ch = i - hr * chunks_per_row;
-      *(u32x4_t*)(dst + (int64_t)i * 16) = *(const lds_u32x4_t*)(lds + hr * srow_bytes + ch * 16);
+    if (nsplit == 1) {  // final rows are not read back by this launch
+      for (int i = tid; i < nchunks; i += G::NW * 64) {
+        const int hr = i / chunks_per_row, ch = i - hr * chunks_per_row;
+        __builtin_nontemporal_store(*(const lds_u32x4_t*)(lds + hr * srow_bytes + ch * 16),
+                                    (u32x4_t*)(dst + (int64_t)i * 16));
+      }
+    } else {
+      for (int i = tid; i < nchunks; i += G::NW * 64) {
+        const int hr = i / chunks_per_row, ch = i - hr * chunks_per_row;
+        *(u32x4_t*)(dst + (int64_t)i * 16) = *(const lds_u32x4_t*)(lds + hr * srow_bytes + ch * 16);
+      }
     }
   };
 
