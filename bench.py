@@ -285,6 +285,18 @@ def other_workloads(dev, reps):
     return res
 
 
+def _cpu_model():
+    """The host CPU's model name (first `model name` line of /proc/cpuinfo), or None."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return None
+
+
 def cpu_baseline(w, nthreads, reps):
     """Time the oracle on one full decode step (all 8 sequences): C indexer chain + C top-k +
     torch sparse attention, median of `reps` after one warm-up."""
@@ -496,6 +508,7 @@ def main():
         print(f"[bench] cpu baseline on {ncores} threads", file=sys.stderr, flush=True)
         med = cpu_baseline(w, ncores, args.cpu_steps)
         cpu = {"value": round(B / med, 2), "unit": "tok/s", "cores": ncores, "kind": "port",
+               "cpu_model": _cpu_model(),
                "sample": f"one full decode step (8 sequences: indexer chain + top-k + attention), "
                          f"median of {args.cpu_steps} after 1 warm-up; {med * 1e3:.1f} ms/step"}
 

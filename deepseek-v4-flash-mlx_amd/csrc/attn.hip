@@ -693,12 +693,8 @@ int launch_mfma(const Plan& p, const void* q, RowSrc src, const float* sink, con
   }
   using C = MfmaCfg<D, 512>;
   auto kern = attn_mfma_kernel<D, 512, FP8>;
-  static bool attr_set = false;
-  if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)C::LDS_BYTES);
-    if (e != hipSuccess) return (int)e;
-    attr_set = true;
-  }
+  static std::atomic<uint64_t> lds_attr{0};  // devices whose limit is raised
+  if (hipError_t e = smla_set_dynamic_lds((const void*)kern, (int)C::LDS_BYTES, lds_attr); e != hipSuccess) return (int)e;
   dim3 grid(p.nsplit, (unsigned)(B * S), p.hgroups);
   if (g_ev_before) (void)hipEventRecord(g_ev_before, stream);
   hipLaunchKernelGGL(kern, grid, dim3(kThreads), C::LDS_BYTES, stream, (const uint16_t*)q, src, sink,

@@ -496,12 +496,8 @@ int launch6(int nsplit, int rows_per_split, const void* q, RowSrc src, const flo
             hipStream_t stream) {
   using G = Geo6<D, NBUF, MAXROWS>;
   auto kern = attn_decode_kernel<D, NBUF, MAXROWS, FP8>;
-  static bool attr_set = false;
-  if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, G::LDS_BYTES);
-    if (e != hipSuccess) return (int)e;
-    attr_set = true;
-  }
+  static std::atomic<uint64_t> lds_attr{0};  // devices whose limit is raised
+  if (hipError_t e = smla_set_dynamic_lds((const void*)kern, G::LDS_BYTES, lds_attr); e != hipSuccess) return (int)e;
   dim3 grid((unsigned)nsplit, (unsigned)(B * S), (unsigned)((H + 63) / 64));
   hipLaunchKernelGGL(kern, grid, dim3(G::NW * 64), G::LDS_BYTES, stream, (const uint16_t*)q, src, sink, idx, (int)T,
                      (int)S, (int)H, rows_per_split, scale, part, out, out_dtype);

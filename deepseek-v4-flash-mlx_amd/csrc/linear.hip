@@ -250,12 +250,8 @@ int launch_linear_lds(const uint16_t* x, const uint16_t* w, int64_t T, int64_t G
                       const int32_t* pos, const float* cos_t, const float* sin_t, int head_dim, int rd, void* y,
                       hipStream_t st) {
   auto kern = linear_lds_kernel<TX, ROPE, YDT>;
-  static bool attr_set = false;
-  if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, kLdsMaxBytes);
-    if (e != hipSuccess) return (int)e;
-    attr_set = true;
-  }
+  static std::atomic<uint64_t> lds_attr{0};  // devices whose limit is raised
+  if (hipError_t e = smla_set_dynamic_lds((const void*)kern, kLdsMaxBytes, lds_attr); e != hipSuccess) return (int)e;
   const int nw = (int)(K / (kLdsSteps * 64));
   const int64_t xbytes = T * (K + 8) * 2, rbytes = (int64_t)nw * 64 * 16;
   const size_t lds = (size_t)(xbytes > rbytes ? xbytes : rbytes);

@@ -4,6 +4,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <atomic>
+
 #include "../../include/smla.h"
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
@@ -234,3 +236,17 @@ int launch_indexer_cert(const uint16_t* q, const uint8_t* keys, const float* ksc
     hipError_t _e = hipGetLastError();                  \
     if (_e != hipSuccess) return (int)_e;               \
   } while (0)
+
+// Raises a kernel's dynamic LDS limit on the current device, once per device: `done` holds one bit
+// per device id (ids from 64 up set the attribute on every call).  Safe to call from several host
+// threads; a lost race only repeats the call.
+inline hipError_t smla_set_dynamic_lds(const void* kern, int bytes, std::atomic<uint64_t>& done) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  const uint64_t bit = dev >= 0 && dev < 64 ? (uint64_t{1} << dev) : 0;
+  if (bit != 0 && (done.load(std::memory_order_acquire) & bit) != 0) return hipSuccess;
+  e = hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+  if (e == hipSuccess && bit != 0) done.fetch_or(bit, std::memory_order_acq_rel);
+  return e;
+}
