@@ -37,6 +37,7 @@ def _inputs(n_raw, S, H, seed, sharp=1.0):
     (4096, 4096 - 48, 48, 64, False),   # full lists: 128 window + 1024 compressed rows
     (4096, 0, 40, 64, True),            # first positions: short lists, mostly -1 padding
     (1024, 500, 33, 32, False),         # partial head group, mid-sequence
+    (1024, 0, 1024, 64, True),          # 1024 query rows: the XCD-chunked row order, every row checked
 ])
 def test_prefill_vs_oracle(dev, n_raw, q_pos0, S, H, use_sink, one_split):
     """one_split forces the single-split plan (3-tile ring, long index table) that the full
