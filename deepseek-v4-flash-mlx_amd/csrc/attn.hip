@@ -617,6 +617,10 @@ Plan make_plan(int64_t B, int64_t S, int64_t H, int64_t D, int64_t DV, int64_t T
   // tiles per split so that rows * nsplit ~ target workgroups
   int64_t per = (tiles * rows + target - 1) / target;
   if (per < 1) per = 1;
+  // a split's fixed costs (its Q block, index table and partial record) outweigh one 32-row tile,
+  // and every split adds a partial to merge: at least two tiles per split once the list has four
+  // (the default plan; an explicit target is taken as given)
+  if (g_target_wgs <= 0 && per < 2 && tiles >= 4) per = 2;
   if ((tiles + per - 1) / per > kMaxSplits) per = (tiles + kMaxSplits - 1) / kMaxSplits;
   if (per > tiles) per = tiles;
   // role-split kernel: splits of up to 8192 rows (the launcher picks the 4-tile ring for splits of
