@@ -282,6 +282,31 @@ def other_workloads(dev, reps):
                      "us": round(ms * 1e3, 3), "bytes": ob, "achieved_gbs": round(ob / (ms * 1e-3) / 1e9, 1),
                      "peak_gbs": HBM_PEAK_GBS}
     del graph, wts
+
+    # ---- decode_layer: the whole attention layer for one token (projections, RoPE, fp8 sim, window
+    # append, compressor ring, take-all ids, attention, output projection), 8 sequences at position
+    # 32767 over filled 32K caches; a graph of 5 steps (each rewrites the same cache rows)
+    from smla import engine
+    g = torch.Generator(device="cpu").manual_seed(5)
+    bf = lambda *s: (torch.randn(*s, generator=g) * 0.02).to(torch.bfloat16).to(dev)
+    f32 = lambda *s: (1.0 + 0.1 * torch.randn(*s, generator=g)).to(dev)
+    lw = engine.LayerWeights(wq_a=bf(1024, 4096), q_a_norm=f32(1024), wq_b=bf(64 * 512, 1024), wkv=bf(512, 4096),
+                             kv_a_norm=f32(512), wo_a=bf(8 * 1024, 4096), wo_b=bf(4096, 8 * 1024), sinks=f32(64),
+                             wkv_c=bf(1024, 4096), wgate_c=bf(1024, 4096), ape=f32(4, 1024), norm_c=f32(512))
+    B, P = 8, 32768
+    layer = engine.DecodeLayer(lw, B, 4, max_pos=P, device=dev)
+    layer.raw.normal_(0, 0.5)
+    layer.comp.normal_(0, 0.5)
+    xn = (torch.randn(B, 4096, generator=g)).to(torch.bfloat16).to(dev)
+    pos = torch.full((B,), P - 1, dtype=torch.int32, device=dev)
+    ms = _time_graph_ms(lambda: layer.step(xn, pos), reps, inner=5)
+    wbytes = sum(t.numel() * t.element_size() for t in (lw.wq_a, lw.wq_b, lw.wkv, lw.wo_a, lw.wo_b, lw.wkv_c,
+                                                         lw.wgate_c))
+    res["decode_layer"] = {"workload": "decode_layer: one attention layer, B=8 tokens at position 32767, 32K window "
+                                       "cache + 8192 compressed rows (take-all: 128 + 8192 ids), 231 MB of bf16 "
+                                       "weights; graph of 5 steps",
+                           "us": round(ms * 1e3, 3), "tok_s": round(B / (ms * 1e-3), 1), "weight_bytes": wbytes}
+    del layer, lw
     return res
 
 

@@ -1,0 +1,116 @@
+"""Decode step of one sparse-MLA attention layer (CPU oracle; test infrastructure only).
+
+Restates ``oracle/decode_engine.py:73-119`` (``layer_fwd``'s decode branch for one token at
+position p, from the attention-normed input xn to ``o_grouped``; ``hc_pre`` / ``hc_post`` are
+outside the path), composed from the oracle's own pieces:
+
+* RoPE tables by layer ratio (``:47,73``): ratio 4 -> YaRN (original 65536, base 160000, factor
+  16, beta 32/1), ratio 0 -> plain base 10000 (original_seq_len 0);
+* q (``:78-80``): q_down, RMSNorm(q_a_norm), q_up to [64, 512], the weightless per-head RMS norm
+  (``v4mlx/mla.py:26-28``), RoPE at p on each head's last 64 dims;
+* kv (``:81-84``): kv_proj, RMSNorm(kv_a_norm), RoPE at p on the last 64 dims, the fp8 round
+  trip on the first 448 (``fp8.act_quant_sim``), appended to the window list;
+* ratio-4 layers (``:96-105``): ``compressor.ring_step`` with the projections x @ wkv_c^T,
+  x @ wgate_c^T and the YaRN frequencies of ``decode_engine.py:48``; an emitted row is appended
+  to the compressed list;
+* attention (``:107-116``): kv buffer [window list; compressed list], ids = positions
+  max(0, p-127)..p, then the first min(n_comp, (p+1)//4) compressed rows; ``sparse_attn`` with
+  the sinks and scale 512^-0.5;
+* output (``:118-119``): ``mla.o_project`` (inverse RoPE at p, then ``o_grouped``).
+
+Products run in float64 (``mla.linear``), norms and rotations in float32 as the pieces define.
+
+Pinning (``tests/test_oracle_engine.py``): the emission schedule (one compressed row after every
+4th token, none for ratio 0), the id lists against a brute-force enumeration, the first step's
+attention against the one-row closed form o = v e^s / (e^s + e^sink), and the window row's
+rotation against the rotation at position p applied to the unrotated row (a wrong position or a
+dropped RoPE fails it).
+"""
+from dataclasses import dataclass
+from typing import Optional
+
+import numpy as np
+import torch
+
+from . import compressor as _comp
+from . import fp8 as _fp8
+from . import mla as _mla
+from . import norm_rope as _nr
+from . import sparse_attn as _sa
+
+RD, WINDOW = 64, 128
+YARN = (65536, 160000.0, 16, 32, 1)
+PLAIN = (0, 10000.0, 40, 32, 1)
+
+
+@dataclass
+class OracleWeights:
+    """fp32 / float64 copies of one layer's attention weights (same names as the checkpoint's
+    ``blk.{L}.attn_*``)."""
+    wq_a: np.ndarray
+    q_a_norm: torch.Tensor
+    wq_b: np.ndarray
+    wkv: np.ndarray
+    kv_a_norm: torch.Tensor
+    wo_a: np.ndarray
+    wo_b: np.ndarray
+    sinks: torch.Tensor
+    wkv_c: Optional[np.ndarray] = None
+    wgate_c: Optional[np.ndarray] = None
+    ape: Optional[torch.Tensor] = None
+    norm_c: Optional[torch.Tensor] = None
+
+
+class LayerState:
+    """``oracle/decode_engine.py:68-69``: the window list, the compressed list and the ring."""
+
+    def __init__(self, ratio, max_pos=65536):
+        self.ratio = ratio
+        self.win, self.comp = [], []
+        self.kvs = torch.zeros(2 * 4, 2 * 512)
+        self.scs = torch.full((2 * 4, 2 * 512), float("-inf"))
+        self.cos, self.sin = _nr.rope_cos_sin(RD, max_pos, *(YARN if ratio else PLAIN))
+        self.freqs_c = _nr.precompute_freqs(RD, 64, *YARN)
+
+
+def rope_at(x, st, p, inverse=False):
+    """Rotate the interleaved pairs of x [..., 64] (fp32) to position p with the layer's table."""
+    cis = torch.complex(st.cos[p:p + 1], st.sin[p:p + 1])                 # [1, 32]
+    lead = x.shape[:-1]
+    y = _nr.apply_rotary_emb(x.reshape(1, 1, -1, RD), cis, inverse=inverse)
+    return y.reshape(*lead, RD)
+
+
+def index_list(p, n_window_rows, n_comp, ratio):
+    """``oracle/decode_engine.py:110-114`` over [window list (one row per position from 0);
+    compressed list]."""
+    widx = list(range(max(0, p - WINDOW + 1), p + 1))
+    nvis = (p + 1) // 4 if ratio == 4 else 0
+    cidx = [n_window_rows + j for j in range(min(n_comp, nvis))]
+    return torch.tensor(widx + cidx, dtype=torch.int32)
+
+
+def decode_step(st, w, xn, p):
+    """One token at position p: xn [dim] (fp32).  Returns (y [dim_out] float64, the window row
+    [512] fp32, ids int32, o [64, 512] fp32 before the output projection)."""
+    x = np.asarray(xn, dtype=np.float64)[None]
+    qa = _nr.rmsnorm(torch.from_numpy(_mla.linear(x, w.wq_a)).float(), w.q_a_norm)
+    q = torch.from_numpy(_mla.linear(qa.numpy(), w.wq_b)).float().reshape(64, 512)
+    q = q * torch.rsqrt(q.pow(2).mean(-1, keepdim=True) + 1e-6)
+    q = torch.cat([q[:, :-RD], rope_at(q[:, -RD:], st, p)], dim=-1)
+    kv = _nr.rmsnorm(torch.from_numpy(_mla.linear(x, w.wkv)).float(), w.kv_a_norm)[0]
+    kv = torch.cat([kv[:-RD], rope_at(kv[-RD:], st, p)])
+    nope, _ = _fp8.act_quant_sim(kv[:-RD].numpy()[None], 64)
+    kv = torch.cat([torch.from_numpy(nope[0]), kv[-RD:]])
+    st.win.append(kv)
+    if st.ratio == 4:
+        kvp = torch.from_numpy(_mla.linear(x, w.wkv_c)).float()[0]
+        scp = torch.from_numpy(_mla.linear(x, w.wgate_c)).float()[0]
+        row = _comp.ring_step(st.kvs, st.scs, kvp, scp, p, w.ape, w.norm_c, st.freqs_c, 4, RD, fp8_sim=True)
+        if row is not None:
+            st.comp.append(row)
+    ids = index_list(p, len(st.win), len(st.comp), st.ratio)
+    kvcat = torch.stack(st.win + st.comp)
+    o = _sa.sparse_attn(q[None], kvcat, w.sinks, ids[None], 512 ** -0.5)          # [1, 64, 512]
+    y = _mla.o_project(o, torch.tensor([p]), st.cos, st.sin, w.wo_a, w.wo_b)
+    return np.asarray(y)[0], kv, ids, o[0]

@@ -1,0 +1,83 @@
+"""GPU parity of the decode-layer wiring (``smla.engine.DecodeLayer``, ``oracle/decode_engine.py:73-119``)
+against the oracle's composition (``oracle/engine.py``), at the model's layer shapes (hidden 4096,
+q rank 1024, 64 heads x 512, output 8 groups x 1024), for two sequences stepped token by token.
+
+Per step: the layer output (relative L2 error <= 2e-2: every product is a bf16 HIP kernel and the
+window and compressed rows are stored in bf16, while the oracle runs float64 products on the same
+bf16 weights), the window row written at p (rope dims <= 1e-2) and every emitted compressed row
+(rope dims <= 2e-2), whose fp8 round-tripped dims are held to 4e-2.  A wrong position, a missing rotation, a misplaced row or a wrong id list changes the
+output by O(1)."""
+import numpy as np
+import pytest
+import torch
+
+from conftest import announce
+from oracle import engine as oe
+
+pytestmark = pytest.mark.gpu
+
+
+def _make_weights(ratio, seed=7):
+    g = torch.Generator().manual_seed(seed)
+    bf = lambda *s, sc=0.02: (torch.randn(*s, generator=g) * sc).to(torch.bfloat16)
+    f32 = lambda *s, sc=0.1, base=0.0: base + torch.randn(*s, generator=g) * sc
+    t = dict(wq_a=bf(1024, 4096), q_a_norm=f32(1024, base=1.0), wq_b=bf(64 * 512, 1024), wkv=bf(512, 4096),
+             kv_a_norm=f32(512, base=1.0), wo_a=bf(8 * 1024, 4096), wo_b=bf(4096, 8 * 1024), sinks=f32(64, sc=1.0))
+    if ratio == 4:
+        t.update(wkv_c=bf(1024, 4096), wgate_c=bf(1024, 4096), ape=f32(4, 1024), norm_c=f32(512, base=1.0))
+    return t
+
+
+def _rel(a, b):
+    a, b = np.asarray(a, dtype=np.float64), np.asarray(b, dtype=np.float64)
+    return float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-30))
+
+
+def _check_row(got, ref, tol, what):
+    """Rope dims (no fp8) within `tol`; the 448 fp8 round-tripped dims within 4e-2: a bf16-sized
+    input difference moves some values across an e4m3 rounding boundary, one step (up to 1/8 of
+    the value) each."""
+    r = _rel(got[-64:], ref[-64:])
+    assert r <= tol, f"{what}: rope dims rel err {r:.3e}"
+    n = _rel(got[:-64], ref[:-64])
+    assert n <= 4e-2, f"{what}: fp8 dims rel err {n:.3e}"
+
+
+@pytest.mark.parametrize("ratio,steps", [(4, 136), (0, 24)])
+def test_decode_layer_vs_oracle(dev, ratio, steps):
+    from smla import engine
+    announce(f"decode layer ratio={ratio} steps={steps}")
+    t = _make_weights(ratio)
+    w = engine.LayerWeights(**{k: v.to(dev) for k, v in t.items()})
+    wo = oe.OracleWeights(**{k: (v.double().numpy() if v.dtype == torch.bfloat16 else v.float())
+                             for k, v in t.items()})
+    B, max_pos = 2, 256
+    layer = engine.DecodeLayer(w, B, ratio, max_pos=max_pos, device=dev)
+    states = [oe.LayerState(ratio, max_pos=max_pos) for _ in range(B)]
+    g = torch.Generator().manual_seed(100 + ratio)
+    worst = 0.0
+    for p in range(steps):
+        xn = torch.randn(B, 4096, generator=g).to(torch.bfloat16)
+        pos = torch.full((B,), p, dtype=torch.int32, device=dev)
+        y = layer.step(xn.to(dev), pos).float().cpu()
+        for b in range(B):
+            yr, kv, ids, _ = oe.decode_step(states[b], wo, xn[b].float(), p)
+            r = _rel(y[b], yr)
+            worst = max(worst, r)
+            assert r <= 2e-2, f"step {p} seq {b}: output rel err {r:.3e}"
+            _check_row(layer.raw[b, p].float().cpu(), kv, 1e-2, f"step {p} seq {b}: window row")
+            if ratio == 4 and (p + 1) % 4 == 0:
+                j = (p + 1) // 4 - 1
+                assert len(states[b].comp) == j + 1
+                _check_row(layer.comp32[b, j].cpu(), states[b].comp[j], 2e-2, f"step {p} seq {b}: compressed row {j}")
+    announce(f"worst output rel err {worst:.3e}")
+
+
+def test_decode_layer_rejects_cpu_and_bad_ratio(dev):
+    from smla import engine
+    t = _make_weights(0)
+    with pytest.raises(ValueError):
+        engine.DecodeLayer(engine.LayerWeights(**{k: v.to(dev) for k, v in t.items()}), 1, ratio=2, max_pos=64,
+                           device=dev)
+    with pytest.raises(Exception):
+        engine.DecodeLayer(engine.LayerWeights(**t), 1, ratio=0, max_pos=64, device=dev)   # CPU weights
