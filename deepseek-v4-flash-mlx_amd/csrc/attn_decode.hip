@@ -61,6 +61,18 @@ struct Geo6 {
 
 __device__ inline uint32_t pack2(float a, float b) { return pack_bf16x2(a, b); }
 
+// Combine v over lanes l, l^16, l^32, l^48 (the four 16-lane rows of a wave) with the gfx950 lane
+// swaps: permlane16_swap returns (even rows, odd rows) each duplicated over their pair, and
+// permlane32_swap (low half, high half) likewise, so one op on the two results is the xor-16
+// (resp. xor-32) step of a butterfly, in VALU registers instead of an LDS permute.
+template <class Op>
+__device__ inline float rows4_reduce(float v, Op op) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = op(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return op(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+
 // The copies are dealt to the value waves only (wave 4 + v issues instructions v, v+8, v+16, ...):
 // a wave whose copy waits at issue for the memory pipeline stalls with it, and the score waves
 // carry the tile loop's critical path while the value waves have slack.
@@ -364,8 +376,7 @@ __global__ __launch_bounds__(768) void attn_decode_kernel(
         float mt = x[0];
 #pragma unroll
         for (int i = 1; i < 8; i++) mt = fmaxf(mt, x[i]);
-        mt = fmaxf(mt, __shfl_xor(mt, 16, 64));
-        mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
+        mt = rows4_reduce(mt, [](float x, float y) { return fmaxf(x, y); });
         float alpha = 1.f;
         if ((mt > m_ref + kRescaleSlack) || (m_ref == -SMLA_INF && mt > -SMLA_INF)) {
           alpha = (m_ref > -SMLA_INF) ? __expf(m_ref - mt) : 0.f;
@@ -387,8 +398,7 @@ __global__ __launch_bounds__(768) void attn_decode_kernel(
       end_iteration(it);
     }
     // publish (m, l) per head: to LDS for the value waves' final scaling, and as the partial state
-    float l_tot = l_lane + __shfl_xor(l_lane, 16, 64);
-    l_tot += __shfl_xor(l_tot, 32, 64);
+    const float l_tot = rows4_reduce(l_lane, [](float x, float y) { return x + y; });
     const int hl = hg * 16 + c;
     if (g == 0) {
       ml_s[hl * 2] = m_ref;
