@@ -14,6 +14,11 @@
 //                        r + pos%r, and on a group boundary pool the ring into one row (same
 //                        epilogue, RoPE position pos+1-r), append it to the compressed cache and
 //                        shift the ring.  One workgroup per sequence; no host synchronisation.
+//  * row_epilogue_kernel : the same epilogue on rows the caller projected (oracle/decode_engine.py:
+//                        78-83: the q_a RMSNorm, the weightless per-head q norm + RoPE, the kv row's
+//                        RMSNorm + RoPE + fp8 round trip written straight into its window-cache row).
+//  * decode_ids_kernel : oracle/decode_engine.py:110-114, the decode id list (window rows, then every
+//                        visible compressed row), plus the bf16 copy of a row the ring just emitted.
 //  * quant_kernel      : act_quant_sim's stored form (v4mlx/compressor.py:11-20): per 64-block pow2
 //                        scale and e4m3 codes, 16 lanes per block.
 #include "smla_internal.h"
@@ -99,8 +104,8 @@ __device__ inline void pool_epilogue(float v0, float v1, int d, int rd, float ep
   const int c0 = 2 * t;
   float ss = block_sum(v0 * v0 + v1 * v1, red);
   float inv = rsqrtf(ss / (float)d + eps);
-  float y0 = norm_w[c0] * (v0 * inv);
-  float y1 = norm_w[c0 + 1] * (v1 * inv);
+  float y0 = (norm_w ? norm_w[c0] : 1.f) * (v0 * inv);   // no weight: the weightless per-head norm
+  float y1 = (norm_w ? norm_w[c0 + 1] : 1.f) * (v1 * inv);
   const int nope = d - rd;
   if (c0 >= nope) {
     int pi = (c0 - nope) >> 1;
@@ -367,6 +372,66 @@ extern "C" int smla_gated_pool(const float* kv, const float* score, const float*
   return SMLA_OK;
 }
 
+// One workgroup of d/2 threads per input row r (fp32, d channels): pool_epilogue (RMSNorm with
+// norm_w, or weightless when it is null; RoPE of the last rd channels at pos[r / rows_per_pos];
+// the `sim` quantisation), written in out_dtype to row r of `out` or, when cache_rows > 0, to row
+// pos of sequence r / rows_per_pos of a cache [.., cache_rows, d].  A position outside the rotation
+// table or the cache leaves the row unwritten.
+__global__ __launch_bounds__(512) void row_epilogue_kernel(const float* __restrict__ x, int d, int rows_per_pos,
+                                                           const int32_t* __restrict__ pos,
+                                                           const float* __restrict__ norm_w,
+                                                           const float* __restrict__ cos_t,
+                                                           const float* __restrict__ sin_t, int64_t n_pos, int rd,
+                                                           float eps, int sim, void* __restrict__ out, int out_dtype,
+                                                           int64_t cache_rows) {
+  __shared__ float red[8];
+  __shared__ float xch[1024];
+  __shared__ float res[1024];
+  const int64_t r = blockIdx.x;
+  const int t = threadIdx.x;
+  const int64_t s = r / rows_per_pos;
+  const int64_t p = pos ? (int64_t)pos[s] : 0;
+  const bool ok = (rd == 0 || (p >= 0 && p < n_pos)) && (cache_rows == 0 || (p >= 0 && p < cache_rows));
+  if (!ok) return;  // uniform over the workgroup
+  const float* xr = x + r * d;
+  pool_epilogue(xr[2 * t], xr[2 * t + 1], d, rd, eps, sim, norm_w, cos_t, sin_t, rd ? p : 0, red, xch, res);
+  const int64_t orow = cache_rows > 0 ? s * cache_rows + p : r;
+  if (out_dtype == SMLA_BF16)
+    ((uint32_t*)out)[(orow * d) / 2 + t] = pack_bf16x2(res[2 * t], res[2 * t + 1]);
+  else
+    ((f32x2_t*)out)[(orow * d) / 2 + t] = f32x2_t{res[2 * t], res[2 * t + 1]};
+}
+
+// ids [B, T] for sequences at positions pos[b]: columns 0..window-1 hold the window rows
+// max(0, p-window+1)..p (then -1), the rest n_raw + j for the (p+1)/ratio visible compressed rows
+// j (then -1).  Workgroup column 0 also copies a row the ring emitted at this step
+// ((p+1) % ratio == 0) from comp32 to comp_out in bf16.
+__global__ __launch_bounds__(256) void decode_ids_kernel(const int32_t* __restrict__ pos, int window, int ratio,
+                                                         int64_t n_raw, int64_t ncomp, int64_t T,
+                                                         int32_t* __restrict__ ids, const float* __restrict__ comp32,
+                                                         uint16_t* __restrict__ comp_out, int d) {
+  const int64_t b = blockIdx.y;
+  const int64_t p = pos[b];
+  const int64_t j = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (j < T) {
+    int64_t id;
+    if (j < window) {
+      const int64_t lo = p - window + 1 > 0 ? p - window + 1 : 0;
+      id = lo + j <= p ? lo + j : -1;
+    } else {
+      const int64_t c = j - window;
+      id = (ratio > 0 && c < ncomp && c < (p + 1) / ratio) ? n_raw + c : -1;
+    }
+    ids[b * T + j] = (int32_t)id;
+  }
+  if (blockIdx.x == 0 && comp_out && ratio > 0 && p >= 0 && (p + 1) % ratio == 0) {
+    const int64_t row = (p + 1) / ratio - 1;
+    if (row < ncomp)
+      for (int c = threadIdx.x; c < d; c += 256)
+        comp_out[(b * ncomp + row) * d + c] = bf16_rne(comp32[(b * ncomp + row) * d + c]);
+  }
+}
+
 extern "C" int smla_ring_step(float* ring_kv, float* ring_sc, const float* kv_p, const float* score_p,
                               const int32_t* pos, const float* ape, const float* norm_w, const float* cos_t,
                               const float* sin_t, int64_t n_pos, int64_t B, int64_t d, int64_t ratio, int64_t rd,
@@ -396,6 +461,43 @@ extern "C" int smla_quant_fp8_pow2(const void* x, int x_dtype, int64_t rows, int
     hipLaunchKernelGGL(quant_kernel<SMLA_F32>, grid, dim3(256), 0, (hipStream_t)stream, x, nb, codes, scales);
   else
     hipLaunchKernelGGL(quant_kernel<SMLA_BF16>, grid, dim3(256), 0, (hipStream_t)stream, x, nb, codes, scales);
+  SMLA_HIP_CHECK_LAUNCH();
+  return SMLA_OK;
+}
+
+extern "C" int smla_row_epilogue(const float* x, int64_t rows, int64_t d, int64_t rows_per_pos, const int32_t* pos,
+                                 const float* norm_w, const float* cos_t, const float* sin_t, int64_t n_pos,
+                                 int64_t rd, float eps, int sim, void* out, int out_dtype, int64_t cache_rows,
+                                 void* stream) {
+  if (!x || !out) return SMLA_E_NULL;
+  if (rows <= 0 || d < 128 || d > 1024 || d % 64 != 0 || rows_per_pos <= 0 || rd < 0 || rd > d || rd % 2 != 0 ||
+      cache_rows < 0 || rows > (int64_t)INT32_MAX)
+    return SMLA_E_SHAPE;
+  if (rd > 0 && (!pos || !cos_t || !sin_t || n_pos <= 0)) return SMLA_E_NULL;
+  if (cache_rows > 0 && !pos) return SMLA_E_NULL;
+  if (sim != SMLA_SIM_NONE && sim != SMLA_SIM_FP8) return SMLA_E_UNSUPPORTED;
+  if (sim == SMLA_SIM_FP8 && (d - rd) % 64 != 0) return SMLA_E_SHAPE;
+  if (out_dtype != SMLA_F32 && out_dtype != SMLA_BF16) return SMLA_E_DTYPE;
+  if (!(eps >= 0.f)) return SMLA_E_RANGE;
+  hipLaunchKernelGGL(row_epilogue_kernel, dim3((unsigned)rows), dim3((unsigned)(d / 2)), 0, (hipStream_t)stream, x,
+                     (int)d, (int)rows_per_pos, pos, norm_w, cos_t, sin_t, n_pos, (int)rd, eps, sim, out, out_dtype,
+                     cache_rows);
+  SMLA_HIP_CHECK_LAUNCH();
+  return SMLA_OK;
+}
+
+extern "C" int smla_decode_ids(const int32_t* pos, int64_t B, int64_t window, int64_t ratio, int64_t n_raw,
+                               int64_t ncomp, int32_t* ids, int64_t T, const float* comp32, uint16_t* comp_out,
+                               int64_t d, void* stream) {
+  if (!pos || !ids) return SMLA_E_NULL;
+  if (B <= 0 || B > 65535 || window <= 0 || ratio < 0 || n_raw <= 0 || ncomp < 0 || T < window || d < 0)
+    return SMLA_E_SHAPE;
+  if ((comp32 == nullptr) != (comp_out == nullptr)) return SMLA_E_NULL;
+  if (comp_out && (ratio == 0 || d <= 0)) return SMLA_E_SHAPE;
+  if (n_raw + ncomp > (int64_t)INT32_MAX) return SMLA_E_RANGE;
+  const dim3 grid((unsigned)((T + 255) / 256), (unsigned)B);
+  hipLaunchKernelGGL(decode_ids_kernel, grid, dim3(256), 0, (hipStream_t)stream, pos, (int)window, (int)ratio, n_raw,
+                     ncomp, T, ids, comp32, comp_out, (int)d);
   SMLA_HIP_CHECK_LAUNCH();
   return SMLA_OK;
 }

@@ -19,16 +19,16 @@ Per token at position p, for each of B sequences:
 
 RoPE tables: ratio-4 layers use YaRN (base 160000, factor 16 over 65536 positions), ratio-0
 layers plain base 10000 (``decode_engine.py:47,73``).  Every step runs on the HIP kernels:
-``smla_linear`` (projections, fp32 results), ``smla_rope``, ``smla_quant_fp8_pow2``, ``smla_ring_step``,
-``smla_sparse_attn`` and ``smla_o_proj``; the norms and the index build are torch element-wise
-work on the GPU.  Caches are device-resident and owned by the layer object.
+``smla_linear`` (projections, fp32 results), ``smla_row_epilogue`` (the norms, RoPE, the fp8 round
+trip and the window-cache write), ``smla_ring_step``, ``smla_decode_ids``, ``smla_sparse_attn`` and
+``smla_o_proj``.  Caches are device-resident and owned by the layer object.
 """
 from dataclasses import dataclass
 from typing import Optional
 
 import torch
 
-from . import mla, ops
+from . import _lib, mla, ops
 from . import compressor as _comp
 from . import indexer as _idx
 from . import norm_rope as _nr
@@ -67,12 +67,6 @@ def _proj(x, W):
     return x.float() @ W.float().t()
 
 
-def _e4m3_table(device):
-    """fp32 value of each of the 256 e4m3 codes (the two NaN codes never occur: the quantiser
-    clamps to +-448)."""
-    return torch.arange(256, dtype=torch.uint8).view(torch.float8_e4m3fn).float().to(device)
-
-
 class DecodeLayer:
     """Decode state and step of one attention layer for B sequences.
 
@@ -98,57 +92,45 @@ class DecodeLayer:
                                    max_pos=max_pos, fp8_sim=True, device=device, rope_args=_YARN)
         else:
             self.comp = torch.zeros(B, 1, HEAD_DIM, dtype=torch.bfloat16, device=device)   # never addressed
-        self.e4m3 = _e4m3_table(device)
-        self.rows = torch.arange(B, device=device)
+        self.q_a_norm = w.q_a_norm.float().contiguous()
+        self.kv_a_norm = w.kv_a_norm.float().contiguous()
 
     # -- pieces (each mirrors one span of decode_engine.py) --------------------------------------
     def q_path(self, xn, pos):
-        """``decode_engine.py:78-80``: q [B, 64, 512] bf16 with its rope dims rotated."""
+        """``decode_engine.py:78-80``: q [B, 64, 512] bf16, per-head normed, rope dims rotated."""
         w = self.w
-        qa = _nr.rmsnorm(_proj(xn, w.wq_a), w.q_a_norm).to(torch.bfloat16)
-        q = _proj(qa, w.wq_b).reshape(self.B, N_HEADS, HEAD_DIM)
-        q = mla.perhead_norm(q).to(torch.bfloat16).contiguous()
-        ops.rope_op_(q, pos, self.cos_t, self.sin_t, False)
+        qa = torch.empty(self.B, w.wq_a.shape[0], dtype=torch.bfloat16, device=xn.device)
+        ops.row_epilogue(_proj(xn, w.wq_a), self.q_a_norm, None, None, None, 0, _lib.SIM_NONE, qa)
+        q = torch.empty(self.B, N_HEADS, HEAD_DIM, dtype=torch.bfloat16, device=xn.device)
+        ops.row_epilogue(_proj(qa, w.wq_b).view(self.B * N_HEADS, HEAD_DIM), None, pos, self.cos_t, self.sin_t,
+                         ROPE_HD, _lib.SIM_NONE, q, rows_per_pos=N_HEADS)
         return q
 
-    def kv_row(self, xn, pos):
-        """``decode_engine.py:81-83``: the token's window row [B, 512] fp32 (RoPE on the last 64
-        dims, fp8 round trip on the other 448)."""
+    def kv_append(self, xn, pos):
+        """``decode_engine.py:81-84``: the token's kv row (RMSNorm, RoPE of the last 64 dims, fp8
+        round trip of the other 448) written as bf16 to window-cache row pos of each sequence."""
         w = self.w
-        kv = _nr.rmsnorm(_proj(xn, w.wkv), w.kv_a_norm).contiguous()   # fp32 from here on
-        ops.rope_op_(kv[:, None, :], pos, self.cos_t, self.sin_t, False)
-        nope = kv[:, :HEAD_DIM - ROPE_HD].contiguous()
-        codes, scales = ops.quant_fp8_pow2_op(nope)
-        kv[:, :HEAD_DIM - ROPE_HD] = self.e4m3[codes.long()] * scales.repeat_interleave(64, dim=-1)
-        return kv
+        ops.row_epilogue(_proj(xn, w.wkv), self.kv_a_norm, pos, self.cos_t, self.sin_t, ROPE_HD, _lib.SIM_FP8,
+                         self.raw, cache_rows=self.max_pos)
 
     def ring_step(self, xn, pos):
-        """``decode_engine.py:96-105``: ring update; an emitted row lands in the compressed cache."""
+        """``decode_engine.py:96-105``: ring update; an emitted row lands in the fp32 compressed
+        cache (its bf16 copy is made with the id list)."""
         w = self.w
-        kvp = _proj(xn, w.wkv_c)
-        scp = _proj(xn, w.wgate_c)
-        self.ring.step(kvp, scp, pos, self.comp32)
-        emitted = (pos + 1) % 4 == 0
-        r = ((pos + 1) // 4 - 1).clamp(min=0).long()
-        cur = self.comp[self.rows, r]
-        self.comp[self.rows, r] = torch.where(emitted[:, None], self.comp32[self.rows, r].to(torch.bfloat16), cur)
+        self.ring.step(_proj(xn, w.wkv_c), _proj(xn, w.wgate_c), pos, self.comp32)
 
     def index_list(self, pos, scores=None, k=2048):
         """``decode_engine.py:110-114``: [B, 128 + n] int32 ids into [window cache; compressed
         cache] (compressed ids offset by max_pos), -1 padded.  Take-all over the visible compressed
-        rows, or, with indexer scores [B, ncap] supplied, the top-k of them."""
-        if scores is not None and self.ratio:
-            return _idx.select_decode_indices(scores, k, pos, WINDOW, self.max_pos)
-        p = pos.long()[:, None]
-        j = torch.arange(WINDOW, device=pos.device)[None]
-        lo = (p - (WINDOW - 1)).clamp(min=0)
-        wid = lo + j
-        wid = torch.where(wid <= p, wid, torch.full_like(wid, -1))
-        if not self.ratio:
-            return wid.to(torch.int32)
-        c = torch.arange(self.ncap, device=pos.device)[None]
-        cid = torch.where(c < (p + 1) // 4, self.max_pos + c, torch.full_like(c, -1))
-        return torch.cat([wid, cid], dim=1).to(torch.int32)
+        rows, or, with indexer scores [B, ncap] supplied, the top-k of them.  Also copies a row the
+        ring emitted at this step to the bf16 compressed cache."""
+        comp = (self.comp32, self.comp) if self.ratio else (None, None)
+        take_all = scores is None or not self.ratio
+        T = WINDOW + (self.ncap if take_all else 0)
+        ids = ops.decode_ids(pos, WINDOW, self.ratio, self.max_pos, self.ncap, T, comp32=comp[0], comp_out=comp[1])
+        if take_all:
+            return ids
+        return _idx.select_decode_indices(scores, k, pos, WINDOW, self.max_pos)
 
     # -- the step --------------------------------------------------------------------------------
     def step(self, xn, pos, scores=None, k=2048):
@@ -160,8 +142,7 @@ class DecodeLayer:
             raise ValueError(f"xn must be [{self.B}, {self.w.wq_a.shape[1]}]")
         pos = pos.to(torch.int32).contiguous()
         q = self.q_path(xn, pos)
-        kv = self.kv_row(xn, pos)
-        self.raw[self.rows, pos.long()] = kv.to(torch.bfloat16)
+        self.kv_append(xn, pos)
         if self.ratio:
             self.ring_step(xn, pos)
         ids = self.index_list(pos, scores, k)

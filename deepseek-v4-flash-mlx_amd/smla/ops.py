@@ -343,6 +343,36 @@ def decode_window_idxs(pos, window, out=None):
     return out
 
 
+def row_epilogue(x, norm_w, pos, cos_t, sin_t, rd, sim, out, rows_per_pos=1, cache_rows=0, eps=1e-6):
+    """``smla_row_epilogue``: rows of x [rows, d] fp32 -> RMSNorm (norm_w [d], or None for the
+    weightless norm) -> RoPE of the last rd channels at pos[row // rows_per_pos] -> `sim` -> out
+    (bf16 or fp32): row r of out [rows, d], or with cache_rows > 0 row pos of sequence
+    r // rows_per_pos of a cache [.., cache_rows, d].  Stream-ordered; returns out."""
+    _on_gpu(x, out, *(t for t in (norm_w, pos, cos_t, sin_t) if t is not None))
+    if x.dtype != torch.float32 or not x.is_contiguous() or not out.is_contiguous():
+        raise ValueError("row_epilogue: x must be contiguous fp32 and out contiguous")
+    d = x.shape[-1]
+    rows = x.numel() // d
+    n_pos = cos_t.shape[0] if cos_t is not None else 0
+    _lib.call("smla_row_epilogue", _p(x), rows, d, rows_per_pos, _p(pos), _p(norm_w), _p(cos_t), _p(sin_t),
+              n_pos, rd, float(eps), int(sim), _p(out), dtype_code(out), cache_rows, _stream(x))
+    return out
+
+
+def decode_ids(pos, window, ratio, n_raw, ncomp, T, out=None, comp32=None, comp_out=None):
+    """``smla_decode_ids``: [B, T] int32 ids (window rows, then the visible compressed rows offset
+    by n_raw); with comp32/comp_out, an emitted compressed row is copied to bf16."""
+    _on_gpu(pos, *(t for t in (out, comp32, comp_out) if t is not None))
+    pos = pos.to(torch.int32).contiguous()
+    B = pos.numel()
+    if out is None:
+        out = torch.empty(B, T, dtype=torch.int32, device=pos.device)
+    d = comp32.shape[-1] if comp32 is not None else 0
+    _lib.call("smla_decode_ids", _p(pos), B, window, ratio, n_raw, ncomp, _p(out), T, _p(comp32), _p(comp_out), d,
+              _stream(pos))
+    return out
+
+
 def select_decode_into(scores, k, pos, window, out, id_offset=0, nvis=None):
     """Window ids then top-k ids per row, in one launch: scores [R, N], pos [R] int32,
     out int32 [R, >= window + k] (row stride out.stride(0))."""

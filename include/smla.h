@@ -22,6 +22,8 @@
  *   smla_gated_pool           ref_torch/compressor.py:41-49    pooling + RMSNorm + RoPE of compressor_prefill
  *   smla_ring_step            oracle/decode_engine.py:96-105   decode compressor ring step and cache append
  *   smla_quant_fp8_pow2       v4mlx/compressor.py:11-20        act_quant_sim (stored form: codes + pow2 scales)
+ *   smla_row_epilogue         oracle/decode_engine.py:78-83    q/kv row norms, RoPE, fp8 sim, window-cache write
+ *   smla_decode_ids           oracle/decode_engine.py:110-114  decode id list (window + visible compressed rows)
  *   smla_rotate_fp4           v4mlx/qat.py:8-31                hadamard_rotate, fp4_act_quant (and stored form)
  *                             v4mlx/compressor.py:57-59        the indexer compressor's key transform
  *   smla_rope                 ref_torch/norm_rope.py:53-62     apply_rotary_emb(x, freqs_cis, inverse) in place
@@ -208,6 +210,29 @@ int smla_ring_step(float* ring_kv, float* ring_sc, const float* kv_p, const floa
                    const float* cos_t, const float* sin_t, int64_t n_pos, int64_t B, int64_t d,
                    int64_t ratio, int64_t rd, float eps, int sim, float* comp_cache,
                    int64_t comp_cap, void* stream);
+
+/* smla_row_epilogue: the per-row work of oracle/decode_engine.py:78-83 on rows the caller has
+ * projected.  x [rows, d] fp32 (128 <= d <= 1024, d % 64 == 0) -> RMSNorm with norm_w [d]
+ * (ref_torch/norm_rope.py:10-16; norm_w NULL gives the weightless per-head norm of v4mlx/mla.py:
+ * 26-28), RoPE of the last rd channels (ref_torch/norm_rope.py:53-62, interleaved pairs, cos/sin
+ * [n_pos, rd/2]) at position pos[r / rows_per_pos], then `sim` (SMLA_SIM_NONE or SMLA_SIM_FP8: the
+ * d-rd other channels fp8 round-tripped, v4mlx/compressor.py:11-20).  Row r goes to row r of out
+ * [rows, d] (SMLA_F32 / SMLA_BF16), or, with cache_rows > 0, to row pos of sequence r / rows_per_pos
+ * of a cache [.., cache_rows, d] (the window append, decode_engine.py:84).  eps: the RMSNorm eps.
+ * A row whose position lies outside [0, n_pos) (when rd > 0) or [0, cache_rows) is not written. */
+int smla_row_epilogue(const float* x, int64_t rows, int64_t d, int64_t rows_per_pos, const int32_t* pos,
+                      const float* norm_w, const float* cos_t, const float* sin_t, int64_t n_pos,
+                      int64_t rd, float eps, int sim, void* out, int out_dtype, int64_t cache_rows,
+                      void* stream);
+
+/* smla_decode_ids: the decode id list of oracle/decode_engine.py:110-114 for B sequences at
+ * positions pos [B]: ids [B, T] int32 (T >= window), columns 0..window-1 = window rows
+ * max(0, p-window+1)..p then -1, columns window.. = n_raw + j for the (p+1)/ratio visible
+ * compressed rows j < ncomp (ratio 0: none), then -1.  With comp32 / comp_out (both or neither;
+ * [B, ncomp, d] fp32 / bf16), a row the ring emitted at this step ((p+1) % ratio == 0) is copied
+ * to comp_out as bf16. */
+int smla_decode_ids(const int32_t* pos, int64_t B, int64_t window, int64_t ratio, int64_t n_raw, int64_t ncomp,
+                    int32_t* ids, int64_t T, const float* comp32, uint16_t* comp_out, int64_t d, void* stream);
 
 /* smla_quant_fp8_pow2: per 64-element block, s = 2^ceil(log2(max(|x|,1e-4)/448)),
  * code = e4m3(clip(x/s, +-448)) (round to nearest even).  x [rows, D] F32|BF16 (D % 64 == 0),

@@ -1,0 +1,135 @@
+"""GPU parity of the decode layer's row kernels (``oracle/decode_engine.py:78-84,110-114``):
+
+* ``smla_row_epilogue`` against the oracle's RMSNorm (``ref_torch/norm_rope.py:10-16``), RoPE
+  (``:53-62``) and fp8 round trip (``v4mlx/compressor.py:11-20``): the rope channels within float32
+  rounding plus half a bf16 ulp; the fp8 channels equal the oracle's except where the float32
+  norm's summation order moves a value across an e4m3 rounding boundary (at most 2 % of them, each
+  by one e4m3 step);
+* ``smla_decode_ids`` equal, id for id, to a brute-force enumeration, and an emitted compressed
+  row copied to bf16 bit for bit.
+"""
+import numpy as np
+import pytest
+import torch
+
+from conftest import announce
+from oracle import fp8 as ofp8
+from oracle import norm_rope as onr
+
+pytestmark = pytest.mark.gpu
+
+YARN = (65536, 160000.0, 16, 32, 1)
+
+
+def _rope_ref(x, cos, sin, p):
+    cis = torch.complex(cos[p:p + 1], sin[p:p + 1])
+    return onr.apply_rotary_emb(x.reshape(1, 1, -1, 64), cis).reshape(x.shape)
+
+
+def _bf16(t):
+    return t.to(torch.bfloat16).float()
+
+
+def test_kv_rows_into_cache(dev):
+    from smla import _lib, ops
+    from smla import norm_rope as snr
+    announce("row_epilogue kv -> cache")
+    g = torch.Generator().manual_seed(21)
+    B, d, rows = 3, 512, 400
+    x = torch.randn(B, d, generator=g) * 3
+    w = 1 + 0.1 * torch.randn(d, generator=g)
+    pos = torch.tensor([0, 77, 399], dtype=torch.int32)
+    cos, sin = onr.rope_cos_sin(64, rows, *YARN)
+    cos_d, sin_d = snr.rope_tables(64, rows, *YARN, device=dev)
+    cache = torch.zeros(B, rows, d, dtype=torch.bfloat16, device=dev)
+    ops.row_epilogue(x.to(dev), w.to(dev), pos.to(dev), cos_d, sin_d, 64, _lib.SIM_FP8, cache, cache_rows=rows)
+    got = cache.float().cpu()
+    flips = 0
+    for b in range(B):
+        p = int(pos[b])
+        y = onr.rmsnorm(x[b], w)
+        rope = _rope_ref(y[-64:], cos, sin, p)
+        nope, scl = ofp8.act_quant_sim(y[:-64].numpy()[None], 64)
+        row = got[b, p]
+        assert torch.allclose(row[-64:], rope, rtol=2.0 ** -8, atol=1e-6)
+        ref8 = torch.from_numpy(nope[0])
+        diff = (row[:-64] - _bf16(ref8)).abs()
+        step = torch.from_numpy(np.repeat(scl[0], 64)) * 2.0 ** (torch.floor(torch.log2(ref8.abs().clamp(min=2 ** -6))) - 3)
+        assert torch.all(diff <= step * 1.01 + 1e-7), "an fp8 value off by more than one e4m3 step"
+        flips += int((diff > 0).sum())
+        others = torch.ones(rows, dtype=torch.bool)
+        others[p] = False
+        assert torch.all(got[b][others] == 0), "rows other than pos were written"
+    assert flips <= 0.02 * B * 448
+
+
+@pytest.mark.parametrize("B", [1, 5])
+def test_q_heads_weightless_norm_and_rope(dev, B):
+    from smla import _lib, ops
+    from smla import norm_rope as snr
+    announce(f"row_epilogue q heads B={B}")
+    g = torch.Generator().manual_seed(B)
+    x = torch.randn(B, 64, 512, generator=g) * 0.7
+    pos = torch.randint(0, 1000, (B,), generator=g, dtype=torch.int32)
+    cos, sin = onr.rope_cos_sin(64, 1000, *YARN)
+    cos_d, sin_d = snr.rope_tables(64, 1000, *YARN, device=dev)
+    out = torch.empty(B, 64, 512, dtype=torch.bfloat16, device=dev)
+    ops.row_epilogue(x.to(dev).view(B * 64, 512), None, pos.to(dev), cos_d, sin_d, 64, _lib.SIM_NONE, out,
+                     rows_per_pos=64)
+    got = out.float().cpu()
+    for b in range(B):
+        q = x[b] * torch.rsqrt(x[b].pow(2).mean(-1, keepdim=True) + 1e-6)
+        q = torch.cat([q[:, :-64], _rope_ref(q[:, -64:], cos, sin, int(pos[b]))], dim=-1)
+        assert torch.allclose(got[b], q, rtol=2.0 ** -8, atol=1e-6)
+
+
+def test_q_a_norm_d1024(dev):
+    from smla import _lib, ops
+    announce("row_epilogue q_a d=1024")
+    g = torch.Generator().manual_seed(4)
+    x = torch.randn(6, 1024, generator=g) * 2
+    w = 1 + 0.1 * torch.randn(1024, generator=g)
+    out = torch.empty(6, 1024, device=dev)
+    ops.row_epilogue(x.to(dev), w.to(dev), None, None, None, 0, _lib.SIM_NONE, out)
+    assert torch.allclose(out.cpu(), onr.rmsnorm(x, w), rtol=1e-5, atol=1e-6)
+
+
+def test_out_of_range_position_writes_nothing(dev):
+    from smla import _lib, ops
+    from smla import norm_rope as snr
+    announce("row_epilogue position past the cache")
+    cos_d, sin_d = snr.rope_tables(64, 64, *YARN, device=dev)
+    cache = torch.zeros(2, 32, 512, dtype=torch.bfloat16, device=dev)
+    x = torch.ones(2, 512, device=dev)
+    ops.row_epilogue(x, None, torch.tensor([5, 40], dtype=torch.int32, device=dev), cos_d, sin_d, 64,
+                     _lib.SIM_FP8, cache, cache_rows=32)
+    c = cache.float().cpu()
+    assert c[0, 5].abs().sum() > 0 and c[1].abs().sum() == 0
+
+
+@pytest.mark.parametrize("ratio", [4, 0])
+def test_decode_ids_brute_force(dev, ratio):
+    from smla import ops
+    announce(f"decode_ids ratio={ratio}")
+    n_raw, ncomp, d, W = 512, 128, 512, 128
+    pos = torch.tensor([0, 3, 126, 127, 128, 300, 511], dtype=torch.int32)
+    B = pos.numel()
+    T = W + (ncomp if ratio else 0)
+    comp32 = torch.randn(B, ncomp, d) if ratio else None
+    comp_out = torch.zeros(B, ncomp, d, dtype=torch.bfloat16, device=dev) if ratio else None
+    ids = ops.decode_ids(pos.to(dev), W, ratio, n_raw, ncomp, T, comp32=None if comp32 is None else comp32.to(dev),
+                         comp_out=comp_out).cpu()
+    for b in range(B):
+        p = int(pos[b])
+        lo = max(0, p - W + 1)
+        win = [t for t in range(lo, p + 1)] + [-1] * (W - (p + 1 - lo))
+        comp = [n_raw + j for j in range(ncomp) if ratio and j < (p + 1) // ratio]
+        comp += [-1] * (T - W - len(comp))
+        assert ids[b].tolist() == win + comp
+        if ratio:
+            got = comp_out[b].cpu()
+            r = (p + 1) // ratio - 1
+            if (p + 1) % ratio == 0:
+                assert torch.equal(got[r], comp32[b, r].to(torch.bfloat16))
+                got[r] = 0
+            assert torch.all(got.float() == 0)
