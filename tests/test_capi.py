@@ -82,6 +82,29 @@ def test_host_validation_rejects_bad_arguments():
     assert lib.smla_quant_fp8_pow2(fake, 1, 4, 100, fake, fake, None) == -2
     assert lib.smla_window_topk_idxs(0, 1, 1, 0, fake, None) == -2
     assert lib.smla_decode_window_idxs(fake, 2, 128, fake, 64, None) == -2
+    # row_epilogue: NULL, row width, rope without tables, sim, fp8 block, dtype, eps
+    assert lib.smla_row_epilogue(None, 2, 512, 1, None, None, None, None, 0, 0, 1e-6, 0, fake, 0, 0, None) == -1
+    assert lib.smla_row_epilogue(fake, 2, 96, 1, None, None, None, None, 0, 0, 1e-6, 0, fake, 0, 0, None) == -2
+    assert lib.smla_row_epilogue(fake, 2, 2048, 1, None, None, None, None, 0, 0, 1e-6, 0, fake, 0, 0, None) == -2
+    assert lib.smla_row_epilogue(fake, 2, 512, 1, None, None, None, None, 0, 64, 1e-6, 0, fake, 0, 0, None) == -1
+    assert lib.smla_row_epilogue(fake, 2, 512, 1, None, None, None, None, 0, 0, 1e-6, 2, fake, 0, 0, None) == -4
+    assert lib.smla_row_epilogue(fake, 2, 512, 1, fake, None, fake, fake, 8, 32, 1e-6, 1, fake, 0, 0, None) == -2
+    assert lib.smla_row_epilogue(fake, 2, 512, 1, None, None, None, None, 0, 0, 1e-6, 0, fake, 9, 0, None) == -3
+    assert lib.smla_row_epilogue(fake, 2, 512, 1, None, None, None, None, 0, 0, -1.0, 0, fake, 0, 0, None) == -6
+    assert lib.smla_row_epilogue(fake, 2, 512, 1, None, None, None, None, 0, 0, 1e-6, 0, fake, 0, 16, None) == -1
+    # decode_ids: NULL, T < window, only one of the compressed-row buffers, copy without ratio
+    assert lib.smla_decode_ids(None, 2, 128, 4, 512, 16, fake, 144, None, None, 0, None) == -1
+    assert lib.smla_decode_ids(fake, 2, 128, 4, 512, 16, fake, 100, None, None, 0, None) == -2
+    assert lib.smla_decode_ids(fake, 2, 128, 4, 512, 16, fake, 144, fake, None, 512, None) == -1
+    assert lib.smla_decode_ids(fake, 2, 128, 0, 512, 16, fake, 144, fake, fake, 512, None) == -2
+
+
+def _cpu_decode_layer():
+    from smla import engine
+    z = lambda *sh: torch.zeros(*sh, dtype=torch.bfloat16)
+    w = engine.LayerWeights(wq_a=z(64, 512), q_a_norm=torch.ones(64), wq_b=z(64 * 512, 64), wkv=z(512, 512),
+                            kv_a_norm=torch.ones(512), wo_a=z(8 * 16, 4096), wo_b=z(512, 128), sinks=torch.zeros(64))
+    return engine.DecodeLayer(w, 1, ratio=0, max_pos=64, device="cpu")
 
 
 def test_python_ops_refuse_cpu_tensors():
@@ -108,6 +131,7 @@ def test_python_ops_refuse_cpu_tensors():
         lambda: sc.compressor_prefill(torch.zeros(1, 8, 16), torch.zeros(256, 16), torch.zeros(256, 16),
                                       torch.zeros(4, 256), torch.ones(128), head_dim=128),
         lambda: sq.rotate_fp4(torch.zeros(4, 128)),
+        lambda: _cpu_decode_layer(),
     ]
     for c in cases:
         with pytest.raises(RuntimeError):
