@@ -224,7 +224,8 @@ __global__ __launch_bounds__(kPoolThreads) void ring_step_kernel(
     float* __restrict__ ring_kv, float* __restrict__ ring_sc, const float* __restrict__ kv_p,
     const float* __restrict__ score_p, const int32_t* __restrict__ pos_arr, const float* __restrict__ ape,
     const float* __restrict__ norm_w, const float* __restrict__ cos_t, const float* __restrict__ sin_t,
-    int64_t n_pos, int d, int ratio, int rd, float eps, int sim, float* __restrict__ comp, int64_t comp_cap) {
+    int64_t n_pos, int d, int ratio, int rd, float eps, int sim, float* __restrict__ comp, int64_t comp_cap,
+    int64_t ldp) {
   __shared__ float red[kPoolThreads / 64];
   __shared__ float xch[2 * kPoolThreads];
   const int64_t b = blockIdx.x;
@@ -240,8 +241,8 @@ __global__ __launch_bounds__(kPoolThreads) void ring_step_kernel(
     const int c = 2 * t + k;
     for (int h = 0; h < 2; h++) {
       int64_t cc = c + h * (int64_t)d;
-      rk[slot * two_d + cc] = kv_p[b * two_d + cc];
-      rs[slot * two_d + cc] = score_p[b * two_d + cc] + ape[(pos % ratio) * two_d + cc];
+      rk[slot * two_d + cc] = kv_p[b * ldp + cc];
+      rs[slot * two_d + cc] = score_p[b * ldp + cc] + ape[(pos % ratio) * two_d + cc];
     }
   }
   if ((pos + 1) % ratio != 0) return;  // block-uniform
@@ -377,7 +378,8 @@ extern "C" int smla_gated_pool(const float* kv, const float* score, const float*
 // the `sim` quantisation), written in out_dtype to row r of `out` or, when cache_rows > 0, to row
 // pos of sequence r / rows_per_pos of a cache [.., cache_rows, d].  A position outside the rotation
 // table or the cache leaves the row unwritten.
-__global__ __launch_bounds__(512) void row_epilogue_kernel(const float* __restrict__ x, int d, int rows_per_pos,
+__global__ __launch_bounds__(512) void row_epilogue_kernel(const float* __restrict__ x, int d, int64_t ldx,
+                                                           int rows_per_pos,
                                                            const int32_t* __restrict__ pos,
                                                            const float* __restrict__ norm_w,
                                                            const float* __restrict__ cos_t,
@@ -393,7 +395,7 @@ __global__ __launch_bounds__(512) void row_epilogue_kernel(const float* __restri
   const int64_t p = pos ? (int64_t)pos[s] : 0;
   const bool ok = (rd == 0 || (p >= 0 && p < n_pos)) && (cache_rows == 0 || (p >= 0 && p < cache_rows));
   if (!ok) return;  // uniform over the workgroup
-  const float* xr = x + r * d;
+  const float* xr = x + r * ldx;
   pool_epilogue(xr[2 * t], xr[2 * t + 1], d, rd, eps, sim, norm_w, cos_t, sin_t, rd ? p : 0, red, xch, res);
   const int64_t orow = cache_rows > 0 ? s * cache_rows + p : r;
   if (out_dtype == SMLA_BF16)
@@ -435,15 +437,15 @@ __global__ __launch_bounds__(256) void decode_ids_kernel(const int32_t* __restri
 extern "C" int smla_ring_step(float* ring_kv, float* ring_sc, const float* kv_p, const float* score_p,
                               const int32_t* pos, const float* ape, const float* norm_w, const float* cos_t,
                               const float* sin_t, int64_t n_pos, int64_t B, int64_t d, int64_t ratio, int64_t rd,
-                              float eps, int sim, float* comp_cache, int64_t comp_cap, void* stream) {
+                              float eps, int sim, float* comp_cache, int64_t comp_cap, int64_t ld_p, void* stream) {
   if (!ring_kv || !ring_sc || !kv_p || !score_p || !pos || !ape || !norm_w || !cos_t || !sin_t || !comp_cache)
     return SMLA_E_NULL;
-  if (B <= 0 || comp_cap < 0 || n_pos <= 0) return SMLA_E_SHAPE;
+  if (B <= 0 || comp_cap < 0 || n_pos <= 0 || (ld_p != 0 && ld_p < 2 * d)) return SMLA_E_SHAPE;
   int rc = check_pool_dims(d, ratio, rd, sim);
   if (rc) return rc;
   hipLaunchKernelGGL(ring_step_kernel, dim3((unsigned)B), dim3((unsigned)(d / 2)), 0, (hipStream_t)stream, ring_kv,
                      ring_sc, kv_p, score_p, pos, ape, norm_w, cos_t, sin_t, n_pos, (int)d, (int)ratio, (int)rd,
-                     eps, sim, comp_cache, comp_cap);
+                     eps, sim, comp_cache, comp_cap, ld_p ? ld_p : 2 * d);
   SMLA_HIP_CHECK_LAUNCH();
   return SMLA_OK;
 }
@@ -465,13 +467,14 @@ extern "C" int smla_quant_fp8_pow2(const void* x, int x_dtype, int64_t rows, int
   return SMLA_OK;
 }
 
-extern "C" int smla_row_epilogue(const float* x, int64_t rows, int64_t d, int64_t rows_per_pos, const int32_t* pos,
+extern "C" int smla_row_epilogue(const float* x, int64_t rows, int64_t d, int64_t ldx, int64_t rows_per_pos,
+                                 const int32_t* pos,
                                  const float* norm_w, const float* cos_t, const float* sin_t, int64_t n_pos,
                                  int64_t rd, float eps, int sim, void* out, int out_dtype, int64_t cache_rows,
                                  void* stream) {
   if (!x || !out) return SMLA_E_NULL;
   if (rows <= 0 || d < 128 || d > 1024 || d % 64 != 0 || rows_per_pos <= 0 || rd < 0 || rd > d || rd % 2 != 0 ||
-      cache_rows < 0 || rows > (int64_t)INT32_MAX)
+      cache_rows < 0 || rows > (int64_t)INT32_MAX || (ldx != 0 && ldx < d))
     return SMLA_E_SHAPE;
   if (rd > 0 && (!pos || !cos_t || !sin_t || n_pos <= 0)) return SMLA_E_NULL;
   if (cache_rows > 0 && !pos) return SMLA_E_NULL;
@@ -480,7 +483,7 @@ extern "C" int smla_row_epilogue(const float* x, int64_t rows, int64_t d, int64_
   if (out_dtype != SMLA_F32 && out_dtype != SMLA_BF16) return SMLA_E_DTYPE;
   if (!(eps >= 0.f)) return SMLA_E_RANGE;
   hipLaunchKernelGGL(row_epilogue_kernel, dim3((unsigned)rows), dim3((unsigned)(d / 2)), 0, (hipStream_t)stream, x,
-                     (int)d, (int)rows_per_pos, pos, norm_w, cos_t, sin_t, n_pos, (int)rd, eps, sim, out, out_dtype,
+                     (int)d, ldx ? ldx : d, (int)rows_per_pos, pos, norm_w, cos_t, sin_t, n_pos, (int)rd, eps, sim, out, out_dtype,
                      cache_rows);
   SMLA_HIP_CHECK_LAUNCH();
   return SMLA_OK;

@@ -94,30 +94,35 @@ class DecodeLayer:
             self.comp = torch.zeros(B, 1, HEAD_DIM, dtype=torch.bfloat16, device=device)   # never addressed
         self.q_a_norm = w.q_a_norm.float().contiguous()
         self.kv_a_norm = w.kv_a_norm.float().contiguous()
+        # the projections of xn in one launch: [wq_a; wkv (; wkv_c; wgate_c)] concatenated once
+        parts = [w.wq_a, w.wkv] + ([w.wkv_c, w.wgate_c] if ratio else [])
+        self.w_in = torch.cat(parts, dim=0).contiguous()
+        self.cuts = [0]
+        for t in parts:
+            self.cuts.append(self.cuts[-1] + t.shape[0])
 
     # -- pieces (each mirrors one span of decode_engine.py) --------------------------------------
-    def q_path(self, xn, pos):
-        """``decode_engine.py:78-80``: q [B, 64, 512] bf16, per-head normed, rope dims rotated."""
-        w = self.w
-        qa = torch.empty(self.B, w.wq_a.shape[0], dtype=torch.bfloat16, device=xn.device)
-        ops.row_epilogue(_proj(xn, w.wq_a), self.q_a_norm, None, None, None, 0, _lib.SIM_NONE, qa)
-        q = torch.empty(self.B, N_HEADS, HEAD_DIM, dtype=torch.bfloat16, device=xn.device)
-        ops.row_epilogue(_proj(qa, w.wq_b).view(self.B * N_HEADS, HEAD_DIM), None, pos, self.cos_t, self.sin_t,
+    def q_path(self, qa_f, pos):
+        """``decode_engine.py:78-80``: q [B, 64, 512] bf16 from the q_down projection qa_f,
+        per-head normed, rope dims rotated."""
+        qa = torch.empty(self.B, qa_f.shape[1], dtype=torch.bfloat16, device=qa_f.device)
+        ops.row_epilogue(qa_f, self.q_a_norm, None, None, None, 0, _lib.SIM_NONE, qa)
+        q = torch.empty(self.B, N_HEADS, HEAD_DIM, dtype=torch.bfloat16, device=qa_f.device)
+        ops.row_epilogue(_proj(qa, self.w.wq_b).view(self.B * N_HEADS, HEAD_DIM), None, pos, self.cos_t, self.sin_t,
                          ROPE_HD, _lib.SIM_NONE, q, rows_per_pos=N_HEADS)
         return q
 
-    def kv_append(self, xn, pos):
-        """``decode_engine.py:81-84``: the token's kv row (RMSNorm, RoPE of the last 64 dims, fp8
-        round trip of the other 448) written as bf16 to window-cache row pos of each sequence."""
-        w = self.w
-        ops.row_epilogue(_proj(xn, w.wkv), self.kv_a_norm, pos, self.cos_t, self.sin_t, ROPE_HD, _lib.SIM_FP8,
-                         self.raw, cache_rows=self.max_pos)
+    def kv_append(self, kv_f, pos):
+        """``decode_engine.py:81-84``: the token's kv row from the kv_proj projection kv_f
+        (RMSNorm, RoPE of the last 64 dims, fp8 round trip of the other 448), written as bf16 to
+        window-cache row pos of each sequence."""
+        ops.row_epilogue(kv_f, self.kv_a_norm, pos, self.cos_t, self.sin_t, ROPE_HD, _lib.SIM_FP8, self.raw,
+                         cache_rows=self.max_pos)
 
-    def ring_step(self, xn, pos):
-        """``decode_engine.py:96-105``: ring update; an emitted row lands in the fp32 compressed
-        cache (its bf16 copy is made with the id list)."""
-        w = self.w
-        self.ring.step(_proj(xn, w.wkv_c), _proj(xn, w.wgate_c), pos, self.comp32)
+    def ring_step(self, kvp, scp, pos):
+        """``decode_engine.py:96-105``: ring update from the compressor projections; an emitted
+        row lands in the fp32 compressed cache (its bf16 copy is made with the id list)."""
+        self.ring.step(kvp, scp, pos, self.comp32)
 
     def index_list(self, pos, scores=None, k=2048):
         """``decode_engine.py:110-114``: [B, 128 + n] int32 ids into [window cache; compressed
@@ -141,10 +146,12 @@ class DecodeLayer:
         if xn.shape != (self.B, self.w.wq_a.shape[1]):
             raise ValueError(f"xn must be [{self.B}, {self.w.wq_a.shape[1]}]")
         pos = pos.to(torch.int32).contiguous()
-        q = self.q_path(xn, pos)
-        self.kv_append(xn, pos)
+        y = _proj(xn, self.w_in)                     # [B, sum of the projection widths] fp32
+        c = self.cuts
+        q = self.q_path(y[:, c[0]:c[1]], pos)
+        self.kv_append(y[:, c[1]:c[2]], pos)
         if self.ratio:
-            self.ring_step(xn, pos)
+            self.ring_step(y[:, c[2]:c[3]], y[:, c[3]:c[4]], pos)
         ids = self.index_list(pos, scores, k)
         o = _sa.sparse_attn_two_source(q[:, None], self.raw, self.comp, self.w.sinks.float(), ids[:, None],
                                        HEAD_DIM ** -0.5, dv=HEAD_DIM)

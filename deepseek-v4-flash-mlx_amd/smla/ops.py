@@ -180,12 +180,17 @@ def ring_step_op(ring_kv: torch.Tensor, ring_sc: torch.Tensor, kv_p: torch.Tenso
             raise ValueError("ring and cache tensors must be contiguous fp32")
     B = ring_kv.shape[0]
     d = ring_kv.shape[-1] // 2
-    kv_p, score_p = kv_p.float().contiguous(), score_p.float().contiguous()
+    # row-strided fp32 views (slices of one wider projection) pass as they are; anything else is packed
+    strided = (kv_p.dtype == score_p.dtype == torch.float32 and kv_p.dim() == score_p.dim() == 2
+               and kv_p.stride(1) == score_p.stride(1) == 1 and kv_p.stride(0) == score_p.stride(0))
+    if not strided:
+        kv_p, score_p = kv_p.float().contiguous(), score_p.float().contiguous()
+    ld = kv_p.stride(0) if kv_p.dim() == 2 else 0
     pos = pos.to(torch.int32).contiguous()
     _lib.call("smla_ring_step", _p(ring_kv), _p(ring_sc), _p(kv_p), _p(score_p), _p(pos),
               _p(ape.float().contiguous()), _p(norm_w.float().contiguous()), _p(cos_t.float().contiguous()),
               _p(sin_t.float().contiguous()), cos_t.shape[0], B, d, ratio, rope_head_dim, float(eps),
-              int(sim), _p(comp_cache), comp_cache.shape[1], _stream(ring_kv))
+              int(sim), _p(comp_cache), comp_cache.shape[1], ld, _stream(ring_kv))
 
 
 @ring_step_op.register_fake
@@ -349,12 +354,15 @@ def row_epilogue(x, norm_w, pos, cos_t, sin_t, rd, sim, out, rows_per_pos=1, cac
     (bf16 or fp32): row r of out [rows, d], or with cache_rows > 0 row pos of sequence
     r // rows_per_pos of a cache [.., cache_rows, d].  Stream-ordered; returns out."""
     _on_gpu(x, out, *(t for t in (norm_w, pos, cos_t, sin_t) if t is not None))
-    if x.dtype != torch.float32 or not x.is_contiguous() or not out.is_contiguous():
-        raise ValueError("row_epilogue: x must be contiguous fp32 and out contiguous")
+    if x.dtype != torch.float32 or x.stride(-1) != 1 or not out.is_contiguous():
+        raise ValueError("row_epilogue: x must be fp32 with unit column stride and out contiguous")
+    if x.dim() != 2:
+        x = x.reshape(-1, x.shape[-1])
     d = x.shape[-1]
-    rows = x.numel() // d
+    rows = x.shape[0]
+    ldx = x.stride(0)
     n_pos = cos_t.shape[0] if cos_t is not None else 0
-    _lib.call("smla_row_epilogue", _p(x), rows, d, rows_per_pos, _p(pos), _p(norm_w), _p(cos_t), _p(sin_t),
+    _lib.call("smla_row_epilogue", _p(x), rows, d, ldx, rows_per_pos, _p(pos), _p(norm_w), _p(cos_t), _p(sin_t),
               n_pos, rd, float(eps), int(sim), _p(out), dtype_code(out), cache_rows, _stream(x))
     return out
 

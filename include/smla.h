@@ -199,7 +199,8 @@ int smla_gated_pool(const float* kv, const float* score, const float* ape, const
 
 /* smla_ring_step: one decode token of the compressor ring (oracle/decode_engine.py:96-105) for
  * B sequences at positions pos[b]:
- *   ring_kv, ring_sc [B, 2*ratio, 2d] fp32 (updated);  kv_p, score_p [B, 2d] fp32 projections;
+ *   ring_kv, ring_sc [B, 2*ratio, 2d] fp32 (updated);  kv_p, score_p: B rows of 2d fp32
+ *   projections, ld_p elements apart (0: 2d);
  *   when (pos+1) % ratio == 0 the ring emits a row (softmax pool, RMSNorm(norm_w), RoPE with
  *   cos/sin [n_pos, rd/2] at position pos+1-ratio, then the `sim` quantisation, SMLA_SIM_*)
  *   written to comp_cache[b, (pos+1)/ratio - 1, :] ([B, comp_cap, d] fp32), then
@@ -209,7 +210,7 @@ int smla_ring_step(float* ring_kv, float* ring_sc, const float* kv_p, const floa
                    const int32_t* pos, const float* ape, const float* norm_w,
                    const float* cos_t, const float* sin_t, int64_t n_pos, int64_t B, int64_t d,
                    int64_t ratio, int64_t rd, float eps, int sim, float* comp_cache,
-                   int64_t comp_cap, void* stream);
+                   int64_t comp_cap, int64_t ld_p, void* stream);
 
 /* smla_row_epilogue: the per-row work of oracle/decode_engine.py:78-83 on rows the caller has
  * projected.  x [rows, d] fp32 (128 <= d <= 1024, d % 64 == 0) -> RMSNorm with norm_w [d]
@@ -219,8 +220,9 @@ int smla_ring_step(float* ring_kv, float* ring_sc, const float* kv_p, const floa
  * d-rd other channels fp8 round-tripped, v4mlx/compressor.py:11-20).  Row r goes to row r of out
  * [rows, d] (SMLA_F32 / SMLA_BF16), or, with cache_rows > 0, to row pos of sequence r / rows_per_pos
  * of a cache [.., cache_rows, d] (the window append, decode_engine.py:84).  eps: the RMSNorm eps.
- * A row whose position lies outside [0, n_pos) (when rd > 0) or [0, cache_rows) is not written. */
-int smla_row_epilogue(const float* x, int64_t rows, int64_t d, int64_t rows_per_pos, const int32_t* pos,
+ * ldx: elements between consecutive input rows (0: d).  A row whose position lies outside
+ * [0, n_pos) (when rd > 0) or [0, cache_rows) is not written. */
+int smla_row_epilogue(const float* x, int64_t rows, int64_t d, int64_t ldx, int64_t rows_per_pos, const int32_t* pos,
                       const float* norm_w, const float* cos_t, const float* sin_t, int64_t n_pos,
                       int64_t rd, float eps, int sim, void* out, int out_dtype, int64_t cache_rows,
                       void* stream);

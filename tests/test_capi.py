@@ -83,15 +83,16 @@ def test_host_validation_rejects_bad_arguments():
     assert lib.smla_window_topk_idxs(0, 1, 1, 0, fake, None) == -2
     assert lib.smla_decode_window_idxs(fake, 2, 128, fake, 64, None) == -2
     # row_epilogue: NULL, row width, rope without tables, sim, fp8 block, dtype, eps
-    assert lib.smla_row_epilogue(None, 2, 512, 1, None, None, None, None, 0, 0, 1e-6, 0, fake, 0, 0, None) == -1
-    assert lib.smla_row_epilogue(fake, 2, 96, 1, None, None, None, None, 0, 0, 1e-6, 0, fake, 0, 0, None) == -2
-    assert lib.smla_row_epilogue(fake, 2, 2048, 1, None, None, None, None, 0, 0, 1e-6, 0, fake, 0, 0, None) == -2
-    assert lib.smla_row_epilogue(fake, 2, 512, 1, None, None, None, None, 0, 64, 1e-6, 0, fake, 0, 0, None) == -1
-    assert lib.smla_row_epilogue(fake, 2, 512, 1, None, None, None, None, 0, 0, 1e-6, 2, fake, 0, 0, None) == -4
-    assert lib.smla_row_epilogue(fake, 2, 512, 1, fake, None, fake, fake, 8, 32, 1e-6, 1, fake, 0, 0, None) == -2
-    assert lib.smla_row_epilogue(fake, 2, 512, 1, None, None, None, None, 0, 0, 1e-6, 0, fake, 9, 0, None) == -3
-    assert lib.smla_row_epilogue(fake, 2, 512, 1, None, None, None, None, 0, 0, -1.0, 0, fake, 0, 0, None) == -6
-    assert lib.smla_row_epilogue(fake, 2, 512, 1, None, None, None, None, 0, 0, 1e-6, 0, fake, 0, 16, None) == -1
+    assert lib.smla_row_epilogue(None, 2, 512, 0, 1, None, None, None, None, 0, 0, 1e-6, 0, fake, 0, 0, None) == -1
+    assert lib.smla_row_epilogue(fake, 2, 512, 256, 1, None, None, None, None, 0, 0, 1e-6, 0, fake, 0, 0, None) == -2
+    assert lib.smla_row_epilogue(fake, 2, 96, 0, 1, None, None, None, None, 0, 0, 1e-6, 0, fake, 0, 0, None) == -2
+    assert lib.smla_row_epilogue(fake, 2, 2048, 0, 1, None, None, None, None, 0, 0, 1e-6, 0, fake, 0, 0, None) == -2
+    assert lib.smla_row_epilogue(fake, 2, 512, 0, 1, None, None, None, None, 0, 64, 1e-6, 0, fake, 0, 0, None) == -1
+    assert lib.smla_row_epilogue(fake, 2, 512, 0, 1, None, None, None, None, 0, 0, 1e-6, 2, fake, 0, 0, None) == -4
+    assert lib.smla_row_epilogue(fake, 2, 512, 0, 1, fake, None, fake, fake, 8, 32, 1e-6, 1, fake, 0, 0, None) == -2
+    assert lib.smla_row_epilogue(fake, 2, 512, 0, 1, None, None, None, None, 0, 0, 1e-6, 0, fake, 9, 0, None) == -3
+    assert lib.smla_row_epilogue(fake, 2, 512, 0, 1, None, None, None, None, 0, 0, -1.0, 0, fake, 0, 0, None) == -6
+    assert lib.smla_row_epilogue(fake, 2, 512, 0, 1, None, None, None, None, 0, 0, 1e-6, 0, fake, 0, 16, None) == -1
     # decode_ids: NULL, T < window, only one of the compressed-row buffers, copy without ratio
     assert lib.smla_decode_ids(None, 2, 128, 4, 512, 16, fake, 144, None, None, 0, None) == -1
     assert lib.smla_decode_ids(fake, 2, 128, 4, 512, 16, fake, 100, None, None, 0, None) == -2
