@@ -595,14 +595,7 @@ hipEvent_t g_ev_before = nullptr, g_ev_after = nullptr;  // profiling: bracket t
 bool g_main_only = false;  // profiling: launch the split kernel alone (partials, no merge)
 int g_decode_kernel = 0;   // bf16 rows: 0 = role-split score/value waves, 1 = 64-head lockstep tiles
 
-int num_cus() {
-  static int n = 0;
-  if (n == 0) {
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
-  }
-  return n;
-}
+int num_cus() { return smla_num_cus(); }
 
 Plan make_plan(int64_t B, int64_t S, int64_t H, int64_t D, int64_t DV, int64_t T, int q_dtype,
                int kv_dtype) {

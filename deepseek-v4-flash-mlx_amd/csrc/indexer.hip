@@ -321,19 +321,6 @@ __global__ __launch_bounds__(256) void indexer_wide_kernel(const void* __restric
   scores[bs * N + n] = kscale ? acc * kscale[row] : acc;
 }
 
-// compute units of the current device (queried once per device id)
-int indexer_cus() {
-  static std::atomic<int> cache[64];
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  int n = cache[dev].load(std::memory_order_relaxed);
-  if (n <= 0) {
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
-    cache[dev].store(n, std::memory_order_relaxed);
-  }
-  return n;
-}
-
 template <int DI, int KDT>
 int launch_k(const void* q, int q_dtype, const void* keys, const float* kscale, const float* w,
              const int32_t* nvis, int64_t B, int64_t S, int64_t Hi, int64_t N, float* scores, hipStream_t st) {
@@ -341,7 +328,7 @@ int launch_k(const void* q, int q_dtype, const void* keys, const float* kscale, 
     const dim3 grid((unsigned)((N + 127) / 128), (unsigned)(B * S));
     // two keys per lane halve the q reads per fma; when that leaves CUs idle (one long sequence),
     // one key per lane doubles the workgroups
-    const bool one = (int64_t)grid.x * grid.y < indexer_cus();
+    const bool one = (int64_t)grid.x * grid.y < smla_num_cus();
     const dim3 grid1((unsigned)((N + 63) / 64), (unsigned)(B * S));
     if (q_dtype == SMLA_BF16 && one)
       hipLaunchKernelGGL((indexer2_kernel<KDT, SMLA_BF16, 1, 16>), grid1, dim3(256), 0, st, q, keys, kscale, w, nvis, S,

@@ -237,6 +237,19 @@ int launch_indexer_cert(const uint16_t* q, const uint8_t* keys, const float* ksc
     if (_e != hipSuccess) return (int)_e;               \
   } while (0)
 
+// Compute units of the current device, queried once per device id (256 if the query fails).
+inline int smla_num_cus() {
+  static std::atomic<int> cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  int n = cache[dev].load(std::memory_order_relaxed);
+  if (n <= 0) {
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cache[dev].store(n, std::memory_order_relaxed);
+  }
+  return n;
+}
+
 // Raises a kernel's dynamic LDS limit on the current device, once per device: `done` holds one bit
 // per device id (ids from 64 up set the attribute on every call).  Safe to call from several host
 // threads; a lost race only repeats the call.
