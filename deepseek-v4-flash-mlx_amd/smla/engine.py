@@ -17,8 +17,8 @@ Per token at position p, for each of B sequences:
 * o = sparse_attn(q, [window; compressed], sinks, ids, 512^-0.5), the inverse RoPE on o's last
   64 dims, then ``o_grouped`` (``:115-119``).
 
-RoPE tables: ratio-4 layers use YaRN (base 160000, factor 16 over 65536 positions), ratio-0
-layers plain base 10000 (``decode_engine.py:47,73``).  Every step runs on the HIP kernels:
+RoPE tables: layers with a nonzero ratio (4 or 128) use YaRN (base 160000, factor 16 over 65536
+positions), ratio-0 layers plain base 10000 (``decode_engine.py:47,73``).  Every step runs on the HIP kernels:
 ``smla_linear`` (projections, fp32 results), ``smla_row_epilogue`` (the norms, RoPE, the fp8 round
 trip and the window-cache write), ``smla_ring_step``, ``smla_decode_ids``, ``smla_sparse_attn`` and
 ``smla_o_proj``.  Caches are device-resident and owned by the layer object.
@@ -70,22 +70,25 @@ def _proj(x, W):
 class DecodeLayer:
     """Decode state and step of one attention layer for B sequences.
 
-    ``ratio`` is the layer's compression ratio (4: compressed rows and the ring; 0: window only).
+    ``ratio`` is the layer's compression ratio (``decode_engine.py:17``): 4 runs the compressor ring
+    and attends to the compressed rows; 0 and 128 attend to the window only (128 with the YaRN
+    tables, as every nonzero ratio).
     ``max_pos`` bounds the positions (window cache rows); the compressed cache holds
     max_pos // 4 rows.  ``step`` advances every sequence by one token.
     """
 
     def __init__(self, w: LayerWeights, B: int, ratio: int, max_pos: int = 65536, device="cuda"):
-        if ratio not in (0, 4):
-            raise ValueError("ratio must be 0 or 4")
+        if ratio not in (0, 4, 128):
+            raise ValueError("ratio must be 0, 4 or 128")
         if ratio == 4 and any(t is None for t in (w.wkv_c, w.wgate_c, w.ape, w.norm_c)):
             raise ValueError("a ratio-4 layer needs the compressor weights")
         ops._on_gpu(w.wq_a, w.wq_b, w.wkv, w.wo_a, w.wo_b)
         self.w, self.B, self.ratio, self.max_pos = w, B, ratio, max_pos
         self.cos_t, self.sin_t = _nr.rope_tables(ROPE_HD, max_pos, *(_YARN if ratio else _PLAIN), device=device)
         self.raw = torch.zeros(B, max_pos, HEAD_DIM, dtype=torch.bfloat16, device=device)
-        self.ncap = max_pos // 4 if ratio else 0
-        if ratio:
+        self.ring_ratio = 4 if ratio == 4 else 0  # only ratio-4 layers run the ring (decode_engine.py:86)
+        self.ncap = max_pos // 4 if self.ring_ratio else 0
+        if self.ring_ratio:
             self.comp32 = torch.zeros(B, self.ncap, HEAD_DIM, device=device)      # the ring writes fp32 rows
             self.comp = torch.zeros(B, self.ncap, HEAD_DIM, dtype=torch.bfloat16, device=device)
             self.ring = _comp.Ring(B, HEAD_DIM, w.ape, w.norm_c, ratio=4, rope_head_dim=ROPE_HD,
@@ -95,7 +98,7 @@ class DecodeLayer:
         self.q_a_norm = w.q_a_norm.float().contiguous()
         self.kv_a_norm = w.kv_a_norm.float().contiguous()
         # the projections of xn in one launch: [wq_a; wkv (; wkv_c; wgate_c)] concatenated once
-        parts = [w.wq_a, w.wkv] + ([w.wkv_c, w.wgate_c] if ratio else [])
+        parts = [w.wq_a, w.wkv] + ([w.wkv_c, w.wgate_c] if self.ring_ratio else [])
         self.w_in = torch.cat(parts, dim=0).contiguous()
         self.cuts = [0]
         for t in parts:
@@ -129,10 +132,11 @@ class DecodeLayer:
         cache] (compressed ids offset by max_pos), -1 padded.  Take-all over the visible compressed
         rows, or, with indexer scores [B, ncap] supplied, the top-k of them.  Also copies a row the
         ring emitted at this step to the bf16 compressed cache."""
-        comp = (self.comp32, self.comp) if self.ratio else (None, None)
-        take_all = scores is None or not self.ratio
+        comp = (self.comp32, self.comp) if self.ring_ratio else (None, None)
+        take_all = scores is None or not self.ring_ratio
         T = WINDOW + (self.ncap if take_all else 0)
-        ids = ops.decode_ids(pos, WINDOW, self.ratio, self.max_pos, self.ncap, T, comp32=comp[0], comp_out=comp[1])
+        ids = ops.decode_ids(pos, WINDOW, self.ring_ratio, self.max_pos, self.ncap, T, comp32=comp[0],
+                             comp_out=comp[1])
         if take_all:
             return ids
         return _idx.select_decode_indices(scores, k, pos, WINDOW, self.max_pos)
@@ -150,7 +154,7 @@ class DecodeLayer:
         c = self.cuts
         q = self.q_path(y[:, c[0]:c[1]], pos)
         self.kv_append(y[:, c[1]:c[2]], pos)
-        if self.ratio:
+        if self.ring_ratio:
             self.ring_step(y[:, c[2]:c[3]], y[:, c[3]:c[4]], pos)
         ids = self.index_list(pos, scores, k)
         o = _sa.sparse_attn_two_source(q[:, None], self.raw, self.comp, self.w.sinks.float(), ids[:, None],

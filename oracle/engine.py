@@ -4,8 +4,9 @@ Restates ``oracle/decode_engine.py:73-119`` (``layer_fwd``'s decode branch for o
 position p, from the attention-normed input xn to ``o_grouped``; ``hc_pre`` / ``hc_post`` are
 outside the path), composed from the oracle's own pieces:
 
-* RoPE tables by layer ratio (``:47,73``): ratio 4 -> YaRN (original 65536, base 160000, factor
-  16, beta 32/1), ratio 0 -> plain base 10000 (original_seq_len 0);
+* RoPE tables by layer ratio (``:47,73``): a nonzero ratio (4 or 128) -> YaRN (original 65536,
+  base 160000, factor 16, beta 32/1), ratio 0 -> plain base 10000 (original_seq_len 0); only
+  ratio-4 layers run the compressor and see compressed rows (``:86,112``);
 * q (``:78-80``): q_down, RMSNorm(q_a_norm), q_up to [64, 512], the weightless per-head RMS norm
   (``v4mlx/mla.py:26-28``), RoPE at p on each head's last 64 dims;
 * kv (``:81-84``): kv_proj, RMSNorm(kv_a_norm), RoPE at p on the last 64 dims, the fp8 round

@@ -43,7 +43,7 @@ def _check_row(got, ref, tol, what):
     assert n <= 4e-2, f"{what}: fp8 dims rel err {n:.3e}"
 
 
-@pytest.mark.parametrize("ratio,steps", [(4, 136), (0, 24)])
+@pytest.mark.parametrize("ratio,steps", [(4, 136), (0, 24), (128, 24)])
 def test_decode_layer_vs_oracle(dev, ratio, steps):
     from smla import engine
     announce(f"decode layer ratio={ratio} steps={steps}")

@@ -30,7 +30,7 @@ def _weights(seed, dim=256, q_lora=128, rank=32, dim_out=192, ratio=4):
     return w, g
 
 
-@pytest.mark.parametrize("ratio", [4, 0])
+@pytest.mark.parametrize("ratio", [4, 0, 128])
 def test_schedule_and_ids(ratio):
     w, g = _weights(1, ratio=ratio)
     st = oe.LayerState(ratio, max_pos=512)
@@ -88,3 +88,13 @@ def test_window_row_rotated_at_its_position():
             c0, s0 = st.cos[p - 1].double(), st.sin[p - 1].double()
             wrong = torch.stack([a * c0 - b * s0, a * s0 + b * c0], dim=-1).reshape(64)
             assert not torch.allclose(v[-64:].double(), wrong, rtol=1e-3, atol=1e-4)
+
+
+def test_rope_tables_by_ratio():
+    """decode_engine.py:47,73: every nonzero ratio (4 and 128) rotates with the YaRN tables, ratio 0
+    with the plain base-10000 ones; the two differ."""
+    yc, _ = onr.rope_cos_sin(64, 256, *oe.YARN)
+    pc, _ = onr.rope_cos_sin(64, 256, *oe.PLAIN)
+    assert not torch.allclose(yc, pc)
+    for ratio, ref in ((4, yc), (128, yc), (0, pc)):
+        assert torch.equal(oe.LayerState(ratio, max_pos=256).cos, ref)
