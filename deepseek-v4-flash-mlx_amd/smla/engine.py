@@ -72,7 +72,7 @@ class DecodeLayer:
 
     ``ratio`` is the layer's compression ratio (``decode_engine.py:17``): 4 runs the compressor ring
     and attends to the compressed rows; 0 and 128 attend to the window only (128 with the YaRN
-    tables, as every nonzero ratio).
+    tables, as every nonzero ratio: ``oracle/v4_fast.py:42-43``).
     ``max_pos`` bounds the positions (window cache rows); the compressed cache holds
     max_pos // 4 rows.  ``step`` advances every sequence by one token.
     """
