@@ -175,24 +175,28 @@ __global__ __launch_bounds__(768) void attn_decode_kernel(
 
   // ---- row ids -> LDS (-1: masked, out of range or past the split), whole tiles; the tiles
   // past the last live id are dropped (index lists padded with -1 at the end cost nothing)
+  // The score waves load the table: they issue no row copies, so their id loads do not queue
+  // behind the Q rows' copies (vmcnt counts in order), and the barriers below wait for LDS only.
   int last = -1;
-  for (int t = tid; t < ntiles_all * kTileRows; t += G::NW * 64) {
-    int r = -1;
-    if (t < nrows) {
-      r = ig[t];
-      r = (r >= 0 && r < ntot) ? r : -1;
+  if (scorer) {
+    for (int t = tid; t < ntiles_all * kTileRows; t += 4 * 64) {
+      int r = -1;
+      if (t < nrows) {
+        r = ig[t];
+        r = (r >= 0 && r < ntot) ? r : -1;
+      }
+      ids_s[t] = r;
+      if (r >= 0) last = t;
     }
-    ids_s[t] = r;
-    if (r >= 0) last = t;
   }
   {
     const float wl = wave_max_dpp((float)last);
     if (lane == 0) al_s[wave] = wl;  // (the rescale buffer is free until iteration 0)
   }
-  __syncthreads();
+  lds_barrier();
   const int last_live = (int)wave_max_dpp(lane < G::NW ? al_s[lane] : -1.f);
   const int ntiles = (last_live + kTileRows) / kTileRows;
-  __syncthreads();  // al_s reads done before any later use
+  lds_barrier();  // al_s reads done before any later use
 
   auto issue_tile = [&](int tl) {
     if constexpr (!FP8) {
