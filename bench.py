@@ -370,7 +370,7 @@ def main():
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world > 1:
         print(json.dumps({"error": "this build measures one GPU; --gpus must be 1 "
-                                   "(the multi-GPU sharding is described in DESIGN.md, not run)"}))
+                                   "(sharding across GPUs is designed, not run)"}))
         sys.exit(2)
 
     import numpy as np
