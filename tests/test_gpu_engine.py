@@ -81,3 +81,39 @@ def test_decode_layer_rejects_cpu_and_bad_ratio(dev):
                            device=dev)
     with pytest.raises(Exception):
         engine.DecodeLayer(engine.LayerWeights(**t), 1, ratio=0, max_pos=64, device=dev)   # CPU weights
+
+
+def test_decode_layer_graph_replays(dev):
+    """One decode step captured in a HIP graph and replayed token by token (new xn and pos copied
+    into the captured inputs, eager work and synchronisations between replays) tracks an identical
+    layer stepped eagerly, bit for bit, cache and ring state included."""
+    from smla import engine
+    announce("decode layer graph replays")
+    t = _make_weights(4, seed=9)
+    w = engine.LayerWeights(**{k: v.to(dev) for k, v in t.items()})
+    B, max_pos = 2, 64
+    eager = engine.DecodeLayer(w, B, 4, max_pos=max_pos, device=dev)
+    graphed = engine.DecodeLayer(w, B, 4, max_pos=max_pos, device=dev)
+    g = torch.Generator().manual_seed(3)
+    xs = [torch.randn(B, 4096, generator=g).to(torch.bfloat16).to(dev) for _ in range(12)]
+    # positions 0..3 eagerly on both, so the captured step starts from a warm state
+    for p in range(4):
+        pos = torch.full((B,), p, dtype=torch.int32, device=dev)
+        eager.step(xs[p], pos)
+        graphed.step(xs[p], pos)
+    x_in = xs[4].clone()
+    pos_in = torch.full((B,), 4, dtype=torch.int32, device=dev)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        y_out = graphed.step(x_in, pos_in)
+    # the capture itself ran nothing: step 4 is the first replay
+    for p in range(4, 12):
+        x_in.copy_(xs[p])
+        pos_in.fill_(p)
+        graph.replay()
+        torch.cuda.synchronize()
+        y_ref = eager.step(xs[p], torch.full((B,), p, dtype=torch.int32, device=dev))
+        torch.cuda.synchronize()
+        assert torch.equal(y_out, y_ref), f"replay at position {p}"
+    assert torch.equal(graphed.raw, eager.raw) and torch.equal(graphed.comp32, eager.comp32)
