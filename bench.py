@@ -39,7 +39,7 @@ def algorithmic_attention_bytes(B, H, T, D=576, DV=512, row_bytes=1152):
 
 BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
 
-KERNEL_NAMES = {0: "attn_decode_kernel<576>", 1: "attn_decode_bf16_kernel<576>"}
+KERNEL_NAME = "attn_decode_kernel<576>"
 
 
 def measured_traffic(kernel, workload="decode_32k"):
@@ -65,10 +65,8 @@ def parse():
     ap.add_argument("--kernel-iters", type=int, default=96)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-steps", type=int, default=3)
-    ap.add_argument("--decode-kernel", type=int, default=0,
-                    help="bf16-row decode kernel: 0 = role-split score/value waves (default), 1 = 64-head lockstep tiles")
-    ap.add_argument("--target-wgs", type=int, default=0,
-                    help="attention split plan: target workgroups (0 = one per CU)")
+    ap.add_argument("--rows-per-split", type=int, default=0,
+                    help="attention split plan: index-list rows per split, a multiple of 32 (0 = the default plan)")
     ap.add_argument("--no-prefill", action="store_true", help="skip the prefill MFMA-utilisation leg")
     ap.add_argument("--prefill-reps", type=int, default=5)
     ap.add_argument("--no-others", action="store_true", help="skip the other workloads and kernels")
@@ -384,8 +382,6 @@ def main():
     from smla import workloads as wl
 
     smla.load()
-    _lib.lib().smla_set_attn_decode_kernel(args.decode_kernel)
-    _lib.lib().smla_set_attn_target_wgs(args.target_wgs)
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     print("[bench] generating decode_32k inputs", file=sys.stderr, flush=True)
@@ -415,7 +411,8 @@ def main():
         raw, comp, keys, ks = copies[r]
         sc = sidx.indexer_score(qi, keys, ks, wt)
         idx = sidx.select_decode_indices(sc[:, 0], k, pos, win, n_raw)
-        return ssa.sparse_attn_two_source(q, raw, comp, None, idx[:, None, :], w["scale"], dv=512)
+        return ops.sparse_attn_ex(q, raw, comp, None, None, None, idx[:, None, :], w["scale"], 512,
+                                  rows_per_split=args.rows_per_split)
 
     ref_out = step(0)
     torch.cuda.synchronize()
@@ -429,9 +426,12 @@ def main():
     torch.cuda.current_stream().wait_stream(s)
     torch.cuda.synchronize()
     graphs = {}
+    timing = [False]
 
     def graph_for(nsteps):
         if nsteps not in graphs:
+            if timing[0]:
+                raise RuntimeError(f"graph of {nsteps} steps was not captured before the timed region")
             g = torch.cuda.CUDAGraph()
             with torch.cuda.graph(g):
                 outs = [step(r) for r in range(nsteps)]
@@ -445,6 +445,11 @@ def main():
         if tail:
             graph_for(tail)[0].replay()
 
+    # every graph the warm-up and the timed steps replay is captured here, outside the timed region
+    for n in (args.rot, args.warmup % args.rot, args.steps % args.rot):
+        if n:
+            graph_for(n)
+    torch.cuda.synchronize()
     g_full, outs = graph_for(args.rot)
     # every replay must reproduce the eager result (copies hold identical data)
     for rep in range(2):
@@ -459,35 +464,42 @@ def main():
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
+    timing[0] = True
     e0.record()
     run_steps(args.steps)
     e1.record()
     torch.cuda.synchronize()
+    timing[0] = False
     ms = e0.elapsed_time(e1)
     ms_per_step = ms / args.steps
     tok_s = B * args.steps / (ms / 1000.0)
     print(f"[bench] {args.steps} steps in {ms:.3f} ms", file=sys.stderr, flush=True)
 
     # ---- dominant kernel: MFMA attention, events around the kernel alone (eager, rotated copies)
-    lib = _lib.lib()
-    ns, rps = _lib.ctypes.c_int(0), _lib.ctypes.c_int(0)
-    lib.smla_attn_plan(B, 1, H, 576, 512, T, _lib.BF16, _lib.BF16, _lib.ctypes.byref(ns), _lib.ctypes.byref(rps))
+    ns, rps, _ = ops.attn_plan(B, 1, H, 576, 512, T, rows_per_split=args.rows_per_split)
     idx_all = []
     for r in range(args.rot):
         raw, comp, keys, ks = copies[r]
         idx_all.append(sidx.index_decode(qi, keys, ks, wt, None, k, pos, win, n_raw, workspace=ws))
     torch.cuda.synchronize()
-    # the split kernel alone: a graph of `rot` launches (one per cache copy, main kernel only), replayed
-    # back to back between two events on the replay stream
-    lib.smla_profile_set_attn_main_only(1)
-    try:
-        gk = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(gk):
-            for r in range(args.rot):
-                ssa.sparse_attn_two_source(q, copies[r][0], copies[r][1], None, idx_all[r][:, None, :], w["scale"],
-                                           dv=512)
-    finally:
-        lib.smla_profile_set_attn_main_only(0)
+    # the split kernel alone (phase SMLA_ATTN_SPLIT): a graph of `rot` launches, one per cache copy, on
+    # preallocated outputs and workspaces, replayed back to back between two events on the replay stream
+    _, _, wsb = ops.attn_plan(B, 1, H, 576, 512, T, rows_per_split=args.rows_per_split)
+    k_out = [torch.empty(B, 1, H, 512, dtype=torch.bfloat16, device=dev) for _ in range(args.rot)]
+    k_ws = [torch.empty(max(wsb, 1), dtype=torch.uint8, device=dev) for _ in range(args.rot)]
+
+    def split_only(r):
+        ops.sparse_attn_ex(q, copies[r][0], copies[r][1], None, None, None, idx_all[r][:, None, :], w["scale"], 512,
+                           rows_per_split=args.rows_per_split, phases=_lib.ATTN_SPLIT, out=k_out[r],
+                           workspace=k_ws[r])
+
+    for r in range(args.rot):
+        split_only(r)
+    torch.cuda.synchronize()
+    gk = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(gk):
+        for r in range(args.rot):
+            split_only(r)
     gk.replay()
     torch.cuda.synchronize()
     reps = max(1, args.kernel_iters // args.rot)
@@ -503,7 +515,8 @@ def main():
     full_ev[0].record()
     for i in range(args.kernel_iters):
         r = i % args.rot
-        ssa.sparse_attn_two_source(q, copies[r][0], copies[r][1], None, idx_all[r][:, None, :], w["scale"], dv=512)
+        ops.sparse_attn_ex(q, copies[r][0], copies[r][1], None, None, None, idx_all[r][:, None, :], w["scale"], 512,
+                           rows_per_split=args.rows_per_split, out=k_out[r], workspace=k_ws[r])
     full_ev[1].record()
     torch.cuda.synchronize()
     attn_op_us = 1000.0 * full_ev[0].elapsed_time(full_ev[1]) / args.kernel_iters
@@ -511,10 +524,10 @@ def main():
     alg_bytes = algorithmic_attention_bytes(B, H, T)
     achieved = alg_bytes / (k_us * 1e-6) / 1e9
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(KERNEL_NAMES[args.decode_kernel]),
+                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(KERNEL_NAME),
                 "traffic_source": "profiles/decode_32k_hbm_counters.md (rocprofv3 --pmc, copy-calibrated)",
-                "kernel": KERNEL_NAMES[args.decode_kernel], "kernel_us": round(k_us, 3),
-                "algorithmic_bytes": alg_bytes, "nsplit": ns.value, "rows_per_split": rps.value}
+                "kernel": KERNEL_NAME, "kernel_us": round(k_us, 3),
+                "algorithmic_bytes": alg_bytes, "nsplit": ns, "rows_per_split": rps}
 
     prefill = None
     if not args.no_prefill:
@@ -529,7 +542,6 @@ def main():
     cpu = None
     if not args.no_cpu_baseline:
         ncores = len(os.sched_getaffinity(0))
-        ncores = min(ncores, 16)
         print(f"[bench] cpu baseline on {ncores} threads", file=sys.stderr, flush=True)
         med = cpu_baseline(w, ncores, args.cpu_steps)
         cpu = {"value": round(B / med, 2), "unit": "tok/s", "cores": ncores, "kind": "port",

@@ -17,23 +17,15 @@ struct RowSrc {
   int64_t n0, n1;
 };
 
-// bf16 rows, D in {576, 512}, DV = 512, H % 16 == 0.  Writes partial states (nsplit > 1) or the
-// final output (nsplit == 1).  Returns SMLA_OK or a hipError_t.
-int launch_decode_bf16(int D, int nsplit, int rows_per_split, const void* q, RowSrc src, const float* sink,
-                       const int32_t* idx, int64_t T, int64_t B, int64_t S, int64_t H, float scale, void* out,
-                       int out_dtype, float* part, hipStream_t stream, hipEvent_t ev_before, hipEvent_t ev_after);
-
 // bf16 or fp8 (e4m3 + per-64 pow2 scales) rows, D in {576, 512}, DV = 512, H % 16 == 0: 12-wave
-// role-split kernel (4 score waves, 8 value waves, 64 heads per workgroup).  Same partial-state
-// layout as launch_decode_bf16.
+// role-split kernel (4 score waves, 8 value waves, 64 heads per workgroup).  Writes the final
+// output (nsplit == 1) or partial states: (m, l) fp32 per (query row, split, head), then the partial
+// O rows (bf16 for bf16 output, else fp32) after all (m, l) records, split-major.
 int launch_decode_v6(int D, bool kv_fp8, int nsplit, int rows_per_split, const void* q, RowSrc src,
                      const float* sink, const int32_t* idx, int64_t T, int64_t B, int64_t S, int64_t H, float scale,
                      void* out, int out_dtype, float* part, hipStream_t stream);
 constexpr int kDecodeV6ShortRows = 256;  // up to here: 4-tile ring; its index table lives in LDS
 constexpr int kDecodeV6MaxRows = 8192;   // beyond: 3-tile ring and a larger index table
-
-// largest rows_per_split the bf16 decode kernels accept (its index table lives in LDS)
-constexpr int kDecodeMaxRowsPerSplit = 1024;
 
 // ---- device helpers shared by the LDS-DMA decode kernels
 typedef __attribute__((address_space(3))) uint8_t lds_u8_t;

@@ -23,7 +23,6 @@
 namespace {
 
 constexpr int kLinWaves = 8;
-int g_linear_form = 0;  // tuning: 1 forces the register form
 constexpr int kLinSteps = 8;  // K steps of 64 whose loads are in flight together
 
 // float32 ops that the compiler may not contract into fma (the reference rounds every product;
@@ -302,7 +301,7 @@ template <bool ROPE, int YDT>
 int launch_linear_t(const uint16_t* x, const uint16_t* w, int64_t T, int64_t G, int64_t N, int64_t K, int64_t ldx,
                     const int32_t* pos, const float* cos_t, const float* sin_t, int head_dim, int rd, void* y,
                     hipStream_t st) {
-  if (lds_form(T, K) && g_linear_form != 1)
+  if (lds_form(T, K))
     return launch_linear_lds<8, ROPE, YDT>(x, w, T, G, N, K, ldx, pos, cos_t, sin_t, head_dim, rd, y, st);
   const dim3 grid((unsigned)(G * N / 16)), blk(64 * kLinWaves);
   if (T <= 16)
@@ -349,9 +348,6 @@ int check_rope_args(const int32_t* pos, const float* cos_t, const float* sin_t, 
 }
 
 }  // namespace
-
-// tuning only: 1 forces the register form of the projection kernel, 0 picks by shape
-extern "C" void smla_set_linear_form(int form) { g_linear_form = form; }
 
 extern "C" int smla_linear(const void* x, int x_dtype, const void* w, int w_dtype, int64_t T, int64_t G, int64_t N,
                            int64_t K, void* y, int y_dtype, void* stream) {

@@ -693,10 +693,6 @@ extern "C" int smla_select_decode(const float* scores, int64_t R, int64_t N, con
   return launch_select(scores, R, N, nvis, k, out, out_stride, id_offset, pos, (int)window, (hipStream_t)stream);
 }
 
-static int g_cert_force_exact = 0;  // tests: 1 = rescore every visible key (the uncertified path)
-
-extern "C" void smla_set_index_cert_force_exact(int on) { g_cert_force_exact = on ? 1 : 0; }
-
 extern "C" size_t smla_index_decode_workspace(int64_t B, int64_t S, int64_t N) {
   if (B <= 0 || S <= 0 || N <= 0) return 0;
   const int64_t R = B * S, nchunk = (N + 255) / 256;
@@ -706,12 +702,13 @@ extern "C" size_t smla_index_decode_workspace(int64_t B, int64_t S, int64_t N) {
 extern "C" int smla_index_decode(const void* q, int q_dtype, const void* keys, int k_dtype, const float* kscale,
                                  const float* weights, const int32_t* nvis, int64_t B, int64_t S, int64_t Hi,
                                  int64_t Di, int64_t N, int64_t k, const int32_t* pos, int64_t window,
-                                 int32_t* out, int64_t out_stride, int32_t id_offset, void* workspace,
-                                 size_t workspace_bytes, void* stream) {
+                                 int32_t* out, int64_t out_stride, int32_t id_offset, int flags,
+                                 void* workspace, size_t workspace_bytes, void* stream) {
   if (!q || !keys || !weights || !out) return SMLA_E_NULL;
   if (window > 0 && !pos) return SMLA_E_NULL;
   if (B <= 0 || S <= 0 || Hi <= 0 || Di <= 0 || N <= 0 || k <= 0 || window < 0 || out_stride < k + window)
     return SMLA_E_SHAPE;
+  if (flags & ~SMLA_INDEX_EXACT) return SMLA_E_RANGE;
   if (!workspace || workspace_bytes < smla_index_decode_workspace(B, S, N)) return SMLA_E_WORKSPACE;
   const int64_t R = B * S;
   if (R > 65535 || k > 0x7fffffff || window > 0x7fffffff || (N + kTopkThreads - 1) / kTopkThreads > 64)
@@ -731,7 +728,7 @@ extern "C" int smla_index_decode(const void* q, int q_dtype, const void* keys, i
                                ebound, st);
   if (rc != SMLA_OK) return rc;
   const CertCtx cc{ebound, (int)((N + 255) / 256), (const uint16_t*)q, (const uint8_t*)keys, kscale, weights, S,
-                   g_cert_force_exact, approx};
+                   (flags & SMLA_INDEX_EXACT) ? 1 : 0, approx};
   return launch_select(approx, R, N, nvis, k, out, out_stride, id_offset, wpos, (int)window, st, &cc);
 }
 

@@ -25,6 +25,10 @@ _SIGNATURES = {
     "smla_sparse_attn": (_int, [_vp, _int, _vp, _i64, _vp, _i64, _int, _vp, _vp, _vp, _vp, _i64,
                                 _i64, _i64, _i64, _i64, _i64, _f32, _vp, _int, _vp, _sz, _vp]),
     "smla_sparse_attn_workspace": (_sz, [_i64, _i64, _i64, _i64, _i64, _i64, _int, _int]),
+    "smla_sparse_attn_plan": (_sz, [_i64, _i64, _i64, _i64, _i64, _i64, _int, _int, _int, _i64,
+                                    ctypes.POINTER(_i64), ctypes.POINTER(_i64)]),
+    "smla_sparse_attn_ex": (_int, [_vp, _int, _vp, _i64, _vp, _i64, _int, _vp, _vp, _vp, _vp, _i64,
+                                   _i64, _i64, _i64, _i64, _i64, _f32, _vp, _int, _i64, _int, _vp, _sz, _vp]),
     "smla_window_topk_idxs": (_int, [_i64, _i64, _i64, _i64, _vp, _vp]),
     "smla_decode_window_idxs": (_int, [_vp, _i64, _i64, _vp, _i64, _vp]),
     "smla_indexer_score": (_int, [_vp, _int, _vp, _int, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64,
@@ -32,7 +36,7 @@ _SIGNATURES = {
     "smla_topk": (_int, [_vp, _i64, _i64, _vp, _i64, _vp, _i64, _i32, _vp]),
     "smla_select_decode": (_int, [_vp, _i64, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _i32, _vp]),
     "smla_index_decode": (_int, [_vp, _int, _vp, _int, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64,
-                                 _vp, _i64, _vp, _i64, _i32, _vp, _sz, _vp]),
+                                 _vp, _i64, _vp, _i64, _i32, _int, _vp, _sz, _vp]),
     "smla_index_decode_workspace": (_sz, [_i64, _i64, _i64]),
     "smla_block_mean_pool": (_int, [_vp, _int, _i64, _i64, _i64, _i64, _vp, _int, _vp]),
     "smla_gated_pool": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _f32,
@@ -54,17 +58,9 @@ _SIGNATURES = {
 SIM_NONE, SIM_FP8, SIM_ROTATE_FP4 = 0, 1, 2
 QAT_ROTATE, QAT_FP4 = 1, 2
 
-# symbols exported for tuning only (not part of the public header)
-_TUNING = {
-    "smla_set_attn_target_wgs": (None, [_int]),
-    "smla_profile_set_attn_events": (None, [_vp, _vp]),
-    "smla_profile_set_attn_main_only": (None, [_int]),
-    "smla_set_attn_decode_kernel": (None, [_int]),
-    "smla_set_index_cert_force_exact": (None, [_int]),
-    "smla_set_linear_form": (None, [_int]),
-    "smla_attn_plan": (None, [_i64, _i64, _i64, _i64, _i64, _i64, _int, _int, ctypes.POINTER(_int),
-                              ctypes.POINTER(_int)]),
-}
+# phases of smla_sparse_attn_ex, flags of smla_index_decode
+ATTN_SPLIT, ATTN_MERGE = 1, 2
+INDEX_EXACT = 1
 
 
 class SmlaLibraryError(RuntimeError):
@@ -93,7 +89,7 @@ def lib():
             handle = ctypes.CDLL(LIB_PATH)
         except OSError as e:  # pragma: no cover - depends on the machine
             raise SmlaLibraryError(f"cannot load {LIB_PATH}: {e}") from e
-        for name, (res, args) in {**_SIGNATURES, **_TUNING}.items():
+        for name, (res, args) in _SIGNATURES.items():
             fn = getattr(handle, name)
             fn.restype = res
             fn.argtypes = args

@@ -130,7 +130,8 @@ class DecodeLayer:
     def index_list(self, pos, scores=None, k=2048):
         """``decode_engine.py:110-114``: [B, 128 + n] int32 ids into [window cache; compressed
         cache] (compressed ids offset by max_pos), -1 padded.  Take-all over the visible compressed
-        rows, or, with indexer scores [B, ncap] supplied, the top-k of them.  Also copies a row the
+        rows, or, with indexer scores [B, ncap] supplied, the top-k of the min((p+1)//4, ncap)
+        visible ones (all of them, -1 padded, while at most k are visible).  Also copies a row the
         ring emitted at this step to the bf16 compressed cache."""
         comp = (self.comp32, self.comp) if self.ring_ratio else (None, None)
         take_all = scores is None or not self.ring_ratio
@@ -139,17 +140,29 @@ class DecodeLayer:
                              comp_out=comp[1])
         if take_all:
             return ids
-        return _idx.select_decode_indices(scores, k, pos, WINDOW, self.max_pos)
+        if scores.shape != (self.B, self.ncap):
+            raise ValueError(f"scores must be [{self.B}, {self.ncap}] (one per compressed slot)")
+        # visible compressed rows at p: (p+1)//4 (decode_engine.py:112), at most the cache's rows
+        nvis = torch.clamp(torch.div(pos + 1, 4, rounding_mode="floor"), max=self.ncap).to(torch.int32)
+        return _idx.select_decode_indices(scores, k, pos, WINDOW, self.max_pos, nvis=nvis)
 
     # -- the step --------------------------------------------------------------------------------
     def step(self, xn, pos, scores=None, k=2048):
         """xn [B, 4096] bf16 (the attention-normed input), pos [B] int32 on the GPU, the same
-        position sequence for every call of a sequence (p, p+1, ...).  Returns the layer's
-        attention output [B, 4096] bf16 (``o_grouped``'s result, before ``hc_post``)."""
+        position sequence for every call of a sequence (p, p+1, ...), each in [0, max_pos).
+        Returns the layer's attention output [B, 4096] bf16 (``o_grouped``'s result, before
+        ``hc_post``).  Outside graph capture the positions are checked against max_pos (one
+        device read); a captured step relies on the caller's positions."""
         ops._on_gpu(xn, pos)
         if xn.shape != (self.B, self.w.wq_a.shape[1]):
             raise ValueError(f"xn must be [{self.B}, {self.w.wq_a.shape[1]}]")
+        if pos.shape != (self.B,):
+            raise ValueError(f"pos must be [{self.B}]")
         pos = pos.to(torch.int32).contiguous()
+        if not torch.cuda.is_current_stream_capturing():
+            lo, hi = torch.aminmax(pos)
+            if int(lo) < 0 or int(hi) >= self.max_pos:
+                raise ValueError(f"positions must lie in [0, {self.max_pos}); got {int(lo)}..{int(hi)}")
         y = _proj(xn, self.w_in)                     # [B, sum of the projection widths] fp32
         c = self.cuts
         q = self.q_path(y[:, c[0]:c[1]], pos)

@@ -22,25 +22,27 @@ def topk(scores, k, nvis=None, id_offset=0):
     return ops.topk_op(scores, k, nvis, id_offset)
 
 
-def select_decode_indices(scores, k, pos, window, n_raw, out=None):
+def select_decode_indices(scores, k, pos, window, n_raw, out=None, nvis=None):
     """The decode attention index list per sequence: the raw-cache window rows pos-window+1..pos
     (columns 0..window-1) followed by the top-k compressed rows offset by ``n_raw`` (the raw
-    cache length, so ids index the virtual [raw; compressed] buffer).
-    scores [B, N] fp32, pos [B] int32 -> out [B, window + k] int32."""
+    cache length, so ids index the virtual [raw; compressed] buffer), ranked among the first
+    nvis[b] scores of each row (all N when nvis is None).
+    scores [B, N] fp32, pos [B] int32, nvis [B] int32 or None -> out [B, window + k] int32."""
     B = scores.shape[0]
     if out is None:
         out = torch.empty(B, window + k, dtype=torch.int32, device=scores.device)
-    ops.select_decode_into(scores.contiguous(), k, pos, window, out, id_offset=n_raw)
+    ops.select_decode_into(scores.contiguous(), k, pos, window, out, id_offset=n_raw, nvis=nvis)
     return out
 
 
-def index_decode(q_idx, keys, kscale, weights, nvis, k, pos, window, n_raw, out=None, workspace=None):
+def index_decode(q_idx, keys, kscale, weights, nvis, k, pos, window, n_raw, out=None, workspace=None, flags=0):
     """Indexer scores and the decode index list in one call: the same list as ``indexer_score``
     followed by ``select_decode_indices`` (bit-exact), with the scores of bf16 q x e4m3 keys
     (64 heads x 64 dims) taken on MFMA under a certified error bound and only the keys near the
     top-k boundary rescored in the fixed order.
     q_idx [B,1,Hi,Di], keys [B,N,Di], kscale [B,N] or None, weights [B,1,Hi], nvis [B,1] or None,
-    pos [B] int32 -> out [B, window + k] int32."""
+    pos [B] int32 -> out [B, window + k] int32.  flags: 0, or ``_lib.INDEX_EXACT`` to rescore every
+    visible key in the fixed order (the path an uncertifiable row takes; the same output)."""
     B, S = q_idx.shape[:2]
     N = keys.shape[1]
     if out is None:
@@ -48,5 +50,5 @@ def index_decode(q_idx, keys, kscale, weights, nvis, k, pos, window, n_raw, out=
     if workspace is None:
         workspace = torch.empty(ops.index_decode_workspace(B, S, N), dtype=torch.uint8, device=q_idx.device)
     ops.index_decode_into(q_idx, keys, kscale, weights, nvis, k, pos if window > 0 else None, window, out,
-                          workspace, id_offset=n_raw)
+                          workspace, id_offset=n_raw, flags=flags)
     return out

@@ -42,14 +42,45 @@ def _c(t):
 
 
 # ----------------------------------------------------------------------------------------------
-@torch.library.custom_op("smla::sparse_attn", mutates_args=(), device_types="cuda")
-def sparse_attn_op(q: torch.Tensor, kv0: torch.Tensor, kv1: Optional[torch.Tensor],
-                   kv0_scale: Optional[torch.Tensor], kv1_scale: Optional[torch.Tensor],
-                   attn_sink: Optional[torch.Tensor], topk_idxs: torch.Tensor, scale: float,
-                   dv: int) -> torch.Tensor:
-    """q [B,S,H,D], kv0 [B,n0,D], kv1 [B,n1,D]|None, scales [B,n,D/64] (fp8 rows),
-    attn_sink [H]|None, topk_idxs [B,S,T] -> out [B,S,H,dv] in q's dtype."""
+def _is_fp8_rows(t):
+    return t.dtype == torch.uint8 or (hasattr(torch, "float8_e4m3fn") and t.dtype == torch.float8_e4m3fn)
+
+
+def _check_attn(q, kv0, kv1, kv0_scale, kv1_scale, attn_sink, topk_idxs, dv):
+    """Shape and type agreement of the attention operands, checked before any launch (a mismatch
+    would send the kernel's row, index or scale addressing past its buffers)."""
+    if q.dim() != 4 or kv0.dim() != 3 or topk_idxs.dim() != 3:
+        raise ValueError("expected q [B,S,H,D], kv0 [B,n0,D], topk_idxs [B,S,T]")
+    B, S, H, D = q.shape
+    if kv0.shape[0] != B or kv0.shape[2] != D:
+        raise ValueError(f"kv0 {tuple(kv0.shape)} does not match q {tuple(q.shape)}: expected [{B}, n0, {D}]")
+    if kv1 is not None:
+        if kv1.dim() != 3 or kv1.shape[0] != B or kv1.shape[2] != D:
+            raise ValueError(f"kv1 {tuple(kv1.shape)} does not match q {tuple(q.shape)}: expected [{B}, n1, {D}]")
+        if kv1.dtype != kv0.dtype:
+            raise ValueError(f"kv1 dtype {kv1.dtype} differs from kv0's {kv0.dtype}")
+    if topk_idxs.shape[0] != B or topk_idxs.shape[1] != S:
+        raise ValueError(f"topk_idxs {tuple(topk_idxs.shape)} does not match q: expected [{B}, {S}, T]")
+    if not 0 < dv <= D:
+        raise ValueError(f"dv={dv} must lie in 1..{D}")
+    if attn_sink is not None and tuple(attn_sink.shape) != (H,):
+        raise ValueError(f"attn_sink {tuple(attn_sink.shape)} must be [{H}]")
+    if _is_fp8_rows(kv0):
+        if D % 64 != 0:
+            raise ValueError("fp8 rows need D % 64 == 0")
+        for kv, sc, name in ((kv0, kv0_scale, "kv0_scale"), (kv1, kv1_scale, "kv1_scale")):
+            if kv is None:
+                continue
+            if sc is None or tuple(sc.shape) != (B, kv.shape[1], D // 64) or sc.dtype != torch.float32:
+                got = None if sc is None else (tuple(sc.shape), sc.dtype)
+                raise ValueError(f"{name} must be fp32 [{B}, {kv.shape[1]}, {D // 64}], got {got}")
+    elif kv0_scale is not None or kv1_scale is not None:
+        raise ValueError("scales are given for fp8 rows only")
+
+
+def _attn_args(q, kv0, kv1, kv0_scale, kv1_scale, attn_sink, topk_idxs, dv):
     _on_gpu(q, kv0, kv1, kv0_scale, kv1_scale, attn_sink, topk_idxs)
+    _check_attn(q, kv0, kv1, kv0_scale, kv1_scale, attn_sink, topk_idxs, dv)
     q, kv0, kv1 = q.contiguous(), kv0.contiguous(), _c(kv1)
     kv0_scale, kv1_scale, attn_sink = _c(kv0_scale), _c(kv1_scale), _c(attn_sink)
     if topk_idxs.dtype != torch.int32:
@@ -57,6 +88,31 @@ def sparse_attn_op(q: torch.Tensor, kv0: torch.Tensor, kv1: Optional[torch.Tenso
     topk_idxs = topk_idxs.contiguous()
     if attn_sink is not None and attn_sink.dtype != torch.float32:
         attn_sink = attn_sink.float()
+    return q, kv0, kv1, kv0_scale, kv1_scale, attn_sink, topk_idxs
+
+
+def attn_plan(B, S, H, D, dv, T, q_dtype=torch.bfloat16, kv_dtype=torch.bfloat16, out_dtype=None,
+              rows_per_split=0):
+    """(nsplit, rows_per_split, workspace bytes) of the attention path's split plan for these sizes
+    (``smla_sparse_attn_plan``); rows_per_split 0 asks for the default plan."""
+    import ctypes
+    ns, rps = ctypes.c_int64(0), ctypes.c_int64(0)
+    qd, kd = _DT[q_dtype], _DT[kv_dtype]
+    od = _DT[out_dtype if out_dtype is not None else q_dtype]
+    wsb = _lib.lib().smla_sparse_attn_plan(B, S, H, D, dv, T, qd, kd, od, rows_per_split, ctypes.byref(ns),
+                                           ctypes.byref(rps))
+    return ns.value, rps.value, int(wsb)
+
+
+@torch.library.custom_op("smla::sparse_attn", mutates_args=(), device_types="cuda")
+def sparse_attn_op(q: torch.Tensor, kv0: torch.Tensor, kv1: Optional[torch.Tensor],
+                   kv0_scale: Optional[torch.Tensor], kv1_scale: Optional[torch.Tensor],
+                   attn_sink: Optional[torch.Tensor], topk_idxs: torch.Tensor, scale: float,
+                   dv: int) -> torch.Tensor:
+    """q [B,S,H,D], kv0 [B,n0,D], kv1 [B,n1,D]|None, scales [B,n,D/64] (fp8 rows),
+    attn_sink [H]|None, topk_idxs [B,S,T] -> out [B,S,H,dv] in q's dtype."""
+    q, kv0, kv1, kv0_scale, kv1_scale, attn_sink, topk_idxs = _attn_args(q, kv0, kv1, kv0_scale, kv1_scale,
+                                                                         attn_sink, topk_idxs, dv)
     B, S, H, D = q.shape
     T = topk_idxs.shape[-1]
     n0 = kv0.shape[1]
@@ -68,6 +124,34 @@ def sparse_attn_op(q: torch.Tensor, kv0: torch.Tensor, kv1: Optional[torch.Tenso
     _lib.call("smla_sparse_attn", _p(q), qd, _p(kv0), n0, _p(kv1), n1, kd, _p(kv0_scale),
               _p(kv1_scale), _p(attn_sink), _p(topk_idxs), T, B, S, H, D, dv, float(scale),
               _p(out), od, _p(ws), wsb, _stream(q))
+    return out
+
+
+def sparse_attn_ex(q, kv0, kv1, kv0_scale, kv1_scale, attn_sink, topk_idxs, scale, dv, rows_per_split=0,
+                   phases=3, out=None, workspace=None):
+    """``smla_sparse_attn_ex``: the attention op with an explicit split plan (rows_per_split, 0 =
+    default) and a choice of launches (phases: 1 split kernel, 2 merge, 3 both), into `out` and
+    `workspace` when given (no allocation then).  Returns out."""
+    q, kv0, kv1, kv0_scale, kv1_scale, attn_sink, topk_idxs = _attn_args(q, kv0, kv1, kv0_scale, kv1_scale,
+                                                                         attn_sink, topk_idxs, dv)
+    B, S, H, D = q.shape
+    T = topk_idxs.shape[-1]
+    n0 = kv0.shape[1]
+    n1 = 0 if kv1 is None else kv1.shape[1]
+    if out is None:
+        out = torch.empty(B, S, H, dv, dtype=q.dtype, device=q.device)
+    elif tuple(out.shape) != (B, S, H, dv) or not out.is_contiguous():
+        raise ValueError(f"out must be a contiguous [{B}, {S}, {H}, {dv}] tensor")
+    _on_gpu(out)
+    qd, kd, od = dtype_code(q), dtype_code(kv0), dtype_code(out)
+    _, _, wsb = attn_plan(B, S, H, D, dv, T, q.dtype, kv0.dtype, out.dtype, rows_per_split)
+    if workspace is None:
+        workspace = torch.empty(max(wsb, 1), dtype=torch.uint8, device=q.device)
+    _on_gpu(workspace)
+    have = workspace.numel() * workspace.element_size()
+    _lib.call("smla_sparse_attn_ex", _p(q), qd, _p(kv0), n0, _p(kv1), n1, kd, _p(kv0_scale), _p(kv1_scale),
+              _p(attn_sink), _p(topk_idxs), T, B, S, H, D, dv, float(scale), _p(out), od, int(rows_per_split),
+              int(phases), _p(workspace), have, _stream(q))
     return out
 
 
@@ -401,11 +485,12 @@ def index_decode_workspace(B, S, N):
     return int(_lib.lib().smla_index_decode_workspace(B, S, N))
 
 
-def index_decode_into(q, keys, kscale, weights, nvis, k, pos, window, out, workspace, id_offset=0):
+def index_decode_into(q, keys, kscale, weights, nvis, k, pos, window, out, workspace, id_offset=0, flags=0):
     """Indexer scores and the decode index build in one call (smla_index_decode): q [B,S,Hi,Di],
     keys [B,N,Di], kscale [B,N]|None, weights [B,S,Hi], nvis [B,S]|None, pos [B*S] int32 (None
     when window == 0), out int32 [B*S, >= window + k] (row stride out.stride(0)), workspace a
-    uint8 tensor of at least index_decode_workspace(B, S, N) bytes."""
+    uint8 tensor of at least index_decode_workspace(B, S, N) bytes; flags: 0, or _lib.INDEX_EXACT to
+    rescore every visible key in the fixed order instead of certifying."""
     _on_gpu(q, keys, kscale, weights, nvis, pos, out, workspace)
     if out.dtype != torch.int32 or out.stride(-1) != 1:
         raise ValueError("out must be an int32 view with unit inner stride")
@@ -422,7 +507,7 @@ def index_decode_into(q, keys, kscale, weights, nvis, k, pos, window, out, works
         kscale = kscale.float().contiguous()
     q, keys, weights = q.contiguous(), keys.contiguous(), weights.float().contiguous()
     _lib.call("smla_index_decode", _p(q), dtype_code(q), _p(keys), dtype_code(keys), _p(kscale), _p(weights),
-              _p(nvis), B, S, Hi, Di, N, k, _p(pos), window, _p(out), out.stride(0), int(id_offset),
+              _p(nvis), B, S, Hi, Di, N, k, _p(pos), window, _p(out), out.stride(0), int(id_offset), int(flags),
               _p(workspace), need, _stream(q))
     return out
 

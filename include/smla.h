@@ -11,6 +11,7 @@
  * Reference counterparts (the reference is plain Python; these replace its functions):
  *   smla_sparse_attn          ref_torch/sparse_attn.py:23-34   sparse_attn(q, kv, attn_sink, topk_idxs, scale)
  *                             v4mlx/sparse_attn.py:26-39       (MLX twin)
+ *   smla_sparse_attn_ex       ref_torch/sparse_attn.py:23-34   (the same, with an explicit split plan / phases)
  *   smla_window_topk_idxs     ref_torch/sparse_attn.py:9-20    get_window_topk_idxs(window_size, bsz, seqlen, start_pos)
  *   smla_decode_window_idxs   oracle/decode_engine.py:110-111  widx = range(max(0, p-127), p+1)
  *   smla_indexer_score        (none: the reference attends every visible compressed row,
@@ -42,7 +43,7 @@
 extern "C" {
 #endif
 
-#define SMLA_API_VERSION 1
+#define SMLA_API_VERSION 2
 
 /* element types */
 enum {
@@ -101,8 +102,38 @@ int smla_sparse_attn(const void* q, int q_dtype,
                      void* out, int out_dtype, void* workspace, size_t workspace_bytes,
                      void* stream);
 
+/* Workspace bytes smla_sparse_attn needs for these sizes (its default split plan), enough for
+ * either output type. */
 size_t smla_sparse_attn_workspace(int64_t B, int64_t S, int64_t H, int64_t D, int64_t DV,
                                   int64_t T, int q_dtype, int kv_dtype);
+
+/* The split plan of the attention path for these sizes, a pure function of the arguments and the
+ * device's compute-unit count.  rows_per_split: index-list rows per split requested (a multiple of
+ * 32), or 0 for the default plan (enough splits to give every compute unit a workgroup, at least
+ * two 32-row tiles each).  Writes the number of splits (0 when the fp32 generic kernel runs, which
+ * does not split) and the rows per split, either pointer may be NULL; returns the workspace bytes
+ * that plan needs for out_dtype (0: none). */
+size_t smla_sparse_attn_plan(int64_t B, int64_t S, int64_t H, int64_t D, int64_t DV, int64_t T,
+                             int q_dtype, int kv_dtype, int out_dtype, int64_t rows_per_split,
+                             int64_t* nsplit, int64_t* rows_per_split_out);
+
+/* Phases of smla_sparse_attn_ex: the split kernel (partial states into the workspace, or the
+ * output itself when the plan has one split) and the merge of the partial states into out. */
+enum { SMLA_ATTN_SPLIT = 1, SMLA_ATTN_MERGE = 2 };
+
+/* smla_sparse_attn with an explicit split plan (rows_per_split as in smla_sparse_attn_plan, 0 =
+ * the default) and a choice of its launches (phases: SMLA_ATTN_SPLIT, SMLA_ATTN_MERGE or both).
+ * Both phases with rows_per_split 0 is smla_sparse_attn.  A merge alone reads the partial states
+ * a split launch with the same arguments left in the workspace; a split alone writes out only
+ * when the plan has one split.  The workspace holds smla_sparse_attn_plan(...) bytes.
+ * Replaces ref_torch/sparse_attn.py:23-34, like smla_sparse_attn. */
+int smla_sparse_attn_ex(const void* q, int q_dtype,
+                        const void* kv0, int64_t n0, const void* kv1, int64_t n1, int kv_dtype,
+                        const float* kv0_scale, const float* kv1_scale,
+                        const float* attn_sink, const int32_t* topk_idxs, int64_t T,
+                        int64_t B, int64_t S, int64_t H, int64_t D, int64_t DV, float scale,
+                        void* out, int out_dtype, int64_t rows_per_split, int phases,
+                        void* workspace, size_t workspace_bytes, void* stream);
 
 /* ---------------------------------------------------------------------------------------------
  * Window index matrix.  Replaces ref_torch/sparse_attn.py:9-20 (get_window_topk_idxs).
@@ -158,12 +189,14 @@ int smla_select_decode(const float* scores, int64_t R, int64_t N, const int32_t*
  * shapes and types run the two-step path.  Replaces the compressed index selection of
  * oracle/decode_engine.py:110-114 with an indexer-ranked one.
  * workspace: smla_index_decode_workspace(B, S, N) bytes.  Requires ceil(N / 1024) <= 64 and
- * B*S <= 65535.
+ * B*S <= 65535.  flags: 0, or SMLA_INDEX_EXACT to rescore every visible key in the fixed order
+ * instead of certifying (the same output, slower; the path uncertifiable rows take).
  */
+enum { SMLA_INDEX_EXACT = 1 };
 int smla_index_decode(const void* q, int q_dtype, const void* keys, int k_dtype, const float* kscale,
                       const float* weights, const int32_t* nvis, int64_t B, int64_t S, int64_t Hi,
                       int64_t Di, int64_t N, int64_t k, const int32_t* pos, int64_t window,
-                      int32_t* out, int64_t out_stride, int32_t id_offset, void* workspace,
+                      int32_t* out, int64_t out_stride, int32_t id_offset, int flags, void* workspace,
                       size_t workspace_bytes, void* stream);
 size_t smla_index_decode_workspace(int64_t B, int64_t S, int64_t N);
 

@@ -35,6 +35,7 @@ import torch
 
 from . import compressor as _comp
 from . import fp8 as _fp8
+from . import indexer as _idx
 from . import mla as _mla
 from . import norm_rope as _nr
 from . import sparse_attn as _sa
@@ -82,17 +83,24 @@ def rope_at(x, st, p, inverse=False):
     return y.reshape(*lead, RD)
 
 
-def index_list(p, n_window_rows, n_comp, ratio):
+def index_list(p, n_window_rows, n_comp, ratio, scores=None, k=2048):
     """``oracle/decode_engine.py:110-114`` over [window list (one row per position from 0);
-    compressed list]."""
+    compressed list].  With indexer scores (one per compressed slot), the compressed ids are the
+    top-k of the min(n_comp, (p+1)//4) visible slots by (score desc, index asc), ascending
+    (``indexer.topk``), in place of all of them."""
     widx = list(range(max(0, p - WINDOW + 1), p + 1))
-    nvis = (p + 1) // 4 if ratio == 4 else 0
-    cidx = [n_window_rows + j for j in range(min(n_comp, nvis))]
+    nvis = min(n_comp, (p + 1) // 4) if ratio == 4 else 0
+    if scores is None or ratio != 4:
+        cidx = [n_window_rows + j for j in range(nvis)]
+    else:
+        sel = _idx.topk(np.asarray(scores, dtype=np.float32)[None], k, nvis=np.array([nvis], dtype=np.int32))[0]
+        cidx = [n_window_rows + int(j) for j in sel if j >= 0]
     return torch.tensor(widx + cidx, dtype=torch.int32)
 
 
-def decode_step(st, w, xn, p):
-    """One token at position p: xn [dim] (fp32).  Returns (y [dim_out] float64, the window row
+def decode_step(st, w, xn, p, scores=None, k=2048):
+    """One token at position p: xn [dim] (fp32); optional indexer scores [n_slots] select the
+    top-k visible compressed rows (``index_list``).  Returns (y [dim_out] float64, the window row
     [512] fp32, ids int32, o [64, 512] fp32 before the output projection)."""
     x = np.asarray(xn, dtype=np.float64)[None]
     qa = _nr.rmsnorm(torch.from_numpy(_mla.linear(x, w.wq_a)).float(), w.q_a_norm)
@@ -110,7 +118,7 @@ def decode_step(st, w, xn, p):
         row = _comp.ring_step(st.kvs, st.scs, kvp, scp, p, w.ape, w.norm_c, st.freqs_c, 4, RD, fp8_sim=True)
         if row is not None:
             st.comp.append(row)
-    ids = index_list(p, len(st.win), len(st.comp), st.ratio)
+    ids = index_list(p, len(st.win), len(st.comp), st.ratio, scores, k)
     kvcat = torch.stack(st.win + st.comp)
     o = _sa.sparse_attn(q[None], kvcat, w.sinks, ids[None], 512 ** -0.5)          # [1, 64, 512]
     y = _mla.o_project(o, torch.tensor([p]), st.cos, st.sin, w.wo_a, w.wo_b)

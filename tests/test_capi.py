@@ -29,7 +29,21 @@ def test_library_exports_every_declared_symbol():
     for n in names:
         assert hasattr(lib, n), n
     assert set(names) == set(_lib.exported_symbols())
-    assert lib.smla_api_version() == 1
+    assert lib.smla_api_version() == 2
+
+
+def test_library_exports_only_declared_symbols():
+    """`nm -D` of libsmla.so lists exactly the functions include/smla.h declares: no tuning hooks,
+    no internal C++ symbols."""
+    import shutil
+    import subprocess
+    from smla import _lib
+    nm = shutil.which("nm")
+    if nm is None:
+        pytest.skip("nm not available")
+    res = subprocess.run([nm, "-D", "--defined-only", _lib.LIB_PATH], capture_output=True, text=True, check=True)
+    exported = {ln.split()[-1] for ln in res.stdout.splitlines() if len(ln.split()) >= 3 and ln.split()[1] in "TtWw"}
+    assert exported == set(_declared()), (exported ^ set(_declared()))
 
 
 def test_strerror_and_status_codes():

@@ -40,18 +40,6 @@ def _lib():
     return _lib.lib()
 
 
-@pytest.fixture(params=[0, 1], ids=["role_split", "lockstep64"])
-def decode_kernel(request):
-    """Both bf16-row decode kernels: score/value role-split waves (the default) and the 64-head
-    lockstep-tile kernel."""
-    lib = _lib()
-    lib.smla_set_attn_decode_kernel(request.param)
-    try:
-        yield request.param
-    finally:
-        lib.smla_set_attn_decode_kernel(0)
-
-
 def test_fp32_generic_path_small(dev):
     from smla import sparse_attn as ssa
     g = torch.Generator().manual_seed(0)
@@ -76,9 +64,9 @@ def test_fp32_generic_path_small(dev):
     (3, 1, 32, 96, 256, 0, True, 512, 10.0),
     (1, 1, 48, 1000, 3000, 0, False, 576, 30.0),
 ])
-def test_bf16_mfma_vs_oracle(dev, decode_kernel, B, S, H, T, n0, n1, use_sink, D, sharp):
+def test_bf16_mfma_vs_oracle(dev, B, S, H, T, n0, n1, use_sink, D, sharp):
     from smla import sparse_attn as ssa
-    announce(f"bf16 mfma kernel={decode_kernel} B={B} S={S} H={H} T={T} n0={n0} n1={n1} D={D} sharp={sharp}")
+    announce(f"bf16 mfma B={B} S={S} H={H} T={T} n0={n0} n1={n1} D={D} sharp={sharp}")
     g = torch.Generator().manual_seed(B * 1000 + T)
     q = (torch.randn(B, S, H, D, generator=g) * 0.05 * sharp).to(torch.bfloat16)
     kv0 = (torch.randn(B, n0, D, generator=g) * 0.5).to(torch.bfloat16)
@@ -97,24 +85,24 @@ def test_bf16_mfma_vs_oracle(dev, decode_kernel, B, S, H, T, n0, n1, use_sink, D
     _check_bf16(out, ref, "bf16 mfma")
 
 
-def test_bf16_split_plans_agree(dev, decode_kernel):
+def test_bf16_split_plans_agree(dev):
     """Every split count (1 = direct epilogue, many = LSE merge) gives the oracle's answer."""
-    from smla import sparse_attn as ssa
+    from smla import ops
     g = torch.Generator().manual_seed(7)
     B, H, D, n, T = 2, 64, 576, 3000, 1500
     q = (torch.randn(B, 1, H, D, generator=g) * 0.5).to(torch.bfloat16)
     kv = (torch.randn(B, n, D, generator=g) * 0.5).to(torch.bfloat16)
     idx = torch.randint(0, n, (B, 1, T), generator=g, dtype=torch.int32)
     ref = _oracle_two_source(q, kv, None, None, idx, D ** -0.5, 512)
-    lib = _lib()
-    try:
-        for target in (1, 2, 37, 256, 4096):
-            announce(f"split plan kernel={decode_kernel} target={target}")
-            lib.smla_set_attn_target_wgs(target)
-            out = ssa.sparse_attn_batched(q.to(dev), kv.to(dev), None, idx.to(dev), D ** -0.5, dv=512)
-            _check_bf16(out, ref, f"target {target}")
-    finally:
-        lib.smla_set_attn_target_wgs(0)
+    qd, kvd, idxd = q.to(dev), kv.to(dev), idx.to(dev)
+    seen = set()
+    for rps in (0, 32, 64, 96, 320, 1504, 8192):
+        ns, got_rps, _ = ops.attn_plan(B, 1, H, D, 512, T, rows_per_split=rps)
+        announce(f"split plan rows_per_split={rps} -> nsplit={ns} rows={got_rps}")
+        seen.add(ns)
+        out = ops.sparse_attn_ex(qd, kvd, None, None, None, None, idxd, D ** -0.5, 512, rows_per_split=rps)
+        _check_bf16(out, ref, f"rows_per_split {rps}")
+    assert 1 in seen and max(seen) >= 40, seen
 
 
 def test_many_splits_merge(dev):
@@ -130,15 +118,11 @@ def test_many_splits_merge(dev):
     idx[:, :, ::7] = -1
     sink = torch.randn(H, generator=g)
     ref = _oracle_two_source(q, kv, None, sink, idx, D ** -0.5, 512)
-    lib = _lib()
-    ns, rps = ctypes.c_int(0), ctypes.c_int(0)
-    try:
-        lib.smla_set_attn_target_wgs(4096)
-        lib.smla_attn_plan(B, 1, H, D, 512, T, 1, 1, ctypes.byref(ns), ctypes.byref(rps))
-        assert ns.value > 128, ns.value
-        out = ssa.sparse_attn_batched(q.to(dev), kv.to(dev), sink.to(dev), idx.to(dev), D ** -0.5, dv=512)
-    finally:
-        lib.smla_set_attn_target_wgs(0)
+    from smla import ops
+    ns, _, _ = ops.attn_plan(B, 1, H, D, 512, T, rows_per_split=32)
+    assert ns > 128, ns
+    out = ops.sparse_attn_ex(q.to(dev), kv.to(dev), None, None, None, sink.to(dev), idx.to(dev), D ** -0.5, 512,
+                             rows_per_split=32)
     _check_bf16(out, ref, "many splits")
 
 

@@ -2,11 +2,12 @@
 against the oracle's composition (``oracle/engine.py``), at the model's layer shapes (hidden 4096,
 q rank 1024, 64 heads x 512, output 8 groups x 1024), for two sequences stepped token by token.
 
-Per step: the layer output (relative L2 error <= 2e-2: every product is a bf16 HIP kernel and the
+Per step: the layer output (relative L2 error <= 1e-2: every product is a bf16 HIP kernel and the
 window and compressed rows are stored in bf16, while the oracle runs float64 products on the same
-bf16 weights), the window row written at p (rope dims <= 1e-2) and every emitted compressed row
-(rope dims <= 2e-2), whose fp8 round-tripped dims are held to 4e-2.  A wrong position, a missing rotation, a misplaced row or a wrong id list changes the
-output by O(1)."""
+bf16 weights; measured worst cases are about 5e-3), the window row written at p (rope dims
+<= 1e-2) and every emitted compressed row (rope dims <= 2e-2), whose fp8 round-tripped dims are
+held to 4e-2.  A wrong position, a missing rotation, a misplaced row or a wrong id list changes
+the output by O(1)."""
 import numpy as np
 import pytest
 import torch
@@ -64,13 +65,52 @@ def test_decode_layer_vs_oracle(dev, ratio, steps):
             yr, kv, ids, _ = oe.decode_step(states[b], wo, xn[b].float(), p)
             r = _rel(y[b], yr)
             worst = max(worst, r)
-            assert r <= 2e-2, f"step {p} seq {b}: output rel err {r:.3e}"
+            assert r <= 1e-2, f"step {p} seq {b}: output rel err {r:.3e}"
             _check_row(layer.raw[b, p].float().cpu(), kv, 1e-2, f"step {p} seq {b}: window row")
             if ratio == 4 and (p + 1) % 4 == 0:
                 j = (p + 1) // 4 - 1
                 assert len(states[b].comp) == j + 1
                 _check_row(layer.comp32[b, j].cpu(), states[b].comp[j], 2e-2, f"step {p} seq {b}: compressed row {j}")
     announce(f"worst output rel err {worst:.3e}")
+
+
+@pytest.mark.parametrize("k,steps", [(8, 72), (40, 200)])
+def test_decode_layer_indexer_topk_vs_oracle(dev, k, steps):
+    """``step(scores=...)``: the compressed ids are the top-k of the min((p+1)//4, ncap) visible
+    slots by (score desc, index asc) instead of all of them.  Positions run from below the point
+    where the visible rows exceed k to well above it; scores carry ties, and slots not yet visible
+    get the largest scores (a list that ranked them would differ).  Per step the id set equals the
+    oracle's exactly and the output is within 1e-2 relative L2."""
+    from smla import engine
+    announce(f"decode layer indexer top-k k={k} steps={steps}")
+    t = _make_weights(4, seed=11)
+    w = engine.LayerWeights(**{kk: v.to(dev) for kk, v in t.items()})
+    wo = oe.OracleWeights(**{kk: (v.double().numpy() if v.dtype == torch.bfloat16 else v.float())
+                             for kk, v in t.items()})
+    B, max_pos = 2, 256
+    layer = engine.DecodeLayer(w, B, 4, max_pos=max_pos, device=dev)
+    states = [oe.LayerState(4, max_pos=max_pos) for _ in range(B)]
+    g = torch.Generator().manual_seed(200 + k)
+    ncap = max_pos // 4
+    for p in range(steps):
+        xn = torch.randn(B, 4096, generator=g).to(torch.bfloat16)
+        # quantised scores (ties), invisible slots above every visible one
+        sc = torch.round(torch.randn(B, ncap, generator=g) * 4) / 4
+        nv = min(ncap, (p + 1) // 4)
+        sc[:, nv:] = 100.0
+        pos = torch.full((B,), p, dtype=torch.int32, device=dev)
+        scd = sc.to(dev)
+        y = layer.step(xn.to(dev), pos, scores=scd, k=k).float().cpu()
+        ids = layer.index_list(pos, scores=scd, k=k).cpu()
+        for b in range(B):
+            yr, _, ids_ref, _ = oe.decode_step(states[b], wo, xn[b].float(), p, scores=sc[b].numpy(), k=k)
+            got = ids[b][ids[b] >= 0].tolist()
+            # window ids are cache positions in both; compressed ids: max_pos + j here, (p + 1) + j there
+            got = sorted(i if i < max_pos else (p + 1) + (i - max_pos) for i in got)
+            assert got == sorted(ids_ref.tolist()), f"step {p} seq {b}: id sets differ"
+            assert len(ids_ref) == min(p + 1, 128) + min(nv, k)
+            r = _rel(y[b], yr)
+            assert r <= 1e-2, f"step {p} seq {b}: output rel err {r:.3e}"
 
 
 def test_decode_layer_rejects_cpu_and_bad_ratio(dev):

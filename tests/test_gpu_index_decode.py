@@ -102,14 +102,9 @@ def test_index_decode_forced_slow_path(dev, kind):
     codes, ks, kvals = _keys(kind, B, N, 64, g)
     nvis = torch.tensor([[N], [N - 100]], dtype=torch.int32)
     pos = torch.tensor([9000, 70], dtype=torch.int32)
-    lib = _lib.lib()
-    try:
-        lib.smla_set_index_cert_force_exact(1)
-        out = sidx.index_decode(q.to(dev), codes.to(dev), ks.to(dev), w.to(dev), nvis.to(dev), k, pos.to(dev),
-                                window, 4 * N)
-        torch.cuda.synchronize()
-    finally:
-        lib.smla_set_index_cert_force_exact(0)
+    out = sidx.index_decode(q.to(dev), codes.to(dev), ks.to(dev), w.to(dev), nvis.to(dev), k, pos.to(dev),
+                            window, 4 * N, flags=_lib.INDEX_EXACT)
+    torch.cuda.synchronize()
     ref = _oracle_ids(q, kvals, ks, w, nvis, k, pos.numpy(), window, 4 * N)
     np.testing.assert_array_equal(out.cpu().numpy(), ref)
 

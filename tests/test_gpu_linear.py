@@ -32,30 +32,25 @@ def _check_linear(got, x, w, G, out_dtype):
     assert np.all(err <= tol), f"max err {err.max():.3e}, worst ratio {(err / np.maximum(tol, 1e-30)).max():.3f}"
 
 
-@pytest.mark.parametrize("T,G,N,K,out_dtype,form", [
-    (8, 8, 1024, 4096, torch.bfloat16, 0),      # o_grouped's grouped product at decode (LDS form)
-    (8, 8, 1024, 4096, torch.bfloat16, 1),      # the same in the register form
-    (8, 1, 4096, 8192, torch.float32, 0),       # its second product (16 waves)
-    (8, 1, 4096, 8192, torch.float32, 1),
-    (1, 1, 256, 4096, torch.float32, 0),
-    (3, 2, 48, 512, torch.float32, 0),          # one wave per workgroup
-    (16, 2, 64, 1024, torch.bfloat16, 0),       # short K slices: the guarded last batch
-    (17, 1, 128, 512, torch.float32, 0),        # two token tiles, one ragged
-    (32, 4, 32, 2048, torch.bfloat16, 0),
+@pytest.mark.parametrize("T,G,N,K,out_dtype", [
+    (8, 8, 1024, 4096, torch.bfloat16),      # o_grouped's grouped product at decode (LDS form)
+    (12, 8, 1024, 4096, torch.bfloat16),     # the same width in the register form (T > 8)
+    (8, 1, 4096, 8192, torch.float32),       # its second product (16 waves)
+    (9, 1, 4096, 8192, torch.float32),       # register form
+    (1, 1, 256, 4096, torch.float32),
+    (3, 2, 48, 512, torch.float32),          # one wave per workgroup
+    (16, 2, 64, 1024, torch.bfloat16),       # short K slices: the guarded last batch
+    (17, 1, 128, 512, torch.float32),        # two token tiles, one ragged
+    (32, 4, 32, 2048, torch.bfloat16),
 ])
-def test_linear_vs_fp64(dev, T, G, N, K, out_dtype, form):
-    from smla import _lib, ops
-    announce(f"linear T={T} G={G} N={N} K={K} out={out_dtype} form={form}")
+def test_linear_vs_fp64(dev, T, G, N, K, out_dtype):
+    from smla import ops
+    announce(f"linear T={T} G={G} N={N} K={K} out={out_dtype}")
     g = torch.Generator().manual_seed(T * 7 + G + N + K)
     x = torch.randn(T, G * K, generator=g).to(torch.bfloat16)
     w = (torch.randn(G * N, K, generator=g) * 0.05).to(torch.bfloat16)
-    lib = _lib.lib()
-    try:
-        lib.smla_set_linear_form(form)
-        y = ops.linear_op(x.to(dev), w.to(dev), G, out_dtype)
-        torch.cuda.synchronize()
-    finally:
-        lib.smla_set_linear_form(0)
+    y = ops.linear_op(x.to(dev), w.to(dev), G, out_dtype)
+    torch.cuda.synchronize()
     assert y.dtype == out_dtype and y.shape == (T, G * N)
     _check_linear(y.float(), x, w, G, out_dtype)
 

@@ -42,12 +42,10 @@ def _inputs(n_raw, S, H, seed, sharp=1.0):
 def test_prefill_vs_oracle(dev, n_raw, q_pos0, S, H, use_sink, one_split):
     """one_split forces the single-split plan (3-tile ring, long index table) that the full
     4096-query prefill uses; otherwise these small query counts get short splits and a merge."""
-    from smla import _lib
     from smla import compressor as scomp
-    from smla import sparse_attn as ssa
+    from smla import ops
     from smla import workloads as wl
     announce(f"prefill n_raw={n_raw} q_pos0={q_pos0} S={S} H={H} sink={use_sink} one_split={one_split}")
-    lib = _lib.lib()
     q, raw = _inputs(n_raw, S, H, seed=q_pos0 + S)
     raw_d = raw.to(dev)
     comp_d = scomp.block_mean_pool(raw_d, 4)
@@ -57,13 +55,13 @@ def test_prefill_vs_oracle(dev, n_raw, q_pos0, S, H, use_sink, one_split):
     idx = idx_all[q_pos0:q_pos0 + S]
     sink = torch.randn(H, generator=torch.Generator().manual_seed(5)) if use_sink else None
     scale = 576 ** -0.5
-    try:
-        lib.smla_set_attn_target_wgs(1 if one_split else 0)
-        out = ssa.sparse_attn_two_source(q.to(dev), raw_d, comp_d, None if sink is None else sink.to(dev),
-                                         idx[None].to(dev), scale, dv=512)
-        torch.cuda.synchronize()
-    finally:
-        lib.smla_set_attn_target_wgs(0)
+    T = idx.shape[-1]
+    rps = (T + 31) // 32 * 32 if one_split else 0
+    out = ops.sparse_attn_ex(q.to(dev), raw_d, comp_d, None, None, None if sink is None else sink.to(dev),
+                             idx[None].to(dev), scale, 512, rows_per_split=rps)
+    if one_split:
+        assert ops.attn_plan(1, S, H, 576, 512, T, rows_per_split=rps)[0] == 1
+    torch.cuda.synchronize()
     kv = torch.cat([raw[0].float(), comp[0].float()])
     ref = osa.sparse_attn(q[0].float(), kv, sink, idx, scale, dv=512)
     _check(out[0], ref, "prefill")
