@@ -154,7 +154,7 @@ __global__ __launch_bounds__(WAVES * 64) void attn_merge_kernel(const float* __r
   constexpr int NT = WAVES * 64;
   constexpr int DV = 512;
   constexpr int CPL = DV / (DVS * NT);                // value columns per thread: 4, 2 or 1
-  // DVS > 1: the row's columns are split over DVS workgroups (blockIdx.y), for row counts too small
+  // DVS > 1: the row's columns are split over DVS workgroups, for row counts too small
   // to spread over the CUs otherwise
   constexpr int LW = BF16P ? (CPL + 1) / 2 : CPL;     // 32-bit words loaded per split
   constexpr int CHUNK = CH < 64 / LW ? CH : 64 / LW;  // splits in flight: at most 64 words per thread
@@ -164,12 +164,15 @@ __global__ __launch_bounds__(WAVES * 64) void attn_merge_kernel(const float* __r
   __shared__ float l_s[kMaxSplits];
   __shared__ float red[2][WAVES];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int64_t rh = blockIdx.x;  // bs*H + head
-  const int64_t bs = rh / H;
-  const int head = (int)(rh % H);
+  // grid (B*S*H, DVS): every head and column slice of query row bs on XCD bs mod 8 (when B*S is a
+  // multiple of 8), the XCD whose L2 holds that row's partials from the split kernel
+  int64_t bs, item;
+  xcd_row_item(BS, (int64_t)H * DVS, bs, item);
+  const int head = (int)(item % H);
+  const int64_t rh = bs * H + head;
   const int64_t rec0 = bs * nsplit * (int64_t)H + head;  // record of split 0; splits are H records apart
   const float* ml = part + rec0 * 2;
-  const int dv0 = (int)blockIdx.y * (DV / DVS) + tid * CPL;
+  const int dv0 = (int)(item / H) * (DV / DVS) + tid * CPL;
   const int64_t jstride = (int64_t)H * DV;  // elements between consecutive splits
   const float* obase = part + BS * H * nsplit * 2;
 

@@ -109,10 +109,22 @@ __global__ __launch_bounds__(768) void attn_decode_kernel(
   const uint32_t lds_base = (uint32_t)(uintptr_t)lds;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int split = blockIdx.x, nsplit = gridDim.x;
-  const int64_t bs = (nsplit == 1 && gridDim.z == 1) ? query_row_of(blockIdx.y, gridDim.y) : (int64_t)blockIdx.y;
+  // grid (nsplit, B*S, head groups).  One split per query row and one head group (prefill): query
+  // rows in XCD chunks (query_row_of); otherwise every split and head group of query row bs on XCD
+  // bs mod 8 (when B*S is a multiple of 8), where the selection left its index list and where the
+  // merge reads the partials back
+  const int nsplit = gridDim.x;
+  int split = 0, hb = 0;  // hb: first head of this workgroup
+  int64_t bs;
+  if (nsplit == 1 && gridDim.z == 1) {
+    bs = query_row_of(blockIdx.y, gridDim.y);
+  } else {
+    int64_t item;
+    xcd_row_item(gridDim.y, (int64_t)nsplit * gridDim.z, bs, item);
+    split = (int)(item % nsplit);
+    hb = (int)(item / nsplit) * 64;
+  }
   const int64_t b = bs / S;
-  const int hb = blockIdx.z * 64;                 // first head of this workgroup
   const int nh = min(64, H - hb);                 // valid heads here
   const int t_begin = split * rows_per_split;
   const int t_end = min(T, t_begin + rows_per_split);

@@ -34,11 +34,12 @@ __global__ __launch_bounds__(256) void indexer_kernel(const void* __restrict__ q
   __shared__ __align__(16) float sq[64 * DI];
   __shared__ float sw[256];
   __shared__ float sr[kKeys][65];  // r[key][head] (padded: lanes read different keys)
-  const int64_t bs = blockIdx.y;
+  int64_t bs, chunk;
+  xcd_row_item(gridDim.y, gridDim.x, bs, chunk);
   const int64_t b = bs / S;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int nwaves = blockDim.x >> 6;
-  const int64_t n = (int64_t)blockIdx.x * kKeys + lane;
+  const int64_t n = chunk * kKeys + lane;
   const int64_t nv = nvis ? (int64_t)nvis[bs] : N;
   const bool live = n < N && n < nv;
   const int64_t nrow = n < N ? n : N - 1;
@@ -177,10 +178,11 @@ __global__ __launch_bounds__(64 * (64 / HPW)) void indexer2_kernel(const void* _
   __shared__ __align__(16) float sq[64 * DI];
   __shared__ float sw[64];
   __shared__ float sr[KEYS][65];  // r[key][head]
-  const int64_t bs = blockIdx.y;
+  int64_t bs, chunk;
+  xcd_row_item(gridDim.y, gridDim.x, bs, chunk);
   const int64_t b = bs / S;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int64_t n0 = (int64_t)blockIdx.x * KEYS + lane;
+  const int64_t n0 = chunk * KEYS + lane;
   const int64_t nv = nvis ? (int64_t)nvis[bs] : N;
 
   // the lane's key rows in registers, in their storage type (converted one 16-wide block at a time)
@@ -286,7 +288,7 @@ __global__ __launch_bounds__(64 * (64 / HPW)) void indexer2_kernel(const void* _
   if (wave >= KPL) return;
   // chain over the heads: wave i for keys 64 i .. 64 i + 63
   const int kl = wave * 64 + lane;
-  const int64_t n = (int64_t)blockIdx.x * KEYS + kl;
+  const int64_t n = chunk * KEYS + kl;
   float acc = 0.f;
 #pragma unroll 8
   for (int h = 0; h < 64; h++) acc = __builtin_fmaf(sw[h], sr[kl][h], acc);
@@ -301,9 +303,10 @@ __global__ __launch_bounds__(256) void indexer_wide_kernel(const void* __restric
                                                            const float* __restrict__ weights,
                                                            const int32_t* __restrict__ nvis, int64_t S, int Hi,
                                                            int64_t N, float* __restrict__ scores) {
-  const int64_t bs = blockIdx.y;
+  int64_t bs, chunk;
+  xcd_row_item(gridDim.y, gridDim.x, bs, chunk);
   const int64_t b = bs / S;
-  const int64_t n = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t n = chunk * blockDim.x + threadIdx.x;
   if (n >= N) return;
   const int64_t nv = nvis ? (int64_t)nvis[bs] : N;
   if (n >= nv) {
@@ -404,9 +407,10 @@ __global__ __launch_bounds__(256) void indexer_cert_kernel(const uint16_t* __res
   __shared__ float red[4];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int g = lane >> 4, c16 = lane & 15;
-  const int64_t r = blockIdx.y;
+  int64_t r, chunk64;
+  xcd_row_item(gridDim.y, gridDim.x, r, chunk64);
   const int64_t b = r / S;
-  const int chunk = blockIdx.x, nchunk = gridDim.x;
+  const int chunk = (int)chunk64, nchunk = gridDim.x;
   int64_t nv = nvis ? (int64_t)nvis[r] : N;
   nv = nv < 0 ? 0 : (nv > N ? N : nv);
   const int64_t k0 = (int64_t)chunk * kCertKeys;

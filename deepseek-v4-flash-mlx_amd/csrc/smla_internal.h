@@ -209,6 +209,33 @@ __device__ inline int wave_incl_scan(int x) {
 }
 
 // ---------------------------------------------------------------------------------------------
+// XCD pinning.  The workgroups of a launch are dealt to the 8 XCDs round-robin in linear order
+// (workgroup L = x + gx (y + gy z) runs on XCD L mod 8), each XCD has its own L2, and what a kernel
+// leaves in an XCD's L2 is still there for the next kernel (a reader on the writer's XCD sees L2
+// latency, about half the latency of data another XCD wrote and a third of HBM's).  A launch over
+// `rows` x `items` workgroups (rows a multiple of 8) that places every item of row r on XCD
+// r mod 8 therefore hands row r's data to the next kernel that pins rows the same way in one L2:
+// the decode step pins its query rows in the indexer, the selection (one workgroup per row), the
+// attention splits and the merge.
+constexpr int kXcds = 8;
+__device__ inline int64_t linear_block_id() {
+  return (int64_t)blockIdx.x + (int64_t)gridDim.x * ((int64_t)blockIdx.y + (int64_t)gridDim.y * blockIdx.z);
+}
+// (row, item) of this workgroup in a launch of rows * items workgroups: row-major when rows is not a
+// multiple of 8, else pinned (row mod 8 == XCD)
+__device__ inline void xcd_row_item(int64_t rows, int64_t items, int64_t& row, int64_t& item) {
+  const int64_t L = linear_block_id();
+  if (rows % kXcds != 0) {
+    row = L / items;
+    item = L % items;
+    return;
+  }
+  const int64_t i = L / kXcds;
+  row = L % kXcds + kXcds * (i / items);
+  item = i % items;
+}
+
+// ---------------------------------------------------------------------------------------------
 // load one element of a given dtype as fp32
 __device__ inline float load_as_f32(const void* p, int64_t i, int dtype) {
   switch (dtype) {

@@ -13,6 +13,8 @@
 //
 // smla_window_topk_idxs mirrors ref_torch/sparse_attn.py:9-20; smla_decode_window_idxs builds the
 // engine's decode window oracle/decode_engine.py:110-111 over an un-ringed raw cache.
+#include <type_traits>
+
 #include "smla_internal.h"
 
 namespace {
@@ -66,7 +68,7 @@ struct CertCtx {
 };
 
 constexpr int kQS = 68;  // LDS row stride (floats) of the staged q rows: 16-byte per-head reads hit all banks
-constexpr int kRescoreBatch = 4;  // keys a wave rescores together (independent chains interleaved)
+constexpr int kRescoreChunk = 128;  // keys rescored per pass (their fp32 rows and ReLU values sit in LDS)
 constexpr int kStageIds = 4096;   // selections up to this size are staged in LDS for coalesced stores
 
 __device__ inline int bucket_of_score(float s, float lmax, float bscale) {
@@ -113,9 +115,9 @@ __global__ __launch_bounds__(NT) void topk_kernel(const float* scores, int64_t N
   __shared__ int s_nan[kWaves];
   __shared__ float q_s[CERT ? 64 * kQS : 1];
   __shared__ float w_s[CERT ? 64 : 1];
-  __shared__ u32x4_t ck_s[CERT ? kMaxCand * 4 : 1];  // key rows being rescored (64 e4m3 codes each)
-  __shared__ float cks_s[CERT ? kMaxCand : 1];       // their kscale
-  __shared__ float r_s[CERT ? kWaves * kRescoreBatch * 64 : 1];  // per wave: ReLU(dot_h) of its keys
+  __shared__ __align__(16) float kf_s[CERT ? kRescoreChunk * 64 : 1];  // key rows being rescored, fp32
+  __shared__ float rl_s[CERT ? kRescoreChunk * 65 : 1];               // their ReLU(dot_h), [key][head]
+  __shared__ float sc_s[CERT ? kRescoreChunk : 1];                     // their fixed-order sums over h
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int64_t r = blockIdx.x;
@@ -163,57 +165,78 @@ __global__ __launch_bounds__(NT) void topk_kernel(const float* scores, int64_t N
   }
   const int64_t bkey = CERT ? r / cc.S : 0;  // batch entry of the key rows
   // the q row (4 bf16 per thread) and weights: loaded now, staged in LDS after the first barrier
-  u32x2_t qraw = {0u, 0u};
+  // (4096 / NT bf16 values per thread)
+  constexpr int kQPT = 4096 / NT;
+  static_assert(kQPT == 4 || kQPT == 8, "q values per thread");
+  using QRawT = typename std::conditional<kQPT == 4, u32x2_t, u32x4_t>::type;
+  QRawT qraw = {};
   float wraw = 0.f;
   if constexpr (CERT) {
-    qraw = *(const u32x2_t*)(cc.q + r * 4096 + 4 * tid);
+    qraw = *(const QRawT*)(cc.q + r * 4096 + kQPT * tid);
     if (tid < 64) wraw = cc.w[r * 64 + tid];
   }
-  // fixed-order scores of kRescoreBatch keys (rows rows[b] of ck_s, 64 codes each), one batch per
-  // wave: lane h runs head h's chain over d for every key of the batch (independent chains, one q
-  // read for all), the ReLU values go to LDS, and every lane runs each key's chain over the heads
-  // in head order (the arithmetic of indexer_kernel).  Returns acc (before the kscale product).
-  auto exact_batch = [&](const int (&rows)[kRescoreBatch], float (&acc)[kRescoreBatch]) {
-    static_assert(kRescoreBatch == 4, "ReLU values are exchanged as one 16-byte vector per head");
-    float dot[kRescoreBatch];
+  // Fixed-order scores (the arithmetic of indexer2_kernel, before the kscale product) of the cnt
+  // <= kRescoreChunk keys whose fp32 rows are in kf_s, into sc_s.  Wave w takes keys w + kWaves i
+  // (i < kKPW) and lane h runs head h's fma chain over d = 0..63 for all of them at once: per block
+  // of 16 dims the q values are read from LDS once and each key's 16 values by LDS broadcast, so
+  // every chain advances in d order.  The ReLU values go to rl_s; then one thread per key runs the
+  // chain over the heads.  Ends with a barrier (sc_s complete).
+  constexpr int kKPW = kRescoreChunk / kWaves;  // keys per wave (8 or 16)
+  auto exact_chunk = [&](int cnt) {
+    const float* qrow = &q_s[lane * kQS];
+    const int mine = wave < cnt ? (cnt - wave + kWaves - 1) / kWaves : 0;  // this wave's keys
+    float d[kKPW];
 #pragma unroll
-    for (int b = 0; b < kRescoreBatch; b++) dot[b] = 0.f;
+    for (int b = 0; b < kKPW; b++) d[b] = 0.f;
 #pragma unroll 1
-    for (int v = 0; v < 4; v++) {
-      u32x4_t kw[kRescoreBatch];
+    for (int jb = 0; jb < 64; jb += 16) {
+      f32x4_t q4[4];
 #pragma unroll
-      for (int b = 0; b < kRescoreBatch; b++) kw[b] = ck_s[4 * rows[b] + v];
+      for (int e = 0; e < 4; e++) q4[e] = *(const f32x4_t*)&qrow[jb + 4 * e];
 #pragma unroll
-      for (int j = 0; j < 4; j++) {
-        const f32x4_t q4 = *(const f32x4_t*)&q_s[lane * kQS + 16 * v + 4 * j];
+      for (int b = 0; b < kKPW; b++) {
+        if (b < mine) {
+          const float* kr = &kf_s[(wave + kWaves * b) * 64 + jb];
 #pragma unroll
-        for (int b = 0; b < kRescoreBatch; b++) {
-          const f32x2_t lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)kw[b][j], false);
-          const f32x2_t hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)kw[b][j], true);
-          dot[b] = __builtin_fmaf(q4[0], lo.x, dot[b]);
-          dot[b] = __builtin_fmaf(q4[1], lo.y, dot[b]);
-          dot[b] = __builtin_fmaf(q4[2], hi.x, dot[b]);
-          dot[b] = __builtin_fmaf(q4[3], hi.y, dot[b]);
+          for (int e = 0; e < 4; e++) {
+            const f32x4_t kk = *(const f32x4_t*)&kr[4 * e];
+            d[b] = __builtin_fmaf(q4[e][0], kk[0], d[b]);
+            d[b] = __builtin_fmaf(q4[e][1], kk[1], d[b]);
+            d[b] = __builtin_fmaf(q4[e][2], kk[2], d[b]);
+            d[b] = __builtin_fmaf(q4[e][3], kk[3], d[b]);
+          }
         }
       }
     }
-    // ReLU values as [head][key]: one 16-byte read per head serves the whole batch
-    float* rw = r_s + wave * kRescoreBatch * 64;
-    *(f32x4_t*)&rw[4 * lane] = f32x4_t{dot[0] > 0.f ? dot[0] : 0.f, dot[1] > 0.f ? dot[1] : 0.f,
-                                       dot[2] > 0.f ? dot[2] : 0.f, dot[3] > 0.f ? dot[3] : 0.f};
-    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's LDS writes are done
 #pragma unroll
-    for (int b = 0; b < kRescoreBatch; b++) acc[b] = 0.f;
-#pragma unroll 1
-    for (int h4 = 0; h4 < 64; h4 += 4) {
-      const f32x4_t w4 = *(const f32x4_t*)&w_s[h4];
-#pragma unroll
-      for (int i = 0; i < 4; i++) {
-        const f32x4_t r4 = *(const f32x4_t*)&rw[4 * (h4 + i)];
-#pragma unroll
-        for (int b = 0; b < kRescoreBatch; b++) acc[b] = __builtin_fmaf(w4[i], r4[b], acc[b]);
-      }
+    for (int b = 0; b < kKPW; b++)
+      if (b < mine) rl_s[(wave + kWaves * b) * 65 + lane] = d[b] > 0.f ? d[b] : 0.f;
+    __syncthreads();
+    if (tid < cnt) {
+      float acc = 0.f;
+#pragma unroll 16
+      for (int h = 0; h < 64; h++) acc = __builtin_fmaf(w_s[h], rl_s[tid * 65 + h], acc);
+      sc_s[tid] = acc;
     }
+    __syncthreads();
+  };
+  // a chunk's code rows are staged kCPT codes per thread: thread t converts codes
+  // kCPT (t % kTPK) .. of key t / kTPK to fp32 in kf_s
+  constexpr int kCPT = kRescoreChunk * 64 / NT;  // 8 or 16
+  constexpr int kTPK = 64 / kCPT;                // threads per key row
+  static_assert(kCPT == 8 || kCPT == 16, "codes per thread");
+  using CodeT = typename std::conditional<kCPT == 8, u32x2_t, u32x4_t>::type;
+  auto stage_key = [&](int c, CodeT codes) {
+    f32x4_t* dst = (f32x4_t*)&kf_s[c * 64 + kCPT * (tid % kTPK)];
+#pragma unroll
+    for (int i = 0; i < kCPT / 4; i++) {
+      const f32x2_t a = __builtin_amdgcn_cvt_pk_f32_fp8((int)codes[i], false);
+      const f32x2_t b = __builtin_amdgcn_cvt_pk_f32_fp8((int)codes[i], true);
+      dst[i] = f32x4_t{a.x, a.y, b.x, b.y};
+    }
+  };
+  auto key_codes = [&](int64_t n) -> CodeT {
+    return *(const CodeT*)(cc.keys + (bkey * N + n) * 64 + kCPT * (tid % kTPK));
   };
   // the bucket holding the k-th entry (bucket 0 = largest scores) and how many of its entries the
   // selection takes: s_int[0], s_int[1].  Thread t owns buckets kBPT t .. kBPT t + kBPT - 1.
@@ -286,9 +309,12 @@ __global__ __launch_bounds__(NT) void topk_kernel(const float* scores, int64_t N
       }
       for (int i = tid; i <= kBuckets; i += NT) bhist[i] = 0;
       if (CERT && pass == 0) {
-        const int h = (4 * tid) >> 6, d0 = (4 * tid) & 63;
-        *(f32x4_t*)&q_s[h * kQS + d0] = f32x4_t{__uint_as_float(qraw[0] << 16), __uint_as_float(qraw[0] & 0xffff0000u),
-                                                __uint_as_float(qraw[1] << 16), __uint_as_float(qraw[1] & 0xffff0000u)};
+        const int h = (kQPT * tid) >> 6, d0 = (kQPT * tid) & 63;
+#pragma unroll
+        for (int i = 0; i < kQPT / 4; i++)
+          *(f32x4_t*)&q_s[h * kQS + d0 + 4 * i] =
+              f32x4_t{__uint_as_float(qraw[2 * i] << 16), __uint_as_float(qraw[2 * i] & 0xffff0000u),
+                      __uint_as_float(qraw[2 * i + 1] << 16), __uint_as_float(qraw[2 * i + 1] & 0xffff0000u)};
         if (tid < 64) w_s[tid] = wraw;
       }
       __syncthreads();
@@ -377,30 +403,24 @@ __global__ __launch_bounds__(NT) void topk_kernel(const float* scores, int64_t N
         __syncthreads();
         const int total = s_int[3], ucnt = s_int[4];
         if (total <= kMaxCand) {
-          // exact scores of the band: its key rows and scales to LDS in one round trip, then one
-          // wave per entry
-          for (int t = tid; t < total * 4; t += NT)
-            ck_s[t] = *(const u32x4_t*)(cc.keys + (bkey * N + cand_idx[t >> 2]) * 64 + 16 * (t & 3));
-          if (cc.kscale)
-            for (int c = tid; c < total; c += NT) cks_s[c] = cc.kscale[bkey * N + cand_idx[c]];
-          __syncthreads();
-          // kRescoreBatch entries per wave at a time: c0 + b * kWaves (past the end: entry c0 again)
+          // exact scores of the band, kRescoreChunk keys per pass (one pass for the usual band):
+          // their code rows to LDS as fp32, the fixed-order chains, then the kscale product
 #pragma unroll 1
-          for (int c0 = wave; c0 < total; c0 += kRescoreBatch * kWaves) {
-            int rows[kRescoreBatch];
-#pragma unroll
-            for (int b = 0; b < kRescoreBatch; b++) rows[b] = c0 + b * kWaves < total ? c0 + b * kWaves : c0;
-            float acc[kRescoreBatch];
-            exact_batch(rows, acc);
-            if (lane == 0) {
-#pragma unroll
-              for (int b = 0; b < kRescoreBatch; b++) {
-                const int c = c0 + b * kWaves;
-                if (c < total) {
-                  const float sx = cc.kscale ? acc[b] * cks_s[c] : acc[b];
-                  cand_pair[c] = ((uint64_t)desc_key(sx) << 32) | (uint32_t)cand_idx[c];
-                }
-              }
+          for (int c0 = 0; c0 < total; c0 += kRescoreChunk) {
+            const int cnt = total - c0 < kRescoreChunk ? total - c0 : kRescoreChunk;
+            const int ck = tid / kTPK;
+            float ksv = 1.f;
+            if (ck < cnt) {
+              const int n = cand_idx[c0 + ck];
+              stage_key(ck, key_codes(n));
+              if (cc.kscale) ksv = cc.kscale[bkey * N + n];
+            }
+            __syncthreads();
+            exact_chunk(cnt);
+            if (tid % kTPK == 0 && ck < cnt) {
+              const float acc = sc_s[ck];
+              const float sx = cc.kscale ? acc * ksv : acc;
+              cand_pair[c0 + ck] = ((uint64_t)desc_key(sx) << 32) | (uint32_t)cand_idx[c0 + ck];
             }
           }
           __syncthreads();
@@ -419,29 +439,24 @@ __global__ __launch_bounds__(NT) void topk_kernel(const float* scores, int64_t N
         }
         in_mask = band_mask = 0;
       }
-      // not certifiable: every visible key's exact score (one wave per key, written over the
-      // approximations), then the exact selection below
+      // not certifiable: every visible key's exact score (written over the approximations), then
+      // the exact selection below; kRescoreChunk consecutive keys per pass, the next pass's code
+      // rows loaded into registers while the current one is scored
       float* resc = cc.rescored + r * N;
-      // kRescoreBatch keys per wave at a time: n0 + b * kWaves; their rows go to the wave's own
-      // ck_s rows (lanes 0 .. 4 kRescoreBatch - 1 load 16 bytes each)
+      {
+        const int ck = tid / kTPK;
+        auto load_next = [&](int n0) -> CodeT { return key_codes(n0 + ck < nv ? n0 + ck : nv - 1); };
+        CodeT nxt = load_next(0);
 #pragma unroll 1
-      for (int n0 = wave; n0 < nv; n0 += kRescoreBatch * kWaves) {
-        const int bl = (lane >> 2) & (kRescoreBatch - 1);
-        const int nl = n0 + bl * kWaves < nv ? n0 + bl * kWaves : n0;
-        if (lane < 4 * kRescoreBatch)
-          ck_s[4 * (wave * kRescoreBatch + bl) + (lane & 3)] =
-              *(const u32x4_t*)(cc.keys + (bkey * N + nl) * 64 + 16 * (lane & 3));
-        __builtin_amdgcn_s_waitcnt(0xc07f);
-        int rows[kRescoreBatch];
-#pragma unroll
-        for (int b = 0; b < kRescoreBatch; b++) rows[b] = wave * kRescoreBatch + b;
-        float acc[kRescoreBatch];
-        exact_batch(rows, acc);
-        if (lane == 0) {
-#pragma unroll
-          for (int b = 0; b < kRescoreBatch; b++) {
-            const int n = n0 + b * kWaves;
-            if (n < nv) resc[n] = cc.kscale ? acc[b] * cc.kscale[bkey * N + n] : acc[b];
+        for (int n0 = 0; n0 < nv; n0 += kRescoreChunk) {
+          const int cnt = nv - n0 < kRescoreChunk ? nv - n0 : kRescoreChunk;
+          stage_key(ck, nxt);
+          if (n0 + kRescoreChunk < nv) nxt = load_next(n0 + kRescoreChunk);
+          __syncthreads();
+          exact_chunk(cnt);
+          if (tid < cnt) {
+            const int n = n0 + tid;
+            resc[n] = cc.kscale ? sc_s[tid] * cc.kscale[bkey * N + n] : sc_s[tid];
           }
         }
       }

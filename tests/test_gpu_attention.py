@@ -145,10 +145,10 @@ def test_all_masked_rows_are_nan(dev):
 @pytest.mark.parametrize("B,T,n,sharp,H,D", [(1, 64, 200, 1.0, 64, 576), (3, 700, 2000, 40.0, 64, 576),
                                            (2, 2048, 2048, 1.0, 64, 576), (2, 333, 900, 10.0, 48, 576),
                                            (2, 300, 500, 5.0, 64, 512)])
-def test_fp8_rows_vs_oracle(dev, decode_kernel, B, T, n, sharp, H, D):
+def test_fp8_rows_vs_oracle(dev, B, T, n, sharp, H, D):
     from smla import sparse_attn as ssa
     from smla import workloads as wl
-    announce(f"fp8 rows kernel={decode_kernel} B={B} T={T} n={n} H={H} D={D}")
+    announce(f"fp8 rows B={B} T={T} n={n} H={H} D={D}")
     g = torch.Generator().manual_seed(T)
     q = (torch.randn(B, 1, H, D, generator=g) * 0.05 * sharp).to(torch.bfloat16)
     x = torch.randn(B, n, D, generator=g) * 0.05
