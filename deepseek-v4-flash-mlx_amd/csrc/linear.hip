@@ -329,13 +329,22 @@ int launch_linear(const void* x, const void* w, int64_t T, int64_t G, int64_t N,
   return launch_linear_t<false, SMLA_F32>(xb, wb, T, G, N, K, ldx, nullptr, nullptr, nullptr, 0, 0, y, st);
 }
 
+// The decode form (the weight-streaming kernels above) takes up to 32 bf16 token rows with N % 16 == 0
+// and K % 512 == 0; everything else goes to the tiled MFMA GEMM (gemm.hip): bf16 or fp32 operands,
+// rows of a multiple of 16 bytes (K % 8 bf16, K % 4 fp32).
+bool decode_form(int x_dtype, int64_t T, int64_t N, int64_t K) {
+  return x_dtype == SMLA_BF16 && T <= 32 && N % 16 == 0 && K % (64 * kLinWaves) == 0;
+}
+
 int check_linear(const void* x, int x_dtype, const void* w, int w_dtype, int64_t T, int64_t G, int64_t N, int64_t K,
                  const void* y, int y_dtype) {
   if (!x || !w || !y) return SMLA_E_NULL;
   if (T <= 0 || G <= 0 || N <= 0 || K <= 0) return SMLA_E_SHAPE;
-  if (x_dtype != SMLA_BF16 || w_dtype != SMLA_BF16 || (y_dtype != SMLA_BF16 && y_dtype != SMLA_F32)) return SMLA_E_DTYPE;
-  if (T > 32 || N % 16 != 0 || K % (64 * kLinWaves) != 0 || G * N / 16 > 0x7fffffff || G * K > 0x7fffffff)
-    return SMLA_E_UNSUPPORTED;
+  if (x_dtype != w_dtype || (x_dtype != SMLA_BF16 && x_dtype != SMLA_F32) ||
+      (y_dtype != SMLA_BF16 && y_dtype != SMLA_F32))
+    return SMLA_E_DTYPE;
+  if (G * N / 16 > 0x7fffffff || G * K > 0x7fffffff || T > 0x7fffffff / 2) return SMLA_E_UNSUPPORTED;
+  if (!decode_form(x_dtype, T, N, K) && K % (x_dtype == SMLA_BF16 ? 8 : 4) != 0) return SMLA_E_UNSUPPORTED;
   if (((uintptr_t)x & 15) || ((uintptr_t)w & 15) || ((uintptr_t)y & 15)) return SMLA_E_UNSUPPORTED;
   return SMLA_OK;
 }
@@ -353,6 +362,9 @@ extern "C" int smla_linear(const void* x, int x_dtype, const void* w, int w_dtyp
                            int64_t K, void* y, int y_dtype, void* stream) {
   int rc = check_linear(x, x_dtype, w, w_dtype, T, G, N, K, y, y_dtype);
   if (rc) return rc;
+  if (!decode_form(x_dtype, T, N, K))
+    return launch_gemm_tiled(x, G * K, x_dtype == SMLA_F32, w, T, G, N, K, nullptr, nullptr, nullptr, 0, y, y_dtype,
+                             (hipStream_t)stream);
   return launch_linear(x, w, T, G, N, K, nullptr, nullptr, nullptr, 0, 0, y, y_dtype, (hipStream_t)stream);
 }
 
@@ -387,18 +399,26 @@ extern "C" int smla_o_proj(const void* o, int o_dtype, const int32_t* pos, const
   if (T <= 0 || heads <= 0 || head_dim <= 0 || G <= 0 || R <= 0 || dim <= 0) return SMLA_E_SHAPE;
   if ((heads * head_dim) % G != 0) return SMLA_E_SHAPE;
   const int64_t Kg = heads * head_dim / G;  // width of one group's slice of o
+  if (o_dtype != SMLA_BF16 || w_dtype != SMLA_BF16) return SMLA_E_DTYPE;
   int rc = check_linear(o, o_dtype, wo_a, w_dtype, T, G, R, Kg, mid, SMLA_BF16);
   if (rc) return rc;
   rc = check_linear(mid, SMLA_BF16, wo_b, w_dtype, T, 1, dim, G * R, y, y_dtype);
   if (rc) return rc;
+  const bool dform = decode_form(o_dtype, T, R, Kg);
   if (pos) {
     rc = check_rope_args(pos, cos_t, sin_t, n_pos, heads, head_dim, rd);
     if (rc) return rc;
-    // every 64-wide K step lies inside one head, all rope dims or none
-    if (head_dim % 64 != 0 || rd % 64 != 0 || Kg % head_dim != 0) return SMLA_E_UNSUPPORTED;
+    // every 64-wide K step lies inside one head, all rope dims or none; the tiled GEMM rotates
+    // exactly the last 64 dims of each head
+    if (head_dim % 64 != 0 || rd % 64 != 0 || Kg % head_dim != 0 || (!dform && rd != 64)) return SMLA_E_UNSUPPORTED;
   }
   hipStream_t st = (hipStream_t)stream;
-  rc = launch_linear(o, wo_a, T, G, R, Kg, pos, cos_t, sin_t, (int)head_dim, (int)rd, mid, SMLA_BF16, st);
+  if (dform)
+    rc = launch_linear(o, wo_a, T, G, R, Kg, pos, cos_t, sin_t, (int)head_dim, (int)rd, mid, SMLA_BF16, st);
+  else
+    rc = launch_gemm_tiled(o, G * Kg, false, wo_a, T, G, R, Kg, pos, cos_t, sin_t, head_dim, mid, SMLA_BF16, st);
   if (rc) return rc;
+  if (!decode_form(SMLA_BF16, T, dim, G * R))
+    return launch_gemm_tiled(mid, G * R, false, wo_b, T, 1, dim, G * R, nullptr, nullptr, nullptr, 0, y, y_dtype, st);
   return launch_linear(mid, wo_b, T, 1, dim, G * R, nullptr, nullptr, nullptr, 0, 0, y, y_dtype, st);
 }

@@ -258,6 +258,13 @@ int launch_indexer_cert(const uint16_t* q, const uint8_t* keys, const float* ksc
                         const int32_t* nvis, int64_t B, int64_t S, int64_t N, float* approx, float* ebound,
                         hipStream_t st);
 
+// tiled MFMA GEMM (gemm.hip): y [T, G*N] = grouped x [T, G*K] (row stride ldx) times w [G*N, K]^T,
+// operands both bf16 or both fp32 (f32_operands), y bf16 or fp32; with pos, inverse RoPE of the
+// last 64 dims of every head_dim-wide head of x (bf16) as it is loaded
+int launch_gemm_tiled(const void* x, int64_t ldx, bool f32_operands, const void* w, int64_t T, int64_t G, int64_t N,
+                      int64_t K, const int32_t* pos, const float* cos_t, const float* sin_t, int64_t head_dim,
+                      void* y, int y_dtype, hipStream_t st);
+
 #define SMLA_HIP_CHECK_LAUNCH()                         \
   do {                                                  \
     hipError_t _e = hipGetLastError();                  \

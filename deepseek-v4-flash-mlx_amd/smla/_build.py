@@ -8,7 +8,7 @@ from concurrent.futures import ThreadPoolExecutor
 _HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(os.path.dirname(_HERE), "csrc")
 SOURCES = ["attn.hip", "attn_decode.hip", "indexer.hip", "topk.hip", "pool.hip", "qat.hip", "linear.hip",
-           "capi.hip"]
+           "gemm.hip", "capi.hip"]
 OUT = os.path.join(_HERE, "libsmla.so")
 # linker version script: only the smla_* C entry points are exported
 EXPORTS = os.path.join(CSRC, "libsmla.map")

@@ -3,8 +3,9 @@
 * ``overlap_transform(tensor, ratio, d, value)`` — ``ref_torch/compressor.py:12-18`` (a layout op,
   done with torch indexing on the device).
 * ``compressor_prefill(x, wkv, wgate, ape, norm_w, ...)`` — ``ref_torch/compressor.py:21-50``:
-  projections with torch.matmul (fp32), pooling + RMSNorm + RoPE in the HIP ``gated_pool``
-  kernel; returns (kv, state) like the reference.  ``fp8_sim`` adds the fp8 round trip of the
+  the two projections in one tiled MFMA GEMM over [wkv; wgate] (fp32 operands for fp32 inputs,
+  bf16 for bf16), pooling + RMSNorm + RoPE in the HIP ``gated_pool`` kernel; returns (kv, state)
+  like the reference.  ``fp8_sim`` adds the fp8 round trip of the
   non-rope channels (``v4mlx/compressor.py:60-62``); ``rotate`` the indexer compressor's
   Hadamard + fp4 round trip of all channels (``v4mlx/compressor.py:57-59``), in the same kernel.
 * ``block_mean_pool(kv, ratio)`` — plain block mean, HIP.
@@ -37,9 +38,7 @@ def compressor_prefill(x, wkv, wgate, ape, norm_w, head_dim=512, ratio=4, rope_h
     """x:[b,s,dim] -> (kv:[b, s//ratio, head_dim] fp32 post-RoPE, state dict)."""
     ops._on_gpu(x, wkv, wgate, ape, norm_w)
     b, s, _ = x.shape
-    xf = x.float()
-    kv = xf @ wkv.float().t()
-    score = xf @ wgate.float().t()
+    kv, score = project_pair(x, wkv, wgate)
     rem = s % ratio
     cut = s - rem
     state = {}
@@ -55,6 +54,20 @@ def compressor_prefill(x, wkv, wgate, ape, norm_w, head_dim=512, ratio=4, rope_h
     out = ops.gated_pool_op(kv[:, :cut], score[:, :cut], ape, norm_w, cos_t, sin_t, ratio, rope_head_dim,
                             1e-6, _sim(fp8_sim, rotate))
     return out, state
+
+
+def project_pair(x, wkv, wgate):
+    """(x @ wkv^T, x @ wgate^T) as fp32 [b, s, 2*head_dim] each, from one ``smla_linear`` call over
+    the stacked weights: fp32 operands unless x and both weights are bf16."""
+    b, s, dim = x.shape
+    wcat = torch.cat([wkv, wgate], dim=0)
+    if x.dtype == torch.bfloat16 and wcat.dtype == torch.bfloat16:
+        y = ops.linear_op(x.reshape(b * s, dim), wcat, 1, torch.float32)
+    else:
+        y = ops.linear_op(x.float().reshape(b * s, dim), wcat.float(), 1, torch.float32)
+    y = y.reshape(b, s, -1)
+    n = wkv.shape[0]
+    return y[..., :n], y[..., n:]
 
 
 def block_mean_pool(kv, ratio=4):

@@ -3,7 +3,9 @@
 ``xn`` to ``o_grouped``; the hyper-connection mixing around it, ``hc_pre`` / ``hc_post``, belongs
 to the model, not to this path).
 
-Per token at position p, for each of B sequences:
+``DecodeLayer.prefill`` ingests a prompt (the branch with ``decode_pos=None``, ``:86-95,107-117``);
+``DecodeLayer.step`` then advances one token per call.  Per token at position p, for each of B
+sequences:
 
 * q  = perhead_norm(q_up(rmsnorm(q_down(xn), q_a_norm))), RoPE on the last 64 dims of each head
   (``decode_engine.py:78-80``);
@@ -60,11 +62,8 @@ class LayerWeights:
 
 
 def _proj(x, W):
-    """x @ W^T with an fp32 result: the HIP projection kernel at decode shapes (bf16 operands, fp32
-    accumulation and output), a float32 product otherwise."""
-    if mla._decode_shape(x, W) and W.shape[0] % 16 == 0:
-        return ops.linear_op(x.contiguous(), W, 1, torch.float32)
-    return x.float() @ W.float().t()
+    """x @ W^T with an fp32 result (bf16 operands, fp32 accumulation), ``smla_linear``."""
+    return ops.linear_op(x.contiguous(), W, 1, torch.float32)
 
 
 class DecodeLayer:
@@ -106,12 +105,13 @@ class DecodeLayer:
 
     # -- pieces (each mirrors one span of decode_engine.py) --------------------------------------
     def q_path(self, qa_f, pos):
-        """``decode_engine.py:78-80``: q [B, 64, 512] bf16 from the q_down projection qa_f,
-        per-head normed, rope dims rotated."""
-        qa = torch.empty(self.B, qa_f.shape[1], dtype=torch.bfloat16, device=qa_f.device)
+        """``decode_engine.py:78-80``: q [rows, 64, 512] bf16 from the q_down projection qa_f
+        [rows, 1024] of tokens at positions pos [rows], per-head normed, rope dims rotated."""
+        rows = qa_f.shape[0]
+        qa = torch.empty(rows, qa_f.shape[1], dtype=torch.bfloat16, device=qa_f.device)
         ops.row_epilogue(qa_f, self.q_a_norm, None, None, None, 0, _lib.SIM_NONE, qa)
-        q = torch.empty(self.B, N_HEADS, HEAD_DIM, dtype=torch.bfloat16, device=qa_f.device)
-        ops.row_epilogue(_proj(qa, self.w.wq_b).view(self.B * N_HEADS, HEAD_DIM), None, pos, self.cos_t, self.sin_t,
+        q = torch.empty(rows, N_HEADS, HEAD_DIM, dtype=torch.bfloat16, device=qa_f.device)
+        ops.row_epilogue(_proj(qa, self.w.wq_b).view(rows * N_HEADS, HEAD_DIM), None, pos, self.cos_t, self.sin_t,
                          ROPE_HD, _lib.SIM_NONE, q, rows_per_pos=N_HEADS)
         return q
 
@@ -145,6 +145,47 @@ class DecodeLayer:
         # visible compressed rows at p: (p+1)//4 (decode_engine.py:112), at most the cache's rows
         nvis = torch.clamp(torch.div(pos + 1, 4, rounding_mode="floor"), max=self.ncap).to(torch.int32)
         return _idx.select_decode_indices(scores, k, pos, WINDOW, self.max_pos, nvis=nvis)
+
+    # -- prompt ingestion ------------------------------------------------------------------------
+    def prefill(self, xn):
+        """``decode_engine.py:73-117`` with ``decode_pos=None``: the prompt of every sequence, xn
+        [B, S, 4096] bf16 at positions 0..S-1 (S <= max_pos), into a fresh layer.  Writes the S
+        window rows; a ratio-4 layer pools the prompt's S // 4 compressed rows (the gated pool of
+        ``compressor_prefill`` with the fp8 round trip, ``:87-89``) and sets the ring from its last
+        group and remainder (``:90-95``); then every position attends to its window and the
+        compressed rows visible to it (``:107-116``).  Returns the layer's attention output
+        [B, S, 4096] bf16; decoding continues with ``step`` at position S."""
+        ops._on_gpu(xn)
+        if xn.dim() != 3 or xn.shape[0] != self.B or xn.shape[2] != self.w.wq_a.shape[1]:
+            raise ValueError(f"xn must be [{self.B}, S, {self.w.wq_a.shape[1]}]")
+        B, S, dim = xn.shape
+        if not 0 < S <= self.max_pos:
+            raise ValueError(f"the prompt length must lie in 1..{self.max_pos}")
+        dev = xn.device
+        pos = torch.arange(S, dtype=torch.int32, device=dev).repeat(B)      # position of each (b, s) row
+        y = _proj(xn.reshape(B * S, dim), self.w_in)                        # [B*S, projection widths] fp32
+        c = self.cuts
+        q = self.q_path(y[:, c[0]:c[1]], pos)                               # [B*S, 64, 512]
+        for b in range(B):                                                  # window rows 0..S-1
+            ops.row_epilogue(y[b * S:(b + 1) * S, c[1]:c[2]], self.kv_a_norm, pos[:S], self.cos_t, self.sin_t,
+                             ROPE_HD, _lib.SIM_FP8, self.raw[b, :S])
+        T = WINDOW
+        if self.ring_ratio:
+            kvp = y[:, c[2]:c[3]].reshape(B, S, -1)
+            scp = y[:, c[3]:c[4]].reshape(B, S, -1)
+            cut = S - S % 4
+            if cut >= 4:
+                comp = ops.gated_pool_op(kvp[:, :cut], scp[:, :cut], self.ring.ape, self.ring.norm_w, self.ring.cos_t,
+                                         self.ring.sin_t, 4, ROPE_HD, 1e-6, _lib.SIM_FP8)
+                self.comp32[:, :cut // 4] = comp
+                self.comp[:, :cut // 4] = comp.to(torch.bfloat16)
+            self.ring.init_from_prefill(kvp, scp)
+            T += S // 4
+        ids = ops.decode_ids(pos, WINDOW, self.ring_ratio, self.max_pos, self.ncap, T)   # [B*S, T]
+        o = _sa.sparse_attn_two_source(q.view(B, S, N_HEADS, HEAD_DIM), self.raw, self.comp, self.w.sinks.float(),
+                                       ids.view(B, S, T), HEAD_DIM ** -0.5, dv=HEAD_DIM)
+        out = mla.o_project(o.view(B * S, N_HEADS, HEAD_DIM), pos, self.cos_t, self.sin_t, self.w.wo_a, self.w.wo_b)
+        return out.view(B, S, -1)
 
     # -- the step --------------------------------------------------------------------------------
     def step(self, xn, pos, scores=None, k=2048):

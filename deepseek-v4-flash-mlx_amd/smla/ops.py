@@ -340,7 +340,8 @@ _YDT = {torch.float32: _lib.F32, torch.bfloat16: _lib.BF16}
 
 @torch.library.custom_op("smla::linear", mutates_args=(), device_types="cuda")
 def linear_op(x: torch.Tensor, w: torch.Tensor, groups: int, out_dtype: torch.dtype) -> torch.Tensor:
-    """x [T, G*K] bf16, w [G*N, K] bf16 -> y [T, G*N] (T <= 32): y[:, gN:(g+1)N] = x[:, gK:(g+1)K] @ w_g^T."""
+    """x [T, G*K], w [G*N, K] (both bf16 or both fp32) -> y [T, G*N]: y[:, gN:(g+1)N] = x[:, gK:(g+1)K] @ w_g^T
+    (the weight-streaming kernel up to 32 bf16 rows, the tiled MFMA GEMM otherwise)."""
     _on_gpu(x, w)
     x, w = x.contiguous(), w.contiguous()
     T = x.shape[0]
@@ -382,7 +383,7 @@ def o_proj_op(o: torch.Tensor, pos: Optional[torch.Tensor], cos_t: Optional[torc
               sin_t: Optional[torch.Tensor], wo_a: torch.Tensor, wo_b: torch.Tensor, groups: int,
               out_dtype: torch.dtype) -> torch.Tensor:
     """o [T, heads, head_dim] bf16 -> [T, dim]: inverse RoPE of the rope dims at pos (when given),
-    grouped projection by wo_a [G*R, heads*head_dim/G], then wo_b [dim, G*R] (T <= 32)."""
+    grouped projection by wo_a [G*R, heads*head_dim/G], then wo_b [dim, G*R] (any T)."""
     tensors = [o, wo_a, wo_b] + ([pos, cos_t, sin_t] if pos is not None else [])
     _on_gpu(*tensors)
     o, wo_a, wo_b = o.contiguous(), wo_a.contiguous(), wo_b.contiguous()

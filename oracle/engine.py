@@ -98,6 +98,48 @@ def index_list(p, n_window_rows, n_comp, ratio, scores=None, k=2048):
     return torch.tensor(widx + cidx, dtype=torch.int32)
 
 
+def prefill(st, w, xn):
+    """The prefill branch of ``oracle/decode_engine.py:73-117`` for a prompt at positions 0..S-1:
+    xn [S, dim] (fp32).  Appends every token's window row, fills the compressed list with the
+    prompt's pooled rows (``compressor.gated_pool`` over the float64 projections, then the fp8
+    round trip of the non-rope dims, ``:87-89``) and sets the ring from the prompt's last group
+    (``compressor.ring_init``, ``:90-95``); then each position i attends to window rows
+    max(0, i-127)..i and the first min(n_comp, (i+1)//4) compressed rows of the whole prompt's
+    [window; compressed] buffer (``:107-116``).  Returns (y [S, dim_out] float64, ids per position,
+    o [S, 64, 512] fp32)."""
+    x = np.asarray(xn, dtype=np.float64)
+    S = x.shape[0]
+    qa = _nr.rmsnorm(torch.from_numpy(_mla.linear(x, w.wq_a)).float(), w.q_a_norm)
+    q = torch.from_numpy(_mla.linear(qa.numpy(), w.wq_b)).float().reshape(S, 64, 512)
+    q = q * torch.rsqrt(q.pow(2).mean(-1, keepdim=True) + 1e-6)
+    q = torch.stack([torch.cat([q[i, :, :-RD], rope_at(q[i, :, -RD:], st, i)], dim=-1) for i in range(S)])
+    kvn = _nr.rmsnorm(torch.from_numpy(_mla.linear(x, w.wkv)).float(), w.kv_a_norm)
+    for i in range(S):
+        kv = torch.cat([kvn[i, :-RD], rope_at(kvn[i, -RD:], st, i)])
+        nope, _ = _fp8.act_quant_sim(kv[:-RD].numpy()[None], 64)
+        st.win.append(torch.cat([torch.from_numpy(nope[0]), kv[-RD:]]))
+    if st.ratio == 4:
+        kvf = torch.from_numpy(_mla.linear(x, w.wkv_c)).float()
+        scf = torch.from_numpy(_mla.linear(x, w.wgate_c)).float()
+        cut = S - S % 4
+        if cut >= 4:
+            freqs = _nr.precompute_freqs_cis(RD, S, *YARN)
+            comp = _comp.gated_pool(kvf[None, :cut], scf[None, :cut], w.ape, w.norm_c, freqs, 4, RD)[0]
+            nope, _ = _fp8.act_quant_sim(comp[:, :-RD].numpy(), 64)
+            comp = torch.cat([torch.from_numpy(nope), comp[:, -RD:]], dim=-1)
+            st.comp = [comp[j] for j in range(comp.shape[0])]
+        st.kvs, st.scs = _comp.ring_init(kvf, scf, w.ape, 4)
+    kvcat = torch.stack(st.win + st.comp)
+    ids_all, o_all = [], []
+    for i in range(S):
+        ids = index_list(i, len(st.win), len(st.comp), st.ratio)
+        ids_all.append(ids)
+        o_all.append(_sa.sparse_attn(q[i][None], kvcat, w.sinks, ids[None], 512 ** -0.5)[0])
+    o = torch.stack(o_all)
+    y = _mla.o_project(o, torch.arange(S), st.cos, st.sin, w.wo_a, w.wo_b)
+    return np.asarray(y), ids_all, o
+
+
 def decode_step(st, w, xn, p, scores=None, k=2048):
     """One token at position p: xn [dim] (fp32); optional indexer scores [n_slots] select the
     top-k visible compressed rows (``index_list``).  Returns (y [dim_out] float64, the window row

@@ -228,7 +228,7 @@ def test_batched_fp8_full_size(dev):
                                   dv=512, kv_scale=w["scales"].to(dev))
     assert out.dtype == torch.bfloat16 and out.shape == (64, 1, 64, 512)
     outs = out.float().cpu()
-    for b in range(0, 64, 7):
+    for b in range(64):
         rows = wl.dequant_e4m3(w["codes"][b], w["scales"][b])
         ref = osa.sparse_attn(w["q"][b].float(), rows, None, w["idx"][b].long(), w["scale"], dv=512)
         _check_bf16(outs[b], ref, f"batched_fp8 b={b}")

@@ -113,6 +113,56 @@ def test_decode_layer_indexer_topk_vs_oracle(dev, k, steps):
             assert r <= 1e-2, f"step {p} seq {b}: output rel err {r:.3e}"
 
 
+@pytest.mark.parametrize("ratio,S,steps", [(4, 37, 6), (4, 140, 5), (0, 30, 3), (128, 133, 3)])
+def test_prefill_then_decode_vs_oracle(dev, ratio, S, steps):
+    """``DecodeLayer.prefill`` on a prompt of S tokens (a remainder group, a window that wraps past
+    128 rows), then ``step`` from position S: every prompt position's output within 1e-2 relative
+    L2 of the oracle prefill, the window and compressed rows as in the decode test, and the decode
+    steps that follow (which read the ring the prefill set) within 1e-2."""
+    from smla import engine
+    announce(f"prefill ratio={ratio} S={S} then {steps} steps")
+    t = _make_weights(ratio, seed=21)
+    w = engine.LayerWeights(**{k: v.to(dev) for k, v in t.items()})
+    wo = oe.OracleWeights(**{k: (v.double().numpy() if v.dtype == torch.bfloat16 else v.float())
+                             for k, v in t.items()})
+    B, max_pos = 2, 256
+    layer = engine.DecodeLayer(w, B, ratio, max_pos=max_pos, device=dev)
+    states = [oe.LayerState(ratio, max_pos=max_pos) for _ in range(B)]
+    g = torch.Generator().manual_seed(300 + S)
+    xp = torch.randn(B, S, 4096, generator=g).to(torch.bfloat16)
+    y = layer.prefill(xp.to(dev)).float().cpu()
+    for b in range(B):
+        yr, _, _ = oe.prefill(states[b], wo, xp[b].float())
+        for i in range(S):
+            r = _rel(y[b, i], yr[i])
+            assert r <= 1e-2, f"prefill seq {b} position {i}: output rel err {r:.3e}"
+            _check_row(layer.raw[b, i].float().cpu(), states[b].win[i], 1e-2, f"prefill seq {b}: window row {i}")
+        assert len(states[b].comp) == (S // 4 if ratio == 4 else 0)
+        for j in range(len(states[b].comp)):
+            _check_row(layer.comp32[b, j].cpu(), states[b].comp[j], 2e-2, f"prefill seq {b}: compressed row {j}")
+    for p in range(S, S + steps):
+        xn = torch.randn(B, 4096, generator=g).to(torch.bfloat16)
+        y = layer.step(xn.to(dev), torch.full((B,), p, dtype=torch.int32, device=dev)).float().cpu()
+        for b in range(B):
+            yr, _, _, _ = oe.decode_step(states[b], wo, xn[b].float(), p)
+            r = _rel(y[b], yr)
+            assert r <= 1e-2, f"step {p} seq {b}: output rel err {r:.3e}"
+            if ratio == 4 and (p + 1) % 4 == 0:
+                j = (p + 1) // 4 - 1
+                _check_row(layer.comp32[b, j].cpu(), states[b].comp[j], 2e-2, f"step {p} seq {b}: compressed row {j}")
+
+
+def test_prefill_rejects_bad_shapes(dev):
+    from smla import engine
+    t = _make_weights(0)
+    layer = engine.DecodeLayer(engine.LayerWeights(**{k: v.to(dev) for k, v in t.items()}), 2, 0, max_pos=64,
+                               device=dev)
+    with pytest.raises(ValueError):
+        layer.prefill(torch.zeros(2, 65, 4096, dtype=torch.bfloat16, device=dev))     # longer than max_pos
+    with pytest.raises(ValueError):
+        layer.prefill(torch.zeros(1, 8, 4096, dtype=torch.bfloat16, device=dev))      # wrong batch
+
+
 def test_decode_layer_rejects_cpu_and_bad_ratio(dev):
     from smla import engine
     t = _make_weights(0)

@@ -67,10 +67,10 @@ def test_prefill_vs_oracle(dev, n_raw, q_pos0, S, H, use_sink, one_split):
     _check(out[0], ref, "prefill")
 
 
-def test_prefill_4k_full_size_sampled(dev):
+def test_prefill_4k_full_size(dev):
     """The full prefill workload (S=4096 queries over a 4096-row sequence): every query's output
-    is computed on the GPU; 64 of them (first, last and random positions) are checked against
-    the oracle, and the empty-set guarantee holds (no NaN anywhere: every query sees itself)."""
+    is computed on the GPU and checked against the oracle, and the empty-set guarantee holds (no
+    NaN anywhere: every query sees itself)."""
     from smla import compressor as scomp
     from smla import sparse_attn as ssa
     from smla import workloads as wl
@@ -83,8 +83,8 @@ def test_prefill_4k_full_size_sampled(dev):
     out = ssa.sparse_attn_two_source(q.to(dev), raw_d, comp_d, None, idx[None].to(dev), w["scale"], dv=512)
     torch.cuda.synchronize()
     assert not torch.isnan(out).any()
-    rng = np.random.default_rng(0)
-    pick = np.unique(np.concatenate([[0, 1, 127, 128, 4095], rng.integers(0, 4096, 59)]))
     kv = torch.cat([raw[0].float(), comp_d.cpu()[0].float()])
-    ref = osa.sparse_attn(q[0, pick].float(), kv, None, idx[pick], w["scale"], dv=512)
-    _check(out[0, pick], ref, "prefill_4k sampled")
+    outs = out[0].float().cpu()
+    for q0 in range(0, 4096, 256):   # every query, 256 at a time (the oracle gathers [256, T, 576])
+        ref = osa.sparse_attn(q[0, q0:q0 + 256].float(), kv, None, idx[q0:q0 + 256], w["scale"], dv=512)
+        _check(outs[q0:q0 + 256], ref, f"prefill_4k queries {q0}..{q0 + 255}")

@@ -23,14 +23,15 @@ def w64(dev):
     w = wl.decode_64k()
     raw = w["raw"].to(dev)
     comp = scomp.block_mean_pool(raw, 4)
-    return w, raw, comp
+    kv = torch.cat([raw[0].cpu().float(), comp[0].cpu().float()])   # the oracle's [raw; compressed] rows
+    return w, raw, comp, kv
 
 
-@pytest.mark.parametrize("step", [0, 3, 4, 19])
+@pytest.mark.parametrize("step", range(20))
 def test_decode_64k_step(dev, w64, step):
     from smla import indexer as sidx
     from smla import sparse_attn as ssa
-    w, raw, comp = w64
+    w, raw, comp, kv = w64
     p = w["pos0"] + step
     nv = (p + 1) // 4
     announce(f"decode_64k step={step} pos={p} visible compressed={nv}")
@@ -51,7 +52,6 @@ def test_decode_64k_step(dev, w64, step):
     ids_ref = np.concatenate([np.arange(p - win + 1, p + 1), np.where(sel >= 0, sel + n_raw, -1)]).astype(np.int32)
     np.testing.assert_array_equal(idx[0].cpu().numpy(), ids_ref)
     # attention
-    kv = torch.cat([raw[0].cpu().float(), comp[0].cpu().float()])
     ref = osa.sparse_attn(w["q"][step].float(), kv, None, torch.from_numpy(ids_ref)[None], w["scale"], dv=512)
     o = out[0].float().cpu()
     assert not torch.isnan(o).any()

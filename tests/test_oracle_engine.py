@@ -98,3 +98,40 @@ def test_rope_tables_by_ratio():
     assert not torch.allclose(yc, pc)
     for ratio, ref in ((4, yc), (128, yc), (0, pc)):
         assert torch.equal(oe.LayerState(ratio, max_pos=256).cos, ref)
+
+
+@pytest.mark.parametrize("ratio,S", [(4, 23), (0, 9), (4, 8)])
+def test_prefill_equals_decode_steps(ratio, S):
+    """The oracle prefill (the reference's prompt branch: every window row, the prompt's pooled
+    compressed rows, the ring from its last group) against S decode steps from an empty state,
+    which are pinned above: identical window rows and id lists, compressed rows and outputs equal
+    to float32 rounding (pooling the whole prompt and stepping the ring order the same sums
+    differently; the fp8 round trip may move a value by one e4m3 step), the same ring contents,
+    and the same output at the next decode step."""
+    w, g = _weights(5, ratio=ratio)
+    xs = torch.randn(S + 1, 256, generator=g)
+    a, b = oe.LayerState(ratio, max_pos=512), oe.LayerState(ratio, max_pos=512)
+    y_pre, ids_pre, _ = oe.prefill(a, w, xs[:S])
+    y_dec = []
+    for p in range(S):
+        y, _, ids, _ = oe.decode_step(b, w, xs[p], p)
+        y_dec.append(y)
+        # the id rule is positional; the compressed offset is the window length (S vs p + 1)
+        want = [t for t in ids.tolist() if t <= p] + [S + (t - p - 1) for t in ids.tolist() if t > p]
+        assert ids_pre[p].tolist() == want
+    assert len(a.win) == len(b.win) == S
+    for p in range(S):
+        assert torch.equal(a.win[p], b.win[p])
+    assert len(a.comp) == len(b.comp)
+    for j in range(len(a.comp)):
+        ra, rb = a.comp[j].numpy(), b.comp[j].numpy()
+        np.testing.assert_allclose(ra[-64:], rb[-64:], rtol=1e-4, atol=1e-6)
+        step = np.abs(rb[:-64]) * 2.0 ** -3 + 1e-6
+        assert np.all(np.abs(ra[:-64] - rb[:-64]) <= step)
+    np.testing.assert_allclose(y_pre, np.stack(y_dec), rtol=1e-3, atol=1e-3 * np.abs(y_pre).max())
+    if ratio == 4:
+        live = 4 + S % 4
+        assert torch.equal(a.kvs[:live], b.kvs[:live]) and torch.equal(a.scs[:live], b.scs[:live])
+    ya, _, _, _ = oe.decode_step(a, w, xs[S], S)
+    yb, _, _, _ = oe.decode_step(b, w, xs[S], S)
+    np.testing.assert_allclose(ya, yb, rtol=1e-3, atol=1e-3 * np.abs(yb).max())
