@@ -10,6 +10,8 @@
 //  * attn_merge_kernel   — log-sum-exp merge of the split partial states that the MFMA split
 //    kernel (attn_decode.hip) writes.
 //  * the split plan and the C entry points.
+#include <mutex>
+
 #include "attn_common.h"
 
 namespace {
@@ -475,4 +477,54 @@ extern "C" int smla_sparse_attn_ex(const void* q, int q_dtype, const void* kv0, 
                                    size_t workspace_bytes, void* stream) {
   return attn_call(q, q_dtype, kv0, n0, kv1, n1, kv_dtype, kv0_scale, kv1_scale, attn_sink, topk_idxs, T, B, S, H,
                    D, DV, scale, out, out_dtype, rows_per_split, phases, workspace, workspace_bytes, stream);
+}
+
+// ---------------------------------------------------------------------------------------------
+// Allocation-free variant: the split partial states live in `scratch`, a buffer of
+// SMLA_NOALLOC_SCRATCH_BYTES that every device the library runs on holds until the process ends.
+// In host code `scratch` names a host-side stand-in, so its device address is taken once per
+// device (hipGetSymbolAddress, with that device current) and only that address reaches kernels.
+namespace {
+static __device__ __align__(256) uint8_t scratch[SMLA_NOALLOC_SCRATCH_BYTES];
+constexpr int kMaxDevices = 64;
+std::atomic<void*> g_scratch_addr[kMaxDevices];
+std::mutex g_scratch_mu;
+
+// device address of the current device's `scratch` (resolved on the first call on that device)
+int scratch_on_current_device(void** addr) {
+  int dev = 0;
+  if (hipError_t e = hipGetDevice(&dev); e != hipSuccess) return (int)e;
+  if (dev < 0 || dev >= kMaxDevices) return SMLA_E_UNSUPPORTED;
+  void* p = g_scratch_addr[dev].load(std::memory_order_acquire);
+  if (!p) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    p = g_scratch_addr[dev].load(std::memory_order_acquire);
+    if (!p) {
+      if (hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)); e != hipSuccess) return (int)e;
+      if (!p) return SMLA_E_UNSUPPORTED;
+      g_scratch_addr[dev].store(p, std::memory_order_release);
+    }
+  }
+  *addr = p;
+  return SMLA_OK;
+}
+}  // namespace
+
+extern "C" int smla_sparse_attn_noalloc(const void* q, int q_dtype, const void* kv0, int64_t n0, const void* kv1,
+                                        int64_t n1, int kv_dtype, const float* kv0_scale, const float* kv1_scale,
+                                        const float* attn_sink, const int32_t* topk_idxs, int64_t T, int64_t B,
+                                        int64_t S, int64_t H, int64_t D, int64_t DV, float scale, void* out,
+                                        int out_dtype, void* stream) {
+  int rc = check_attn_args(q, q_dtype, kv0, n0, kv1, n1, kv_dtype, kv0_scale, kv1_scale, topk_idxs, T, B, S, H, D,
+                           DV, out, out_dtype);
+  if (rc != SMLA_OK) return rc;
+  // the default plan's partial states must fit the buffer (checked before anything runs)
+  const Plan p = make_plan(B, S, H, D, DV, T, q_dtype, kv_dtype, 0);
+  if (plan_workspace(p, B, S, H, DV, out_dtype) > SMLA_NOALLOC_SCRATCH_BYTES) return SMLA_E_WORKSPACE;
+  void* ws = nullptr;
+  rc = scratch_on_current_device(&ws);
+  if (rc != SMLA_OK) return rc;
+  return attn_call(q, q_dtype, kv0, n0, kv1, n1, kv_dtype, kv0_scale, kv1_scale, attn_sink, topk_idxs, T, B, S, H,
+                   D, DV, scale, out, out_dtype, 0, SMLA_ATTN_SPLIT | SMLA_ATTN_MERGE, ws, SMLA_NOALLOC_SCRATCH_BYTES,
+                   stream);
 }

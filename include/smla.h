@@ -135,6 +135,23 @@ int smla_sparse_attn_ex(const void* q, int q_dtype,
                         void* out, int out_dtype, int64_t rows_per_split, int phases,
                         void* workspace, size_t workspace_bytes, void* stream);
 
+/* smla_sparse_attn without a workspace argument: the same plan, kernels and output, with the split
+ * partial states in a buffer of SMLA_NOALLOC_SCRATCH_BYTES that the library holds on each device
+ * (from the first call on that device until the process ends).  No counterpart in the reference:
+ * it is for callers that cannot allocate (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  Allocates nothing; returns SMLA_E_WORKSPACE, before any
+ * launch, when the plan's partial states exceed the buffer (smla_sparse_attn_workspace gives the
+ * size).  Every call on a device shares that device's buffer: calls that overlap on one device
+ * (concurrent streams, threads) race and must be serialised by the caller.  The partial states
+ * are fully written before they are read, so nothing needs clearing between calls. */
+#define SMLA_NOALLOC_SCRATCH_BYTES (32u << 20)
+int smla_sparse_attn_noalloc(const void* q, int q_dtype,
+                             const void* kv0, int64_t n0, const void* kv1, int64_t n1, int kv_dtype,
+                             const float* kv0_scale, const float* kv1_scale,
+                             const float* attn_sink, const int32_t* topk_idxs, int64_t T,
+                             int64_t B, int64_t S, int64_t H, int64_t D, int64_t DV, float scale,
+                             void* out, int out_dtype, void* stream);
+
 /* ---------------------------------------------------------------------------------------------
  * Window index matrix.  Replaces ref_torch/sparse_attn.py:9-20 (get_window_topk_idxs).
  * out: [bsz, w] int32 when start_pos > 0 (ring or partial window), [bsz, seqlen, min(seqlen, w)]
