@@ -71,9 +71,11 @@ constexpr int kQS = 68;  // LDS row stride (floats) of the staged q rows: 16-byt
 constexpr int kRescoreChunk = 128;  // keys rescored per pass (their fp32 rows and ReLU values sit in LDS)
 constexpr int kStageIds = 4096;   // selections up to this size are staged in LDS for coalesced stores
 
+// floor((lmax - s) * bscale) clamped to [0, kBuckets), as one fma (one rounding of the exact
+// lmax bscale - s bscale, monotone non-increasing in s), a clamp in float and a conversion in range
 __device__ inline int bucket_of_score(float s, float lmax, float bscale) {
-  const float t = (lmax - s) * bscale;
-  return t < 1.f ? 0 : (t >= (float)kBuckets ? kBuckets - 1 : (int)t);
+  const float t = __builtin_fmaf(-s, bscale, lmax * bscale);
+  return (int)__builtin_amdgcn_fmed3f(t, 0.f, (float)(kBuckets - 1));
 }
 // monotone bucket of a finite score: 0 holds the largest scores
 __device__ inline int bucket_of(uint32_t key, float lmax, float bscale) {
@@ -605,7 +607,8 @@ __global__ __launch_bounds__(NT) void topk_kernel(const float* scores, int64_t N
   const int nsel = __builtin_popcountll(selm);
   int tot_sel;
   int pos = block_excl_scan<kWaves>(nsel, tmp, &tot_sel);
-  const bool stage = take <= kStageIds;
+  // ids go straight to their output positions (each wave's selected ids fill one contiguous run)
+  const bool stage = false;
 #pragma unroll
   for (int j = 0; j < PER; j++) {
     if ((selm >> j) & 1ull) {
