@@ -330,11 +330,12 @@ int launch_k(const void* q, int q_dtype, const void* keys, const float* kscale, 
   if (Hi == 64 && DI == 64) {
     const dim3 grid((unsigned)((N + 127) / 128), (unsigned)(B * S));
     // two keys per lane halve the q reads per fma; when that leaves CUs idle (one long sequence),
-    // one key per lane doubles the workgroups
+    // one key per lane doubles the workgroups, and 8 heads per wave (8 waves) keeps two waves per
+    // SIMD to hide the q reads (16384 keys: 8.1 -> 7.1 us; with 8 sequences 16 heads per wave wins)
     const bool one = (int64_t)grid.x * grid.y < smla_num_cus();
     const dim3 grid1((unsigned)((N + 63) / 64), (unsigned)(B * S));
     if (q_dtype == SMLA_BF16 && one)
-      hipLaunchKernelGGL((indexer2_kernel<KDT, SMLA_BF16, 1, 16>), grid1, dim3(256), 0, st, q, keys, kscale, w, nvis, S,
+      hipLaunchKernelGGL((indexer2_kernel<KDT, SMLA_BF16, 1, 8>), grid1, dim3(512), 0, st, q, keys, kscale, w, nvis, S,
                          N, scores);
     else if (q_dtype == SMLA_BF16)
       hipLaunchKernelGGL((indexer2_kernel<KDT, SMLA_BF16, 2, 16>), grid, dim3(256), 0, st, q, keys, kscale, w, nvis, S,
