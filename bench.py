@@ -216,6 +216,16 @@ def other_workloads(dev, reps):
                             "us": round(ms * 1e3, 3), "bound": "valu fp32",
                             "achieved_tflops": round(flops / (ms * 1e-3) / 1e12, 2), "peak_tflops": 157.3,
                             "hbm_bytes": B * N * (Di + 4) + B * N * 4}
+    # the same scores over keys in the indexer compressor's fp4 form (Hadamard + e2m1, ue8m0 per 32)
+    from smla import qat as sqat
+    kc4, ks4 = sqat.fp4_pack(torch.randn(B, N, Di, device=dev), rotate=True)
+    ms = _time_graph_ms(lambda: sidx.indexer_score_fp4(qi, kc4, ks4, ks, wt), reps)
+    res["indexer_score_fp4"] = {"shape": "B=8 Hi=64 Di=64 N=8192, bf16 q x fp4 keys (packed e2m1 + ue8m0 per 32), "
+                                         "fixed-order fp32 fma chains",
+                                "us": round(ms * 1e3, 3), "bound": "valu fp32",
+                                "achieved_tflops": round(flops / (ms * 1e-3) / 1e12, 2), "peak_tflops": 157.3,
+                                "hbm_bytes": B * N * (Di // 2 + Di // 32 + 4) + B * N * 4}
+    del kc4, ks4
     sc = sidx.indexer_score(qi, keys, ks, wt)
     pos = torch.full((B,), w["pos"], dtype=torch.int32, device=dev)
     ms = _time_graph_ms(lambda: sidx.select_decode_indices(sc[:, 0], w["k"], pos, w["window"], raw.shape[1]), reps)

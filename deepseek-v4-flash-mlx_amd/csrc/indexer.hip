@@ -12,6 +12,8 @@
 // wave-wide broadcasts) and wave 0 runs each key's chain over the heads.  HBM traffic per query
 // row: N * (Di * sizeof(key) + 4) bytes of keys and scales, N * 4 bytes of scores.
 // The fp32 FMA work (N * Hi * Di per query row) is the bound: VALU, fixed order, no MFMA.
+#include <type_traits>
+
 #include "smla_internal.h"
 
 namespace {
@@ -19,6 +21,37 @@ namespace {
 constexpr int kMaxQ = 64 * 128;  // Hi * Di fp32 in LDS (at most 32 KiB)
 constexpr int kKeys = 64;        // keys per workgroup (one per lane)
 constexpr int kHG = 16;          // heads per wave
+constexpr int kFp4 = 16;         // key type tag: packed e2m1 codes + one ue8m0 scale byte per 32
+
+// Two code words of the gfx950 scaled fp4 converter, lanes of byte SEL: elements 2 SEL, 2 SEL + 1.
+template <int SEL>
+__device__ inline f32x2_t cvt_fp4_pair(uint32_t w, float s) {
+  return __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, s, SEL);
+}
+
+// scale bytes for which every e2m1 x 2^(sb - 127) is a normal finite float
+__device__ inline bool fp4_scale_in_range(uint32_t sb) { return sb - 2u <= 250u; }
+
+// 16 key values from two code words (element 2i in the low nibble of byte i, bit 3 the sign) of a
+// block with scale byte sb: e2m1 x 2^(sb - 127), exact in fp32.  FOLD (sb in range): the scaled
+// converter applies 2^(sb - 127) itself, two values per instruction; otherwise the converter gives
+// the e2m1 value (all normal) and an fp32 multiply applies the scale (subnormal products, overflow
+// to inf, the NaN byte).
+template <bool FOLD>
+__device__ inline void fp4_block16(uint32_t w0, uint32_t w1, uint32_t sb, float* o) {
+  const float s = FOLD ? exp2i_f32((int)sb - 127) : 1.0f;
+  const f32x2_t a0 = cvt_fp4_pair<0>(w0, s), a1 = cvt_fp4_pair<1>(w0, s), a2 = cvt_fp4_pair<2>(w0, s),
+                a3 = cvt_fp4_pair<3>(w0, s);
+  const f32x2_t b0 = cvt_fp4_pair<0>(w1, s), b1 = cvt_fp4_pair<1>(w1, s), b2 = cvt_fp4_pair<2>(w1, s),
+                b3 = cvt_fp4_pair<3>(w1, s);
+  o[0] = a0.x, o[1] = a0.y, o[2] = a1.x, o[3] = a1.y, o[4] = a2.x, o[5] = a2.y, o[6] = a3.x, o[7] = a3.y;
+  o[8] = b0.x, o[9] = b0.y, o[10] = b1.x, o[11] = b1.y, o[12] = b2.x, o[13] = b2.y, o[14] = b3.x, o[15] = b3.y;
+  if constexpr (!FOLD) {
+    const float m = ue8m0_to_f32(sb);
+#pragma unroll
+    for (int e = 0; e < 16; e++) o[e] *= m;
+  }
+}
 
 // One workgroup = 64 keys x all heads.  Wave w computes r_h = ReLU(dot_h) for heads
 // 16w .. 16w+15 (lane = key, key row in VGPRs, q rows read from LDS as wave-wide broadcasts);
@@ -27,6 +60,7 @@ constexpr int kHG = 16;          // heads per wave
 template <int DI, int KDT, int QDT>
 __global__ __launch_bounds__(256) void indexer_kernel(const void* __restrict__ q, int q_dtype,
                                                       const void* __restrict__ keys,
+                                                      const uint8_t* __restrict__ kbs,
                                                       const float* __restrict__ kscale,
                                                       const float* __restrict__ weights,
                                                       const int32_t* __restrict__ nvis, int64_t S, int Hi,
@@ -61,6 +95,15 @@ __global__ __launch_bounds__(256) void indexer_kernel(const void* __restrict__ q
         kr[16 * v + 4 * j + 2] = hi.x;
         kr[16 * v + 4 * j + 3] = hi.y;
       }
+    }
+  } else if constexpr (KDT == kFp4) {
+    const u32x4_t* kp = (const u32x4_t*)((const uint8_t*)keys + row * (DI / 2));
+#pragma unroll
+    for (int v = 0; v < DI / 32; v++) {  // one 16-byte word = one 32-element scale block
+      const u32x4_t w = kp[v];
+      const uint32_t sb = kbs[row * (DI / 32) + v];
+      fp4_block16<false>(w[0], w[1], sb, kr + 32 * v);
+      fp4_block16<false>(w[2], w[3], sb, kr + 32 * v + 16);
     }
   } else if constexpr (KDT == SMLA_BF16) {
     const u32x4_t* kp = (const u32x4_t*)((const uint16_t*)keys + row * DI);
@@ -166,6 +209,7 @@ __global__ __launch_bounds__(256) void indexer_kernel(const void* __restrict__ q
 template <int KDT, int QDT, int KPL, int HPW>
 __global__ __launch_bounds__(64 * (64 / HPW)) void indexer2_kernel(const void* __restrict__ q,
                                                                   const void* __restrict__ keys,
+                                                                  const uint8_t* __restrict__ kbs,
                                                                   const float* __restrict__ kscale,
                                                                   const float* __restrict__ weights,
                                                                   const int32_t* __restrict__ nvis, int64_t S,
@@ -186,18 +230,27 @@ __global__ __launch_bounds__(64 * (64 / HPW)) void indexer2_kernel(const void* _
   const int64_t nv = nvis ? (int64_t)nvis[bs] : N;
 
   // the lane's key rows in registers, in their storage type (converted one 16-wide block at a time)
-  constexpr int KW = KDT == SMLA_FP8_E4M3 ? 4 : (KDT == SMLA_BF16 ? 8 : 16);  // 16-byte words per row
+  // 16-byte words per row
+  constexpr int KW = KDT == kFp4 ? 2 : KDT == SMLA_FP8_E4M3 ? 4 : (KDT == SMLA_BF16 ? 8 : 16);
   u32x4_t kr[KPL][KW];
+  uint32_t ksb[KPL];  // fp4: the row's two scale bytes
 #pragma unroll
   for (int i = 0; i < KPL; i++) {
     const int64_t n = n0 + 64 * i;
-    const u32x4_t* pk = (const u32x4_t*)((const uint8_t*)keys + (b * N + (n < N ? n : N - 1)) * DI * (KW / 4));
+    const int64_t row = b * N + (n < N ? n : N - 1);
+    const u32x4_t* pk = (const u32x4_t*)((const uint8_t*)keys + row * DI * KW / 4);
 #pragma unroll
     for (int v = 0; v < KW; v++) kr[i][v] = pk[v];
+    if constexpr (KDT == kFp4) ksb[i] = ((const uint16_t*)kbs)[row];
   }
-  // 16 values of a key row starting at d0 = 16 db, as fp32
-  auto block16 = [&](const u32x4_t (&row)[KW], int db, float (&o)[16]) {
-    if constexpr (KDT == SMLA_FP8_E4M3) {
+  // 16 values of key i's row starting at d0 = 16 db, as fp32 (fold: see fp4_block16)
+  auto block16 = [&](int i, int db, float (&o)[16], auto fold) {
+    const u32x4_t(&row)[KW] = kr[i];
+    if constexpr (KDT == kFp4) {
+      const u32x4_t w = row[db >> 1];
+      fp4_block16<decltype(fold)::value>(w[2 * (db & 1)], w[2 * (db & 1) + 1], (ksb[i] >> (8 * (db >> 1))) & 0xffu,
+                                         o);
+    } else if constexpr (KDT == SMLA_FP8_E4M3) {
       const u32x4_t w = row[db];
 #pragma unroll
       for (int j = 0; j < 4; j++) {
@@ -254,11 +307,12 @@ __global__ __launch_bounds__(64 * (64 / HPW)) void indexer2_kernel(const void* _
 #pragma unroll
     for (int hh = 0; hh < HPW; hh++) dot[i][hh] = 0.f;
   const int h0 = wave * HPW;
+  auto run = [&](auto fold) {
 #pragma unroll
   for (int db = 0; db < 4; db++) {
     float x[KPL][16];
 #pragma unroll
-    for (int i = 0; i < KPL; i++) block16(kr[i], db, x[i]);
+    for (int i = 0; i < KPL; i++) block16(i, db, x[i], fold);
     // the next head's 16 q values are read before this head's fmas (one head of lookahead)
     f32x4_t qn[4];
 #pragma unroll
@@ -280,6 +334,18 @@ __global__ __launch_bounds__(64 * (64 / HPW)) void indexer2_kernel(const void* _
           for (int i = 0; i < KPL; i++) dot[i][hh] = __builtin_fmaf(qc[v][j], x[i][4 * v + j], dot[i][hh]);
     }
   }
+  };
+  if constexpr (KDT == kFp4) {
+    // fp4 keys: the folded conversion when every scale byte of the wave's keys allows it (a
+    // wave-uniform branch, so each variant keeps its own registers)
+    bool fold = true;
+#pragma unroll
+    for (int i = 0; i < KPL; i++) fold = fold && fp4_scale_in_range(ksb[i] & 0xffu) && fp4_scale_in_range(ksb[i] >> 8);
+    if (__all(fold)) run(std::true_type{});
+    else run(std::false_type{});
+  } else {
+    run(std::true_type{});
+  }
 #pragma unroll
   for (int i = 0; i < KPL; i++)
 #pragma unroll
@@ -299,6 +365,7 @@ __global__ __launch_bounds__(64 * (64 / HPW)) void indexer2_kernel(const void* _
 template <int DI, int KDT>
 __global__ __launch_bounds__(256) void indexer_wide_kernel(const void* __restrict__ q, int q_dtype,
                                                            const void* __restrict__ keys,
+                                                           const uint8_t* __restrict__ kbs,
                                                            const float* __restrict__ kscale,
                                                            const float* __restrict__ weights,
                                                            const int32_t* __restrict__ nvis, int64_t S, int Hi,
@@ -314,18 +381,25 @@ __global__ __launch_bounds__(256) void indexer_wide_kernel(const void* __restric
     return;
   }
   const int64_t row = b * N + n;
+  auto key_at = [&](int d) -> float {
+    if constexpr (KDT == kFp4) {
+      const uint32_t c = (((const uint8_t*)keys)[row * (DI / 2) + d / 2] >> (4 * (d & 1))) & 15u;
+      return e2m1_to_f32(c) * ue8m0_to_f32(kbs[row * (DI / 32) + d / 32]);
+    } else {
+      return load_as_f32(keys, row * DI + d, KDT);
+    }
+  };
   float acc = 0.f;
   for (int h = 0; h < Hi; h++) {
     float dot = 0.f;
-    for (int d = 0; d < DI; d++)
-      dot = __builtin_fmaf(load_as_f32(q, (bs * Hi + h) * DI + d, q_dtype), load_as_f32(keys, row * DI + d, KDT), dot);
+    for (int d = 0; d < DI; d++) dot = __builtin_fmaf(load_as_f32(q, (bs * Hi + h) * DI + d, q_dtype), key_at(d), dot);
     acc = __builtin_fmaf(weights[bs * Hi + h], dot > 0.f ? dot : 0.f, acc);
   }
   scores[bs * N + n] = kscale ? acc * kscale[row] : acc;
 }
 
 template <int DI, int KDT>
-int launch_k(const void* q, int q_dtype, const void* keys, const float* kscale, const float* w,
+int launch_k(const void* q, int q_dtype, const void* keys, const uint8_t* kbs, const float* kscale, const float* w,
              const int32_t* nvis, int64_t B, int64_t S, int64_t Hi, int64_t N, float* scores, hipStream_t st) {
   if (Hi == 64 && DI == 64) {
     const dim3 grid((unsigned)((N + 127) / 128), (unsigned)(B * S));
@@ -335,40 +409,42 @@ int launch_k(const void* q, int q_dtype, const void* keys, const float* kscale, 
     const bool one = (int64_t)grid.x * grid.y < smla_num_cus();
     const dim3 grid1((unsigned)((N + 63) / 64), (unsigned)(B * S));
     if (q_dtype == SMLA_BF16 && one)
-      hipLaunchKernelGGL((indexer2_kernel<KDT, SMLA_BF16, 1, 8>), grid1, dim3(512), 0, st, q, keys, kscale, w, nvis, S,
+      hipLaunchKernelGGL((indexer2_kernel<KDT, SMLA_BF16, 1, 8>), grid1, dim3(512), 0, st, q, keys, kbs, kscale, w, nvis, S,
                          N, scores);
     else if (q_dtype == SMLA_BF16)
-      hipLaunchKernelGGL((indexer2_kernel<KDT, SMLA_BF16, 2, 16>), grid, dim3(256), 0, st, q, keys, kscale, w, nvis, S,
+      hipLaunchKernelGGL((indexer2_kernel<KDT, SMLA_BF16, 2, 16>), grid, dim3(256), 0, st, q, keys, kbs, kscale, w, nvis, S,
                          N, scores);
     else
-      hipLaunchKernelGGL((indexer2_kernel<KDT, SMLA_F32, 2, 16>), grid, dim3(256), 0, st, q, keys, kscale, w, nvis, S,
+      hipLaunchKernelGGL((indexer2_kernel<KDT, SMLA_F32, 2, 16>), grid, dim3(256), 0, st, q, keys, kbs, kscale, w, nvis, S,
                          N, scores);
   } else if (Hi <= 64) {
     dim3 grid((unsigned)((N + kKeys - 1) / kKeys), (unsigned)(B * S));
     const int threads = (int)(((Hi + kHG - 1) / kHG) * 64);
     if (q_dtype == SMLA_BF16)
-      hipLaunchKernelGGL((indexer_kernel<DI, KDT, SMLA_BF16>), grid, dim3(threads), 0, st, q, q_dtype, keys, kscale,
-                         w, nvis, S, (int)Hi, N, scores);
+      hipLaunchKernelGGL((indexer_kernel<DI, KDT, SMLA_BF16>), grid, dim3(threads), 0, st, q, q_dtype, keys, kbs,
+                         kscale, w, nvis, S, (int)Hi, N, scores);
     else
-      hipLaunchKernelGGL((indexer_kernel<DI, KDT, SMLA_F32>), grid, dim3(threads), 0, st, q, q_dtype, keys, kscale,
-                         w, nvis, S, (int)Hi, N, scores);
+      hipLaunchKernelGGL((indexer_kernel<DI, KDT, SMLA_F32>), grid, dim3(threads), 0, st, q, q_dtype, keys, kbs,
+                         kscale, w, nvis, S, (int)Hi, N, scores);
   } else {
     dim3 grid((unsigned)((N + 255) / 256), (unsigned)(B * S));
-    hipLaunchKernelGGL((indexer_wide_kernel<DI, KDT>), grid, dim3(256), 0, st, q, q_dtype, keys, kscale, w, nvis, S,
-                       (int)Hi, N, scores);
+    hipLaunchKernelGGL((indexer_wide_kernel<DI, KDT>), grid, dim3(256), 0, st, q, q_dtype, keys, kbs, kscale, w, nvis,
+                       S, (int)Hi, N, scores);
   }
   SMLA_HIP_CHECK_LAUNCH();
   return SMLA_OK;
 }
 
 template <int DI>
-int launch_di(const void* q, int q_dtype, const void* keys, int k_dtype, const float* kscale,
+int launch_di(const void* q, int q_dtype, const void* keys, int k_dtype, const uint8_t* kbs, const float* kscale,
               const float* w, const int32_t* nvis, int64_t B, int64_t S, int64_t Hi, int64_t N,
               float* scores, hipStream_t st) {
+  if (k_dtype == kFp4) return launch_k<DI, kFp4>(q, q_dtype, keys, kbs, kscale, w, nvis, B, S, Hi, N, scores, st);
   if (k_dtype == SMLA_FP8_E4M3)
-    return launch_k<DI, SMLA_FP8_E4M3>(q, q_dtype, keys, kscale, w, nvis, B, S, Hi, N, scores, st);
-  if (k_dtype == SMLA_BF16) return launch_k<DI, SMLA_BF16>(q, q_dtype, keys, kscale, w, nvis, B, S, Hi, N, scores, st);
-  return launch_k<DI, SMLA_F32>(q, q_dtype, keys, kscale, w, nvis, B, S, Hi, N, scores, st);
+    return launch_k<DI, SMLA_FP8_E4M3>(q, q_dtype, keys, kbs, kscale, w, nvis, B, S, Hi, N, scores, st);
+  if (k_dtype == SMLA_BF16)
+    return launch_k<DI, SMLA_BF16>(q, q_dtype, keys, kbs, kscale, w, nvis, B, S, Hi, N, scores, st);
+  return launch_k<DI, SMLA_F32>(q, q_dtype, keys, kbs, kscale, w, nvis, B, S, Hi, N, scores, st);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -538,20 +614,38 @@ int launch_indexer_cert(const uint16_t* q, const uint8_t* keys, const float* ksc
 }
 
 
+namespace {
+int indexer_score_any(const void* q, int q_dtype, const void* keys, int k_dtype, const uint8_t* kbs,
+                      const float* kscale, const float* weights, const int32_t* nvis, int64_t B, int64_t S,
+                      int64_t Hi, int64_t Di, int64_t N, float* scores, void* stream) {
+  if (!q || !keys || !weights || !scores || (k_dtype == kFp4 && !kbs)) return SMLA_E_NULL;
+  if (B <= 0 || S <= 0 || Hi <= 0 || Di <= 0 || N <= 0) return SMLA_E_SHAPE;
+  if (q_dtype != SMLA_F32 && q_dtype != SMLA_BF16) return SMLA_E_DTYPE;
+  if (Hi > 256 || (Hi <= 64 && Hi * Di > kMaxQ) || (N + 63) / 64 > 0x7fffffff || B * S > 65535)
+    return SMLA_E_UNSUPPORTED;
+  // q rows and key rows are read as 16-byte words, fp4 scale bytes of a row as one 2-byte word
+  if (((uintptr_t)q & 15) || ((uintptr_t)keys & 15) || ((uintptr_t)kbs & 1)) return SMLA_E_UNSUPPORTED;
+  hipStream_t st = (hipStream_t)stream;
+  switch (Di) {
+    case 32: return launch_di<32>(q, q_dtype, keys, k_dtype, kbs, kscale, weights, nvis, B, S, Hi, N, scores, st);
+    case 64: return launch_di<64>(q, q_dtype, keys, k_dtype, kbs, kscale, weights, nvis, B, S, Hi, N, scores, st);
+    case 128: return launch_di<128>(q, q_dtype, keys, k_dtype, kbs, kscale, weights, nvis, B, S, Hi, N, scores, st);
+  }
+  return SMLA_E_UNSUPPORTED;
+}
+}  // namespace
+
 extern "C" int smla_indexer_score(const void* q, int q_dtype, const void* keys, int k_dtype, const float* kscale,
                                   const float* weights, const int32_t* nvis, int64_t B, int64_t S, int64_t Hi,
                                   int64_t Di, int64_t N, float* scores, void* stream) {
-  if (!q || !keys || !weights || !scores) return SMLA_E_NULL;
-  if (B <= 0 || S <= 0 || Hi <= 0 || Di <= 0 || N <= 0) return SMLA_E_SHAPE;
-  if (q_dtype != SMLA_F32 && q_dtype != SMLA_BF16) return SMLA_E_DTYPE;
   if (k_dtype != SMLA_F32 && k_dtype != SMLA_BF16 && k_dtype != SMLA_FP8_E4M3) return SMLA_E_DTYPE;
-  if (Hi > 256 || (Hi <= 64 && Hi * Di > kMaxQ) || (N + 63) / 64 > 0x7fffffff || B * S > 65535)
-    return SMLA_E_UNSUPPORTED;
-  hipStream_t st = (hipStream_t)stream;
-  switch (Di) {
-    case 32: return launch_di<32>(q, q_dtype, keys, k_dtype, kscale, weights, nvis, B, S, Hi, N, scores, st);
-    case 64: return launch_di<64>(q, q_dtype, keys, k_dtype, kscale, weights, nvis, B, S, Hi, N, scores, st);
-    case 128: return launch_di<128>(q, q_dtype, keys, k_dtype, kscale, weights, nvis, B, S, Hi, N, scores, st);
-  }
-  return SMLA_E_UNSUPPORTED;
+  return indexer_score_any(q, q_dtype, keys, k_dtype, nullptr, kscale, weights, nvis, B, S, Hi, Di, N, scores,
+                           stream);
+}
+
+extern "C" int smla_indexer_score_fp4(const void* q, int q_dtype, const uint8_t* codes, const uint8_t* block_scales,
+                                      const float* kscale, const float* weights, const int32_t* nvis, int64_t B,
+                                      int64_t S, int64_t Hi, int64_t Di, int64_t N, float* scores, void* stream) {
+  return indexer_score_any(q, q_dtype, codes, kFp4, block_scales, kscale, weights, nvis, B, S, Hi, Di, N, scores,
+                           stream);
 }

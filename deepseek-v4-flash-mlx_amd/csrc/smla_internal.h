@@ -141,6 +141,14 @@ __host__ __device__ inline float exp2i_f32(int k) {
   __builtin_memcpy(&f, &u, 4);
   return f;
 }
+// ue8m0 scale byte b -> 2^(b-127) as float32: 0 gives the subnormal 2^-127, 255 the E8M0 NaN
+__host__ __device__ inline float ue8m0_to_f32(uint32_t b) {
+  // selects, not branches: inside unrolled loops a branch splits the schedule
+  const uint32_t u = b == 0u ? 0x00400000u : (b == 255u ? 0x7fc00000u : b << 23);
+  float f;
+  __builtin_memcpy(&f, &u, 4);
+  return f;
+}
 // float32(n^-0.5) for n = 2^lg: 2^-(lg/2), times float32(sqrt(0.5)) = 0x3F3504F3 when lg is odd
 __host__ __device__ inline float hadamard_scale(int lg) {
   const float p = exp2i_f32(-(lg >> 1));

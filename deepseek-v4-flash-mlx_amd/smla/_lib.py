@@ -35,6 +35,8 @@ _SIGNATURES = {
     "smla_decode_window_idxs": (_int, [_vp, _i64, _i64, _vp, _i64, _vp]),
     "smla_indexer_score": (_int, [_vp, _int, _vp, _int, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64,
                                   _vp, _vp]),
+    "smla_indexer_score_fp4": (_int, [_vp, _int, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64,
+                                      _vp, _vp]),
     "smla_topk": (_int, [_vp, _i64, _i64, _vp, _i64, _vp, _i64, _i32, _vp]),
     "smla_select_decode": (_int, [_vp, _i64, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _i32, _vp]),
     "smla_index_decode": (_int, [_vp, _int, _vp, _int, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64,

@@ -17,6 +17,13 @@ def indexer_score(q_idx, keys, kscale, weights, nvis=None):
     return ops.indexer_score_op(q_idx, keys, kscale, weights, nvis)
 
 
+def indexer_score_fp4(q_idx, codes, block_scales, kscale, weights, nvis=None):
+    """The same scores over keys stored as packed e2m1 codes [B,N,Di/2] and ue8m0 scales
+    [B,N,Di/32] (the form ``qat.fp4_quantize`` and ``smla_rotate_fp4`` write), bit-identical to
+    ``indexer_score`` on the decoded fp32 keys."""
+    return ops.indexer_score_fp4_op(q_idx, codes, block_scales, kscale, weights, nvis)
+
+
 def topk(scores, k, nvis=None, id_offset=0):
     """scores [..., N] -> int32 [..., k]."""
     return ops.topk_op(scores, k, nvis, id_offset)

@@ -186,6 +186,37 @@ def _(q, keys, kscale, weights, nvis):
     return q.new_empty(q.shape[0], q.shape[1], keys.shape[1], dtype=torch.float32)
 
 
+@torch.library.custom_op("smla::indexer_score_fp4", mutates_args=(), device_types="cuda")
+def indexer_score_fp4_op(q: torch.Tensor, codes: torch.Tensor, block_scales: torch.Tensor,
+                         kscale: Optional[torch.Tensor], weights: torch.Tensor,
+                         nvis: Optional[torch.Tensor]) -> torch.Tensor:
+    """q [B,S,Hi,Di] f32|bf16, codes [B,N,Di/2] uint8 (packed e2m1), block_scales [B,N,Di/32] uint8
+    (ue8m0), kscale [B,N]|None, weights [B,S,Hi], nvis [B,S]|None -> scores [B,S,N] fp32."""
+    _on_gpu(q, codes, block_scales, kscale, weights, nvis)
+    B, S, Hi, Di = q.shape
+    N = codes.shape[1]
+    if codes.dtype != torch.uint8 or block_scales.dtype != torch.uint8:
+        raise ValueError("fp4 keys are uint8 codes and uint8 ue8m0 block scales")
+    if tuple(codes.shape) != (B, N, Di // 2) or tuple(block_scales.shape) != (B, N, Di // 32):
+        raise ValueError(f"fp4 keys {tuple(codes.shape)} / scales {tuple(block_scales.shape)} do not match "
+                         f"q {tuple(q.shape)}")
+    q, codes, block_scales, weights = q.contiguous(), codes.contiguous(), block_scales.contiguous(), \
+        weights.float().contiguous()
+    if nvis is not None:
+        nvis = nvis.to(torch.int32).contiguous()
+    if kscale is not None:
+        kscale = kscale.float().contiguous()
+    out = torch.empty(B, S, N, dtype=torch.float32, device=q.device)
+    _lib.call("smla_indexer_score_fp4", _p(q), dtype_code(q), _p(codes), _p(block_scales), _p(kscale),
+              _p(weights), _p(nvis), B, S, Hi, Di, N, _p(out), _stream(q))
+    return out
+
+
+@indexer_score_fp4_op.register_fake
+def _(q, codes, block_scales, kscale, weights, nvis):
+    return q.new_empty(q.shape[0], q.shape[1], codes.shape[1], dtype=torch.float32)
+
+
 # ----------------------------------------------------------------------------------------------
 @torch.library.custom_op("smla::topk", mutates_args=(), device_types="cuda")
 def topk_op(scores: torch.Tensor, k: int, nvis: Optional[torch.Tensor], id_offset: int) -> torch.Tensor:

@@ -16,6 +16,7 @@
  *   smla_decode_window_idxs   oracle/decode_engine.py:110-111  widx = range(max(0, p-127), p+1)
  *   smla_indexer_score        (none: the reference attends every visible compressed row,
  *                              oracle/decode_engine.py:112-114; the indexer is the build's)
+ *   smla_indexer_score_fp4    (none, as above; keys in the form v4mlx/compressor.py:57-59 gives them)
  *   smla_topk                 oracle/decode_engine.py:112-114  cidx selection (take-all when nvis <= k)
  *   smla_select_decode        oracle/decode_engine.py:110-114  widx + cidx in one launch
  *   smla_index_decode         oracle/decode_engine.py:110-114  indexer scores + widx + cidx (fused)
@@ -178,6 +179,19 @@ int smla_indexer_score(const void* q, int q_dtype, const void* keys, int k_dtype
                        const float* kscale, const float* weights, const int32_t* nvis,
                        int64_t B, int64_t S, int64_t Hi, int64_t Di, int64_t N,
                        float* scores, void* stream);
+
+/* The same score over keys in the indexer compressor's stored fp4 form (v4mlx/compressor.py:57-59
+ * applies v4mlx/qat.py:23-31 to every indexer key; smla_rotate_fp4 writes this form):
+ *   codes         [B,N,Di/2] uint8, element 2i of a row in the low nibble of byte i, bit 3 the sign
+ *                 (e2m1: magnitudes 0, 0.5, 1, 1.5, 2, 3, 4, 6);
+ *   block_scales  [B,N,Di/32] uint8 ue8m0: k[b,n,d] = e2m1(code) * 2^(block_scales[b,n,d/32] - 127)
+ *                 (byte 0 = 2^-127, byte 255 = NaN), exact in fp32.
+ * Every score equals smla_indexer_score's on the decoded fp32 keys, bit for bit.  Di is 32, 64 or
+ * 128; q and codes 16-byte aligned, block_scales 2-byte aligned.  Other arguments as above. */
+int smla_indexer_score_fp4(const void* q, int q_dtype, const uint8_t* codes,
+                           const uint8_t* block_scales, const float* kscale, const float* weights,
+                           const int32_t* nvis, int64_t B, int64_t S, int64_t Hi, int64_t Di,
+                           int64_t N, float* scores, void* stream);
 
 /* ---------------------------------------------------------------------------------------------
  * Top-k selection over rows of scores [R, N]: rank the first nvis[r] entries (NULL = N) by

@@ -12,7 +12,7 @@ Restates ``v4mlx/qat.py``, the key-side transform of the indexer compressor
   ties to the even code.  The grid is {0, 0.5, 1, 1.5, 2, 3, 4, 6}.
 * ``fp4_quantize``: the stored form of the same quantisation (the form the HIP kernel writes):
   packed e2m1 codes (element 2i in the low nibble of byte i, bit 3 the sign) and one ue8m0 scale
-  byte per block (log2(s) + 127).
+  byte per block (log2(s) + 127); ``fp4_dequantize`` decodes it (the indexer's fp4 keys).
 
 The scale exponent is computed exactly from the float32 bits of ``amax / 6`` (the unbiased
 exponent, plus one unless the value is a power of two).  The reference takes a float32 ``log2``
@@ -27,7 +27,9 @@ Pinning (``tests/test_oracle_qat.py``):
   computed bottom-up, on random inputs, bit for bit;
 * e2m1 rounding equals a brute-force nearest search over the 15 values with ties to the even code,
   on every midpoint and on random values;
-* the scale equals a brute-force search for the smallest power of two s with fl32(amax/6) <= s.
+* the scale equals a brute-force search for the smallest power of two s with fl32(amax/6) <= s;
+* the decode equals the OCP MX definition (sign, 2-bit exponent, 1-bit mantissa; E8M0 scale,
+  0xFF NaN) evaluated exactly in rationals, for every code byte and every scale byte.
 ``ml_dtypes`` is absent here, so its own float4 cast is parity unpinned beyond agreeing with that
 definition.
 """
@@ -103,12 +105,20 @@ def fp4_quantize(x, block=32):
     return packed, (k[..., 0] + 127).astype(np.uint8)
 
 
+def ue8m0_value(scales):
+    """ue8m0 scale bytes -> float32 2^(b - 127); byte 0 is the subnormal 2^-127, byte 255 NaN."""
+    b = np.asarray(scales, dtype=np.int64)
+    s = np.exp2(np.minimum(b, 254) - 127).astype(np.float32)
+    return np.where(b == 255, np.float32(np.nan), s).astype(np.float32)
+
+
 def fp4_dequantize(packed, scales, block=32):
-    """Inverse of the stored form: float32 [..., 2 * packed.shape[-1]]."""
+    """Inverse of the stored form: float32 [..., 2 * packed.shape[-1]], each value the exact
+    float32 product e2m1(code) * 2^(scale - 127) (overflow to inf, NaN for scale byte 255)."""
     p = np.asarray(packed, dtype=np.uint8)
     codes = np.stack([p & 15, p >> 4], axis=-1).reshape(*p.shape[:-1], -1)
     v = e2m1_value(codes)
-    s = np.exp2(np.asarray(scales, dtype=np.int64) - 127).astype(np.float32)
+    s = ue8m0_value(scales)
     vb = v.reshape(*v.shape[:-1], v.shape[-1] // block, block) * s[..., None]
     return vb.reshape(v.shape).astype(np.float32)
 

@@ -55,6 +55,87 @@ def test_indexer_bit_exact(dev, qdt, kdt, use_scale, Hi, Di, N):
         np.testing.assert_array_equal(_bits(out[b]), _bits(ref))
 
 
+def _same(a, b):
+    """Bit-identical, except that any NaN matches any NaN (the payload of a NaN made by inf - inf
+    differs between the GPU and the host)."""
+    a, b = np.asarray(a, np.float32), np.asarray(b, np.float32)
+    nan = np.isnan(a)
+    np.testing.assert_array_equal(nan, np.isnan(b))
+    np.testing.assert_array_equal(_bits(a)[~nan], _bits(b)[~nan])
+
+
+@pytest.mark.parametrize("qdt,use_scale,Hi,Di,N,edges", [
+    ("bf16", True, 64, 64, 8192, False),   # two keys per lane, 16 heads per wave
+    ("bf16", False, 64, 64, 100, True),    # one key per lane, 8 heads per wave
+    ("f32", True, 64, 64, 1000, True),
+    ("f32", False, 16, 64, 700, True),     # generic kernel
+    ("bf16", True, 8, 128, 1000, False),
+    ("f32", True, 3, 32, 333, True),
+    ("bf16", True, 100, 64, 300, True),    # more than 64 heads: one thread per key
+])
+def test_indexer_fp4_bit_exact(dev, qdt, use_scale, Hi, Di, N, edges):
+    """Keys in the stored fp4 form (packed e2m1 codes + ue8m0 per 32), the rotation + fp4 of the
+    indexer compressor, scored bit-identically to the oracle chain over the decoded keys.  With
+    ``edges``, some key blocks carry every code under the extreme scale bytes (0, 1: subnormal
+    products; 2 and 252: the ends of the converter's range; 253, 254: overflow; 255: NaN)."""
+    from oracle import qat
+    from smla import indexer as sidx
+    announce(f"indexer fp4 q={qdt} scale={use_scale} Hi={Hi} Di={Di} N={N} edges={edges}")
+    g = torch.Generator().manual_seed(3 * N + Hi)
+    B, S = 2, 2
+    q = torch.randn(B, S, Hi, Di, generator=g)
+    if qdt == "bf16":
+        q = q.to(torch.bfloat16)
+    kf = torch.randn(B, N, Di, generator=g).numpy() * np.exp2(
+        torch.randint(-20, 20, (B, N, 1), generator=g).numpy()).astype(np.float32)
+    codes, scales = qat.fp4_quantize(qat.hadamard_rotate(kf))
+    if edges:
+        rng = np.random.default_rng(N)
+        rows = rng.choice(N, size=min(N, 40), replace=False)
+        for i, r in enumerate(rows):
+            codes[i % B, r] = rng.integers(0, 256, Di // 2, dtype=np.uint8)
+            codes[i % B, r, :16] = np.arange(0, 256, 17, dtype=np.uint8)  # every code in both nibbles
+            scales[i % B, r] = [0, 1, 2, 252, 253, 254, 255, 127][i % 8]
+    kvals = qat.fp4_dequantize(codes, scales)
+    ks = (torch.rand(B, N, generator=g) + 0.5) if use_scale else None
+    w = torch.randn(B, S, Hi, generator=g)
+    nvis = torch.randint(0, N + 1, (B, S), generator=g, dtype=torch.int32)
+    nvis[0, 0] = N
+    out = sidx.indexer_score_fp4(q.to(dev), torch.from_numpy(codes).to(dev), torch.from_numpy(scales).to(dev),
+                                 None if ks is None else ks.to(dev), w.to(dev), nvis.to(dev)).cpu().numpy()
+    for b in range(B):
+        ref = oidx.indexer_score(q[b].float().numpy(), kvals[b], None if ks is None else ks[b].numpy(),
+                                 w[b].numpy(), nvis[b].numpy())
+        _same(out[b], ref)
+
+
+def test_indexer_key_path_end_to_end(dev):
+    """fp32 compressed keys -> Hadamard + fp4 on the GPU (smla_rotate_fp4, stored form) -> fp4
+    scores -> top-2048, against the oracle's rotate_fp4 -> score -> top-k on the same keys; the
+    fp4 scores also equal the fp32-key scorer's on the GPU's own round trip."""
+    from oracle import qat
+    from smla import indexer as sidx
+    from smla import qat as sqat
+    announce("indexer key path: rotate_fp4 -> indexer_score_fp4 -> topk, B=2 N=8192")
+    g = torch.Generator().manual_seed(11)
+    B, N, Hi, Di, k = 2, 8192, 64, 64, 2048
+    kf = torch.randn(B, N, Di, generator=g)
+    q = torch.randn(B, 1, Hi, Di, generator=g).to(torch.bfloat16)
+    w = torch.randn(B, 1, Hi, generator=g)
+    ks = torch.rand(B, N, generator=g) + 0.5
+    nvis = torch.tensor([[N], [5000]], dtype=torch.int32)
+    codes, scales = sqat.fp4_pack(kf.to(dev), rotate=True)
+    sc = sidx.indexer_score_fp4(q.to(dev), codes, scales, ks.to(dev), w.to(dev), nvis.to(dev))
+    ids = sidx.topk(sc[:, 0], k, nvis[:, 0].to(dev)).cpu().numpy()
+    sc_rt = sidx.indexer_score(q.to(dev), sqat.rotate_fp4(kf.to(dev)), ks.to(dev), w.to(dev), nvis.to(dev))
+    _same(sc.cpu().numpy(), sc_rt.cpu().numpy())
+    for b in range(B):
+        ref = oidx.indexer_score(q[b].float().numpy(), qat.rotate_fp4(kf[b].numpy()), ks[b].numpy(), w[b].numpy(),
+                                 nvis[b].numpy())
+        _same(sc[b].cpu().numpy(), ref)
+        np.testing.assert_array_equal(ids[b], oidx.topk(ref, k, nvis[b].numpy())[0])
+
+
 @pytest.mark.parametrize("R,N,k,ties", [
     (1, 100, 10, False), (3, 1024, 512, True), (2, 1025, 1000, True), (8, 8192, 2048, False),
     (8, 8192, 2048, True), (1, 16384, 2048, True), (2, 65536, 2048, False), (4, 3000, 1, True),

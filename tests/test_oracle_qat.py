@@ -4,6 +4,8 @@ Each check is independent of the oracle's own formula: scipy's Hadamard matrix, 
 recursion for the rounding order, a brute-force nearest search for e2m1, a brute-force power-of-two
 search for the scale.  A planted mistake (a descending stage order, ties away from zero, a scale one
 binade off) fails one of them."""
+from fractions import Fraction
+
 import numpy as np
 import pytest
 import scipy.linalg
@@ -138,3 +140,35 @@ def test_rotate_fp4_composition():
     rng = np.random.default_rng(6)
     x = rng.standard_normal((4, 128)).astype(np.float32)
     np.testing.assert_array_equal(qat.rotate_fp4(x), qat.fp4_act_quant(qat.hadamard_rotate(x)))
+
+
+def _e2m1_ocp(c):
+    """OCP MX FP4 (E2M1): sign bit 3, exponent bits 2..1 (bias 1), mantissa bit 0; exponent 0 is
+    subnormal (mantissa / 2)."""
+    sign = -1 if c & 8 else 1
+    e, m = (c >> 1) & 3, c & 1
+    mag = Fraction(m, 2) if e == 0 else Fraction(2) ** (e - 1) * (1 + Fraction(m, 2))
+    return sign, mag
+
+
+def test_fp4_dequantize_matches_ocp_definition():
+    """Every packed byte (two codes) under every E8M0 scale byte, against exact rationals rounded
+    once to float32 (the product of a grid value and a power of two is exact unless it overflows)."""
+    packed = np.arange(256, dtype=np.uint8)[:, None].repeat(256, 1).reshape(256, 256, 1)
+    scales = np.arange(256, dtype=np.uint8)[None, :, None].repeat(256, 0)
+    got = qat.fp4_dequantize(packed.reshape(-1, 1).repeat(16, 1), scales.reshape(-1, 1), block=32)
+    got = got.reshape(256, 256, 32)
+    fmax = Fraction(np.finfo(np.float32).max.item())
+    for byte in range(256):
+        for half, c in enumerate((byte & 15, byte >> 4)):
+            sign, mag = _e2m1_ocp(c)
+            for sb in range(256):
+                v = got[byte, sb, half]
+                if sb == 255:
+                    assert np.isnan(v), (byte, sb)
+                    continue
+                exact = mag * Fraction(2) ** (sb - 127)
+                if exact > fmax:
+                    assert np.isinf(v) and np.sign(v) == sign, (byte, sb, v)
+                else:
+                    assert Fraction(float(abs(v))) == exact and (np.signbit(v) == (sign < 0)), (byte, sb, v)
