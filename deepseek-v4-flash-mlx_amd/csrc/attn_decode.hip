@@ -255,12 +255,25 @@ __global__ __launch_bounds__(768) void attn_decode_kernel(
       const int r = ci / F8_CH, cc = ci - r * F8_CH;
       if (ci < kTileRows * F8_CH) {
         uint32_t w[8];
+        // a normal power-of-two scale (the fp8 simulation's form): code x scale is a bf16 value,
+        // which the scaled converter gives exactly, two per instruction (it applies the scale's
+        // exponent only); any other scale: fp32 product rounded to bf16
+        const uint32_t su = __float_as_uint(fr.s[k]);
+        if ((su & 0x7fffffu) == 0 && su - 0x00800000u < 0x7f000000u) {
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-          const f32x2_t lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)fr.v[k][j], false);
-          const f32x2_t hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)fr.v[k][j], true);
-          w[2 * j] = pack_bf16x2(lo.x * fr.s[k], lo.y * fr.s[k]);
-          w[2 * j + 1] = pack_bf16x2(hi.x * fr.s[k], hi.y * fr.s[k]);
+          for (int j = 0; j < 4; j++) {
+            w[2 * j] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(fr.v[k][j], fr.s[k], false));
+            w[2 * j + 1] =
+                __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(fr.v[k][j], fr.s[k], true));
+          }
+        } else {
+#pragma unroll
+          for (int j = 0; j < 4; j++) {
+            const f32x2_t lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)fr.v[k][j], false);
+            const f32x2_t hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)fr.v[k][j], true);
+            w[2 * j] = pack_bf16x2(lo.x * fr.s[k], lo.y * fr.s[k]);
+            w[2 * j + 1] = pack_bf16x2(hi.x * fr.s[k], hi.y * fr.s[k]);
+          }
         }
         const u32x4_t w0 = {w[0], w[1], w[2], w[3]}, w1 = {w[4], w[5], w[6], w[7]};
         if (cc < 32) {

@@ -142,17 +142,25 @@ def test_all_masked_rows_are_nan(dev):
     assert torch.isnan(out32[1]).all() and not torch.isnan(out32[0]).any()
 
 
-@pytest.mark.parametrize("B,T,n,sharp,H,D", [(1, 64, 200, 1.0, 64, 576), (3, 700, 2000, 40.0, 64, 576),
-                                           (2, 2048, 2048, 1.0, 64, 576), (2, 333, 900, 10.0, 48, 576),
-                                           (2, 300, 500, 5.0, 64, 512)])
-def test_fp8_rows_vs_oracle(dev, B, T, n, sharp, H, D):
+@pytest.mark.parametrize("B,T,n,sharp,H,D,pow2", [(1, 64, 200, 1.0, 64, 576, True), (3, 700, 2000, 40.0, 64, 576, True),
+                                                (2, 2048, 2048, 1.0, 64, 576, True), (2, 333, 900, 10.0, 48, 576, True),
+                                                (2, 300, 500, 5.0, 64, 512, True), (2, 700, 1500, 10.0, 64, 576, False)])
+def test_fp8_rows_vs_oracle(dev, B, T, n, sharp, H, D, pow2):
+    """e4m3 rows with per-64 fp32 scales: powers of two (the fp8 simulation's form) and, with
+    pow2=False, amax/448 (any fp32 scale: row value = decode(code) * scale)."""
     from smla import sparse_attn as ssa
     from smla import workloads as wl
-    announce(f"fp8 rows B={B} T={T} n={n} H={H} D={D}")
+    announce(f"fp8 rows B={B} T={T} n={n} H={H} D={D} pow2={pow2}")
     g = torch.Generator().manual_seed(T)
     q = (torch.randn(B, 1, H, D, generator=g) * 0.05 * sharp).to(torch.bfloat16)
     x = torch.randn(B, n, D, generator=g) * 0.05
-    codes, scales = wl.quant_e4m3_pow2(x)
+    if pow2:
+        codes, scales = wl.quant_e4m3_pow2(x)
+    else:
+        blk = x.reshape(B, n, D // 64, 64)
+        scales = blk.abs().amax(-1).clamp_min(1e-4) / 448.0
+        codes = (blk / scales[..., None]).clamp(-448.0, 448.0).to(torch.float8_e4m3fn).view(torch.uint8).reshape(B, n, D)
+        assert (scales.view(torch.int32) & 0x7FFFFF).ne(0).float().mean() > 0.9  # not powers of two
     idx = torch.randint(0, n, (B, 1, T), generator=g, dtype=torch.int32)
     idx[..., :3] = -1
     idx[..., -2:] = -1
