@@ -58,6 +58,18 @@ __device__ inline void inv_rope16(u32x4_t& w0, u32x4_t& w1, const float* __restr
   }
 }
 
+// the same for 4 pairs in one u32x4 word
+__device__ inline void inv_rope8(u32x4_t& w, const float* __restrict__ cs, const float* __restrict__ sn) {
+  const f32x4_t c = *(const f32x4_t*)cs, sv = *(const f32x4_t*)sn;
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    const float x0 = __uint_as_float(w[j] << 16), x1 = __uint_as_float(w[j] & 0xffff0000u);
+    const float o0 = add_rn(mul_rn(x0, c[j]), mul_rn(x1, sv[j]));
+    const float o1 = sub_rn(mul_rn(x1, c[j]), mul_rn(x0, sv[j]));
+    w[j] = pack_bf16x2(o0, o1);
+  }
+}
+
 template <int TT, bool ROPE, int YDT>
 __global__ __launch_bounds__(64 * kLinWaves) void linear_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ w, int T, int N, int K, int64_t ldx,
@@ -160,17 +172,17 @@ __global__ __launch_bounds__(64 * kLinWaves) void linear_kernel(
   }
 }
 
-// The same product with x staged once per workgroup in LDS (T <= 8, K <= 8192): K / 512 waves,
-// each streaming exactly 8 steps (its 512-wide K slice) of the workgroup's 16 weight rows.  The
-// staging loads are issued before the weight loads (both are counted in order, so the weights
-// stay in flight while x is written to LDS); x rows are padded by 16 bytes so that the 16 token
-// rows read by one b128 pass fall in distinct banks.  Per-lane x registers drop from 64 VGPRs to
-// 8, so two workgroups fit on a CU for K = 4096.
-constexpr int kLdsSteps = 8;
+// The same product with x staged once per workgroup in LDS (T <= 8, K <= 8192): K / (64 STEPS)
+// waves, each streaming STEPS steps of 64 (its K slice) of the workgroup's 16 weight rows.  The
+// staging loads are issued before the weight loads and every load before the first wait (vmcnt
+// counts in order, so the weights stay in flight while x is written to LDS); x rows are padded by
+// 16 bytes so that the 16 token rows read by one b128 pass fall in distinct banks.  Per-lane x
+// registers drop from 64 VGPRs to 8 (16 with STEPS = 16), so two workgroups fit on a CU for
+// K = 4096.
 constexpr int kLdsMaxBytes = 160 * 1024;
 
-template <int TX, bool ROPE, int YDT>
-__global__ __launch_bounds__(1024) void linear_lds_kernel(
+template <int TX, bool ROPE, int YDT, int STEPS>
+__global__ __launch_bounds__(STEPS == 16 ? 512 : 1024) void linear_lds_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ w, int T, int N, int K, int64_t ldx,
     const int32_t* __restrict__ pos, const float* __restrict__ cos_t, const float* __restrict__ sin_t, int head_dim,
     int rd, void* __restrict__ y, int64_t ldy) {
@@ -181,42 +193,57 @@ __global__ __launch_bounds__(1024) void linear_lds_kernel(
   const int64_t row0 = (int64_t)blockIdx.x * 16;
   const int64_t g = row0 / N;
   const int xst = K + 8;  // padded LDS row (elements)
-  // 1. this thread's 16-byte chunk k = 8 * threadIdx.x of every token row (nw * 64 * 8 == K)
-  const int kc = 8 * threadIdx.x;
-  u32x4_t xr[TX];
-#pragma unroll
-  for (int c = 0; c < TX; c++) xr[c] = *(const u32x4_t*)(x + (int64_t)min(c, T - 1) * ldx + g * K + kc);
-  // 2. the wave's weight slice: 8 steps of 64, 32 bytes per lane each
-  const int kbeg = wave * (kLdsSteps * 64);
-  const uint16_t* wp = w + (row0 + m) * (int64_t)K + kbeg + 16 * q;
-  u32x4_t wv[kLdsSteps][2];
-#pragma unroll
-  for (int s = 0; s < kLdsSteps; s++) {
-    wv[s][0] = *(const u32x4_t*)(wp + s * 64);
-    wv[s][1] = *(const u32x4_t*)(wp + s * 64 + 8);
-  }
-  // 3. x into LDS
+  // 1. this thread's 16-byte chunks k = 8 (threadIdx.x + j blockDim.x) of every token row
+  // (nw * 64 * 8 * STEPS / 8 == K)
+  constexpr int XJ = STEPS / 8;
+  u32x4_t xr[TX][XJ];
 #pragma unroll
   for (int c = 0; c < TX; c++)
-    if (c < T) *(u32x4_t*)(xs + c * xst + kc) = xr[c];
+#pragma unroll
+    for (int j = 0; j < XJ; j++)
+      xr[c][j] = *(const u32x4_t*)(x + (int64_t)min(c, T - 1) * ldx + g * K + 8 * (threadIdx.x + j * blockDim.x));
+  // keep the x loads ahead of the weight loads: vmcnt counts in issue order, so the x rows can then
+  // be written to LDS while the weights are still in flight (unpinned, the compiler may issue the
+  // weights first, and the wait for x then drains every load)
+  __builtin_amdgcn_sched_barrier(0);
+  // 2. the wave's weight slice: STEPS steps of 64 (two MFMA K-blocks of 32 each); lane (m, q)
+  // takes k 8q .. 8q+7 of both blocks, so each load instruction reads 64 contiguous bytes of 16 rows
+  const int kbeg = wave * (STEPS * 64);
+  const uint16_t* wp = w + (row0 + m) * (int64_t)K + kbeg + 8 * q;
+  u32x4_t wv[STEPS][2];
+#pragma unroll
+  for (int s = 0; s < STEPS; s++) {
+    wv[s][0] = *(const u32x4_t*)(wp + s * 64);
+    wv[s][1] = *(const u32x4_t*)(wp + s * 64 + 32);
+  }
+  __builtin_amdgcn_sched_barrier(0);  // every weight load issued before the first wait for x
+  // 3. x into LDS, all TX rows (rows past T repeat row T-1 and are not read); a guard here would
+  // let the compiler sink the row's loads into it, behind the weight loads
+#pragma unroll
+  for (int c = 0; c < TX; c++)
+#pragma unroll
+    for (int j = 0; j < XJ; j++) *(u32x4_t*)(xs + c * xst + 8 * (threadIdx.x + j * blockDim.x)) = xr[c][j];
   __syncthreads();
   // 4. MFMAs: token column m reads its row (rows past T read row T-1 and are not stored)
-  const uint16_t* xrow = xs + min(m, T - 1) * xst + kbeg + 16 * q;
+  const uint16_t* xrow = xs + min(m, T - 1) * xst + kbeg + 8 * q;
   const float* csp = nullptr;
   const float* snp = nullptr;
   if constexpr (ROPE) {
     const int64_t p = pos[min(m, T - 1)];
-    csp = cos_t + p * (rd / 2) + 8 * q;
-    snp = sin_t + p * (rd / 2) + 8 * q;
+    csp = cos_t + p * (rd / 2) + 4 * q;
+    snp = sin_t + p * (rd / 2) + 4 * q;
   }
   const int nope = head_dim - rd;
   f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int s = 0; s < kLdsSteps; s++) {
-    u32x4_t x0 = *(const u32x4_t*)(xrow + s * 64), x1 = *(const u32x4_t*)(xrow + s * 64 + 8);
+  for (int s = 0; s < STEPS; s++) {
+    u32x4_t x0 = *(const u32x4_t*)(xrow + s * 64), x1 = *(const u32x4_t*)(xrow + s * 64 + 32);
     if constexpr (ROPE) {
       const int d0 = (kbeg + s * 64) % head_dim;  // the step is all rope dims or none
-      if (d0 >= nope) inv_rope16(x0, x1, csp + (d0 - nope) / 2, snp + (d0 - nope) / 2);
+      if (d0 >= nope) {  // pairs (d0 - nope)/2 + 4q .. +3 and 16 further
+        inv_rope8(x0, csp + (d0 - nope) / 2, snp + (d0 - nope) / 2);
+        inv_rope8(x1, csp + (d0 - nope) / 2 + 16, snp + (d0 - nope) / 2 + 16);
+      }
     }
     acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(wv[s][0]), as_bf16x8(x0), acc, 0, 0, 0);
     acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(wv[s][1]), as_bf16x8(x1), acc, 0, 0, 0);
@@ -244,15 +271,15 @@ __global__ __launch_bounds__(1024) void linear_lds_kernel(
   }
 }
 
-template <int TX, bool ROPE, int YDT>
+template <int TX, bool ROPE, int YDT, int STEPS>
 int launch_linear_lds(const uint16_t* x, const uint16_t* w, int64_t T, int64_t G, int64_t N, int64_t K, int64_t ldx,
                       const int32_t* pos, const float* cos_t, const float* sin_t, int head_dim, int rd, void* y,
                       hipStream_t st) {
-  auto kern = linear_lds_kernel<TX, ROPE, YDT>;
+  auto kern = linear_lds_kernel<TX, ROPE, YDT, STEPS>;
   static std::atomic<uint64_t> lds_attr{0};  // devices whose limit is raised
   if (hipError_t e = smla_set_dynamic_lds((const void*)kern, kLdsMaxBytes, lds_attr); e != hipSuccess) return (int)e;
-  const int nw = (int)(K / (kLdsSteps * 64));
-  const int64_t xbytes = T * (K + 8) * 2, rbytes = (int64_t)nw * 64 * 16;
+  const int nw = (int)(K / (STEPS * 64));
+  const int64_t xbytes = TX * (K + 8) * 2, rbytes = (int64_t)nw * 64 * 16;
   const size_t lds = (size_t)(xbytes > rbytes ? xbytes : rbytes);
   hipLaunchKernelGGL(kern, dim3((unsigned)(G * N / 16)), dim3(64 * nw), lds, st, x, w, (int)T, (int)N, (int)K, ldx,
                      pos, cos_t, sin_t, head_dim, rd, y, G * N);
@@ -262,9 +289,10 @@ int launch_linear_lds(const uint16_t* x, const uint16_t* w, int64_t T, int64_t G
 
 // the LDS form applies: T <= 8, K a multiple of 512 of at most 16 waves (x then fits: 8 rows of
 // at most 8200 bf16)
-bool lds_form(int64_t T, int64_t K) {
-  return T <= 8 && K % (kLdsSteps * 64) == 0 && K / (kLdsSteps * 64) <= 16;
-}
+bool lds_form(int64_t T, int64_t K) { return T <= 8 && K % 512 == 0 && K / 512 <= 16; }
+// K steps of 64 per wave: 16 for K = 8192 (8 waves of 512 threads, each with 32 weight loads in
+// flight; the 16-wave form streams 6 % slower), else 8
+int lds_steps(int64_t K) { return (K % 1024 == 0 && K / 1024 == 8) ? 16 : 8; }
 
 // one thread per (token, head, pair)
 template <int XDT>
@@ -302,7 +330,9 @@ int launch_linear_t(const uint16_t* x, const uint16_t* w, int64_t T, int64_t G, 
                     const int32_t* pos, const float* cos_t, const float* sin_t, int head_dim, int rd, void* y,
                     hipStream_t st) {
   if (lds_form(T, K))
-    return launch_linear_lds<8, ROPE, YDT>(x, w, T, G, N, K, ldx, pos, cos_t, sin_t, head_dim, rd, y, st);
+    return lds_steps(K) == 16
+               ? launch_linear_lds<8, ROPE, YDT, 16>(x, w, T, G, N, K, ldx, pos, cos_t, sin_t, head_dim, rd, y, st)
+               : launch_linear_lds<8, ROPE, YDT, 8>(x, w, T, G, N, K, ldx, pos, cos_t, sin_t, head_dim, rd, y, st);
   const dim3 grid((unsigned)(G * N / 16)), blk(64 * kLinWaves);
   if (T <= 16)
     hipLaunchKernelGGL((linear_kernel<1, ROPE, YDT>), grid, blk, 0, st, x, w, (int)T, (int)N, (int)K, ldx, pos, cos_t,
