@@ -189,16 +189,38 @@ __global__ __launch_bounds__(768) void attn_decode_kernel(
   // past the last live id are dropped (index lists padded with -1 at the end cost nothing)
   // The score waves load the table: they issue no row copies, so their id loads do not queue
   // behind the Q rows' copies (vmcnt counts in order), and the barriers below wait for LDS only.
+  // Past 256 ids (one per score thread), four per thread are requested before any is written (one
+  // round trip per 1024 ids; loads at clamped indexes, so none is conditional and none sinks
+  // behind a wait).
   int last = -1;
-  if (scorer) {
-    for (int t = tid; t < ntiles_all * kTileRows; t += 4 * 64) {
-      int r = -1;
-      if (t < nrows) {
-        r = ig[t];
-        r = (r >= 0 && r < ntot) ? r : -1;
+  const int nt = ntiles_all * kTileRows;
+  if (MAXROWS <= 4 * 64 || nt <= 4 * 64) {
+    if (scorer) {
+      for (int t = tid; t < nt; t += 4 * 64) {
+        int r = -1;
+        if (t < nrows) {
+          r = ig[t];
+          r = (r >= 0 && r < ntot) ? r : -1;
+        }
+        ids_s[t] = r;
+        if (r >= 0) last = t;
       }
-      ids_s[t] = r;
-      if (r >= 0) last = t;
+    }
+  } else if (scorer) {
+    for (int t0 = tid; t0 < nt; t0 += 4 * 4 * 64) {
+      int v[4];
+#pragma unroll
+      for (int u = 0; u < 4; u++) v[u] = ig[min(t0 + u * 4 * 64, nrows - 1)];
+#pragma unroll
+      for (int u = 0; u < 4; u++) {
+        const int t = t0 + u * 4 * 64;
+        if (t < nt) {
+          int r = t < nrows ? v[u] : -1;
+          r = (r >= 0 && r < ntot) ? r : -1;
+          ids_s[t] = r;
+          if (r >= 0) last = t;
+        }
+      }
     }
   }
   {

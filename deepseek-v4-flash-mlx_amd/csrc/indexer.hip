@@ -277,12 +277,23 @@ __global__ __launch_bounds__(64 * (64 / HPW)) void indexer2_kernel(const void* _
         for (int j = 0; j < 4; j++) o[4 * v + j] = __uint_as_float(row[4 * db + v][j]);
     }
   };
-  // q rows -> LDS as fp32, weights
+  // q rows -> LDS as fp32, weights: every load issued before the first LDS write (one round trip
+  // for keys, q and weights together; vmcnt counts in order)
   {
-    if constexpr (QDT == SMLA_BF16) {
-      const u32x4_t* qp = (const u32x4_t*)((const uint16_t*)q + bs * 64 * DI);
-      for (int i = tid; i < 64 * DI / 8; i += NT) {
-        const u32x4_t v = qp[i];
+    constexpr int QW = QDT == SMLA_BF16 ? 8 : 4;  // q values per 16-byte word
+    constexpr int QIT = 64 * DI / QW / NT;         // words per thread
+    static_assert(QIT * NT * QW == 64 * DI, "q words split evenly over the workgroup");
+    const u32x4_t* qp = (const u32x4_t*)((const uint8_t*)q + bs * 64 * DI * (16 / QW));
+    u32x4_t qv[QIT];
+#pragma unroll
+    for (int k = 0; k < QIT; k++) qv[k] = qp[tid + k * NT];
+    const float wt = tid < 64 ? weights[bs * 64 + tid] : 0.f;
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int k = 0; k < QIT; k++) {
+      const int i = tid + k * NT;
+      const u32x4_t v = qv[k];
+      if constexpr (QDT == SMLA_BF16) {
         f32x4_t lo, hi;
 #pragma unroll
         for (int j = 0; j < 2; j++) {
@@ -293,12 +304,11 @@ __global__ __launch_bounds__(64 * (64 / HPW)) void indexer2_kernel(const void* _
         }
         *(f32x4_t*)(sq + 8 * i) = lo;
         *(f32x4_t*)(sq + 8 * i + 4) = hi;
+      } else {
+        *(u32x4_t*)(sq + 4 * i) = v;
       }
-    } else {
-      const f32x4_t* qp = (const f32x4_t*)((const float*)q + bs * 64 * DI);
-      for (int i = tid; i < 64 * DI / 4; i += NT) *(f32x4_t*)(sq + 4 * i) = qp[i];
     }
-    if (tid < 64) sw[tid] = weights[bs * 64 + tid];
+    if (tid < 64) sw[tid] = wt;
   }
   __syncthreads();
   float dot[KPL][HPW];
