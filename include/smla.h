@@ -30,7 +30,7 @@
  *                             v4mlx/compressor.py:57-59        the indexer compressor's key transform
  *   smla_rope                 ref_torch/norm_rope.py:53-62     apply_rotary_emb(x, freqs_cis, inverse) in place
  *                             v4mlx/norm_rope.py:46-62         (MLX twin, cos/sin tables)
- *   smla_linear               v4mlx/mla.py:16-18               linear(x, W) for T <= 32 tokens (decode)
+ *   smla_linear               v4mlx/mla.py:16-18               linear(x, W) (and the grouped form of mla.py:49-53)
  *   smla_o_proj               oracle/decode_engine.py:118-119  inverse RoPE of o's rope dims + o_grouped
  *                             v4mlx/mla.py:42-56               o_grouped(o, wo_a, wo_b)
  */
@@ -341,9 +341,10 @@ int smla_rope(void* x, int x_dtype, int64_t T, int64_t heads, int64_t head_dim, 
 
 /* smla_linear: y[t, g*N + n] = sum_k x[t, g*K + k] * w[g*N + n, k] for G groups of N rows (G = 1
  * is v4mlx/mla.py:16-18, y = x @ W^T; G > 1 is the grouped product of v4mlx/mla.py:49-53).
- *   x [T, G*K] BF16, w [G*N, K] BF16, y [T, G*N] BF16 or F32; float32 accumulation.
- *   T <= 32 (the decode step's tokens), N % 16 == 0, K % 512 == 0, 16-byte aligned pointers.
- *   Bound by streaming w from HBM once. */
+ *   x [T, G*K], w [G*N, K]: both BF16 or both F32; y [T, G*N] BF16 or F32; float32 accumulation.
+ *   16-byte aligned pointers; K % 8 == 0 (BF16) or K % 4 == 0 (F32); any T >= 1.
+ *   Decode shapes (BF16, T <= 32, N % 16 == 0, K % 512 == 0) stream w from HBM once (the bound);
+ *   other shapes run a tiled MFMA GEMM (128 x 128 tiles, bf16 or fp32 MFMA by operand type). */
 int smla_linear(const void* x, int x_dtype, const void* w, int w_dtype, int64_t T, int64_t G,
                 int64_t N, int64_t K, void* y, int y_dtype, void* stream);
 
@@ -352,9 +353,9 @@ int smla_linear(const void* x, int x_dtype, const void* w, int w_dtype, int64_t 
  *   (inverse RoPE at pos[t], cos_t/sin_t [n_pos, rd/2] fp32) on the fly, rounded to bf16;
  *   mid [T, G*R] BF16 (caller workspace) = grouped projection with wo_a [G*R, heads*head_dim/G];
  *   y [T, dim] BF16 or F32 = mid @ wo_b^T with wo_b [dim, G*R].  w_dtype: BF16.
- *   Same limits as smla_linear; with RoPE head_dim % 64 == 0, rd % 64 == 0 and each group's
- *   slice a whole number of heads.  Replaces v4mlx/mla.py:42-56 (o_grouped) after the inverse
- *   rotary call. */
+ *   Same limits as smla_linear (BF16 operands); with RoPE head_dim % 64 == 0, rd % 64 == 0 and
+ *   each group's slice a whole number of heads, and rd == 64 outside the decode shapes.
+ *   Replaces v4mlx/mla.py:42-56 (o_grouped) after the inverse rotary call. */
 int smla_o_proj(const void* o, int o_dtype, const int32_t* pos, const float* cos_t,
                 const float* sin_t, int64_t n_pos, int64_t T, int64_t heads, int64_t head_dim,
                 int64_t rd, int64_t G, int64_t R, const void* wo_a, const void* wo_b, int w_dtype,
