@@ -11,14 +11,6 @@ import torch
 
 from . import ops
 
-_MAX_DECODE_ROWS = 32
-
-
-def _decode_shape(x, *ws, k_mult=512):
-    rows = x.numel() // x.shape[-1] if x.dim() else 0
-    return (x.is_cuda and 0 < rows <= _MAX_DECODE_ROWS and x.dtype == torch.bfloat16
-            and all(w.dtype == torch.bfloat16 for w in ws) and x.shape[-1] % k_mult == 0)
-
 N_HEADS, HEAD_DIM, ROPE_HD = 64, 512, 64
 N_GROUPS, O_LORA = 8, 1024
 

@@ -54,16 +54,6 @@ def dequant_e4m3(codes, scales, block=64):
     return (v * scales[..., None]).reshape(sh)
 
 
-def mean_pool_ref_free(kv, ratio=4):
-    """Block mean in fp32 (row order) -> same dtype as kv.  Host helper for workload setup."""
-    b, n, d = kv.shape
-    blk = kv[:, : (n // ratio) * ratio].float().reshape(b, n // ratio, ratio, d)
-    acc = blk[:, :, 0]
-    for j in range(1, ratio):
-        acc = acc + blk[:, :, j]
-    return (acc * (1.0 / ratio)).to(kv.dtype)
-
-
 def fp32_plumbing():
     g = _gen(0)
     q = torch.randn(1, 16, D, generator=g) * 0.1

@@ -160,6 +160,22 @@ def test_topk_exact(dev, R, N, k, ties):
     np.testing.assert_array_equal(got0, np.where(ref0 >= 0, ref0 + 5, -1))
 
 
+def test_topk_into_strided_view(dev):
+    """ops.topk_into writes the same selection into a column slice of a wider int32 buffer (its
+    row stride), leaving the other columns alone."""
+    from smla import indexer as sidx
+    from smla import ops
+    announce("topk_into strided view R=4 N=3000 k=700")
+    g = torch.Generator().manual_seed(21)
+    sc = torch.randn(4, 3000, generator=g).to(dev)
+    nvis = torch.tensor([3000, 10, 700, 2500], dtype=torch.int32, device=dev)
+    buf = torch.full((4, 900), -7, dtype=torch.int32, device=dev)
+    ops.topk_into(sc, 700, buf[:, 100:800], id_offset=5, nvis=nvis)
+    ref = sidx.topk(sc, 700, nvis, id_offset=5)
+    torch.testing.assert_close(buf[:, 100:800], ref, rtol=0, atol=0)
+    assert (buf[:, :100] == -7).all() and (buf[:, 800:] == -7).all()
+
+
 def test_topk_all_equal_and_ragged(dev):
     from smla import indexer as sidx
     announce("topk all equal")
