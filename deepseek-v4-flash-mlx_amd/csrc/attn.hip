@@ -10,6 +10,7 @@
 //  * attn_merge_kernel   — log-sum-exp merge of the split partial states that the MFMA split
 //    kernel (attn_decode.hip) writes.
 //  * the split plan and the C entry points.
+#include <algorithm>
 #include <mutex>
 
 #include "attn_common.h"
@@ -441,6 +442,31 @@ static int attn_call(const void* q, int q_dtype, const void* kv0, int64_t n0, co
   if (need > 0 && (!ws || ws_bytes < need)) return SMLA_E_WORKSPACE;
   return attn_launch(p, phases, q, q_dtype, src, kv_dtype, attn_sink, topk_idxs, T, B, S, H, D, DV, scale, out,
                           out_dtype, ws, (hipStream_t)stream);
+}
+
+// Prompt attention with the row sets of oracle/decode_engine.py:107-117 computed in the kernel:
+// one workgroup per (query, 64-head group), lists as ImplicitRows describes, queries longest first.
+extern "C" int smla_prefill_attn(const void* q, int q_dtype, const void* kv_raw, int64_t n_raw, const void* kv_comp,
+                                 int64_t n_comp, int kv_dtype, const float* attn_sink, int64_t q_pos0,
+                                 int64_t window, int64_t ratio, int64_t B, int64_t S, int64_t H, int64_t D,
+                                 int64_t DV, float scale, void* out, int out_dtype, void* stream) {
+  if (!q || !kv_raw || !out || (ratio > 0 && n_comp > 0 && !kv_comp)) return SMLA_E_NULL;
+  if (B <= 0 || S <= 0 || H <= 0 || n_raw <= 0 || n_comp < 0) return SMLA_E_SHAPE;
+  if (q_dtype != SMLA_BF16 || kv_dtype != SMLA_BF16 || (out_dtype != SMLA_BF16 && out_dtype != SMLA_F32))
+    return SMLA_E_DTYPE;
+  if ((D != 576 && D != 512) || DV != 512 || H % 16 != 0) return SMLA_E_UNSUPPORTED;
+  if (window <= 0 || ratio < 0 || q_pos0 < 0 || q_pos0 + S > n_raw) return SMLA_E_RANGE;
+  if (((uintptr_t)q & 15) || ((uintptr_t)kv_raw & 15) || ((uintptr_t)kv_comp & 15) || ((uintptr_t)out & 15))
+    return SMLA_E_UNSUPPORTED;
+  const int64_t nc_max = ratio > 0 ? std::min((q_pos0 + S) / ratio, n_comp) : 0;
+  const int64_t T = window + nc_max;
+  const int64_t rows = (T + kTileRows - 1) / kTileRows * kTileRows;
+  if (rows > smla_attn::kDecodeV6MaxRows || B * S > 65535 || window > 0x7fffffff) return SMLA_E_UNSUPPORTED;
+  const smla_attn::RowSrc src{kv_raw, nc_max > 0 ? kv_comp : nullptr, nullptr, nullptr, n_raw,
+                              nc_max > 0 ? n_comp : 0};
+  const smla_attn::ImplicitRows ir{q_pos0, (int)window, (int)ratio, 1};
+  return smla_attn::launch_decode_v6((int)D, false, 1, (int)rows, q, src, attn_sink, nullptr, T, B, S, H, scale, out,
+                                     out_dtype, nullptr, (hipStream_t)stream, ir);
 }
 
 extern "C" size_t smla_sparse_attn_workspace(int64_t B, int64_t S, int64_t H, int64_t D, int64_t DV,

@@ -17,13 +17,25 @@ struct RowSrc {
   int64_t n0, n1;
 };
 
+// Prefill row sets computed in the kernel instead of read from an index list: query s of a
+// sequence sits at position p = q_pos0 + s; list entry t < window is raw row max(0, p-window+1) + t
+// (-1 past p), entry window + c is compressed row c (id n0 + c) for c < (p+1)/ratio, else -1 --
+// the lists oracle/decode_engine.py:110-114 builds for every position of a prompt.  Workgroups
+// then take the queries longest first.
+struct ImplicitRows {
+  int64_t q_pos0;
+  int window;
+  int ratio;  // 0: window rows only
+  int enabled;
+};
+
 // bf16 or fp8 (e4m3 + per-64 pow2 scales) rows, D in {576, 512}, DV = 512, H % 16 == 0: 12-wave
 // role-split kernel (4 score waves, 8 value waves, 64 heads per workgroup).  Writes the final
 // output (nsplit == 1) or partial states: (m, l) fp32 per (query row, split, head), then the partial
 // O rows (bf16 for bf16 output, else fp32) after all (m, l) records, split-major.
 int launch_decode_v6(int D, bool kv_fp8, int nsplit, int rows_per_split, const void* q, RowSrc src,
                      const float* sink, const int32_t* idx, int64_t T, int64_t B, int64_t S, int64_t H, float scale,
-                     void* out, int out_dtype, float* part, hipStream_t stream);
+                     void* out, int out_dtype, float* part, hipStream_t stream, ImplicitRows ir = ImplicitRows{});
 constexpr int kDecodeV6ShortRows = 256;  // up to here: 4-tile ring; its index table lives in LDS
 constexpr int kDecodeV6MaxRows = 8192;   // beyond: 3-tile ring and a larger index table
 

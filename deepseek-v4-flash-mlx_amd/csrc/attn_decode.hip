@@ -100,7 +100,7 @@ template <int D, int NBUF, int MAXROWS, bool FP8>
 __global__ __launch_bounds__(768) void attn_decode_kernel(
     const uint16_t* __restrict__ q, RowSrc src, const float* __restrict__ sink, const int32_t* __restrict__ idx,
     int T, int S, int H, int rows_per_split, float scale, float* __restrict__ part, void* __restrict__ out,
-    int out_dtype) {
+    int out_dtype, ImplicitRows ir) {
   using G = Geo6<D, NBUF, MAXROWS>;
   extern __shared__ __align__(16) uint8_t lds_generic[];
   lds_u8_t* lds = (lds_u8_t*)lds_generic;
@@ -118,6 +118,7 @@ __global__ __launch_bounds__(768) void attn_decode_kernel(
   int64_t bs;
   if (nsplit == 1 && gridDim.z == 1) {
     bs = query_row_of(blockIdx.y, gridDim.y);
+    if (ir.enabled) bs = gridDim.y - 1 - bs;  // prompt positions grow with s: longest lists first
   } else {
     int64_t item;
     xcd_row_item(gridDim.y, (int64_t)nsplit * gridDim.z, bs, item);
@@ -131,7 +132,7 @@ __global__ __launch_bounds__(768) void attn_decode_kernel(
   const int nrows = max(0, t_end - t_begin);
   const int ntiles_all = (nrows + kTileRows - 1) / kTileRows;
   const int64_t n0 = src.n0, n1 = src.n1, ntot = n0 + n1;
-  const int32_t* ig = idx + bs * (int64_t)T + t_begin;
+  const int32_t* ig = idx ? idx + bs * (int64_t)T + t_begin : nullptr;
   const bool scorer = wave < 4;
   const int g = lane >> 4, c = lane & 15;
 
@@ -194,7 +195,25 @@ __global__ __launch_bounds__(768) void attn_decode_kernel(
   // behind a wait).
   int last = -1;
   const int nt = ntiles_all * kTileRows;
-  if (MAXROWS <= 4 * 64 || nt <= 4 * 64) {
+  if (ir.enabled) {
+    // the list of the query at position p, entry by entry (no loads)
+    if (scorer) {
+      const int64_t p = ir.q_pos0 + bs % S;
+      const int64_t lo = p - ir.window + 1 > 0 ? p - ir.window + 1 : 0;
+      const int64_t ncv = ir.ratio > 0 ? (p + 1) / ir.ratio : 0;
+      const int64_t nc = ncv < n1 ? ncv : n1;
+      for (int t = tid; t < nt; t += 4 * 64) {
+        const int e = t_begin + t;
+        int r = -1;
+        if (t < nrows) {
+          if (e < ir.window) r = lo + e <= p ? (int)(lo + e) : -1;
+          else r = e - ir.window < nc ? (int)(n0 + (e - ir.window)) : -1;
+        }
+        ids_s[t] = r;
+        if (r >= 0) last = t;
+      }
+    }
+  } else if (MAXROWS <= 4 * 64 || nt <= 4 * 64) {
     if (scorer) {
       for (int t = tid; t < nt; t += 4 * 64) {
         int r = -1;
@@ -554,14 +573,14 @@ __global__ __launch_bounds__(768) void attn_decode_kernel(
 template <int D, int NBUF, int MAXROWS, bool FP8>
 int launch6(int nsplit, int rows_per_split, const void* q, RowSrc src, const float* sink, const int32_t* idx,
             int64_t T, int64_t B, int64_t S, int64_t H, float scale, void* out, int out_dtype, float* part,
-            hipStream_t stream) {
+            hipStream_t stream, ImplicitRows ir) {
   using G = Geo6<D, NBUF, MAXROWS>;
   auto kern = attn_decode_kernel<D, NBUF, MAXROWS, FP8>;
   static std::atomic<uint64_t> lds_attr{0};  // devices whose limit is raised
   if (hipError_t e = smla_set_dynamic_lds((const void*)kern, G::LDS_BYTES, lds_attr); e != hipSuccess) return (int)e;
   dim3 grid((unsigned)nsplit, (unsigned)(B * S), (unsigned)((H + 63) / 64));
   hipLaunchKernelGGL(kern, grid, dim3(G::NW * 64), G::LDS_BYTES, stream, (const uint16_t*)q, src, sink, idx, (int)T,
-                     (int)S, (int)H, rows_per_split, scale, part, out, out_dtype);
+                     (int)S, (int)H, rows_per_split, scale, part, out, out_dtype, ir);
   SMLA_HIP_CHECK_LAUNCH();
   return SMLA_OK;
 }
@@ -573,14 +592,14 @@ int launch6(int nsplit, int rows_per_split, const void* q, RowSrc src, const flo
 // long single-sequence lists)
 int launch_decode_v6(int D, bool kv_fp8, int nsplit, int rows_per_split, const void* q, RowSrc src,
                      const float* sink, const int32_t* idx, int64_t T, int64_t B, int64_t S, int64_t H, float scale,
-                     void* out, int out_dtype, float* part, hipStream_t stream) {
+                     void* out, int out_dtype, float* part, hipStream_t stream, ImplicitRows ir) {
   if (rows_per_split > kDecodeV6MaxRows || rows_per_split % kTileRows != 0 || B * S > 65535) return SMLA_E_UNSUPPORTED;
   const bool sh = rows_per_split <= kDecodeV6ShortRows;
 #define SMLA_V6(DD, F8)                                                                                           \
   return sh ? launch6<DD, 4, kDecodeV6ShortRows, F8>(nsplit, rows_per_split, q, src, sink, idx, T, B, S, H, scale, \
-                                                     out, out_dtype, part, stream)                                 \
+                                                     out, out_dtype, part, stream, ir)                             \
             : launch6<DD, 3, kDecodeV6MaxRows, F8>(nsplit, rows_per_split, q, src, sink, idx, T, B, S, H, scale,   \
-                                                   out, out_dtype, part, stream);
+                                                   out, out_dtype, part, stream, ir);
   if (D == 576) {
     if (kv_fp8) SMLA_V6(576, true) else SMLA_V6(576, false)
   }

@@ -31,6 +31,8 @@ _SIGNATURES = {
                                    _i64, _i64, _i64, _i64, _i64, _f32, _vp, _int, _i64, _int, _vp, _sz, _vp]),
     "smla_sparse_attn_noalloc": (_int, [_vp, _int, _vp, _i64, _vp, _i64, _int, _vp, _vp, _vp, _vp, _i64,
                                         _i64, _i64, _i64, _i64, _i64, _f32, _vp, _int, _vp]),
+    "smla_prefill_attn": (_int, [_vp, _int, _vp, _i64, _vp, _i64, _int, _vp, _i64, _i64, _i64, _i64, _i64, _i64,
+                                 _i64, _i64, _f32, _vp, _int, _vp]),
     "smla_window_topk_idxs": (_int, [_i64, _i64, _i64, _i64, _vp, _vp]),
     "smla_decode_window_idxs": (_int, [_vp, _i64, _i64, _vp, _i64, _vp]),
     "smla_indexer_score": (_int, [_vp, _int, _vp, _int, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64,

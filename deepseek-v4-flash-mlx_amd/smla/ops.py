@@ -46,6 +46,9 @@ def _is_fp8_rows(t):
     return t.dtype == torch.uint8 or (hasattr(torch, "float8_e4m3fn") and t.dtype == torch.float8_e4m3fn)
 
 
+_YDT_ATTN = {torch.float32: _lib.F32, torch.bfloat16: _lib.BF16}
+
+
 def _check_attn(q, kv0, kv1, kv0_scale, kv1_scale, attn_sink, topk_idxs, dv):
     """Shape and type agreement of the attention operands, checked before any launch (a mismatch
     would send the kernel's row, index or scale addressing past its buffers)."""
@@ -102,6 +105,42 @@ def attn_plan(B, S, H, D, dv, T, q_dtype=torch.bfloat16, kv_dtype=torch.bfloat16
     wsb = _lib.lib().smla_sparse_attn_plan(B, S, H, D, dv, T, qd, kd, od, rows_per_split, ctypes.byref(ns),
                                            ctypes.byref(rps))
     return ns.value, rps.value, int(wsb)
+
+
+@torch.library.custom_op("smla::prefill_attn", mutates_args=(), device_types="cuda")
+def prefill_attn_op(q: torch.Tensor, kv_raw: torch.Tensor, kv_comp: Optional[torch.Tensor],
+                    attn_sink: Optional[torch.Tensor], q_pos0: int, window: int, ratio: int, scale: float,
+                    dv: int, out_dtype: torch.dtype) -> torch.Tensor:
+    """q [B,S,H,D] bf16 at positions q_pos0..q_pos0+S-1, kv_raw [B,n_raw,D] bf16, kv_comp
+    [B,n_comp,D] bf16 or None -> [B,S,H,dv]: every query attends its window rows and the compressed
+    rows causally visible to it (the row sets are computed in the kernel)."""
+    _on_gpu(q, kv_raw, kv_comp, attn_sink)
+    if q.dim() != 4 or kv_raw.dim() != 3:
+        raise ValueError("expected q [B,S,H,D] and kv_raw [B,n_raw,D]")
+    B, S, H, D = q.shape
+    if kv_raw.shape[0] != B or kv_raw.shape[2] != D:
+        raise ValueError(f"kv_raw {tuple(kv_raw.shape)} does not match q {tuple(q.shape)}")
+    if kv_comp is not None and (kv_comp.dim() != 3 or kv_comp.shape[0] != B or kv_comp.shape[2] != D):
+        raise ValueError(f"kv_comp {tuple(kv_comp.shape)} does not match q {tuple(q.shape)}")
+    if attn_sink is not None and tuple(attn_sink.shape) != (H,):
+        raise ValueError(f"attn_sink {tuple(attn_sink.shape)} must be [{H}]")
+    if q.dtype != torch.bfloat16 or kv_raw.dtype != torch.bfloat16 or (kv_comp is not None and
+                                                                      kv_comp.dtype != torch.bfloat16):
+        raise TypeError("prefill_attn takes bf16 q and rows")
+    q, kv_raw, kv_comp = q.contiguous(), kv_raw.contiguous(), _c(kv_comp)
+    if attn_sink is not None:
+        attn_sink = attn_sink.float().contiguous()
+    n_comp = kv_comp.shape[1] if kv_comp is not None else 0
+    out = torch.empty(B, S, H, dv, dtype=out_dtype, device=q.device)
+    _lib.call("smla_prefill_attn", _p(q), _lib.BF16, _p(kv_raw), kv_raw.shape[1], _p(kv_comp), n_comp, _lib.BF16,
+              _p(attn_sink), int(q_pos0), int(window), int(ratio), B, S, H, D, dv, float(scale), _p(out),
+              _YDT_ATTN[out_dtype], _stream(q))
+    return out
+
+
+@prefill_attn_op.register_fake
+def _(q, kv_raw, kv_comp, attn_sink, q_pos0, window, ratio, scale, dv, out_dtype):
+    return q.new_empty(*q.shape[:3], dv, dtype=out_dtype)
 
 
 @torch.library.custom_op("smla::sparse_attn", mutates_args=(), device_types="cuda")

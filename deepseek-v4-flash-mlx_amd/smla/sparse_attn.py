@@ -44,6 +44,16 @@ def sparse_attn_batched(q, kv, attn_sink, topk_idxs, scale, dv=None, kv_scale=No
     return ops.sparse_attn_op(q, kv, None, kv_scale, None, attn_sink, topk_idxs, float(scale), dv)
 
 
+def prefill_attn(q, kv_raw, kv_comp, attn_sink, scale, q_pos0=0, window=128, ratio=4, dv=512, out_dtype=None):
+    """Prompt attention of ``oracle/decode_engine.py:107-117`` without index lists: query s (position
+    q_pos0 + s) attends raw rows max(0, p-window+1)..p and, for ratio > 0, the compressed rows
+    0..(p+1)//ratio - 1 -- the same result, bit for bit, as ``sparse_attn_two_source`` over
+    ``workloads.prefill_indices`` lists.  q [B,S,H,D] bf16, kv_raw [B,n_raw,D], kv_comp [B,n_comp,D]
+    or None -> [B,S,H,dv] (q's dtype unless out_dtype is given)."""
+    return ops.prefill_attn_op(q, kv_raw, kv_comp if ratio > 0 else None, attn_sink, int(q_pos0), int(window),
+                               int(ratio), float(scale), int(dv), out_dtype or q.dtype)
+
+
 def sparse_attn_two_source(q, kv0, kv1, attn_sink, topk_idxs, scale, dv=None, kv0_scale=None, kv1_scale=None):
     """Ids index the virtual concatenation [kv0; kv1] along rows (per batch entry)."""
     dv = q.shape[-1] if dv is None else dv

@@ -12,6 +12,7 @@
  *   smla_sparse_attn          ref_torch/sparse_attn.py:23-34   sparse_attn(q, kv, attn_sink, topk_idxs, scale)
  *                             v4mlx/sparse_attn.py:26-39       (MLX twin)
  *   smla_sparse_attn_ex       ref_torch/sparse_attn.py:23-34   (the same, with an explicit split plan / phases)
+ *   smla_prefill_attn         oracle/decode_engine.py:107-117  per-position prompt attention (row sets on device)
  *   smla_window_topk_idxs     ref_torch/sparse_attn.py:9-20    get_window_topk_idxs(window_size, bsz, seqlen, start_pos)
  *   smla_decode_window_idxs   oracle/decode_engine.py:110-111  widx = range(max(0, p-127), p+1)
  *   smla_indexer_score        (none: the reference attends every visible compressed row,
@@ -152,6 +153,23 @@ int smla_sparse_attn_noalloc(const void* q, int q_dtype,
                              const float* attn_sink, const int32_t* topk_idxs, int64_t T,
                              int64_t B, int64_t S, int64_t H, int64_t D, int64_t DV, float scale,
                              void* out, int out_dtype, void* stream);
+
+/* ---------------------------------------------------------------------------------------------
+ * Prompt (prefill) attention with the row sets computed on the device.  Replaces the per-position
+ * loop of oracle/decode_engine.py:107-117 with decode_pos = None: query s of sequence b sits at
+ * position p = q_pos0 + s and attends
+ *   raw rows max(0, p-window+1) .. p            (ids 0 .. n_raw-1, list entries 0 .. window-1)
+ *   compressed rows 0 .. min((p+1)/ratio, n_comp)-1 (ratio > 0; list entries window ..)
+ * exactly the sparse_attn call of the reference for that position (same result as
+ * smla_sparse_attn over those index lists, bit for bit).  No index tensor and no workspace.
+ *   q [B,S,H,D] BF16, kv_raw [B,n_raw,D] BF16, kv_comp [B,n_comp,D] BF16 or NULL (ratio 0),
+ *   D 576 or 512, DV 512, H % 16 == 0, q_pos0 + S <= n_raw, window + (q_pos0+S)/ratio <= 8192,
+ *   out [B,S,H,DV] BF16 or F32.  Workgroups take the queries longest list first. */
+int smla_prefill_attn(const void* q, int q_dtype, const void* kv_raw, int64_t n_raw,
+                      const void* kv_comp, int64_t n_comp, int kv_dtype, const float* attn_sink,
+                      int64_t q_pos0, int64_t window, int64_t ratio, int64_t B, int64_t S,
+                      int64_t H, int64_t D, int64_t DV, float scale, void* out, int out_dtype,
+                      void* stream);
 
 /* ---------------------------------------------------------------------------------------------
  * Window index matrix.  Replaces ref_torch/sparse_attn.py:9-20 (get_window_topk_idxs).

@@ -75,6 +75,57 @@ def test_prefill_vs_oracle(dev, n_raw, q_pos0, S, H, use_sink, one_split):
     _check(out[0], ref, "prefill")
 
 
+@pytest.mark.parametrize("n_raw,q_pos0,S,H,ratio,use_sink", [
+    (4096, 4096 - 48, 48, 64, 4, False),  # full lists
+    (4096, 0, 40, 64, 4, True),           # first positions: windows shorter than 128
+    (1024, 500, 33, 32, 4, False),        # partial head group, mid-sequence
+    (1024, 0, 1024, 64, 4, True),         # XCD-chunked, longest-first order over 1024 queries
+    (600, 100, 200, 64, 0, False),        # a window-only layer (ratio 0)
+    (2000, 1500, 64, 128, 4, True),       # two head groups
+])
+def test_prefill_attn_implicit_rows(dev, n_raw, q_pos0, S, H, ratio, use_sink):
+    """smla_prefill_attn (row sets computed in the kernel) equals the single-split attention over
+    the explicit prefill index lists bit for bit, and the oracle within the bf16 tolerance."""
+    from smla import compressor as scomp
+    from smla import ops
+    from smla import sparse_attn as ssa
+    from smla import workloads as wl
+    announce(f"prefill_attn n_raw={n_raw} q_pos0={q_pos0} S={S} H={H} ratio={ratio} sink={use_sink}")
+    q, raw = _inputs(n_raw, S, H, seed=q_pos0 + S + 7)
+    raw_d = raw.to(dev)
+    comp_d = scomp.block_mean_pool(raw_d, 4) if ratio else None
+    sink = torch.randn(H, generator=torch.Generator().manual_seed(6)) if use_sink else None
+    sink_d = None if sink is None else sink.to(dev)
+    scale = 576 ** -0.5
+    out = ssa.prefill_attn(q.to(dev), raw_d, comp_d, sink_d, scale, q_pos0=q_pos0, window=128, ratio=ratio)
+    idx_all = wl.prefill_indices(n_raw, ratio=4, window=128, n_raw=n_raw)
+    idx = (idx_all if ratio else idx_all[:, :128])[q_pos0:q_pos0 + S]
+    T = idx.shape[-1]
+    rps = (T + 31) // 32 * 32
+    ref_gpu = ops.sparse_attn_ex(q.to(dev), raw_d, comp_d, None, None, sink_d, idx[None].to(dev), scale, 512,
+                                 rows_per_split=rps)
+    torch.cuda.synchronize()
+    assert torch.equal(out.view(torch.int16), ref_gpu.view(torch.int16)), "implicit rows differ from the index lists"
+    kv = raw[0].float() if not ratio else torch.cat([raw[0].float(), comp_d.cpu()[0].float()])
+    ref = osa.sparse_attn(q[0].float(), kv, sink, idx, scale, dv=512)
+    _check(out[0], ref, "prefill_attn")
+
+
+def test_prefill_attn_rejects(dev):
+    """Positions past the raw rows, and an over-long list, are refused before any launch."""
+    from smla import _lib
+    from smla import sparse_attn as ssa
+    q = torch.zeros(1, 8, 64, 576, dtype=torch.bfloat16, device=dev)
+    raw = torch.zeros(1, 100, 576, dtype=torch.bfloat16, device=dev)
+    comp = torch.zeros(1, 25, 576, dtype=torch.bfloat16, device=dev)
+    with pytest.raises(_lib.SmlaError):
+        ssa.prefill_attn(q, raw, comp, None, 0.04, q_pos0=95)          # positions 95..102 > 99
+    big_raw = torch.zeros(1, 40000, 576, dtype=torch.bfloat16, device=dev)
+    big_comp = torch.zeros(1, 10000, 576, dtype=torch.bfloat16, device=dev)
+    with pytest.raises(_lib.SmlaError):
+        ssa.prefill_attn(q, big_raw, big_comp, None, 0.04, q_pos0=39000)  # 128 + 9752 rows > 8192
+
+
 def test_prefill_4k_full_size(dev):
     """The full prefill workload (S=4096 queries over a 4096-row sequence): every query's output
     is computed on the GPU and checked against the oracle, and the empty-set guarantee holds (no
@@ -89,7 +140,10 @@ def test_prefill_4k_full_size(dev):
     comp_d = scomp.block_mean_pool(raw_d, 4)
     idx = wl.prefill_indices(4096, ratio=4, window=128, n_raw=4096)
     out = ssa.sparse_attn_two_source(q.to(dev), raw_d, comp_d, None, idx[None].to(dev), w["scale"], dv=512)
+    # the prefill entry with its row sets computed in the kernel: the same bits
+    out_implicit = ssa.prefill_attn(q.to(dev), raw_d, comp_d, None, w["scale"], q_pos0=0, window=128, ratio=4)
     torch.cuda.synchronize()
+    assert torch.equal(out.view(torch.int16), out_implicit.view(torch.int16))
     assert not torch.isnan(out).any()
     kv = torch.cat([raw[0].float(), comp_d.cpu()[0].float()])
     outs = out[0].float().cpu()
