@@ -446,6 +446,7 @@ static int attn_call(const void* q, int q_dtype, const void* kv0, int64_t n0, co
 
 // Prompt attention with the row sets of oracle/decode_engine.py:107-117 computed in the kernel:
 // one workgroup per (query, 64-head group), lists as ImplicitRows describes, queries longest first.
+// With no index table in LDS the list length is not bounded by a table.
 extern "C" int smla_prefill_attn(const void* q, int q_dtype, const void* kv_raw, int64_t n_raw, const void* kv_comp,
                                  int64_t n_comp, int kv_dtype, const float* attn_sink, int64_t q_pos0,
                                  int64_t window, int64_t ratio, int64_t B, int64_t S, int64_t H, int64_t D,
@@ -461,7 +462,7 @@ extern "C" int smla_prefill_attn(const void* q, int q_dtype, const void* kv_raw,
   const int64_t nc_max = ratio > 0 ? std::min((q_pos0 + S) / ratio, n_comp) : 0;
   const int64_t T = window + nc_max;
   const int64_t rows = (T + kTileRows - 1) / kTileRows * kTileRows;
-  if (rows > smla_attn::kDecodeV6MaxRows || B * S > 65535 || window > 0x7fffffff) return SMLA_E_UNSUPPORTED;
+  if (rows > (1 << 24) || B * S > 65535 || window > (1 << 24)) return SMLA_E_UNSUPPORTED;
   const smla_attn::RowSrc src{kv_raw, nc_max > 0 ? kv_comp : nullptr, nullptr, nullptr, n_raw,
                               nc_max > 0 ? n_comp : 0};
   const smla_attn::ImplicitRows ir{q_pos0, (int)window, (int)ratio, 1};

@@ -45,7 +45,7 @@ struct Geo6 {
   static constexpr int P_OFF = NBUF * TILE_BYTES;
   static constexpr int AL_OFF = P_OFF + 2 * PBUF;        // rescale factors: 2 x 64 floats
   static constexpr int IDS_OFF = AL_OFF + 2 * 64 * 4;
-  static constexpr int MAX_ROWS = MAXROWS_;             // rows per split (index table in LDS)
+  static constexpr int MAX_ROWS = MAXROWS_;             // rows per split (index table in LDS; 0: none)
   static constexpr int ML_OFF = IDS_OFF + MAX_ROWS * 4;  // (m, l) per head after the loop
   static constexpr int LDS_BYTES = ML_OFF + 64 * 2 * 4;
   static constexpr int NW = 12;
@@ -96,7 +96,7 @@ __device__ inline int64_t query_row_of(int64_t L, int64_t n) {
   return r * kX * kC + pos * kC + j;
 }
 
-template <int D, int NBUF, int MAXROWS, bool FP8>
+template <int D, int NBUF, int MAXROWS, bool FP8, bool IMPL = false>
 __global__ __launch_bounds__(768) void attn_decode_kernel(
     const uint16_t* __restrict__ q, RowSrc src, const float* __restrict__ sink, const int32_t* __restrict__ idx,
     int T, int S, int H, int rows_per_split, float scale, float* __restrict__ part, void* __restrict__ out,
@@ -133,6 +133,17 @@ __global__ __launch_bounds__(768) void attn_decode_kernel(
   const int ntiles_all = (nrows + kTileRows - 1) / kTileRows;
   const int64_t n0 = src.n0, n1 = src.n1, ntot = n0 + n1;
   const int32_t* ig = idx ? idx + bs * (int64_t)T + t_begin : nullptr;
+  // IMPL: no index table; entry e of the list of the query at position p (ImplicitRows) is
+  //   e <= p - lo                       -> raw row lo + e       (window, lo = max(0, p - window + 1))
+  //   window <= e < window + nc         -> compressed row e - window (id n0 + e - window)
+  //   otherwise                         -> masked
+  // with nc = min((p + 1) / ratio, n1), computed where it is needed, without branches
+  const int64_t ip = ir.q_pos0 + bs % S;
+  const int64_t ilo = ip - ir.window + 1 > 0 ? ip - ir.window + 1 : 0;
+  const int64_t incv = ir.ratio > 0 ? (ip + 1) / ir.ratio : 0;
+  const int i_nc = (int)(incv < n1 ? incv : n1);
+  const int i_wlast = (int)(ip - ilo);
+  auto impl_ok = [&](int e) -> bool { return (e <= i_wlast) | ((unsigned)(e - ir.window) < (unsigned)i_nc); };
   const bool scorer = wave < 4;
   const int g = lane >> 4, c = lane & 15;
 
@@ -142,6 +153,14 @@ __global__ __launch_bounds__(768) void attn_decode_kernel(
     const uint8_t* p0 = (const uint8_t*)src.kv0 + (b * n0 + rid) * (int64_t)G::ROWB;
     const uint8_t* p1 = (const uint8_t*)src.kv1 + (b * n1 + (rid - n0)) * (int64_t)G::ROWB;
     return rid < 0 ? row0 : (rid < n0 ? p0 : p1);
+  };
+  // IMPL: the row of list entry e (masked entries read row 0, like -1 ids); entry e of the window
+  // is raw row lo + e, entry e of the compressed part compressed row e - window
+  const uintptr_t i_wbase = (uintptr_t)src.kv0 + (uintptr_t)((b * n0 + ilo) * (int64_t)G::ROWB);
+  const uintptr_t i_cbase = (uintptr_t)src.kv1 + (uintptr_t)((b * n1 - ir.window) * (int64_t)G::ROWB);
+  auto impl_ptr = [&](int e) -> const uint8_t* {
+    const uintptr_t a = (e < ir.window ? i_wbase : i_cbase) + (uintptr_t)((int64_t)e * G::ROWB);
+    return impl_ok(e) ? (const uint8_t*)a : row0;
   };
   // this wave's share of the copies of one 32-row tile into ring slot `slot` (G::NDMA instructions
   // per tile, dealt round-robin over the value waves: one per row for columns 0..511, one per 8 rows
@@ -154,10 +173,12 @@ __global__ __launch_bounds__(768) void attn_decode_kernel(
       const int x = wave - 4 + kDmaWaves * k;
       if (x < kTileRows) {
         const uint32_t ld = __builtin_amdgcn_readfirstlane(tbase + x * G::MSTRIDE);
+        // IMPL: the row is wave-uniform; computed in scalar registers
+        const int xr = IMPL ? __builtin_amdgcn_readfirstlane(x) : x;
         if (nt)
-          dma16_nt(rowp(x) + 16 * lane, ld);
+          dma16_nt(rowp(xr) + 16 * lane, ld);
         else
-          dma16(rowp(x) + 16 * lane, ld);
+          dma16(rowp(xr) + 16 * lane, ld);
       } else if (x < G::NDMA) {
         const int r0 = (x - kTileRows) * 8;
         const int r = r0 + (lane >> 3);
@@ -195,24 +216,9 @@ __global__ __launch_bounds__(768) void attn_decode_kernel(
   // behind a wait).
   int last = -1;
   const int nt = ntiles_all * kTileRows;
-  if (ir.enabled) {
-    // the list of the query at position p, entry by entry (no loads)
-    if (scorer) {
-      const int64_t p = ir.q_pos0 + bs % S;
-      const int64_t lo = p - ir.window + 1 > 0 ? p - ir.window + 1 : 0;
-      const int64_t ncv = ir.ratio > 0 ? (p + 1) / ir.ratio : 0;
-      const int64_t nc = ncv < n1 ? ncv : n1;
-      for (int t = tid; t < nt; t += 4 * 64) {
-        const int e = t_begin + t;
-        int r = -1;
-        if (t < nrows) {
-          if (e < ir.window) r = lo + e <= p ? (int)(lo + e) : -1;
-          else r = e - ir.window < nc ? (int)(n0 + (e - ir.window)) : -1;
-        }
-        ids_s[t] = r;
-        if (r >= 0) last = t;
-      }
-    }
+  if constexpr (IMPL) {
+    // the last live entry: the last visible compressed row, else the window's last (p itself)
+    if (scorer) last = i_nc > 0 ? ir.window + i_nc - 1 : i_wlast;
   } else if (MAXROWS <= 4 * 64 || nt <= 4 * 64) {
     if (scorer) {
       for (int t = tid; t < nt; t += 4 * 64) {
@@ -253,11 +259,16 @@ __global__ __launch_bounds__(768) void attn_decode_kernel(
 
   auto issue_tile = [&](int tl) {
     if constexpr (!FP8) {
-      const lds_i32_t* tid_s = ids_s + tl * kTileRows;
-      issue_rows(tl % G::NBUF, [&](int r) { return row_ptr(tid_s[r]); }, false);
+      if constexpr (IMPL) {
+        issue_rows(tl % G::NBUF, [&](int r) { return impl_ptr(tl * kTileRows + r); }, false);
+      } else {
+        const lds_i32_t* tid_s = ids_s + tl * kTileRows;
+        issue_rows(tl % G::NBUF, [&](int r) { return row_ptr(tid_s[r]); }, false);
+      }
     }
   };
-  const int my_dma = FP8 ? 0 : dma_count<G>(wave);  // a data tile's DMA instructions of this wave
+  // a data tile's DMA instructions of this wave (wave-uniform: the waits on it branch on scalars)
+  const int my_dma = FP8 ? 0 : __builtin_amdgcn_readfirstlane(dma_count<G>(wave));
 
   // ---- fp8 rows (e4m3 codes + one fp32 power-of-two scale per 64 columns): the value waves load
   // a tile's 32 x D codes into registers (16 codes per lane-chunk, chunks dealt over the 512
@@ -434,14 +445,22 @@ __global__ __launch_bounds__(768) void attn_decode_kernel(
           __builtin_amdgcn_sched_barrier(0);  // keep the reads PF steps ahead of their MFMAs
         }
         // online softmax over rows 4g+i and 16+4g+i for head hg*16 + c
-        const lds_i32_t* tid_s = ids_s + it * kTileRows;
-        const i32x4_t v0 = *(const lds_i32x4_t*)(tid_s + 4 * g);
-        const i32x4_t v1 = *(const lds_i32x4_t*)(tid_s + 16 + 4 * g);
         float x[8];
+        if constexpr (IMPL) {
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-          x[i] = v0[i] >= 0 ? s0[i] * scale : -SMLA_INF;
-          x[4 + i] = v1[i] >= 0 ? s1[i] * scale : -SMLA_INF;
+          for (int i = 0; i < 4; i++) {
+            x[i] = impl_ok(it * kTileRows + 4 * g + i) ? s0[i] * scale : -SMLA_INF;
+            x[4 + i] = impl_ok(it * kTileRows + 16 + 4 * g + i) ? s1[i] * scale : -SMLA_INF;
+          }
+        } else {
+          const lds_i32_t* tid_s = ids_s + it * kTileRows;
+          const i32x4_t v0 = *(const lds_i32x4_t*)(tid_s + 4 * g);
+          const i32x4_t v1 = *(const lds_i32x4_t*)(tid_s + 16 + 4 * g);
+#pragma unroll
+          for (int i = 0; i < 4; i++) {
+            x[i] = v0[i] >= 0 ? s0[i] * scale : -SMLA_INF;
+            x[4 + i] = v1[i] >= 0 ? s1[i] * scale : -SMLA_INF;
+          }
         }
         float mt = x[0];
 #pragma unroll
@@ -570,12 +589,12 @@ __global__ __launch_bounds__(768) void attn_decode_kernel(
   copy_out();
 }
 
-template <int D, int NBUF, int MAXROWS, bool FP8>
+template <int D, int NBUF, int MAXROWS, bool FP8, bool IMPL = false>
 int launch6(int nsplit, int rows_per_split, const void* q, RowSrc src, const float* sink, const int32_t* idx,
             int64_t T, int64_t B, int64_t S, int64_t H, float scale, void* out, int out_dtype, float* part,
             hipStream_t stream, ImplicitRows ir) {
   using G = Geo6<D, NBUF, MAXROWS>;
-  auto kern = attn_decode_kernel<D, NBUF, MAXROWS, FP8>;
+  auto kern = attn_decode_kernel<D, NBUF, MAXROWS, FP8, IMPL>;
   static std::atomic<uint64_t> lds_attr{0};  // devices whose limit is raised
   if (hipError_t e = smla_set_dynamic_lds((const void*)kern, G::LDS_BYTES, lds_attr); e != hipSuccess) return (int)e;
   dim3 grid((unsigned)nsplit, (unsigned)(B * S), (unsigned)((H + 63) / 64));
@@ -593,6 +612,18 @@ int launch6(int nsplit, int rows_per_split, const void* q, RowSrc src, const flo
 int launch_decode_v6(int D, bool kv_fp8, int nsplit, int rows_per_split, const void* q, RowSrc src,
                      const float* sink, const int32_t* idx, int64_t T, int64_t B, int64_t S, int64_t H, float scale,
                      void* out, int out_dtype, float* part, hipStream_t stream, ImplicitRows ir) {
+  // prefill with implicit row sets: no index table (any list length), one split per query; the
+  // 3-slot ring (a 4th slot measured slower: 0.46 vs 0.45 ms over the 4096-query prompt)
+  if (ir.enabled) {
+    if (kv_fp8 || nsplit != 1 || rows_per_split % kTileRows != 0 || B * S > 65535) return SMLA_E_UNSUPPORTED;
+    if (D == 576)
+      return launch6<576, 3, 0, false, true>(1, rows_per_split, q, src, sink, idx, T, B, S, H, scale, out, out_dtype,
+                                             part, stream, ir);
+    if (D == 512)
+      return launch6<512, 3, 0, false, true>(1, rows_per_split, q, src, sink, idx, T, B, S, H, scale, out, out_dtype,
+                                             part, stream, ir);
+    return SMLA_E_UNSUPPORTED;
+  }
   if (rows_per_split > kDecodeV6MaxRows || rows_per_split % kTileRows != 0 || B * S > 65535) return SMLA_E_UNSUPPORTED;
   const bool sh = rows_per_split <= kDecodeV6ShortRows;
 #define SMLA_V6(DD, F8)                                                                                           \

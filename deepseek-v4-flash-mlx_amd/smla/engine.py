@@ -37,7 +37,6 @@ from . import norm_rope as _nr
 from . import sparse_attn as _sa
 
 HEAD_DIM, ROPE_HD, N_HEADS, WINDOW = 512, 64, 64, 128
-PREFILL_MAX_ROWS = 8192  # the longest row list smla_prefill_attn takes (window + compressed rows)
 _YARN = (65536, 160000.0, 16, 32, 1)   # original_seq_len, base, factor, beta_fast, beta_slow
 _PLAIN = (0, 10000.0, 40, 32, 1)
 
@@ -182,14 +181,10 @@ class DecodeLayer:
                 self.comp[:, :cut // 4] = comp.to(torch.bfloat16)
             self.ring.init_from_prefill(kvp, scp)
             T += S // 4
-        qv = q.view(B, S, N_HEADS, HEAD_DIM)
-        if T <= PREFILL_MAX_ROWS:  # row sets computed in the kernel (smla_prefill_attn)
-            o = _sa.prefill_attn(qv, self.raw, self.comp if self.ring_ratio else None, self.w.sinks.float(),
-                                 HEAD_DIM ** -0.5, q_pos0=0, window=WINDOW, ratio=self.ring_ratio, dv=HEAD_DIM)
-        else:                      # longer prompts: explicit lists, split over workgroups
-            ids = ops.decode_ids(pos, WINDOW, self.ring_ratio, self.max_pos, self.ncap, T)   # [B*S, T]
-            o = _sa.sparse_attn_two_source(qv, self.raw, self.comp, self.w.sinks.float(), ids.view(B, S, T),
-                                           HEAD_DIM ** -0.5, dv=HEAD_DIM)
+        # every position's window and visible compressed rows, computed in the kernel (smla_prefill_attn)
+        o = _sa.prefill_attn(q.view(B, S, N_HEADS, HEAD_DIM), self.raw, self.comp if self.ring_ratio else None,
+                             self.w.sinks.float(), HEAD_DIM ** -0.5, q_pos0=0, window=WINDOW, ratio=self.ring_ratio,
+                             dv=HEAD_DIM)
         out = mla.o_project(o.view(B * S, N_HEADS, HEAD_DIM), pos, self.cos_t, self.sin_t, self.w.wo_a, self.w.wo_b)
         return out.view(B, S, -1)
 

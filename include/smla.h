@@ -163,7 +163,7 @@ int smla_sparse_attn_noalloc(const void* q, int q_dtype,
  * exactly the sparse_attn call of the reference for that position (same result as
  * smla_sparse_attn over those index lists, bit for bit).  No index tensor and no workspace.
  *   q [B,S,H,D] BF16, kv_raw [B,n_raw,D] BF16, kv_comp [B,n_comp,D] BF16 or NULL (ratio 0),
- *   D 576 or 512, DV 512, H % 16 == 0, q_pos0 + S <= n_raw, window + (q_pos0+S)/ratio <= 8192,
+ *   D 576 or 512, DV 512, H % 16 == 0, q_pos0 + S <= n_raw, B*S <= 65535,
  *   out [B,S,H,DV] BF16 or F32.  Workgroups take the queries longest list first. */
 int smla_prefill_attn(const void* q, int q_dtype, const void* kv_raw, int64_t n_raw,
                       const void* kv_comp, int64_t n_comp, int kv_dtype, const float* attn_sink,

@@ -111,8 +111,34 @@ def test_prefill_attn_implicit_rows(dev, n_raw, q_pos0, S, H, ratio, use_sink):
     _check(out[0], ref, "prefill_attn")
 
 
+def test_prefill_attn_long_lists(dev):
+    """Lists past the 8192 rows an index table holds (positions near 40000: 128 window rows and up
+    to 10000 compressed rows per query) against the oracle; the queries straddle the point where
+    the compressed part stops growing (n_comp rows)."""
+    from smla import compressor as scomp
+    from smla import sparse_attn as ssa
+    from smla import workloads as wl
+    n_raw, q_pos0, S, H = 40000, 39990, 10, 16
+    announce(f"prefill_attn long lists n_raw={n_raw} q_pos0={q_pos0} S={S} H={H}")
+    q, raw = _inputs(n_raw, S, H, seed=11, sharp=4.0)
+    raw_d = raw.to(dev)
+    comp_d = scomp.block_mean_pool(raw_d, 4)[:, :9998]  # the last rows of the last queries cut off
+    sink = torch.randn(H, generator=torch.Generator().manual_seed(8))
+    scale = 576 ** -0.5
+    out = ssa.prefill_attn(q.to(dev), raw_d, comp_d, sink.to(dev), scale, q_pos0=q_pos0, window=128, ratio=4)
+    torch.cuda.synchronize()
+    n_comp = comp_d.shape[1]
+    idx = wl.prefill_indices(S, ratio=4, window=128, n_raw=n_raw, q_pos0=q_pos0)
+    idx = idx[:, :128 + n_comp]
+    idx = torch.where(idx >= n_raw + n_comp, torch.full_like(idx, -1), idx)
+    kv = torch.cat([raw[0].float(), comp_d.cpu()[0].float()])
+    ref = osa.sparse_attn(q[0].float(), kv, sink, idx, scale, dv=512)
+    _check(out[0], ref, "prefill_attn long lists")
+
+
 def test_prefill_attn_rejects(dev):
-    """Positions past the raw rows, and an over-long list, are refused before any launch."""
+    """Positions past the raw rows are refused before any launch; lists longer than the 8192-row
+    index table of the list path are taken (no table)."""
     from smla import _lib
     from smla import sparse_attn as ssa
     q = torch.zeros(1, 8, 64, 576, dtype=torch.bfloat16, device=dev)
@@ -122,8 +148,9 @@ def test_prefill_attn_rejects(dev):
         ssa.prefill_attn(q, raw, comp, None, 0.04, q_pos0=95)          # positions 95..102 > 99
     big_raw = torch.zeros(1, 40000, 576, dtype=torch.bfloat16, device=dev)
     big_comp = torch.zeros(1, 10000, 576, dtype=torch.bfloat16, device=dev)
-    with pytest.raises(_lib.SmlaError):
-        ssa.prefill_attn(q, big_raw, big_comp, None, 0.04, q_pos0=39000)  # 128 + 9752 rows > 8192
+    out = ssa.prefill_attn(q, big_raw, big_comp, None, 0.04, q_pos0=39000)  # lists of 128 + 9752 rows
+    torch.cuda.synchronize()
+    assert not torch.isnan(out).any() and float(out.float().abs().max()) == 0.0  # zero rows attend to zero
 
 
 def test_prefill_4k_full_size(dev):
