@@ -51,7 +51,7 @@ __global__ __launch_bounds__(kThreads) void attn_generic_kernel(
   const int tid = threadIdx.x;
   const int64_t h = blockIdx.x % H;
   const int64_t bs = blockIdx.x / H;
-  const int64_t b = bs / S;
+  const int64_t b = batch_of(bs, S);
   const int64_t ntot = src.n0 + src.n1;
   const int es = dtype_size(kv_dtype);
 
@@ -171,11 +171,11 @@ __global__ __launch_bounds__(WAVES * 64) void attn_merge_kernel(const float* __r
   // multiple of 8), the XCD whose L2 holds that row's partials from the split kernel
   int64_t bs, item;
   xcd_row_item(BS, (int64_t)H * DVS, bs, item);
-  const int head = (int)(item % H);
+  const int head = DVS == 1 ? (int)item : (int)((uint32_t)item % (uint32_t)H);
   const int64_t rh = bs * H + head;
   const int64_t rec0 = bs * nsplit * (int64_t)H + head;  // record of split 0; splits are H records apart
   const float* ml = part + rec0 * 2;
-  const int dv0 = (int)(item / H) * (DV / DVS) + tid * CPL;
+  const int dv0 = (DVS == 1 ? 0 : (int)((uint32_t)item / (uint32_t)H)) * (DV / DVS) + tid * CPL;
   const int64_t jstride = (int64_t)H * DV;  // elements between consecutive splits
   const float* obase = part + BS * H * nsplit * 2;
 

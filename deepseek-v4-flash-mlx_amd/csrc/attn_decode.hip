@@ -107,6 +107,14 @@ __global__ __launch_bounds__(768) void attn_decode_kernel(
   lds_i32_t* ids_s = (lds_i32_t*)(lds + G::IDS_OFF);
   lds_f32_t* al_s = (lds_f32_t*)(lds + G::AL_OFF);
   const uint32_t lds_base = (uint32_t)(uintptr_t)lds;
+  // every launch argument read in one round trip of scalar loads: left to the compiler, the grid
+  // size, the index-list arguments and the row sources come in three dependent round trips
+  {
+    const uint32_t gx = gridDim.x, gy = gridDim.y, gz = gridDim.z;
+    asm volatile("" ::"s"(gx), "s"(gy), "s"(gz), "s"(q), "s"(src.kv0), "s"(src.kv1), "s"(src.n0), "s"(src.n1),
+                 "s"(idx), "s"(T), "s"(S), "s"(H), "s"(rows_per_split), "s"(part), "s"(out), "s"(sink),
+                 "s"(scale), "s"(out_dtype), "s"(ir.q_pos0), "s"(ir.window), "s"(ir.ratio), "s"(ir.enabled));
+  }
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   // grid (nsplit, B*S, head groups).  One split per query row and one head group (prefill): query
@@ -122,10 +130,15 @@ __global__ __launch_bounds__(768) void attn_decode_kernel(
   } else {
     int64_t item;
     xcd_row_item(gridDim.y, (int64_t)nsplit * gridDim.z, bs, item);
-    split = (int)(item % nsplit);
-    hb = (int)(item / nsplit) * 64;
+    if (gridDim.z == 1) {
+      split = (int)item;
+    } else {
+      const uint32_t hg = (uint32_t)item / (uint32_t)nsplit;
+      split = (int)((uint32_t)item - hg * nsplit);
+      hb = (int)hg * 64;
+    }
   }
-  const int64_t b = bs / S;
+  const int64_t b = batch_of(bs, S);
   const int nh = min(64, H - hb);                 // valid heads here
   const int t_begin = split * rows_per_split;
   const int t_end = min(T, t_begin + rows_per_split);
@@ -138,7 +151,7 @@ __global__ __launch_bounds__(768) void attn_decode_kernel(
   //   window <= e < window + nc         -> compressed row e - window (id n0 + e - window)
   //   otherwise                         -> masked
   // with nc = min((p + 1) / ratio, n1), computed where it is needed, without branches
-  const int64_t ip = ir.q_pos0 + bs % S;
+  const int64_t ip = ir.q_pos0 + (bs - b * S);
   const int64_t ilo = ip - ir.window + 1 > 0 ? ip - ir.window + 1 : 0;
   const int64_t incv = ir.ratio > 0 ? (ip + 1) / ir.ratio : 0;
   const int i_nc = (int)(incv < n1 ? incv : n1);

@@ -70,7 +70,7 @@ __global__ __launch_bounds__(256) void indexer_kernel(const void* __restrict__ q
   __shared__ float sr[kKeys][65];  // r[key][head] (padded: lanes read different keys)
   int64_t bs, chunk;
   xcd_row_item(gridDim.y, gridDim.x, bs, chunk);
-  const int64_t b = bs / S;
+  const int64_t b = batch_of(bs, S);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int nwaves = blockDim.x >> 6;
   const int64_t n = chunk * kKeys + lane;
@@ -224,7 +224,7 @@ __global__ __launch_bounds__(64 * (64 / HPW)) void indexer2_kernel(const void* _
   __shared__ float sr[KEYS][65];  // r[key][head]
   int64_t bs, chunk;
   xcd_row_item(gridDim.y, gridDim.x, bs, chunk);
-  const int64_t b = bs / S;
+  const int64_t b = batch_of(bs, S);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int64_t n0 = chunk * KEYS + lane;
   const int64_t nv = nvis ? (int64_t)nvis[bs] : N;
@@ -382,7 +382,7 @@ __global__ __launch_bounds__(256) void indexer_wide_kernel(const void* __restric
                                                            int64_t N, float* __restrict__ scores) {
   int64_t bs, chunk;
   xcd_row_item(gridDim.y, gridDim.x, bs, chunk);
-  const int64_t b = bs / S;
+  const int64_t b = batch_of(bs, S);
   const int64_t n = chunk * blockDim.x + threadIdx.x;
   if (n >= N) return;
   const int64_t nv = nvis ? (int64_t)nvis[bs] : N;
@@ -496,7 +496,7 @@ __global__ __launch_bounds__(256) void indexer_cert_kernel(const uint16_t* __res
   const int g = lane >> 4, c16 = lane & 15;
   int64_t r, chunk64;
   xcd_row_item(gridDim.y, gridDim.x, r, chunk64);
-  const int64_t b = r / S;
+  const int64_t b = batch_of(r, S);
   const int chunk = (int)chunk64, nchunk = gridDim.x;
   int64_t nv = nvis ? (int64_t)nvis[r] : N;
   nv = nv < 0 ? 0 : (nv > N ? N : nv);

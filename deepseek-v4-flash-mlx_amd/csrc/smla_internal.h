@@ -230,17 +230,25 @@ __device__ inline int64_t linear_block_id() {
   return (int64_t)blockIdx.x + (int64_t)gridDim.x * ((int64_t)blockIdx.y + (int64_t)gridDim.y * blockIdx.z);
 }
 // (row, item) of this workgroup in a launch of rows * items workgroups: row-major when rows is not a
-// multiple of 8, else pinned (row mod 8 == XCD)
+// multiple of 8, else pinned (row mod 8 == XCD).  Launches hold fewer than 2^32 workgroups, so the
+// arithmetic is 32-bit: a 64-bit division by a launch-time value is a long dependent scalar
+// sequence at the start of every workgroup.
 __device__ inline void xcd_row_item(int64_t rows, int64_t items, int64_t& row, int64_t& item) {
-  const int64_t L = linear_block_id();
-  if (rows % kXcds != 0) {
-    row = L / items;
-    item = L % items;
+  const uint32_t L = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
+  const uint32_t n = (uint32_t)items;
+  if ((uint32_t)rows % kXcds != 0) {
+    const uint32_t q = L / n;
+    row = q;
+    item = L - q * n;
     return;
   }
-  const int64_t i = L / kXcds;
-  row = L % kXcds + kXcds * (i / items);
-  item = i % items;
+  const uint32_t i = L / kXcds, q = i / n;
+  row = (L % kXcds) + kXcds * q;
+  item = i - q * n;
+}
+// batch entry of query row bs with S query rows per entry (bs < 2^32: a grid dimension)
+__device__ inline int64_t batch_of(int64_t bs, int64_t S) {
+  return S == 1 ? bs : (int64_t)((uint32_t)bs / (uint32_t)S);
 }
 
 // ---------------------------------------------------------------------------------------------
