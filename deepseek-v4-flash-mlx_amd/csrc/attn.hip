@@ -166,6 +166,12 @@ __global__ __launch_bounds__(WAVES * 64) void attn_merge_kernel(const float* __r
   __shared__ __align__(16) float m_s[kMaxSplits];
   __shared__ float l_s[kMaxSplits];
   __shared__ float red[2][WAVES];
+  // every launch argument read in one round trip of scalar loads
+  {
+    const uint32_t gx = gridDim.x, gy = gridDim.y, gz = gridDim.z;
+    asm volatile("" ::"s"(gx), "s"(gy), "s"(gz), "s"(part), "s"(nsplit), "s"(BS), "s"(H), "s"(sink), "s"(out),
+                 "s"(out_dtype));
+  }
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   // grid (B*S*H, DVS): every head and column slice of query row bs on XCD bs mod 8 (when B*S is a
   // multiple of 8), the XCD whose L2 holds that row's partials from the split kernel

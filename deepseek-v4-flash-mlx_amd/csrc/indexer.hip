@@ -222,6 +222,13 @@ __global__ __launch_bounds__(64 * (64 / HPW)) void indexer2_kernel(const void* _
   __shared__ __align__(16) float sq[64 * DI];
   __shared__ float sw[64];
   __shared__ float sr[KEYS][65];  // r[key][head]
+  // every launch argument read in one round trip of scalar loads (the compiler would otherwise
+  // load the grid size, then the row arguments, then the rest, each behind a wait)
+  {
+    const uint32_t gx = gridDim.x, gy = gridDim.y, gz = gridDim.z;
+    asm volatile("" ::"s"(gx), "s"(gy), "s"(gz), "s"(q), "s"(keys), "s"(kbs), "s"(kscale), "s"(weights), "s"(nvis),
+                 "s"(S), "s"(N), "s"(scores));
+  }
   int64_t bs, chunk;
   xcd_row_item(gridDim.y, gridDim.x, bs, chunk);
   const int64_t b = batch_of(bs, S);
