@@ -7,11 +7,13 @@
 //   score = acc * kscale[n]   (or acc when kscale == NULL);  -inf for n >= nvis
 //
 // The order is fixed so that every score is reproducible bit for bit by the CPU oracle; the top-k
-// that follows can then be compared exactly.  A workgroup scores 64 keys (one per lane, key row in
-// VGPRs as fp32); its waves split the heads 16 at a time (q and w staged in LDS as fp32, read as
-// wave-wide broadcasts) and wave 0 runs each key's chain over the heads.  HBM traffic per query
-// row: N * (Di * sizeof(key) + 4) bytes of keys and scales, N * 4 bytes of scores.
-// The fp32 FMA work (N * Hi * Di per query row) is the bound: VALU, fixed order, no MFMA.
+// that follows can then be compared exactly.  Hi = Di = 64 (the decode shape) runs the dot-product
+// chains on the matrix cores (indexer_mfma_kernel: K = 1 fp32 MFMAs, each one rounding, so the
+// chain is the same sequence of fmas); other head counts run them on the vector ALUs
+// (indexer_kernel: 64 keys per workgroup, one per lane, key row in VGPRs as fp32, waves splitting
+// the heads 16 at a time with q and w staged in LDS as fp32 and read as wave-wide broadcasts).
+// HBM traffic per query row: N * (Di * sizeof(key) + 4) bytes of keys and scales, N * 4 bytes of
+// scores.  The fp32 multiply-add work (N * Hi * Di per query row) is the bound.
 #include <type_traits>
 
 #include "smla_internal.h"
@@ -200,30 +202,28 @@ __global__ __launch_bounds__(256) void indexer_kernel(const void* __restrict__ q
   if (n < N) scores[bs * N + n] = live ? (kscale ? acc * kscale[row] : acc) : -SMLA_INF;
 }
 
-// Hi = Di = 64: each lane scores KPL keys (n, n + 64, ... of a 64*KPL-key workgroup) over its
-// wave's HPW heads (64 / HPW waves), walking d in four blocks of 16 in order, so every q read from
-// LDS serves KPL keys' fma chains.  Launched as KPL = 2, HPW = 16 (4 waves, 128 keys): measured
-// against 4 x 8, 2 x 8, 4 x 4 and q through scalar loads, it is the fastest; the 2048 fmas per lane
-// at two waves per SIMD are the bound.  Same arithmetic order as indexer_kernel: per (head, key)
-// one fma chain over d = 0..63, then the chain over the heads.
-template <int KDT, int QDT, int KPL, int HPW>
-__global__ __launch_bounds__(64 * (64 / HPW)) void indexer2_kernel(const void* __restrict__ q,
-                                                                  const void* __restrict__ keys,
-                                                                  const uint8_t* __restrict__ kbs,
-                                                                  const float* __restrict__ kscale,
-                                                                  const float* __restrict__ weights,
-                                                                  const int32_t* __restrict__ nvis, int64_t S,
-                                                                  int64_t N, float* __restrict__ scores) {
+// Hi = Di = 64 on the matrix cores.  v_mfma_f32_32x32x1_2b_f32 (K = 1) adds one product to each
+// accumulator with a single rounding, so a chain of 64 of them over d = 0..63 is, element for
+// element, the fma chain dot_h = fma(q[h,d], k[n,d], dot_h) of the definition above (bit for bit:
+// checked against fmaf over 6.7e7 operand triples, subnormal, cancelling and overflowing ones
+// included), at twice the rate of fp32 fma on the vector ALUs.  A wave computes a tile of 64 heads x
+// 32 keys: A = q[h][d] with h = lane (block 0 takes heads 0..31 from lanes 0..31, block 1 heads
+// 32..63 from lanes 32..63), B = k[n][d] with n = lane mod 32 (both blocks take the same 32 keys).
+// Accumulator register r of lane l then holds head 32 (r / 16) + 8 ((r mod 16) / 4) + 4 (l / 32) +
+// r mod 4 of key l mod 32.  The chain over the heads walks h = 0..63 in order: heads 8t..8t+3 sit
+// in lanes 0..31 and heads 8t+4..8t+7 in lanes 32..63, both in registers 16 (t / 4) + 4 (t mod 4) +
+// 0..3, so the running sum crosses between the two halves with a lane swap every four heads (the
+// weights are wave-uniform scalars).  One tile per wave and two waves per SIMD (4-wave workgroups
+// of 128 keys) measured faster than two interleaved tiles per wave at one wave per SIMD.
+template <int KDT, int QDT>
+__global__ __launch_bounds__(256) void indexer_mfma_kernel(const void* __restrict__ q, const void* __restrict__ keys,
+                                                       const uint8_t* __restrict__ kbs,
+                                                       const float* __restrict__ kscale,
+                                                       const float* __restrict__ weights,
+                                                       const int32_t* __restrict__ nvis, int64_t S, int64_t N,
+                                                       float* __restrict__ scores) {
   constexpr int DI = 64;
-  constexpr int NWV = 64 / HPW;    // waves
-  constexpr int KEYS = 64 * KPL;   // keys per workgroup
-  constexpr int NT = 64 * NWV;
-  static_assert(KPL <= NWV, "the head chain takes one key per lane on the first KPL waves");
-  __shared__ __align__(16) float sq[64 * DI];
-  __shared__ float sw[64];
-  __shared__ float sr[KEYS][65];  // r[key][head]
-  // every launch argument read in one round trip of scalar loads (the compiler would otherwise
-  // load the grid size, then the row arguments, then the rest, each behind a wait)
+  constexpr int KEYS = 4 * 32;  // keys per workgroup: 4 waves x one tile of 32 keys
   {
     const uint32_t gx = gridDim.x, gy = gridDim.y, gz = gridDim.z;
     asm volatile("" ::"s"(gx), "s"(gy), "s"(gz), "s"(q), "s"(keys), "s"(kbs), "s"(kscale), "s"(weights), "s"(nvis),
@@ -232,31 +232,48 @@ __global__ __launch_bounds__(64 * (64 / HPW)) void indexer2_kernel(const void* _
   int64_t bs, chunk;
   xcd_row_item(gridDim.y, gridDim.x, bs, chunk);
   const int64_t b = batch_of(bs, S);
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int64_t n0 = chunk * KEYS + lane;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t kb = chunk * KEYS + wave * 32;  // first key of this wave's tile
   const int64_t nv = nvis ? (int64_t)nvis[bs] : N;
 
-  // the lane's key rows in registers, in their storage type (converted one 16-wide block at a time)
-  // 16-byte words per row
+  // the row of key kb + lane mod 32 in its storage type, then the q row of head `lane`
   constexpr int KW = KDT == kFp4 ? 2 : KDT == SMLA_FP8_E4M3 ? 4 : (KDT == SMLA_BF16 ? 8 : 16);
-  u32x4_t kr[KPL][KW];
-  uint32_t ksb[KPL];  // fp4: the row's two scale bytes
-#pragma unroll
-  for (int i = 0; i < KPL; i++) {
-    const int64_t n = n0 + 64 * i;
+  u32x4_t kr[KW];
+  uint32_t ksb = 0;  // fp4: the row's two scale bytes
+  {
+    const int64_t n = kb + (lane & 31);
     const int64_t row = b * N + (n < N ? n : N - 1);
     const u32x4_t* pk = (const u32x4_t*)((const uint8_t*)keys + row * DI * KW / 4);
 #pragma unroll
-    for (int v = 0; v < KW; v++) kr[i][v] = pk[v];
-    if constexpr (KDT == kFp4) ksb[i] = ((const uint16_t*)kbs)[row];
+    for (int v = 0; v < KW; v++) kr[v] = pk[v];
+    if constexpr (KDT == kFp4) ksb = ((const uint16_t*)kbs)[row];
   }
-  // 16 values of key i's row starting at d0 = 16 db, as fp32 (fold: see fp4_block16)
-  auto block16 = [&](int i, int db, float (&o)[16], auto fold) {
-    const u32x4_t(&row)[KW] = kr[i];
+  constexpr int QW = QDT == SMLA_BF16 ? 8 : 16;  // 16-byte words per head row
+  u32x4_t qw[QW];
+  {
+    const u32x4_t* qp = (const u32x4_t*)((const uint8_t*)q + (bs * 64 + lane) * (int64_t)(QW * 16));
+#pragma unroll
+    for (int v = 0; v < QW; v++) qw[v] = qp[v];
+  }
+  const float* wrow = weights + bs * 64;  // uniform: scalar loads
+  float qf[DI];
+#pragma unroll
+  for (int v = 0; v < QW; v++)
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      if constexpr (QDT == SMLA_BF16) {
+        qf[8 * v + 2 * j] = __uint_as_float(qw[v][j] << 16);
+        qf[8 * v + 2 * j + 1] = __uint_as_float(qw[v][j] & 0xffff0000u);
+      } else {
+        qf[4 * v + j] = __uint_as_float(qw[v][j]);
+      }
+    }
+  // 16 values of the key row starting at d0 = 16 db, as fp32 (fold: see fp4_block16)
+  auto block16 = [&](int db, float (&o)[16], auto fold) {
+    const u32x4_t(&row)[KW] = kr;
     if constexpr (KDT == kFp4) {
       const u32x4_t w = row[db >> 1];
-      fp4_block16<decltype(fold)::value>(w[2 * (db & 1)], w[2 * (db & 1) + 1], (ksb[i] >> (8 * (db >> 1))) & 0xffu,
-                                         o);
+      fp4_block16<decltype(fold)::value>(w[2 * (db & 1)], w[2 * (db & 1) + 1], (ksb >> (8 * (db >> 1))) & 0xffu, o);
     } else if constexpr (KDT == SMLA_FP8_E4M3) {
       const u32x4_t w = row[db];
 #pragma unroll
@@ -284,98 +301,45 @@ __global__ __launch_bounds__(64 * (64 / HPW)) void indexer2_kernel(const void* _
         for (int j = 0; j < 4; j++) o[4 * v + j] = __uint_as_float(row[4 * db + v][j]);
     }
   };
-  // q rows -> LDS as fp32, weights: every load issued before the first LDS write (one round trip
-  // for keys, q and weights together; vmcnt counts in order)
-  {
-    constexpr int QW = QDT == SMLA_BF16 ? 8 : 4;  // q values per 16-byte word
-    constexpr int QIT = 64 * DI / QW / NT;         // words per thread
-    static_assert(QIT * NT * QW == 64 * DI, "q words split evenly over the workgroup");
-    const u32x4_t* qp = (const u32x4_t*)((const uint8_t*)q + bs * 64 * DI * (16 / QW));
-    u32x4_t qv[QIT];
+  f32x32_t acc;
 #pragma unroll
-    for (int k = 0; k < QIT; k++) qv[k] = qp[tid + k * NT];
-    const float wt = tid < 64 ? weights[bs * 64 + tid] : 0.f;
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int k = 0; k < QIT; k++) {
-      const int i = tid + k * NT;
-      const u32x4_t v = qv[k];
-      if constexpr (QDT == SMLA_BF16) {
-        f32x4_t lo, hi;
-#pragma unroll
-        for (int j = 0; j < 2; j++) {
-          lo[2 * j] = __uint_as_float(v[j] << 16);
-          lo[2 * j + 1] = __uint_as_float(v[j] & 0xffff0000u);
-          hi[2 * j] = __uint_as_float(v[j + 2] << 16);
-          hi[2 * j + 1] = __uint_as_float(v[j + 2] & 0xffff0000u);
-        }
-        *(f32x4_t*)(sq + 8 * i) = lo;
-        *(f32x4_t*)(sq + 8 * i + 4) = hi;
-      } else {
-        *(u32x4_t*)(sq + 4 * i) = v;
-      }
-    }
-    if (tid < 64) sw[tid] = wt;
-  }
-  __syncthreads();
-  float dot[KPL][HPW];
-#pragma unroll
-  for (int i = 0; i < KPL; i++)
-#pragma unroll
-    for (int hh = 0; hh < HPW; hh++) dot[i][hh] = 0.f;
-  const int h0 = wave * HPW;
+  for (int r = 0; r < 32; r++) acc[r] = 0.f;
   auto run = [&](auto fold) {
 #pragma unroll
-  for (int db = 0; db < 4; db++) {
-    float x[KPL][16];
+    for (int db = 0; db < 4; db++) {
+      float x[16];
+      block16(db, x, fold);
 #pragma unroll
-    for (int i = 0; i < KPL; i++) block16(i, db, x[i], fold);
-    // the next head's 16 q values are read before this head's fmas (one head of lookahead)
-    f32x4_t qn[4];
-#pragma unroll
-    for (int v = 0; v < 4; v++) qn[v] = ((const f32x4_t*)(sq + h0 * DI + 16 * db))[v];
-#pragma unroll
-    for (int hh = 0; hh < HPW; hh++) {
-      f32x4_t qc[4];
-#pragma unroll
-      for (int v = 0; v < 4; v++) qc[v] = qn[v];
-      if (hh + 1 < HPW) {
-#pragma unroll
-        for (int v = 0; v < 4; v++) qn[v] = ((const f32x4_t*)(sq + (h0 + hh + 1) * DI + 16 * db))[v];
-      }
-#pragma unroll
-      for (int v = 0; v < 4; v++)
-#pragma unroll
-        for (int j = 0; j < 4; j++)
-#pragma unroll
-          for (int i = 0; i < KPL; i++) dot[i][hh] = __builtin_fmaf(qc[v][j], x[i][4 * v + j], dot[i][hh]);
+      for (int dd = 0; dd < 16; dd++) acc = __builtin_amdgcn_mfma_f32_32x32x1f32(qf[16 * db + dd], x[dd], acc, 0, 0, 0);
     }
-  }
   };
   if constexpr (KDT == kFp4) {
-    // fp4 keys: the folded conversion when every scale byte of the wave's keys allows it (a
-    // wave-uniform branch, so each variant keeps its own registers)
-    bool fold = true;
-#pragma unroll
-    for (int i = 0; i < KPL; i++) fold = fold && fp4_scale_in_range(ksb[i] & 0xffu) && fp4_scale_in_range(ksb[i] >> 8);
+    // the folded conversion when every scale byte of the wave's keys allows it (wave-uniform)
+    const bool fold = fp4_scale_in_range(ksb & 0xffu) && fp4_scale_in_range(ksb >> 8);
     if (__all(fold)) run(std::true_type{});
     else run(std::false_type{});
   } else {
     run(std::true_type{});
   }
+  // chain over the heads, then the key's scale; lanes l and l + 32 end with the same sum.  After
+  // four heads in lanes 0..31 the swap hands every lane the low half's sum ([0]); after four in
+  // lanes 32..63, the high half's ([1]).
+  float sum = 0.f;
 #pragma unroll
-  for (int i = 0; i < KPL; i++)
+  for (int tt = 0; tt < 8; tt++) {
+    const int R = 16 * (tt >> 2) + 4 * (tt & 3);
+    float r[4];
 #pragma unroll
-    for (int hh = 0; hh < HPW; hh++) sr[64 * i + lane][h0 + hh] = dot[i][hh] > 0.f ? dot[i][hh] : 0.f;
-  __syncthreads();
-  if (wave >= KPL) return;
-  // chain over the heads: wave i for keys 64 i .. 64 i + 63
-  const int kl = wave * 64 + lane;
-  const int64_t n = chunk * KEYS + kl;
-  float acc = 0.f;
-#pragma unroll 8
-  for (int h = 0; h < 64; h++) acc = __builtin_fmaf(sw[h], sr[kl][h], acc);
-  if (n < N) scores[bs * N + n] = n < nv ? (kscale ? acc * kscale[b * N + n] : acc) : -SMLA_INF;
+    for (int rr = 0; rr < 4; rr++) r[rr] = acc[R + rr] > 0.f ? acc[R + rr] : 0.f;
+#pragma unroll
+    for (int rr = 0; rr < 4; rr++) sum = __builtin_fmaf(wrow[8 * tt + rr], r[rr], sum);
+    sum = __uint_as_float(__builtin_amdgcn_permlane32_swap(__float_as_uint(sum), __float_as_uint(sum), false, false)[0]);
+#pragma unroll
+    for (int rr = 0; rr < 4; rr++) sum = __builtin_fmaf(wrow[8 * tt + 4 + rr], r[rr], sum);
+    sum = __uint_as_float(__builtin_amdgcn_permlane32_swap(__float_as_uint(sum), __float_as_uint(sum), false, false)[1]);
+  }
+  const int64_t n = kb + lane;
+  if (lane < 32 && n < N) scores[bs * N + n] = n < nv ? (kscale ? sum * kscale[b * N + n] : sum) : -SMLA_INF;
 }
 
 // Hi > 64: one thread per key, sequential over all heads (same arithmetic order)
@@ -419,20 +383,13 @@ template <int DI, int KDT>
 int launch_k(const void* q, int q_dtype, const void* keys, const uint8_t* kbs, const float* kscale, const float* w,
              const int32_t* nvis, int64_t B, int64_t S, int64_t Hi, int64_t N, float* scores, hipStream_t st) {
   if (Hi == 64 && DI == 64) {
+    // 128 keys per workgroup (a 64-head x 32-key tile per wave)
     const dim3 grid((unsigned)((N + 127) / 128), (unsigned)(B * S));
-    // two keys per lane halve the q reads per fma; when that leaves CUs idle (one long sequence),
-    // one key per lane doubles the workgroups, and 8 heads per wave (8 waves) keeps two waves per
-    // SIMD to hide the q reads (16384 keys: 8.1 -> 7.1 us; with 8 sequences 16 heads per wave wins)
-    const bool one = (int64_t)grid.x * grid.y < smla_num_cus();
-    const dim3 grid1((unsigned)((N + 63) / 64), (unsigned)(B * S));
-    if (q_dtype == SMLA_BF16 && one)
-      hipLaunchKernelGGL((indexer2_kernel<KDT, SMLA_BF16, 1, 8>), grid1, dim3(512), 0, st, q, keys, kbs, kscale, w, nvis, S,
-                         N, scores);
-    else if (q_dtype == SMLA_BF16)
-      hipLaunchKernelGGL((indexer2_kernel<KDT, SMLA_BF16, 2, 16>), grid, dim3(256), 0, st, q, keys, kbs, kscale, w, nvis, S,
+    if (q_dtype == SMLA_BF16)
+      hipLaunchKernelGGL((indexer_mfma_kernel<KDT, SMLA_BF16>), grid, dim3(256), 0, st, q, keys, kbs, kscale, w, nvis, S,
                          N, scores);
     else
-      hipLaunchKernelGGL((indexer2_kernel<KDT, SMLA_F32, 2, 16>), grid, dim3(256), 0, st, q, keys, kbs, kscale, w, nvis, S,
+      hipLaunchKernelGGL((indexer_mfma_kernel<KDT, SMLA_F32>), grid, dim3(256), 0, st, q, keys, kbs, kscale, w, nvis, S,
                          N, scores);
   } else if (Hi <= 64) {
     dim3 grid((unsigned)((N + kKeys - 1) / kKeys), (unsigned)(B * S));

@@ -177,7 +177,7 @@ __global__ __launch_bounds__(NT) void topk_kernel(const float* scores, int64_t N
     qraw = *(const QRawT*)(cc.q + r * 4096 + kQPT * tid);
     if (tid < 64) wraw = cc.w[r * 64 + tid];
   }
-  // Fixed-order scores (the arithmetic of indexer2_kernel, before the kscale product) of the cnt
+  // Fixed-order scores (the indexer's arithmetic, before the kscale product) of the cnt
   // <= kRescoreChunk keys whose fp32 rows are in kf_s, into sc_s.  Wave w takes keys w + kWaves i
   // (i < kKPW) and lane h runs head h's fma chain over d = 0..63 for all of them at once: per block
   // of 16 dims the q values are read from LDS once and each key's 16 values by LDS broadcast, so
