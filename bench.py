@@ -246,8 +246,8 @@ def other_workloads(dev, reps):
     ws = torch.empty(ops.index_decode_workspace(B, 1, N), dtype=torch.uint8, device=dev)
     ms = _time_graph_ms(lambda: sidx.index_decode(qi, keys, ks, wt, None, w["k"], pos, w["window"], raw.shape[1],
                                             workspace=ws), reps)
-    res["index_decode"] = {"shape": "B=8 Hi=64 Di=64 N=8192 -> window 128 + top-2048 ids: MFMA scores with a "
-                                    "certified bound, band rescoring, exact selection (two launches)",
+    res["index_decode"] = {"shape": "B=8 Hi=64 Di=64 N=8192 -> window 128 + top-2048 ids: fixed-order scores "
+                                    "on the matrix cores, exact selection (two launches in one call)",
                            "us": round(ms * 1e3, 3)}
     ms = _time_graph_ms(lambda: scomp.block_mean_pool(raw, 4), max(2, reps // 2))
     mb = raw.numel() * 2 + raw.numel() // 4 * 2

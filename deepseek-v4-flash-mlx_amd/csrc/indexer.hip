@@ -421,174 +421,6 @@ int launch_di(const void* q, int q_dtype, const void* keys, int k_dtype, const u
   return launch_k<DI, SMLA_F32>(q, q_dtype, keys, kbs, kscale, w, nvis, B, S, Hi, N, scores, st);
 }
 
-// ---------------------------------------------------------------------------------------------
-// Certified MFMA scoring (Hi = Di = 64, bf16 q, e4m3 keys).  The approximate score of key n,
-//   a_n = kscale[n] * sum_h w_h ReLU(Q_h . K_n),
-// takes its dot products from v_mfma_f32_16x16x32_bf16 (e4m3 -> bf16 is exact and bf16 x e4m3
-// products are exact in fp32), together with a bound e_n >= |a_n - s_n| on its distance from the
-// fixed-order score s_n of indexer_kernel:
-//   e_n = (|kscale[n]| (2^-15 W1 + 2^-14 PW + 2^-100 (|w|_1 + 1)) + 2^-22 |a_n| + 2^-126) (1 + 2^-10)
-//   W1 = sum_h |w_h| ReLU(dot_h),  PW = sum_h |w_h| P_h,  P_h = sum_d |q_hd k_nd| (a second MFMA
-//   on |q| and |k|).
-// Why it holds (u = 2^-24): a 64-step fma chain is within 64u of the exact sum relative to the sum
-// of absolute terms; the MFMA dot products are allowed 256u (a 32-product step that rounded, even by
-// truncation, after every addition stays below 2 x 33u); ReLU does not increase distances; the two
-// head chains add 2 x 66u relative to W1 and the final products 2u |a|; flushed or subnormal
-// products add at most 2^-120 per dot product.  So |a - s| <= |ks| (132u W1 + 1.01 (64u + 256u) PW)
-// + 2u |a| + tiny, and each term above carries a factor of 3 or more on top.  A key whose a_n or
-// e_n is not finite (NaN or infinite inputs, overflow) gets e_n = +inf.
-//
-// One workgroup = 256 keys of one query row (4 waves x 4 groups of 16; keys as the MFMA's N, heads
-// as M).  It writes a_n (-inf past nvis) and the max of e_n over its visible keys to
-// ebound[row * nchunk + chunk].
-constexpr int kCertKeys = 256;
-
-// bf16 bits of two fp32 values that are exactly representable in bf16, packed (lo, hi)
-__device__ inline uint32_t pack_hi16(float lo, float hi) {
-  return __builtin_amdgcn_perm(__float_as_uint(hi), __float_as_uint(lo), 0x07060302u);
-}
-
-template <bool KS>
-__global__ __launch_bounds__(256) void indexer_cert_kernel(const uint16_t* __restrict__ q,
-                                                           const uint8_t* __restrict__ keys,
-                                                           const float* __restrict__ kscale,
-                                                           const float* __restrict__ weights,
-                                                           const int32_t* __restrict__ nvis, int64_t S, int64_t N,
-                                                           float* __restrict__ approx, float* __restrict__ ebound) {
-  __shared__ float red[4];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int g = lane >> 4, c16 = lane & 15;
-  int64_t r, chunk64;
-  xcd_row_item(gridDim.y, gridDim.x, r, chunk64);
-  const int64_t b = batch_of(r, S);
-  const int chunk = (int)chunk64, nchunk = gridDim.x;
-  int64_t nv = nvis ? (int64_t)nvis[r] : N;
-  nv = nv < 0 ? 0 : (nv > N ? N : nv);
-  const int64_t k0 = (int64_t)chunk * kCertKeys;
-  float* arow = approx + r * N;
-  if (k0 >= nv) {  // the whole chunk is past nvis (uniform over the workgroup)
-    for (int64_t n = k0 + tid; n < N && n < k0 + kCertKeys; n += 256) arow[n] = -SMLA_INF;
-    if (tid == 0) ebound[r * nchunk + chunk] = 0.f;
-    return;
-  }
-  // A operands: q row of head 16hb + c16, dims 16g .. 16g+7 (k-step 0) and 16g+8 .. 16g+15
-  // (k-step 1); the key operands use the same dim order, which the dot product does not see.
-  const uint16_t* qr = q + r * 4096;
-  u32x4_t qa[4][2], qb[4][2];
-#pragma unroll
-  for (int hb = 0; hb < 4; hb++) {
-    const u32x4_t* p = (const u32x4_t*)(qr + (16 * hb + c16) * 64 + 16 * g);
-    qa[hb][0] = p[0];
-    qa[hb][1] = p[1];
-  }
-  // weights of the accumulator rows (heads 16hb + 4g + i) and |w|_1
-  f32x4_t wv[4];
-  float wn1 = 0.f;
-#pragma unroll
-  for (int hb = 0; hb < 4; hb++) {
-    wv[hb] = *(const f32x4_t*)(weights + r * 64 + 16 * hb + 4 * g);
-    wn1 += fabsf(wv[hb][0]) + fabsf(wv[hb][1]) + fabsf(wv[hb][2]) + fabsf(wv[hb][3]);
-  }
-  wn1 += __shfl_xor(wn1, 16);
-  wn1 += __shfl_xor(wn1, 32);
-#pragma unroll
-  for (int hb = 0; hb < 4; hb++)
-#pragma unroll
-    for (int s = 0; s < 2; s++)
-#pragma unroll
-      for (int c = 0; c < 4; c++) qb[hb][s][c] = qa[hb][s][c] & 0x7fff7fffu;
-  const f32x4_t zero = {0.f, 0.f, 0.f, 0.f};
-  float emax = 0.f;
-  const int64_t nb0 = k0 + wave * 64;
-  // the wave's 4 x 16 key rows (16 bytes per lane each) and scales, all in flight at once
-  u32x4_t kwg[4];
-  float ksg[4];
-#pragma unroll
-  for (int grp = 0; grp < 4; grp++) {
-    const int64_t n = nb0 + grp * 16 + c16;
-    const int64_t nrow = n < N ? n : N - 1;
-    kwg[grp] = *(const u32x4_t*)(keys + (b * N + nrow) * 64 + 16 * g);
-    ksg[grp] = KS ? kscale[b * N + nrow] : 1.f;
-  }
-#pragma unroll
-  for (int grp = 0; grp < 4; grp++) {
-    const int64_t n = nb0 + grp * 16 + c16;
-    const bool inN = n < N, live = n < nv;
-    const u32x4_t kw = kwg[grp];
-    u32x4_t kb0, kb1;
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-      const f32x2_t lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)kw[j], false);
-      const f32x2_t hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)kw[j], true);
-      const uint32_t p0 = pack_hi16(lo.x, lo.y), p1 = pack_hi16(hi.x, hi.y);
-      if (j < 2) {
-        kb0[2 * j] = p0;
-        kb0[2 * j + 1] = p1;
-      } else {
-        kb1[2 * j - 4] = p0;
-        kb1[2 * j - 3] = p1;
-      }
-    }
-    const u32x4_t ka0 = kb0 & 0x7fff7fffu, ka1 = kb1 & 0x7fff7fffu;
-    f32x4_t d[4], pa[4];
-#pragma unroll
-    for (int hb = 0; hb < 4; hb++) {
-      d[hb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(qa[hb][0]), as_bf16x8(kb0), zero, 0, 0, 0);
-      d[hb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(qa[hb][1]), as_bf16x8(kb1), d[hb], 0, 0, 0);
-      pa[hb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(qb[hb][0]), as_bf16x8(ka0), zero, 0, 0, 0);
-      pa[hb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(qb[hb][1]), as_bf16x8(ka1), pa[hb], 0, 0, 0);
-    }
-    // lane: heads 16hb + 4g + i of key c16
-    float acc = 0.f, w1 = 0.f, pw = 0.f;
-#pragma unroll
-    for (int hb = 0; hb < 4; hb++)
-#pragma unroll
-      for (int i = 0; i < 4; i++) {
-        const float x = d[hb][i];
-        const float rr = x > 0.f ? x : 0.f;
-        const float aw = fabsf(wv[hb][i]);
-        acc = __builtin_fmaf(wv[hb][i], rr, acc);
-        w1 = __builtin_fmaf(aw, rr, w1);
-        pw = __builtin_fmaf(aw, pa[hb][i], pw);
-      }
-    acc += __shfl_xor(acc, 16);
-    acc += __shfl_xor(acc, 32);
-    w1 += __shfl_xor(w1, 16);
-    w1 += __shfl_xor(w1, 32);
-    pw += __shfl_xor(pw, 16);
-    pw += __shfl_xor(pw, 32);
-    const float ks = ksg[grp];
-    const float a = KS ? acc * ks : acc;
-    float e = (fabsf(ks) * (0x1p-15f * w1 + 0x1p-14f * pw + 0x1p-100f * (wn1 + 1.f)) + 0x1p-22f * fabsf(a) +
-               0x1p-126f) * (1.f + 0x1p-10f);
-    if (!(__builtin_isfinite(a) && __builtin_isfinite(e))) e = SMLA_INF;
-    if (live) emax = fmaxf(emax, e);
-    if (g == 0 && inN) arow[n] = live ? a : -SMLA_INF;
-  }
-  emax = wave_max_dpp(emax);
-  if (lane == 0) red[wave] = emax;
-  __syncthreads();
-  if (tid == 0) ebound[r * nchunk + chunk] = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-}
-
-}  // namespace
-
-int launch_indexer_cert(const uint16_t* q, const uint8_t* keys, const float* kscale, const float* weights,
-                        const int32_t* nvis, int64_t B, int64_t S, int64_t N, float* approx, float* ebound,
-                        hipStream_t st) {
-  const dim3 grid((unsigned)((N + kCertKeys - 1) / kCertKeys), (unsigned)(B * S));
-  if (kscale)
-    hipLaunchKernelGGL(indexer_cert_kernel<true>, grid, dim3(256), 0, st, q, keys, kscale, weights, nvis, S, N,
-                       approx, ebound);
-  else
-    hipLaunchKernelGGL(indexer_cert_kernel<false>, grid, dim3(256), 0, st, q, keys, kscale, weights, nvis, S, N,
-                       approx, ebound);
-  SMLA_HIP_CHECK_LAUNCH();
-  return SMLA_OK;
-}
-
-
-namespace {
 int indexer_score_any(const void* q, int q_dtype, const void* keys, int k_dtype, const uint8_t* kbs,
                       const float* kscale, const float* weights, const int32_t* nvis, int64_t B, int64_t S,
                       int64_t Hi, int64_t Di, int64_t N, float* scores, void* stream) {

@@ -269,12 +269,6 @@ __device__ inline void store_from_f32(void* p, int64_t i, int dtype, float v) {
   else if (dtype == SMLA_F16) ((_Float16*)p)[i] = (_Float16)v;
 }
 
-// certified MFMA indexer scores (indexer.hip): approx [B*S, N] and per-chunk bounds
-// ebound [B*S, ceil(N / 256)]; q [B, S, 64, 64] bf16, keys [B, N, 64] e4m3
-int launch_indexer_cert(const uint16_t* q, const uint8_t* keys, const float* kscale, const float* weights,
-                        const int32_t* nvis, int64_t B, int64_t S, int64_t N, float* approx, float* ebound,
-                        hipStream_t st);
-
 // tiled MFMA GEMM (gemm.hip): y [T, G*N] = grouped x [T, G*K] (row stride ldx) times w [G*N, K]^T,
 // operands both bf16 or both fp32 (f32_operands), y bf16 or fp32; with pos, inverse RoPE of the
 // last 64 dims of every head_dim-wide head of x (bf16) as it is loaded

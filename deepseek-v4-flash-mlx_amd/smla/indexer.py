@@ -43,13 +43,11 @@ def select_decode_indices(scores, k, pos, window, n_raw, out=None, nvis=None):
 
 
 def index_decode(q_idx, keys, kscale, weights, nvis, k, pos, window, n_raw, out=None, workspace=None, flags=0):
-    """Indexer scores and the decode index list in one call: the same list as ``indexer_score``
-    followed by ``select_decode_indices`` (bit-exact), with the scores of bf16 q x e4m3 keys
-    (64 heads x 64 dims) taken on MFMA under a certified error bound and only the keys near the
-    top-k boundary rescored in the fixed order.
+    """Indexer scores and the decode index list in one call: ``indexer_score`` into the workspace
+    followed by ``select_decode_indices`` (the same list, bit for bit).
     q_idx [B,1,Hi,Di], keys [B,N,Di], kscale [B,N] or None, weights [B,1,Hi], nvis [B,1] or None,
-    pos [B] int32 -> out [B, window + k] int32.  flags: 0, or ``_lib.INDEX_EXACT`` to rescore every
-    visible key in the fixed order (the path an uncertifiable row takes; the same output)."""
+    pos [B] int32 -> out [B, window + k] int32.  flags: 0 or ``_lib.INDEX_EXACT`` (the same
+    output: the scores are always the fixed-order ones)."""
     B, S = q_idx.shape[:2]
     N = keys.shape[1]
     if out is None:

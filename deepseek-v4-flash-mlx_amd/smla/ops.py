@@ -560,8 +560,8 @@ def index_decode_into(q, keys, kscale, weights, nvis, k, pos, window, out, works
     """Indexer scores and the decode index build in one call (smla_index_decode): q [B,S,Hi,Di],
     keys [B,N,Di], kscale [B,N]|None, weights [B,S,Hi], nvis [B,S]|None, pos [B*S] int32 (None
     when window == 0), out int32 [B*S, >= window + k] (row stride out.stride(0)), workspace a
-    uint8 tensor of at least index_decode_workspace(B, S, N) bytes; flags: 0, or _lib.INDEX_EXACT to
-    rescore every visible key in the fixed order instead of certifying."""
+    uint8 tensor of at least index_decode_workspace(B, S, N) bytes (the scores); flags: 0 or
+    _lib.INDEX_EXACT (no effect: the scores are always the fixed-order ones)."""
     _on_gpu(q, keys, kscale, weights, nvis, pos, out, workspace)
     if out.dtype != torch.int32 or out.stride(-1) != 1:
         raise ValueError("out must be an int32 view with unit inner stride")

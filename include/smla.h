@@ -229,17 +229,13 @@ int smla_select_decode(const float* scores, int64_t R, int64_t N, const int32_t*
                        const int32_t* pos, int64_t window, int32_t* out, int64_t out_stride,
                        int32_t id_offset, void* stream);
 
-/* Indexer score and decode index build fused: the same output as smla_indexer_score into scores
+/* Indexer score and decode index build in one call: smla_indexer_score into the workspace
  * followed by smla_select_decode (or smla_topk when window == 0; pos may then be NULL), for
- * R = B*S query rows.  Bit-exact to that pair (the selected sets are the fixed-order scores'
- * top-k).  For bf16 q, e4m3 keys and Hi == Di == 64 the scores are first computed on MFMA
- * together with a certified error bound; only keys whose rank the bound leaves open are
- * rescored in the fixed order (rows that cannot be certified are rescored in full).  Other
- * shapes and types run the two-step path.  Replaces the compressed index selection of
- * oracle/decode_engine.py:110-114 with an indexer-ranked one.
- * workspace: smla_index_decode_workspace(B, S, N) bytes.  Requires ceil(N / 1024) <= 64 and
- * B*S <= 65535.  flags: 0, or SMLA_INDEX_EXACT to rescore every visible key in the fixed order
- * instead of certifying (the same output, slower; the path uncertifiable rows take).
+ * R = B*S query rows, with the same output bit for bit.  Replaces the compressed index selection
+ * of oracle/decode_engine.py:110-114 with an indexer-ranked one.
+ * workspace: smla_index_decode_workspace(B, S, N) bytes (the B*S*N fp32 scores).  Requires
+ * ceil(N / 1024) <= 64 and B*S <= 65535.  flags: 0 or SMLA_INDEX_EXACT (accepted, no effect:
+ * the scores are always the fixed-order ones).
  */
 enum { SMLA_INDEX_EXACT = 1 };
 int smla_index_decode(const void* q, int q_dtype, const void* keys, int k_dtype, const float* kscale,

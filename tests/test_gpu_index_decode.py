@@ -1,10 +1,9 @@
 """GPU parity of smla_index_decode (indexer scores + decode index build in one call).
 
 The output must equal, bit for bit, the oracle's fixed-order indexer scores followed by its exact
-top-k (window ids first, compressed ids offset by n_raw): on the certified MFMA path, on the slow
-path that rescores every key (forced, or taken by rows that cannot be certified: equal scores,
-overflow), and on the two-step path of shapes without the MFMA form.  Near-ties are built on
-purpose: duplicated keys (exact ties broken by index) and key pairs one e4m3 code apart."""
+top-k (window ids first, compressed ids offset by n_raw), with either flag value, over rows with
+equal scores and overflow, and for shapes without the 64 x 64 matrix-core form.  Near-ties are
+built on purpose: duplicated keys (exact ties broken by index) and key pairs one e4m3 code apart."""
 import numpy as np
 import pytest
 import torch
@@ -90,11 +89,11 @@ def test_index_decode_vs_oracle(dev, B, S, N, k, window, kind, use_scale):
 
 
 @pytest.mark.parametrize("kind", ["random", "near"])
-def test_index_decode_forced_slow_path(dev, kind):
-    """Every key rescored in the fixed order (the path of rows that cannot be certified)."""
+def test_index_decode_exact_flag(dev, kind):
+    """SMLA_INDEX_EXACT gives the same list (the scores are always the fixed-order ones)."""
     from smla import _lib
     from smla import indexer as sidx
-    announce(f"index_decode forced slow path kind={kind}")
+    announce(f"index_decode exact flag kind={kind}")
     g = torch.Generator().manual_seed(3)
     B, N, k, window = 2, 4096, 1024, 64
     q = torch.randn(B, 1, 64, 64, generator=g).to(torch.bfloat16)
@@ -110,8 +109,8 @@ def test_index_decode_forced_slow_path(dev, kind):
 
 
 def test_index_decode_matches_two_step(dev):
-    """The fused call and indexer_score + select_decode_indices agree on the decode_32k step, and
-    a shape without the MFMA form (32 heads, fp32 q) runs the two-step path itself."""
+    """The one-call form and indexer_score + select_decode_indices agree on the decode_32k step,
+    and on a shape outside the 64 x 64 matrix-core form (32 heads, fp32 q)."""
     from smla import indexer as sidx
     from smla import workloads as wl
     announce("index_decode vs two-step")
@@ -124,7 +123,7 @@ def test_index_decode_matches_two_step(dev):
     sc = sidx.indexer_score(q, codes, ks, w, nvis)
     two = sidx.select_decode_indices(sc[:, 0], w32["k"], pos, w32["window"], 32768)
     assert torch.equal(fused, two)
-    # 32 heads, fp32 q: the two-step path inside the same entry point
+    # 32 heads, fp32 q
     g = torch.Generator().manual_seed(4)
     q2 = torch.randn(2, 1, 32, 64, generator=g)
     w2 = torch.randn(2, 1, 32, generator=g)
