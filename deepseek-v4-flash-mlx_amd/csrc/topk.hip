@@ -3,90 +3,34 @@
 // smla_topk: per row, rank the first nvis scores by (score desc, index asc) with -0 == +0, keep
 // min(k, nvis), emit ascending ids (+ id_offset), -1 padded to k.  One workgroup of 1024 threads
 // per row; each thread owns a contiguous run of PER keys in registers (key = order-preserving
-// uint32, larger score -> smaller key).  The k-th best entry (Kt, It) is found by a bucket select
-// (monotone value buckets, exact ranking of the boundary bucket) or, for degenerate spreads, by
-// 4 radix passes plus a tie rank; a block-wide scan in index order then places every selected id
-// at its ascending position.  Bit-exact by construction: only comparisons and counts.  When
+// uint32, larger score -> smaller key).  The k-th best entry (Kt, It) comes from the row selection
+// of select_row.h; a block-wide scan in index order then places every selected id at its
+// ascending position.  Bit-exact by construction: only comparisons and counts.  When
 // nvis <= k every visible id is taken (oracle/decode_engine.py:112-114, "all causally visible
 // compressed rows").  smla_select_decode also writes the decode window ids in front (one launch
 // for the engine's whole index build, oracle/decode_engine.py:110-114).
 //
 // smla_window_topk_idxs mirrors ref_torch/sparse_attn.py:9-20; smla_decode_window_idxs builds the
 // engine's decode window oracle/decode_engine.py:110-111 over an un-ringed raw cache.
+#include "select_row.h"
 #include "smla_internal.h"
 
 namespace {
 
+using smla_select::block_excl_scan;
+
 constexpr int kTopkThreads = 1024;  // the largest workgroup (sizes the per-thread run PER)
 
-__device__ inline uint32_t desc_key(float f) {
-  if (f == 0.f) f = 0.f;  // -0 -> +0
-  uint32_t u = __float_as_uint(f);
-  uint32_t asc = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-  return ~asc;
-}
-
-// exclusive scan of one value per thread over a block of NW waves; returns the exclusive prefix
-// and the block total.  `tmp` holds NW ints.  One barrier: every wave scans the per-wave totals
-// itself.  The caller separates two scans on the same `tmp` by a barrier.
-template <int NW>
-__device__ inline int block_excl_scan(int v, int* tmp, int* total) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int x = wave_incl_scan(v);
-  if (lane == 63) tmp[wave] = x;
-  __syncthreads();
-  const int wi = wave_incl_scan(lane < NW ? tmp[lane] : 0);
-  const int before = wave > 0 ? __builtin_amdgcn_readlane(wi, wave - 1) : 0;
-  *total = __builtin_amdgcn_readlane(wi, NW - 1);
-  return before + x - v;
-}
-
-constexpr int kBuckets = 2048;
-constexpr int kMaxCand = 256;
-
-// inverse of desc_key (the score with -0 folded to +0)
-__device__ inline float key_score(uint32_t key) {
-  const uint32_t asc = ~key;
-  return __uint_as_float((asc & 0x80000000u) ? (asc ^ 0x80000000u) : ~asc);
-}
-
-
-// floor((lmax - s) * bscale) clamped to [0, kBuckets), as one fma (one rounding of the exact
-// lmax bscale - s bscale, monotone non-increasing in s), a clamp in float and a conversion in range
-__device__ inline int bucket_of_score(float s, float lmax, float bscale) {
-  const float t = __builtin_fmaf(-s, bscale, lmax * bscale);
-  return (int)__builtin_amdgcn_fmed3f(t, 0.f, (float)(kBuckets - 1));
-}
-// monotone bucket of a finite score: 0 holds the largest scores
-__device__ inline int bucket_of(uint32_t key, float lmax, float bscale) {
-  return bucket_of_score(key_score(key), lmax, bscale);
-}
-
-// Row selection.  Produces the threshold pair (Kt, It) of the k-th best entry in the order
-// (key asc == score desc, index asc); entry n is selected iff key < Kt or (key == Kt && n <= It).
-//  * fast path: monotone buckets of (max - s) * 2048 / (max - min); the bucket holding the k-th
-//    entry is found from a histogram + scan, and its (few) candidates are ranked exactly;
-//  * fallback (degenerate spreads, > 256 candidates in the boundary bucket): 4 radix passes of 8
-//    bits over the keys, then the tie rank among entries equal to the k-th key.
-// Output: window ids (optional), then the selected ids ascending (+ id_offset), then -1.
+// One row per workgroup of NT threads: window ids (optional), then the selected ids ascending
+// (+ id_offset), then -1.
 template <int PER, int NT>
 __global__ __launch_bounds__(NT) void topk_kernel(const float* scores, int64_t N, const int32_t* __restrict__ nvis,
                                                   int k, int32_t* __restrict__ out, int64_t out_stride,
                                                   int32_t id_offset, const int32_t* __restrict__ wpos, int window) {
   constexpr int kWaves = NT / 64;
-  constexpr int kBPT = kBuckets / NT;  // histogram buckets owned by each thread in the scan
-  static_assert(kBPT * NT == kBuckets, "buckets per thread");
   static_assert(PER <= 64, "per-thread selection masks are 64 bits");
-  __shared__ int hist[kWaves][256];
-  __shared__ int bhist[kBuckets + 1];  // + a slot that absorbs the counts of entries past nvis
-  __shared__ int tmp[kWaves + 1];
-  __shared__ float redf[5 * kWaves];
-  __shared__ uint64_t cand_pair[kMaxCand];  // (key << 32) | index: the selection order is the integer order
-  __shared__ int cand_idx[kMaxCand];
-  __shared__ int s_int[5];
-  __shared__ int s_nan[kWaves];
+  __shared__ smla_select::Lds<NT> sm;
   const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6;
   const int64_t r = blockIdx.x;
   // N <= 65536 (PER * NT): every index of the row fits 32 bits
   const int base = tid * PER;
@@ -94,7 +38,8 @@ __global__ __launch_bounds__(NT) void topk_kernel(const float* scores, int64_t N
   // 16-byte aligned (rows of N floats: N % 4 == 0), element loads otherwise.  Issued first: the
   // window-id stores below may alias the scores, so loads placed after them would wait for them.
   float fv[PER];
-  auto load_scores = [&](const float* row) {
+  {
+    const float* row = scores + r * N;
     if (PER % 4 == 0 && (N & 3) == 0 && base + PER <= N) {
 #pragma unroll
       for (int j = 0; j < PER; j += 4) {
@@ -108,8 +53,7 @@ __global__ __launch_bounds__(NT) void topk_kernel(const float* scores, int64_t N
 #pragma unroll
       for (int j = 0; j < PER; j++) fv[j] = base + j < N ? row[base + j] : 0.f;
     }
-  };
-  load_scores(scores + r * N);
+  }
   int nv = nvis ? nvis[r] : (int)N;
   if (nv > (int)N) nv = (int)N;
   if (nv < 0) nv = 0;
@@ -130,227 +74,15 @@ __global__ __launch_bounds__(NT) void topk_kernel(const float* scores, int64_t N
     for (int j = tid; j < k; j += NT) orow[j] = j < nv ? j + id_offset : -1;
     return;
   }
-  // the bucket holding the k-th entry (bucket 0 = largest scores) and how many of its entries the
-  // selection takes: s_int[0], s_int[1].  Thread t owns buckets kBPT t .. kBPT t + kBPT - 1.
-  auto find_boundary = [&](int t) {
-    int c[kBPT], sum = 0;
-#pragma unroll
-    for (int i = 0; i < kBPT; i++) {
-      c[i] = bhist[kBPT * t + i];
-      sum += c[i];
-    }
-    int tot;
-    int before = block_excl_scan<kWaves>(sum, tmp, &tot);
-#pragma unroll
-    for (int i = 0; i < kBPT; i++) {
-      if (before < k && k <= before + c[i]) {
-        s_int[0] = kBPT * t + i;
-        s_int[1] = k - before;
-      }
-      before += c[i];
-    }
-  };
-  // rank of candidate c among the first `total` in the order (key asc, index asc)
-  auto rank_of = [&](int c, int total) -> int {
-    const uint64_t me = cand_pair[c];
-    int rank = 0;
-#pragma unroll 16
-    for (int j = 0; j < total; j++) rank += cand_pair[j] < me;
-    return rank;
-  };
-
   uint32_t key[PER];
-  uint32_t Kt = 0;
-  int It = -1;
-  {
-    float lmin = SMLA_INF, lmax = -SMLA_INF;
-    bool nan_seen = false;
-#pragma unroll
-    for (int j = 0; j < PER; j++) {
-      const bool vis = j < nloc;
-      const float f = fv[j];
-      key[j] = vis ? desc_key(f) : 0xffffffffu;
-      lmin = fminf(lmin, vis ? f : SMLA_INF);
-      lmax = fmaxf(lmax, vis ? f : -SMLA_INF);
-      nan_seen |= vis && f != f;
-    }
-    // ---- row min / max (and whether a NaN is visible)
-    {
-      const float a = wave_min_dpp(lmin), bmx = wave_max_dpp(lmax);
-      const bool wnan = __builtin_amdgcn_ballot_w64(nan_seen) != 0;
-      if (lane == 0) {
-        redf[wave] = a;
-        redf[kWaves + wave] = bmx;
-        s_nan[wave] = wnan;
-      }
-      for (int i = tid; i <= kBuckets; i += NT) bhist[i] = 0;
-      __syncthreads();
-      // every wave reduces the kWaves per-wave results itself (one LDS read per lane)
-      const int wl = lane < kWaves ? lane : 0;
-      lmin = wave_min_dpp(redf[wl]);
-      lmax = wave_max_dpp(redf[kWaves + wl]);
-      nan_seen = __builtin_amdgcn_ballot_w64(lane < kWaves && s_nan[wl] != 0) != 0;
-    }
-    // The plain selection buckets the finite scores: -inf scores (the indexer's mark of masked
-    // keys) go to the absorbing slot and are never selected as long as k finite scores are visible
-    // (with fewer, the radix fallback ranks them).  The finite minimum and the -inf count are only
-    // reduced when the row minimum is -inf (a block-uniform condition).
-    float lminf = lmin, ninf = 0.f;
-    if (lmin == -SMLA_INF && !nan_seen && lmax > -SMLA_INF) {
-      float mf = SMLA_INF, ni = 0.f;
-#pragma unroll
-      for (int j = 0; j < PER; j++) {
-        const bool vis = j < nloc;
-        mf = fminf(mf, vis && fv[j] > -SMLA_INF ? fv[j] : SMLA_INF);
-        ni += (vis && fv[j] == -SMLA_INF) ? 1.f : 0.f;
-      }
-      mf = wave_min_dpp(mf);
-      ni = wave_sum_dpp(ni);
-      if (lane == 0) {
-        redf[3 * kWaves + wave] = mf;
-        redf[4 * kWaves + wave] = ni;
-      }
-      __syncthreads();
-      const int wl = lane < kWaves ? lane : 0;
-      lminf = wave_min_dpp(redf[3 * kWaves + wl]);
-      ninf = wave_sum_dpp(lane < kWaves ? redf[4 * kWaves + wl] : 0.f);  // exact: an integer <= 65536
-    }
-    const bool ninf_ok = (float)nv - ninf >= (float)k;
-    const float lo = lminf;
-    const float bscale = (float)kBuckets / (lmax - lo);
-    const bool spread_ok = !nan_seen && ninf_ok && bscale < SMLA_INF && bscale > 0.f && lo > -SMLA_INF &&
-                           lmax < SMLA_INF;
-    bool done = false;
-    if (lmax == lmin && !nan_seen) {
-      // every visible score equal: the k lowest indices
-      Kt = desc_key(lmax);
-      It = k - 1;
-      done = true;
-    }
-    if (!done && spread_ok) {
-      // ---- bucket histogram (bucket 0 holds the largest scores).  Each entry's bucket is
-      // computed once, from the score itself (key_score(key) only folds -0 to +0, which the
-      // subtraction from lmax does not see); entries past nvis go to the absorbing slot.
-      int bk[PER];
-#pragma unroll
-      for (int j = 0; j < PER; j++) bk[j] = (j < nloc && fv[j] > -SMLA_INF) ? bucket_of_score(fv[j], lmax, bscale) : kBuckets;
-#pragma unroll
-      for (int j = 0; j < PER; j++) atomicAdd(&bhist[bk[j]], 1);
-      __syncthreads();
-      find_boundary(tid);
-      if (tid == 0) s_int[3] = 0;  // candidate counter
-      __syncthreads();
-      const int bb = s_int[0], need = s_int[1];
-      const int cb = bhist[bb];
-      if (cb <= kMaxCand) {
-        // candidates of the boundary bucket: per-thread count, wave offsets by scan, one LDS
-        // atomic per wave
-        int mine = 0;
-#pragma unroll
-        for (int j = 0; j < PER; j++) mine += bk[j] == bb;
-        const int incl = wave_incl_scan(mine);
-        int wbase = 0;
-        if (lane == 63 && incl > 0) wbase = atomicAdd(&s_int[3], incl);
-        wbase = __builtin_amdgcn_readlane(wbase, 63);
-        int slot = wbase + incl - mine;
-#pragma unroll
-        for (int j = 0; j < PER; j++) {
-          if (bk[j] == bb) {
-            if (slot < kMaxCand) cand_pair[slot] = ((uint64_t)key[j] << 32) | (uint32_t)(base + j);
-            slot++;
-          }
-        }
-        __syncthreads();
-        if (tid < cb && rank_of(tid, cb) == need - 1) {
-          const uint64_t pr = cand_pair[tid];
-          s_int[0] = (int)(uint32_t)(pr >> 32);
-          s_int[1] = (int)(uint32_t)pr;
-        }
-        __syncthreads();
-        Kt = (uint32_t)s_int[0];
-        It = s_int[1];
-        done = true;
-      }
-      __syncthreads();
-    }
-    if (!done) {
-      // ---- radix select over the 32-bit keys
-      uint32_t prefix = 0, pmask = 0;
-      int remaining = k;
-#pragma unroll 1
-      for (int shift = 24; shift >= 0; shift -= 8) {
-        for (int i = lane; i < 256; i += 64) hist[wave][i] = 0;
-        __syncthreads();
-#pragma unroll
-        for (int j = 0; j < PER; j++) {
-          if (j < nloc && (key[j] & pmask) == prefix) atomicAdd(&hist[wave][(key[j] >> shift) & 255u], 1);
-        }
-        __syncthreads();
-        if (wave == 0) {
-          int cc4[4];
-          int t4 = 0;
-#pragma unroll 1
-          for (int i = 0; i < 4; i++) {
-            int sacc = 0;
-#pragma unroll 4
-            for (int w = 0; w < kWaves; w++) sacc += hist[w][lane * 4 + i];
-            cc4[i] = sacc;
-            t4 += sacc;
-          }
-          const int incl = wave_incl_scan(t4);
-          const int bef = incl - t4;
-          if (bef < remaining && remaining <= incl) {
-            int cum = bef;
-            for (int i = 0; i < 4; i++) {
-              if (remaining <= cum + cc4[i]) {
-                s_int[0] = lane * 4 + i;
-                s_int[1] = cum;
-                break;
-              }
-              cum += cc4[i];
-            }
-          }
-        }
-        __syncthreads();
-        prefix |= (uint32_t)s_int[0] << shift;
-        pmask |= 255u << shift;
-        remaining -= s_int[1];
-        __syncthreads();
-      }
-      // index of the `remaining`-th entry equal to the k-th key (index order)
-      int nt = 0;
-#pragma unroll
-      for (int j = 0; j < PER; j++) nt += (j < nloc && key[j] == prefix);
-      int tot_ties;
-      const int trank = block_excl_scan<kWaves>(nt, tmp, &tot_ties);
-      if (trank < remaining && remaining <= trank + nt) {
-        int cnt = trank;
-#pragma unroll
-        for (int j = 0; j < PER; j++) {
-          if (j < nloc && key[j] == prefix) {
-            cnt++;
-            if (cnt == remaining) s_int[2] = (int)(base + j);
-          }
-        }
-      }
-      __syncthreads();
-      Kt = prefix;
-      It = s_int[2];
-    }
-  }
-  // ---- emit the selected ids in ascending order: the selection as a bit mask, evaluated once for
-  // the count and the placement
-  uint64_t selm = 0;  // PER <= 64
-#pragma unroll
-  for (int j = 0; j < PER; j++) {
-    const int n = base + j;
-    const bool sel = j < nloc && (key[j] < Kt || (key[j] == Kt && n <= It));
-    selm |= (uint64_t)sel << j;
-  }
-  const int nsel = __builtin_popcountll(selm);
+  uint32_t Kt;
+  int It;
+  smla_select::row_threshold<PER, NT>(fv, nloc, base, nv, k, sm, key, Kt, It);
+  // ---- emit the selected ids in ascending order; ids go straight to their output positions
+  // (each wave's selected ids fill one contiguous run)
+  const uint64_t selm = smla_select::selected_mask<PER>(key, nloc, base, Kt, It);
   int tot_sel;
-  int pos = block_excl_scan<kWaves>(nsel, tmp, &tot_sel);
-  // ids go straight to their output positions (each wave's selected ids fill one contiguous run)
+  int pos = block_excl_scan<kWaves>(__builtin_popcountll(selm), sm.tmp, &tot_sel);
 #pragma unroll
   for (int j = 0; j < PER; j++) {
     if ((selm >> j) & 1ull) {
