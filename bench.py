@@ -67,6 +67,9 @@ def parse():
     ap.add_argument("--cpu-steps", type=int, default=3)
     ap.add_argument("--rows-per-split", type=int, default=0,
                     help="attention split plan: index-list rows per split, a multiple of 32 (0 = the default plan)")
+    ap.add_argument("--decode-path", choices=("lists", "select-in-attn"), default="lists",
+                    help="timed decode step: indexer, selection launch, list attention (the default), or "
+                         "indexer then smla_decode_attn (the selection inside the attention workgroups)")
     ap.add_argument("--no-prefill", action="store_true", help="skip the prefill MFMA-utilisation leg")
     ap.add_argument("--prefill-reps", type=int, default=10)
     ap.add_argument("--no-others", action="store_true", help="skip the other workloads and kernels")
@@ -429,12 +432,22 @@ def main():
 
     ws = torch.empty(ops.index_decode_workspace(B, 1, keys0.shape[1]), dtype=torch.uint8, device=dev)
 
-    def step(r):
+    wsd = torch.empty(ops.decode_attn_workspace(B, 1, H, 576, 512, win, k), dtype=torch.uint8, device=dev)
+
+    def step_fused(r):
+        raw, comp, keys, ks = copies[r]
+        sc = sidx.indexer_score(qi, keys, ks, wt)
+        return ssa.decode_attn(q, raw, comp, None, sc[:, 0], pos, win, k, w["scale"], dv=512, workspace=wsd)
+
+    def step_lists(r):
         raw, comp, keys, ks = copies[r]
         sc = sidx.indexer_score(qi, keys, ks, wt)
         idx = sidx.select_decode_indices(sc[:, 0], k, pos, win, n_raw)
         return ops.sparse_attn_ex(q, raw, comp, None, None, None, idx[:, None, :], w["scale"], 512,
                                   rows_per_split=args.rows_per_split)
+
+    fused = args.decode_path == "select-in-attn" and args.rows_per_split == 0
+    step = step_fused if fused else step_lists
 
     ref_out = step(0)
     torch.cuda.synchronize()
@@ -551,6 +564,26 @@ def main():
                 "kernel": KERNEL_NAME, "kernel_us": round(k_us, 3),
                 "algorithmic_bytes": alg_bytes, "nsplit": ns, "rows_per_split": rps}
 
+    # the other decode-step form, timed the same way (graph replays over the rotated copies)
+    alt_step = step_lists if fused else step_fused
+    g_alt = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g_alt):
+        alt_outs = [alt_step(r) for r in range(args.rot)]
+    g_alt.replay()
+    torch.cuda.synchronize()
+    if not all(torch.equal(o, ref_out) for o in alt_outs):
+        raise SystemExit("the two decode-step forms differ")
+    alt_reps = max(1, args.steps // args.rot)
+    ea, eb = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ea.record()
+    for _ in range(alt_reps):
+        g_alt.replay()
+    eb.record()
+    torch.cuda.synchronize()
+    alt_us = 1000.0 * ea.elapsed_time(eb) / (alt_reps * args.rot)
+    alt = {"decode_path": "lists" if fused else "select-in-attn", "us_per_step": round(alt_us, 3),
+           "tok_s": round(B / (alt_us * 1e-6), 1), "output": "bit-identical to the timed step"}
+
     prefill = None
     if not args.no_prefill:
         print("[bench] prefill leg", file=sys.stderr, flush=True)
@@ -586,12 +619,14 @@ def main():
         "data": "synthetic: seeded N(0,1)*0.05 q/latent rows (bf16), fp8 indexer keys, seed 1",
         "config": {"workload": "decode_32k: B=8 H=64 rows 576 bf16, raw [8,32768,576], mean-pooled "
                                "[8,8192,576], fp8 keys [8,8192,64], top-k 2048 + window 128",
-                   "global_batch": B, "seq_len": 32768, "parallelism": "single GPU"},
+                   "global_batch": B, "seq_len": 32768, "parallelism": "single GPU",
+                   "decode_path": "select-in-attn" if fused else "lists"},
         "roofline": roofline,
         "cpu_baseline": cpu,
         "prefill": prefill,
         "other": others,
         "attention_op_us": round(attn_op_us, 3),
+        "other_decode_path": alt,
         "rotated_copies": args.rot,
     }
     print(json.dumps(line), flush=True)

@@ -411,7 +411,8 @@ int check_attn_args(const void* q, int q_dtype, const void* kv0, int64_t n0, con
 // checked by the caller.
 static int attn_launch(const Plan& p, int phases, const void* q, int q_dtype, RowSrc src, int kv_dtype,
                      const float* attn_sink, const int32_t* topk_idxs, int64_t T, int64_t B, int64_t S, int64_t H,
-                     int64_t D, int64_t DV, float scale, void* out, int out_dtype, void* ws, hipStream_t st) {
+                     int64_t D, int64_t DV, float scale, void* out, int out_dtype, void* ws, hipStream_t st,
+                     smla_attn::SelectRows sr = smla_attn::SelectRows{}) {
   if (!p.mfma) {
     if (!(phases & SMLA_ATTN_SPLIT)) return SMLA_OK;
     const size_t lds = (size_t)D * 4 + kThreads * 8;
@@ -424,7 +425,7 @@ static int attn_launch(const Plan& p, int phases, const void* q, int q_dtype, Ro
   if (phases & SMLA_ATTN_SPLIT) {
     const int rc = smla_attn::launch_decode_v6((int)D, kv_dtype == SMLA_FP8_E4M3, p.nsplit, p.rows_per_split, q, src,
                                                attn_sink, topk_idxs, T, B, S, H, scale, out, out_dtype, (float*)ws,
-                                               st);
+                                               st, smla_attn::ImplicitRows{}, sr);
     if (rc != SMLA_OK) return rc;
   }
   if (phases & SMLA_ATTN_MERGE) return launch_merge(p, B, S, H, attn_sink, out, out_dtype, ws, st);
@@ -474,6 +475,59 @@ extern "C" int smla_prefill_attn(const void* q, int q_dtype, const void* kv_raw,
   const smla_attn::ImplicitRows ir{q_pos0, (int)window, (int)ratio, 1};
   return smla_attn::launch_decode_v6((int)D, false, 1, (int)rows, q, src, attn_sink, nullptr, T, B, S, H, scale, out,
                                      out_dtype, nullptr, (hipStream_t)stream, ir);
+}
+
+// Decode attention over the engine's index build (window ids of pos, then the top-k of the
+// indexer scores: the list smla_select_decode writes), with the selection run by the attention
+// workgroups themselves when the shape allows (bf16 rows, the short-split plan, N <= 18432): the
+// list never goes through memory and the selection launch disappears.  Other shapes build the
+// list in the workspace and run the list path.  Output bit-identical to smla_select_decode
+// followed by smla_sparse_attn with the default plan.
+namespace {
+size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+bool select_in_kernel(const Plan& p, int kv_dtype, int64_t N) {
+  return p.mfma && kv_dtype == SMLA_BF16 && p.rows_per_split <= smla_attn::kDecodeV6ShortRows &&
+         smla_attn::select_per(N) != 0;
+}
+}  // namespace
+
+extern "C" size_t smla_decode_attn_workspace(int64_t B, int64_t S, int64_t H, int64_t D, int64_t DV, int64_t window,
+                                             int64_t k, int q_dtype, int kv_dtype, int out_dtype) {
+  if (B <= 0 || S <= 0 || H <= 0 || window < 0 || k <= 0) return 0;
+  const int64_t T = window + k;
+  const Plan p = make_plan(B, S, H, D, DV, T, q_dtype, kv_dtype, 0);
+  // the split partials, then room for the lists of the path that builds them in memory
+  return align256(plan_workspace(p, B, S, H, DV, out_dtype)) + (size_t)(B * S * T) * sizeof(int32_t);
+}
+
+extern "C" int smla_decode_attn(const void* q, int q_dtype, const void* kv_raw, int64_t n_raw, const void* kv_comp,
+                                int64_t n_comp, int kv_dtype, const float* attn_sink, const float* scores, int64_t N,
+                                const int32_t* nvis, const int32_t* pos, int64_t window, int64_t k, int64_t B,
+                                int64_t S, int64_t H, int64_t D, int64_t DV, float scale, void* out, int out_dtype,
+                                void* workspace, size_t workspace_bytes, void* stream) {
+  if (!scores || !pos) return SMLA_E_NULL;
+  if (N <= 0 || window < 0 || k <= 0 || window + k > 0x7fffffff || N > 0x7fffffff) return SMLA_E_SHAPE;
+  const int64_t T = window + k;
+  // the list arguments are checked with a stand-in for the list pointer
+  int rc = check_attn_args(q, q_dtype, kv_raw, n_raw, kv_comp, n_comp, kv_dtype, nullptr, nullptr, (const int32_t*)pos,
+                           T, B, S, H, D, DV, out, out_dtype);
+  if (rc != SMLA_OK) return rc;
+  if (kv_dtype == SMLA_FP8_E4M3) return SMLA_E_DTYPE;  // fp8 rows carry scale arrays: the list entry takes them
+  const size_t need = smla_decode_attn_workspace(B, S, H, D, DV, window, k, q_dtype, kv_dtype, out_dtype);
+  if (!workspace || workspace_bytes < need) return SMLA_E_WORKSPACE;
+  const Plan p = make_plan(B, S, H, D, DV, T, q_dtype, kv_dtype, 0);
+  hipStream_t st = (hipStream_t)stream;
+  const RowSrc src{kv_raw, kv_comp, nullptr, nullptr, n_raw, n_comp};
+  if (select_in_kernel(p, kv_dtype, N)) {
+    const smla_attn::SelectRows sr{scores, nvis, pos, (int)N, (int)window, (int)k, 1};
+    return attn_launch(p, SMLA_ATTN_SPLIT | SMLA_ATTN_MERGE, q, q_dtype, src, kv_dtype, attn_sink, nullptr, T, B, S,
+                       H, D, DV, scale, out, out_dtype, workspace, st, sr);
+  }
+  int32_t* ids = (int32_t*)((uint8_t*)workspace + align256(plan_workspace(p, B, S, H, DV, out_dtype)));
+  rc = smla_select_decode(scores, B * S, N, nvis, k, pos, window, ids, T, (int32_t)n_raw, stream);
+  if (rc != SMLA_OK) return rc;
+  return attn_launch(p, SMLA_ATTN_SPLIT | SMLA_ATTN_MERGE, q, q_dtype, src, kv_dtype, attn_sink, ids, T, B, S, H, D,
+                     DV, scale, out, out_dtype, workspace, st);
 }
 
 extern "C" size_t smla_sparse_attn_workspace(int64_t B, int64_t S, int64_t H, int64_t D, int64_t DV,

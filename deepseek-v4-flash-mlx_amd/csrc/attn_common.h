@@ -29,13 +29,30 @@ struct ImplicitRows {
   int enabled;
 };
 
+// Decode lists built in the kernel from indexer scores: the engine's decode index build
+// (oracle/decode_engine.py:110-114 with an indexer-ranked compressed part, the list
+// smla_select_decode writes).  Entry t < window of query row r is raw row pos[r] - window + 1 + t
+// (-1 below 0); entry window + j is the j-th of the selected compressed rows in ascending order
+// (id n0 + c), where the selection is the min(k, nvis[r]) best of the first nvis[r] scores of row
+// r (score descending, index ascending, -0 == +0), -1 past it.  Every workgroup whose split
+// reaches past the window runs the selection itself, so no index list goes through memory.
+struct SelectRows {
+  const float* scores;   // [rows, N]
+  const int32_t* nvis;   // [rows] or null (all N visible)
+  const int32_t* pos;    // [rows]
+  int N, window, k, enabled;
+};
+
 // bf16 or fp8 (e4m3 + per-64 pow2 scales) rows, D in {576, 512}, DV = 512, H % 16 == 0: 12-wave
 // role-split kernel (4 score waves, 8 value waves, 64 heads per workgroup).  Writes the final
 // output (nsplit == 1) or partial states: (m, l) fp32 per (query row, split, head), then the partial
 // O rows (bf16 for bf16 output, else fp32) after all (m, l) records, split-major.
 int launch_decode_v6(int D, bool kv_fp8, int nsplit, int rows_per_split, const void* q, RowSrc src,
                      const float* sink, const int32_t* idx, int64_t T, int64_t B, int64_t S, int64_t H, float scale,
-                     void* out, int out_dtype, float* part, hipStream_t stream, ImplicitRows ir = ImplicitRows{});
+                     void* out, int out_dtype, float* part, hipStream_t stream, ImplicitRows ir = ImplicitRows{},
+                     SelectRows sr = SelectRows{});
+// the selection's scores per thread of the 768-thread workgroup for N scores (0: not supported)
+constexpr int select_per(int64_t N) { return N <= 768 * 12 ? 12 : N <= 768 * 24 ? 24 : 0; }
 constexpr int kDecodeV6ShortRows = 256;  // up to here: 4-tile ring; its index table lives in LDS
 constexpr int kDecodeV6MaxRows = 8192;   // beyond: 3-tile ring and a larger index table
 

@@ -22,6 +22,7 @@
 //
 // Output: final rows (one split) or (m, l, O) partial states in the layout attn_merge_kernel reads.
 #include "attn_common.h"
+#include "select_row.h"
 
 namespace smla_attn {
 namespace {
@@ -96,11 +97,11 @@ __device__ inline int64_t query_row_of(int64_t L, int64_t n) {
   return r * kX * kC + pos * kC + j;
 }
 
-template <int D, int NBUF, int MAXROWS, bool FP8, bool IMPL = false>
+template <int D, int NBUF, int MAXROWS, bool FP8, bool IMPL = false, int SELPER = 0>
 __global__ __launch_bounds__(768) void attn_decode_kernel(
     const uint16_t* __restrict__ q, RowSrc src, const float* __restrict__ sink, const int32_t* __restrict__ idx,
     int T, int S, int H, int rows_per_split, float scale, float* __restrict__ part, void* __restrict__ out,
-    int out_dtype, ImplicitRows ir) {
+    int out_dtype, ImplicitRows ir, SelectRows sr) {
   using G = Geo6<D, NBUF, MAXROWS>;
   extern __shared__ __align__(16) uint8_t lds_generic[];
   lds_u8_t* lds = (lds_u8_t*)lds_generic;
@@ -114,6 +115,8 @@ __global__ __launch_bounds__(768) void attn_decode_kernel(
     asm volatile("" ::"s"(gx), "s"(gy), "s"(gz), "s"(q), "s"(src.kv0), "s"(src.kv1), "s"(src.n0), "s"(src.n1),
                  "s"(idx), "s"(T), "s"(S), "s"(H), "s"(rows_per_split), "s"(part), "s"(out), "s"(sink),
                  "s"(scale), "s"(out_dtype), "s"(ir.q_pos0), "s"(ir.window), "s"(ir.ratio), "s"(ir.enabled));
+    if constexpr (SELPER > 0)
+      asm volatile("" ::"s"(sr.scores), "s"(sr.nvis), "s"(sr.pos), "s"(sr.N), "s"(sr.window), "s"(sr.k));
   }
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -232,6 +235,67 @@ __global__ __launch_bounds__(768) void attn_decode_kernel(
   if constexpr (IMPL) {
     // the last live entry: the last visible compressed row, else the window's last (p itself)
     if (scorer) last = i_nc > 0 ? ir.window + i_nc - 1 : i_wlast;
+  } else if constexpr (SELPER > 0) {
+    // SelectRows: the window entries of the split, then (when the split reaches past the window)
+    // the selection by the whole workgroup, its LDS in ring slot 0 (tile 0 is requested only after
+    // the table is complete); each selected id lands at its list position if that is in the split
+    using SL = smla_select::Lds<768>;
+    static_assert(sizeof(SL) <= G::TILE_BYTES, "selection scratch fits a ring slot");
+    SL& sm = *(SL*)lds_generic;
+    const int p = sr.pos[bs];
+    auto valid = [&](int64_t r) -> int { return (r >= 0 && r < ntot) ? (int)r : -1; };
+    for (int t = tid; t < nt; t += 768) {
+      const int e = t_begin + t;
+      ids_s[t] = (t < nrows && e < sr.window) ? valid((int64_t)p - sr.window + 1 + e) : -1;
+    }
+    if (t_end > sr.window) {  // uniform over the workgroup
+      int nv = sr.nvis ? sr.nvis[bs] : sr.N;
+      nv = nv < 0 ? 0 : (nv > sr.N ? sr.N : nv);
+      const int lo = t_begin - sr.window, hi = t_end - sr.window;  // selected ranks of this split
+      if (nv <= sr.k) {
+        // every visible row, in index order
+        for (int t = tid; t < nrows; t += 768) {
+          const int rk = t_begin + t - sr.window;
+          if (rk >= 0 && rk < nv) ids_s[t] = valid(n0 + rk);
+        }
+      } else {
+        const int base = tid * SELPER;
+        const float* row = sr.scores + bs * (int64_t)sr.N;
+        float fv[SELPER];
+        if ((sr.N & 3) == 0 && base + SELPER <= sr.N) {
+#pragma unroll
+          for (int j = 0; j < SELPER; j += 4) {
+            const f32x4_t v4 = *(const f32x4_t*)(row + base + j);
+            fv[j] = v4[0];
+            fv[j + 1] = v4[1];
+            fv[j + 2] = v4[2];
+            fv[j + 3] = v4[3];
+          }
+        } else {
+#pragma unroll
+          for (int j = 0; j < SELPER; j++) fv[j] = base + j < sr.N ? row[base + j] : 0.f;
+        }
+        const int nloc = nv - base < 0 ? 0 : (nv - base > SELPER ? SELPER : nv - base);
+        uint32_t key[SELPER];
+        uint32_t Kt;
+        int It;
+        smla_select::row_threshold<SELPER, 768>(fv, nloc, base, nv, sr.k, sm, key, Kt, It);
+        const uint64_t selm = smla_select::selected_mask<SELPER>(key, nloc, base, Kt, It);
+        int tot;
+        int rk = smla_select::block_excl_scan<12>(__builtin_popcountll(selm), sm.tmp, &tot);
+#pragma unroll
+        for (int j = 0; j < SELPER; j++) {
+          if ((selm >> j) & 1ull) {
+            if (rk >= lo && rk < hi) ids_s[sr.window + rk - t_begin] = valid(n0 + base + j);
+            rk++;
+          }
+        }
+      }
+    }
+    __syncthreads();  // the table is complete; the selection scratch is no longer read
+    if (scorer)
+      for (int t = tid; t < nt; t += 4 * 64)
+        if (ids_s[t] >= 0) last = t;
   } else if (MAXROWS <= 4 * 64 || nt <= 4 * 64) {
     if (scorer) {
       for (int t = tid; t < nt; t += 4 * 64) {
@@ -602,17 +666,17 @@ __global__ __launch_bounds__(768) void attn_decode_kernel(
   copy_out();
 }
 
-template <int D, int NBUF, int MAXROWS, bool FP8, bool IMPL = false>
+template <int D, int NBUF, int MAXROWS, bool FP8, bool IMPL = false, int SELPER = 0>
 int launch6(int nsplit, int rows_per_split, const void* q, RowSrc src, const float* sink, const int32_t* idx,
             int64_t T, int64_t B, int64_t S, int64_t H, float scale, void* out, int out_dtype, float* part,
-            hipStream_t stream, ImplicitRows ir) {
+            hipStream_t stream, ImplicitRows ir, SelectRows sr = SelectRows{}) {
   using G = Geo6<D, NBUF, MAXROWS>;
-  auto kern = attn_decode_kernel<D, NBUF, MAXROWS, FP8, IMPL>;
+  auto kern = attn_decode_kernel<D, NBUF, MAXROWS, FP8, IMPL, SELPER>;
   static std::atomic<uint64_t> lds_attr{0};  // devices whose limit is raised
   if (hipError_t e = smla_set_dynamic_lds((const void*)kern, G::LDS_BYTES, lds_attr); e != hipSuccess) return (int)e;
   dim3 grid((unsigned)nsplit, (unsigned)(B * S), (unsigned)((H + 63) / 64));
   hipLaunchKernelGGL(kern, grid, dim3(G::NW * 64), G::LDS_BYTES, stream, (const uint16_t*)q, src, sink, idx, (int)T,
-                     (int)S, (int)H, rows_per_split, scale, part, out, out_dtype, ir);
+                     (int)S, (int)H, rows_per_split, scale, part, out, out_dtype, ir, sr);
   SMLA_HIP_CHECK_LAUNCH();
   return SMLA_OK;
 }
@@ -624,7 +688,26 @@ int launch6(int nsplit, int rows_per_split, const void* q, RowSrc src, const flo
 // long single-sequence lists)
 int launch_decode_v6(int D, bool kv_fp8, int nsplit, int rows_per_split, const void* q, RowSrc src,
                      const float* sink, const int32_t* idx, int64_t T, int64_t B, int64_t S, int64_t H, float scale,
-                     void* out, int out_dtype, float* part, hipStream_t stream, ImplicitRows ir) {
+                     void* out, int out_dtype, float* part, hipStream_t stream, ImplicitRows ir,
+                     SelectRows sr) {
+  // decode lists selected in the kernel (SelectRows): bf16 rows, short splits (the 4-slot ring)
+  if (sr.enabled) {
+    const int per = select_per(sr.N);
+    if (kv_fp8 || per == 0 || rows_per_split > kDecodeV6ShortRows || rows_per_split % kTileRows != 0 ||
+        B * S > 65535 || T != (int64_t)sr.window + sr.k)
+      return SMLA_E_UNSUPPORTED;
+#define SMLA_V6S(DD, P)                                                                                            \
+  return launch6<DD, 4, kDecodeV6ShortRows, false, false, P>(nsplit, rows_per_split, q, src, sink, nullptr, T, B, S, \
+                                                             H, scale, out, out_dtype, part, stream, ir, sr);
+    if (D == 576) {
+      if (per == 12) SMLA_V6S(576, 12) else SMLA_V6S(576, 24)
+    }
+    if (D == 512) {
+      if (per == 12) SMLA_V6S(512, 12) else SMLA_V6S(512, 24)
+    }
+#undef SMLA_V6S
+    return SMLA_E_UNSUPPORTED;
+  }
   // prefill with implicit row sets: no index table (any list length), one split per query; the
   // 3-slot ring (a 4th slot measured slower: 0.46 vs 0.45 ms over the 4096-query prompt)
   if (ir.enabled) {

@@ -33,6 +33,9 @@ _SIGNATURES = {
                                         _i64, _i64, _i64, _i64, _i64, _f32, _vp, _int, _vp]),
     "smla_prefill_attn": (_int, [_vp, _int, _vp, _i64, _vp, _i64, _int, _vp, _i64, _i64, _i64, _i64, _i64, _i64,
                                  _i64, _i64, _f32, _vp, _int, _vp]),
+    "smla_decode_attn_workspace": (_sz, [_i64, _i64, _i64, _i64, _i64, _i64, _i64, _int, _int, _int]),
+    "smla_decode_attn": (_int, [_vp, _int, _vp, _i64, _vp, _i64, _int, _vp, _vp, _i64, _vp, _vp, _i64, _i64, _i64,
+                                _i64, _i64, _i64, _i64, _f32, _vp, _int, _vp, _sz, _vp]),
     "smla_window_topk_idxs": (_int, [_i64, _i64, _i64, _i64, _vp, _vp]),
     "smla_decode_window_idxs": (_int, [_vp, _i64, _i64, _vp, _i64, _vp]),
     "smla_indexer_score": (_int, [_vp, _int, _vp, _int, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64,

@@ -551,6 +551,51 @@ def select_decode_into(scores, k, pos, window, out, id_offset=0, nvis=None):
     return out
 
 
+def decode_attn_workspace(B, S, H, D, dv, window, k, q_dtype=torch.bfloat16, kv_dtype=torch.bfloat16,
+                          out_dtype=torch.bfloat16):
+    """Bytes of workspace smla_decode_attn needs."""
+    return int(_lib.lib().smla_decode_attn_workspace(B, S, H, D, dv, window, k, _DT[q_dtype], _DT[kv_dtype],
+                                                      _YDT_ATTN[out_dtype]))
+
+
+def decode_attn_into(q, kv_raw, kv_comp, attn_sink, scores, nvis, pos, window, k, scale, dv, out, workspace):
+    """The decode index build and the attention over it in one call (smla_decode_attn): q [B,S,H,D],
+    kv_raw [B,n_raw,D], kv_comp [B,n_comp,D], attn_sink [H]|None, scores [B*S, N] fp32, nvis
+    [B*S]|None, pos [B*S] int32, out [B,S,H,dv] (bf16 or fp32), workspace a uint8 tensor of at least
+    decode_attn_workspace(...) bytes.  Same output as select_decode_into + sparse_attn_two_source."""
+    _on_gpu(q, kv_raw, kv_comp, attn_sink, scores, nvis, pos, out, workspace)
+    if q.dim() != 4 or kv_raw.dim() != 3 or kv_comp.dim() != 3 or scores.dim() != 2:
+        raise ValueError("expected q [B,S,H,D], kv_raw / kv_comp [B,n,D], scores [B*S,N]")
+    B, S, H, D = q.shape
+    for name, kv in (("kv_raw", kv_raw), ("kv_comp", kv_comp)):
+        if kv.shape[0] != B or kv.shape[2] != D:
+            raise ValueError(f"{name} {tuple(kv.shape)} does not match q {tuple(q.shape)}")
+    if kv_comp.dtype != kv_raw.dtype:
+        raise TypeError("kv_raw and kv_comp must share a dtype")
+    R, N = scores.shape
+    if R != B * S or scores.dtype != torch.float32:
+        raise ValueError(f"scores must be fp32 [{B * S}, N], got {tuple(scores.shape)} {scores.dtype}")
+    if tuple(pos.shape) != (R,) or (nvis is not None and tuple(nvis.shape) != (R,)):
+        raise ValueError("pos (and nvis) must be [B*S]")
+    if attn_sink is not None and tuple(attn_sink.shape) != (H,):
+        raise ValueError(f"attn_sink {tuple(attn_sink.shape)} must be [{H}]")
+    if tuple(out.shape) != (B, S, H, dv) or out.dtype not in _YDT_ATTN or not out.is_contiguous():
+        raise ValueError(f"out must be a contiguous [{B},{S},{H},{dv}] bf16 or fp32 tensor")
+    need = decode_attn_workspace(B, S, H, D, dv, window, k, q.dtype, kv_raw.dtype, out.dtype)
+    if workspace.dtype != torch.uint8 or workspace.numel() < need:
+        raise ValueError(f"workspace must be a uint8 tensor of at least {need} bytes")
+    q, kv_raw, kv_comp, scores = q.contiguous(), kv_raw.contiguous(), kv_comp.contiguous(), scores.contiguous()
+    if attn_sink is not None:
+        attn_sink = attn_sink.float().contiguous()
+    if nvis is not None:
+        nvis = nvis.to(torch.int32).contiguous()
+    pos = pos.to(torch.int32).contiguous()
+    _lib.call("smla_decode_attn", _p(q), dtype_code(q), _p(kv_raw), kv_raw.shape[1], _p(kv_comp), kv_comp.shape[1],
+              dtype_code(kv_raw), _p(attn_sink), _p(scores), N, _p(nvis), _p(pos), int(window), int(k), B, S, H, D,
+              dv, float(scale), _p(out), _YDT_ATTN[out.dtype], _p(workspace), workspace.numel(), _stream(q))
+    return out
+
+
 def index_decode_workspace(B, S, N):
     """Bytes of workspace smla_index_decode needs for B*S query rows over N keys."""
     return int(_lib.lib().smla_index_decode_workspace(B, S, N))

@@ -8,6 +8,9 @@
 * ``sparse_attn_batched`` / ``sparse_attn_two_source`` — the same op over a batch of caches and
   over the engine's virtual [window; compressed] buffer (``oracle/decode_engine.py:108-115``)
   without building the concatenation.
+* ``prefill_attn`` — the prompt's per-position loop (``oracle/decode_engine.py:107-117``) with the
+  row sets computed on the device; ``decode_attn`` — the decode index build over indexer scores
+  and the attention over it (``oracle/decode_engine.py:110-117``) in one call.
 
 Everything runs in libsmla's HIP kernels; tensors must live on the GPU.
 """
@@ -58,3 +61,21 @@ def sparse_attn_two_source(q, kv0, kv1, attn_sink, topk_idxs, scale, dv=None, kv
     """Ids index the virtual concatenation [kv0; kv1] along rows (per batch entry)."""
     dv = q.shape[-1] if dv is None else dv
     return ops.sparse_attn_op(q, kv0, kv1, kv0_scale, kv1_scale, attn_sink, topk_idxs, float(scale), dv)
+
+
+def decode_attn(q, kv_raw, kv_comp, attn_sink, scores, pos, window, k, scale, dv=512, nvis=None, out=None,
+                workspace=None):
+    """Decode attention over the index list ``select_decode_indices(scores, k, pos, window, n_raw,
+    nvis)`` builds, without the list going through memory when the shape allows (the attention
+    workgroups select the rows themselves) -- the same output, bit for bit, as that list followed by
+    ``sparse_attn_two_source``.  q [B,1,H,D] (or [B,S,H,D] with scores/pos of B*S rows), kv_raw
+    [B,n_raw,D], kv_comp [B,n_comp,D], scores [B*S,N] fp32, pos [B*S] int32 -> [B,S,H,dv]."""
+    B, S, H, D = q.shape
+    if out is None:
+        out = torch.empty(B, S, H, dv, dtype=q.dtype if q.dtype in (torch.bfloat16, torch.float32) else torch.float32,
+                          device=q.device)
+    if workspace is None:
+        workspace = torch.empty(ops.decode_attn_workspace(B, S, H, D, dv, window, k, q.dtype, kv_raw.dtype,
+                                                          out.dtype), dtype=torch.uint8, device=q.device)
+    return ops.decode_attn_into(q, kv_raw, kv_comp, attn_sink, scores, nvis, pos, window, k, scale, dv, out,
+                                workspace)

@@ -13,6 +13,7 @@
  *                             v4mlx/sparse_attn.py:26-39       (MLX twin)
  *   smla_sparse_attn_ex       ref_torch/sparse_attn.py:23-34   (the same, with an explicit split plan / phases)
  *   smla_prefill_attn         oracle/decode_engine.py:107-117  per-position prompt attention (row sets on device)
+ *   smla_decode_attn          oracle/decode_engine.py:110-117  decode index build + attention (indexer-ranked cidx)
  *   smla_window_topk_idxs     ref_torch/sparse_attn.py:9-20    get_window_topk_idxs(window_size, bsz, seqlen, start_pos)
  *   smla_decode_window_idxs   oracle/decode_engine.py:110-111  widx = range(max(0, p-127), p+1)
  *   smla_indexer_score        (none: the reference attends every visible compressed row,
@@ -170,6 +171,30 @@ int smla_prefill_attn(const void* q, int q_dtype, const void* kv_raw, int64_t n_
                       int64_t q_pos0, int64_t window, int64_t ratio, int64_t B, int64_t S,
                       int64_t H, int64_t D, int64_t DV, float scale, void* out, int out_dtype,
                       void* stream);
+
+/* ---------------------------------------------------------------------------------------------
+ * Decode attention over the engine's index build in one call.  Replaces
+ * oracle/decode_engine.py:110-117 (widx + cidx, then sparse_attn over [window; compressed]) with
+ * the compressed part ranked by indexer scores: query row r (of R = B*S) attends
+ *   raw rows pos[r]-window+1 .. pos[r] (those >= 0)  (ids 0 .. n_raw-1)
+ *   the min(k, nvis[r]) best of scores[r, 0 .. nvis[r]-1] (score descending, index ascending,
+ *   -0 == +0), compressed row c as id n_raw + c
+ * i.e. the list smla_select_decode(scores, R, N, nvis, k, pos, window, ids, window+k, n_raw)
+ * writes, followed by smla_sparse_attn(q, kv_raw, n_raw, kv_comp, n_comp, ..., ids, window+k).
+ * The output equals that pair's bit for bit.  With bf16 rows, the short-split plan and
+ * N <= 18432, the attention workgroups run the selection themselves (no list in memory, one
+ * launch fewer); otherwise the list is built in the workspace first.
+ *   q [B,S,H,D] BF16, kv_raw [B,n_raw,D], kv_comp [B,n_comp,D] BF16 (or F32 / F16: list path),
+ *   scores [R,N] F32, nvis [R] int32 or NULL (all N), pos [R] int32, out [B,S,H,DV] BF16 or F32.
+ * workspace: smla_decode_attn_workspace(B, S, H, D, DV, window, k, q_dtype, kv_dtype, out_dtype)
+ * bytes.  Requires N <= 65536. */
+size_t smla_decode_attn_workspace(int64_t B, int64_t S, int64_t H, int64_t D, int64_t DV, int64_t window,
+                                  int64_t k, int q_dtype, int kv_dtype, int out_dtype);
+int smla_decode_attn(const void* q, int q_dtype, const void* kv_raw, int64_t n_raw, const void* kv_comp,
+                     int64_t n_comp, int kv_dtype, const float* attn_sink, const float* scores, int64_t N,
+                     const int32_t* nvis, const int32_t* pos, int64_t window, int64_t k, int64_t B,
+                     int64_t S, int64_t H, int64_t D, int64_t DV, float scale, void* out, int out_dtype,
+                     void* workspace, size_t workspace_bytes, void* stream);
 
 /* ---------------------------------------------------------------------------------------------
  * Window index matrix.  Replaces ref_torch/sparse_attn.py:9-20 (get_window_topk_idxs).
