@@ -280,12 +280,12 @@ __global__ __launch_bounds__(768) void attn_decode_kernel(
         uint32_t Kt;
         int It;
         smla_select::row_threshold<SELPER, 768>(fv, nloc, base, nv, sr.k, sm, key, Kt, It);
-        const uint64_t selm = smla_select::selected_mask<SELPER>(key, nloc, base, Kt, It);
+        const auto selm = smla_select::selected_mask<SELPER>(key, nloc, base, Kt, It);
         int tot;
-        int rk = smla_select::block_excl_scan<12>(__builtin_popcountll(selm), sm.tmp, &tot);
+        int rk = smla_select::block_excl_scan<12>(smla_select::sel_count<SELPER>(selm), sm.tmp, &tot);
 #pragma unroll
         for (int j = 0; j < SELPER; j++) {
-          if ((selm >> j) & 1ull) {
+          if ((selm >> j) & 1u) {
             if (rk >= lo && rk < hi) ids_s[sr.window + rk - t_begin] = valid(n0 + base + j);
             rk++;
           }

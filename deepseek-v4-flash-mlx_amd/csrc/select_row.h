@@ -5,18 +5,20 @@
 // (monotone value buckets, exact ranking of the boundary bucket) or, for degenerate spreads, 4
 // radix passes plus a tie rank: only comparisons and counts, so the result is exact.
 #pragma once
+#include <type_traits>
+
 #include "smla_internal.h"
 
 namespace smla_select {
 
 constexpr int kMaxCand = 256;  // boundary-bucket entries ranked exactly (more: the radix path)
 
-// order-preserving key (larger score -> smaller key; -0 folded to +0) and its inverse
+// order-preserving key (larger score -> smaller key; -0 folded to +0): a non-negative score's bits
+// with the 31 low bits inverted, a negative score's bits as they are
 __device__ inline uint32_t desc_key(float f) {
-  if (f == 0.f) f = 0.f;  // -0 -> +0
   uint32_t u = __float_as_uint(f);
-  uint32_t asc = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-  return ~asc;
+  u = u == 0x80000000u ? 0u : u;                              // -0 -> +0
+  return u ^ (~(uint32_t)((int32_t)u >> 31) & 0x7fffffffu);  // sign clear: flip bits 0..30
 }
 
 // exclusive scan of one value per thread over a block of NW waves; returns the exclusive prefix
@@ -279,16 +281,23 @@ __device__ inline void row_threshold(const float (&fv)[PER], int nloc, int base,
   }
 }
 
-// this thread's selected entries as a bit mask (PER <= 64)
+// this thread's selected entries as a bit mask (PER <= 64; 32-bit for PER <= 32)
 template <int PER>
-__device__ inline uint64_t selected_mask(const uint32_t (&key)[PER], int nloc, int base, uint32_t Kt, int It) {
-  uint64_t selm = 0;
+using SelMask = typename std::conditional<(PER <= 32), uint32_t, uint64_t>::type;
+template <int PER>
+__device__ inline SelMask<PER> selected_mask(const uint32_t (&key)[PER], int nloc, int base, uint32_t Kt, int It) {
+  SelMask<PER> selm = 0;
 #pragma unroll
   for (int j = 0; j < PER; j++) {
     const bool sel = j < nloc && (key[j] < Kt || (key[j] == Kt && base + j <= It));
-    selm |= (uint64_t)sel << j;
+    selm |= (SelMask<PER>)sel << j;
   }
   return selm;
+}
+template <int PER>
+__device__ inline int sel_count(SelMask<PER> m) {
+  if constexpr (PER <= 32) return __builtin_popcount(m);
+  else return __builtin_popcountll(m);
 }
 
 }  // namespace smla_select

@@ -80,12 +80,12 @@ __global__ __launch_bounds__(NT) void topk_kernel(const float* scores, int64_t N
   smla_select::row_threshold<PER, NT>(fv, nloc, base, nv, k, sm, key, Kt, It);
   // ---- emit the selected ids in ascending order; ids go straight to their output positions
   // (each wave's selected ids fill one contiguous run)
-  const uint64_t selm = smla_select::selected_mask<PER>(key, nloc, base, Kt, It);
+  const auto selm = smla_select::selected_mask<PER>(key, nloc, base, Kt, It);
   int tot_sel;
-  int pos = block_excl_scan<kWaves>(__builtin_popcountll(selm), sm.tmp, &tot_sel);
+  int pos = block_excl_scan<kWaves>(smla_select::sel_count<PER>(selm), sm.tmp, &tot_sel);
 #pragma unroll
   for (int j = 0; j < PER; j++) {
-    if ((selm >> j) & 1ull) {
+    if ((selm >> j) & 1u) {
       if (pos < take) orow[pos] = (int32_t)(base + j) + id_offset;
       pos++;
     }
