@@ -46,6 +46,10 @@ def _check_linear(got, x, w, G, out_dtype):
     (16, 2, 64, 1024, torch.bfloat16),       # short K slices: the guarded last batch
     (17, 1, 128, 512, torch.float32),        # two token tiles, one ragged
     (32, 4, 32, 2048, torch.bfloat16),
+    # the LDS form over 8192 rows: 2 and 4 waves, one wave with K = 512
+    (5, 1, 8192, 1024, torch.float32),
+    (8, 4, 2048, 2048, torch.bfloat16),
+    (2, 1, 8192, 512, torch.float32),
     # the tiled MFMA GEMM
     (64, 1, 1024, 4096, torch.float32),
     (4096, 1, 1024, 4096, torch.bfloat16),     # prefill's q_down
