@@ -178,8 +178,7 @@ __global__ __launch_bounds__(64 * kLinWaves) void linear_kernel(
 // counts in order, so the weights stay in flight while x is written to LDS); x rows are padded by
 // 16 bytes so that the 16 token rows read by one b128 pass fall in distinct banks.  Per-lane x
 // registers drop from 64 VGPRs to 8 (16 with STEPS = 16), so two workgroups fit on a CU for
-// K = 4096.  Weights are read once per call and load non-temporally, leaving L2 to x, which every
-// workgroup copies whole.
+// K = 4096.
 constexpr int kLdsMaxBytes = 160 * 1024;
 
 template <int TX, bool ROPE, int YDT, int STEPS>
@@ -214,8 +213,8 @@ __global__ __launch_bounds__(STEPS == 16 ? 512 : 1024) void linear_lds_kernel(
   u32x4_t wv[STEPS][2];
 #pragma unroll
   for (int s = 0; s < STEPS; s++) {
-    wv[s][0] = __builtin_nontemporal_load((const u32x4_t*)(wp + s * 64));
-    wv[s][1] = __builtin_nontemporal_load((const u32x4_t*)(wp + s * 64 + 32));
+    wv[s][0] = *(const u32x4_t*)(wp + s * 64);
+    wv[s][1] = *(const u32x4_t*)(wp + s * 64 + 32);
   }
   __builtin_amdgcn_sched_barrier(0);  // every weight load issued before the first wait for x
   // 3. x into LDS, all TX rows (rows past T repeat row T-1 and are not read); a guard here would
