@@ -334,15 +334,24 @@ def other_workloads(dev, reps):
 
 
 def _cpu_model():
-    """The host CPU's model name (first `model name` line of /proc/cpuinfo), or None."""
+    """The host CPU as /proc/cpuinfo names it: the first `model name` line with the cpu family,
+    model and stepping numbers (virtual machines often shorten the name to the vendor line), or
+    None."""
+    fields = {}
     try:
         with open("/proc/cpuinfo") as f:
             for line in f:
-                if line.startswith("model name"):
-                    return line.split(":", 1)[1].strip()
+                if not line.strip():
+                    break  # the first processor's block
+                key, _, val = line.partition(":")
+                fields.setdefault(key.strip(), val.strip())
     except OSError:
-        pass
-    return None
+        return None
+    name = fields.get("model name")
+    if name is None:
+        return None
+    ids = [f"{k} {fields[k]}" for k in ("cpu family", "model", "stepping") if k in fields]
+    return f"{name} ({', '.join(ids)})" if ids else name
 
 
 def cpu_baseline(w, nthreads, reps):
