@@ -215,7 +215,15 @@ __global__ __launch_bounds__(256) void indexer_kernel(const void* __restrict__ q
 // 0..3, so the running sum crosses between the two halves with a lane swap every four heads (the
 // weights are wave-uniform scalars).  One tile per wave and two waves per SIMD (4-wave workgroups
 // of 128 keys) measured faster than two interleaved tiles per wave at one wave per SIMD.
-template <int KDT, int QDT>
+//
+// KT = 16: tiles of 64 heads x 16 keys on v_mfma_f32_16x16x1_4b_f32 (also one rounding per product:
+// checked against fmaf over 1.7e7 triples), for rows too few to give every CU a 128-key workgroup.
+// A dependent step takes about 0.6 of the 32-key step, so a wave's chain ends sooner, at 0.8 of the
+// 32-key form's throughput per product.  Block b takes heads 16b..16b+15 from lanes 16b..16b+15
+// (h = lane again) and the key n = lane mod 16; register j of lane l holds head 16 (j / 4) + 4 (l / 16)
+// + j mod 4.  The head chain walks the 16-lane rows: after the four heads of row g, every row takes
+// row g's sum (two lane swaps).
+template <int KDT, int QDT, int KT = 32>
 __global__ __launch_bounds__(256) void indexer_mfma_kernel(const void* __restrict__ q, const void* __restrict__ keys,
                                                        const uint8_t* __restrict__ kbs,
                                                        const float* __restrict__ kscale,
@@ -223,7 +231,8 @@ __global__ __launch_bounds__(256) void indexer_mfma_kernel(const void* __restric
                                                        const int32_t* __restrict__ nvis, int64_t S, int64_t N,
                                                        float* __restrict__ scores) {
   constexpr int DI = 64;
-  constexpr int KEYS = 4 * 32;  // keys per workgroup: 4 waves x one tile of 32 keys
+  static_assert(KT == 32 || KT == 16, "key tiles of 32 or 16");
+  constexpr int KEYS = 4 * KT;  // keys per workgroup: 4 waves x one tile of KT keys
   {
     const uint32_t gx = gridDim.x, gy = gridDim.y, gz = gridDim.z;
     asm volatile("" ::"s"(gx), "s"(gy), "s"(gz), "s"(q), "s"(keys), "s"(kbs), "s"(kscale), "s"(weights), "s"(nvis),
@@ -233,15 +242,15 @@ __global__ __launch_bounds__(256) void indexer_mfma_kernel(const void* __restric
   xcd_row_item(gridDim.y, gridDim.x, bs, chunk);
   const int64_t b = batch_of(bs, S);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int64_t kb = chunk * KEYS + wave * 32;  // first key of this wave's tile
+  const int64_t kb = chunk * KEYS + wave * KT;  // first key of this wave's tile
   const int64_t nv = nvis ? (int64_t)nvis[bs] : N;
 
-  // the row of key kb + lane mod 32 in its storage type, then the q row of head `lane`
+  // the row of key kb + lane mod KT in its storage type, then the q row of head `lane`
   constexpr int KW = KDT == kFp4 ? 2 : KDT == SMLA_FP8_E4M3 ? 4 : (KDT == SMLA_BF16 ? 8 : 16);
   u32x4_t kr[KW];
   uint32_t ksb = 0;  // fp4: the row's two scale bytes
   {
-    const int64_t n = kb + (lane & 31);
+    const int64_t n = kb + (lane & (KT - 1));
     const int64_t row = b * N + (n < N ? n : N - 1);
     const u32x4_t* pk = (const u32x4_t*)((const uint8_t*)keys + row * DI * KW / 4);
 #pragma unroll
@@ -301,16 +310,22 @@ __global__ __launch_bounds__(256) void indexer_mfma_kernel(const void* __restric
         for (int j = 0; j < 4; j++) o[4 * v + j] = __uint_as_float(row[4 * db + v][j]);
     }
   };
-  f32x32_t acc;
+  using Acc = typename std::conditional<KT == 32, f32x32_t, f32x16_t>::type;
+  Acc acc;
 #pragma unroll
-  for (int r = 0; r < 32; r++) acc[r] = 0.f;
+  for (int r = 0; r < KT; r++) acc[r] = 0.f;
   auto run = [&](auto fold) {
 #pragma unroll
     for (int db = 0; db < 4; db++) {
       float x[16];
       block16(db, x, fold);
 #pragma unroll
-      for (int dd = 0; dd < 16; dd++) acc = __builtin_amdgcn_mfma_f32_32x32x1f32(qf[16 * db + dd], x[dd], acc, 0, 0, 0);
+      for (int dd = 0; dd < 16; dd++) {
+        if constexpr (KT == 32)
+          acc = __builtin_amdgcn_mfma_f32_32x32x1f32(qf[16 * db + dd], x[dd], acc, 0, 0, 0);
+        else
+          acc = __builtin_amdgcn_mfma_f32_16x16x1f32(qf[16 * db + dd], x[dd], acc, 0, 0, 0);
+      }
     }
   };
   if constexpr (KDT == kFp4) {
@@ -325,21 +340,41 @@ __global__ __launch_bounds__(256) void indexer_mfma_kernel(const void* __restric
   // four heads in lanes 0..31 the swap hands every lane the low half's sum ([0]); after four in
   // lanes 32..63, the high half's ([1]).
   float sum = 0.f;
+  if constexpr (KT == 32) {
 #pragma unroll
-  for (int tt = 0; tt < 8; tt++) {
-    const int R = 16 * (tt >> 2) + 4 * (tt & 3);
-    float r[4];
+    for (int tt = 0; tt < 8; tt++) {
+      const int R = 16 * (tt >> 2) + 4 * (tt & 3);
+      float r[4];
 #pragma unroll
-    for (int rr = 0; rr < 4; rr++) r[rr] = acc[R + rr] > 0.f ? acc[R + rr] : 0.f;
+      for (int rr = 0; rr < 4; rr++) r[rr] = acc[R + rr] > 0.f ? acc[R + rr] : 0.f;
 #pragma unroll
-    for (int rr = 0; rr < 4; rr++) sum = __builtin_fmaf(wrow[8 * tt + rr], r[rr], sum);
-    sum = __uint_as_float(__builtin_amdgcn_permlane32_swap(__float_as_uint(sum), __float_as_uint(sum), false, false)[0]);
+      for (int rr = 0; rr < 4; rr++) sum = __builtin_fmaf(wrow[8 * tt + rr], r[rr], sum);
+      sum = __uint_as_float(__builtin_amdgcn_permlane32_swap(__float_as_uint(sum), __float_as_uint(sum), false, false)[0]);
 #pragma unroll
-    for (int rr = 0; rr < 4; rr++) sum = __builtin_fmaf(wrow[8 * tt + 4 + rr], r[rr], sum);
-    sum = __uint_as_float(__builtin_amdgcn_permlane32_swap(__float_as_uint(sum), __float_as_uint(sum), false, false)[1]);
+      for (int rr = 0; rr < 4; rr++) sum = __builtin_fmaf(wrow[8 * tt + 4 + rr], r[rr], sum);
+      sum = __uint_as_float(__builtin_amdgcn_permlane32_swap(__float_as_uint(sum), __float_as_uint(sum), false, false)[1]);
+    }
+  } else {
+    // heads 16bk + 4g .. +3 sit in row g = lane / 16, registers 4bk .. 4bk+3: each row adds its
+    // four onto the running sum, then every row takes row g's result (permlane16_swap gives the
+    // even or odd rows over each pair, permlane32_swap the low or high pair over both halves)
+#pragma unroll
+    for (int bk = 0; bk < 4; bk++) {
+      float r[4];
+#pragma unroll
+      for (int rr = 0; rr < 4; rr++) r[rr] = acc[4 * bk + rr] > 0.f ? acc[4 * bk + rr] : 0.f;
+#pragma unroll
+      for (int g = 0; g < 4; g++) {
+#pragma unroll
+        for (int rr = 0; rr < 4; rr++) sum = __builtin_fmaf(wrow[16 * bk + 4 * g + rr], r[rr], sum);
+        const uint32_t y =
+            __builtin_amdgcn_permlane16_swap(__float_as_uint(sum), __float_as_uint(sum), false, false)[g & 1];
+        sum = __uint_as_float(__builtin_amdgcn_permlane32_swap(y, y, false, false)[g >> 1]);
+      }
+    }
   }
   const int64_t n = kb + lane;
-  if (lane < 32 && n < N) scores[bs * N + n] = n < nv ? (kscale ? sum * kscale[b * N + n] : sum) : -SMLA_INF;
+  if (lane < KT && n < N) scores[bs * N + n] = n < nv ? (kscale ? sum * kscale[b * N + n] : sum) : -SMLA_INF;
 }
 
 // Hi > 64: one thread per key, sequential over all heads (same arithmetic order)
@@ -383,14 +418,19 @@ template <int DI, int KDT>
 int launch_k(const void* q, int q_dtype, const void* keys, const uint8_t* kbs, const float* kscale, const float* w,
              const int32_t* nvis, int64_t B, int64_t S, int64_t Hi, int64_t N, float* scores, hipStream_t st) {
   if (Hi == 64 && DI == 64) {
-    // 128 keys per workgroup (a 64-head x 32-key tile per wave)
-    const dim3 grid((unsigned)((N + 127) / 128), (unsigned)(B * S));
-    if (q_dtype == SMLA_BF16)
-      hipLaunchKernelGGL((indexer_mfma_kernel<KDT, SMLA_BF16>), grid, dim3(256), 0, st, q, keys, kbs, kscale, w, nvis, S,
-                         N, scores);
-    else
-      hipLaunchKernelGGL((indexer_mfma_kernel<KDT, SMLA_F32>), grid, dim3(256), 0, st, q, keys, kbs, kscale, w, nvis, S,
-                         N, scores);
+    // 128 keys per workgroup (a 64-head x 32-key tile per wave), or 64 (16-key tiles) when 128-key
+    // workgroups would leave CUs idle
+    const bool k16 = (N + 127) / 128 * B * S < smla_num_cus();
+    const dim3 grid((unsigned)(k16 ? (N + 63) / 64 : (N + 127) / 128), (unsigned)(B * S));
+#define SMLA_IDX_MFMA(QT, KTT)                                                                                  \
+  hipLaunchKernelGGL((indexer_mfma_kernel<KDT, QT, KTT>), grid, dim3(256), 0, st, q, keys, kbs, kscale, w, nvis, S, \
+                     N, scores)
+    if (q_dtype == SMLA_BF16) {
+      if (k16) SMLA_IDX_MFMA(SMLA_BF16, 16); else SMLA_IDX_MFMA(SMLA_BF16, 32);
+    } else {
+      if (k16) SMLA_IDX_MFMA(SMLA_F32, 16); else SMLA_IDX_MFMA(SMLA_F32, 32);
+    }
+#undef SMLA_IDX_MFMA
   } else if (Hi <= 64) {
     dim3 grid((unsigned)((N + kKeys - 1) / kKeys), (unsigned)(B * S));
     const int threads = (int)(((Hi + kHG - 1) / kHG) * 64);
