@@ -306,6 +306,23 @@ def other_workloads(dev, reps):
                      "peak_gbs": HBM_PEAK_GBS}
     del graph, wts
 
+    # ---- prompt-size projections through the tiled MFMA GEMM (smla_linear beyond 32 token rows):
+    # 4096 tokens, bf16 operands; MFMA utilisation against the dense bf16 peak
+    gemm = {}
+    for name, T, G, N, K, odt in (("q_down", 4096, 1, 1024, 4096, torch.float32),
+                                  ("wq_b_wkv", 4096, 1, 8192, 4096, torch.float32),
+                                  ("wo_a_grouped", 4096, 8, 1024, 4096, torch.bfloat16),
+                                  ("wo_b", 4096, 1, 4096, 8192, torch.bfloat16)):
+        x = (torch.randn(T, G * K, device=dev) * 0.1).to(torch.bfloat16)
+        wm = (torch.randn(G * N, K, device=dev) * 0.02).to(torch.bfloat16)
+        ms = _time_graph_ms(lambda: ops.linear_op(x, wm, G, odt), max(4, reps // 4))
+        fl = 2.0 * T * G * N * K
+        gemm[name] = {"shape": f"[{T},{G * K}] x [{G * N},{K}]^T" + (f" in {G} groups" if G > 1 else ""),
+                      "us": round(ms * 1e3, 2), "tflops": round(fl / (ms * 1e-3) / 1e12, 1),
+                      "mfma_util": round(fl / (ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4)}
+        del x, wm
+    res["prefill_gemm"] = gemm
+
     # ---- decode_layer: the whole attention layer for one token (projections, RoPE, fp8 sim, window
     # append, compressor ring, take-all ids, attention, output projection), 8 sequences at position
     # 32767 over filled 32K caches; a graph of 5 steps (each rewrites the same cache rows)

@@ -17,6 +17,21 @@
 // holds the last rd = 64 dims of a head has its (x0, x1) pairs rotated back to position 0 while it
 // is loaded (inverse RoPE at pos[t], every product and sum rounded in float32, then bf16), the
 // arithmetic of smla_rope.
+//
+// Large bf16 products (gemm_dma_kernel: enough 256 x 256 tiles for every CU, K a multiple of 64):
+// 8 waves per workgroup, each a 128 x 64 quarter-octant as 4 x 2 blocks of
+// v_mfma_f32_32x32x16_bf16.  Operands go HBM -> LDS by global_load_lds_dwordx4 (no register
+// staging) into a ring of two 64 KB stages; a K step (64 k) is 32 MFMAs per wave, two waves per
+// SIMD, long enough to cover the next step's copies, with one barrier per step.  A copy
+// instruction lands 64 x 16 bytes contiguously (8 rows of 128 bytes), so the rows cannot be
+// padded: chunk c of row r is stored in slot c ^ ((r / 2) mod 8) instead, so that the fragment
+// reads of 16 consecutive rows (two rows per 256-byte bank cycle) fall in distinct banks.  A
+// 128 x 128 tile per workgroup with register staging (gemm_kernel) moves twice the operand bytes
+// per product through LDS and had only 16 MFMAs per step to hide its next loads: 370-660 TFLOP/s
+// on the prompt-size projections against 1.0-1.2 PFLOP/s here.  Measured and not kept: the same
+// tile with register-staged operands (0.98-1.04), a 4-stage ring of 32-k steps (0.98-1.02),
+// fragments of the next sub-step read ahead of the MFMAs (equal).
+#include "attn_common.h"
 #include "smla_internal.h"
 
 namespace {
@@ -199,6 +214,134 @@ __global__ __launch_bounds__(256) void gemm_kernel(const uint8_t* __restrict__ x
     }
 }
 
+constexpr int kBig = 256;                              // tile rows (tokens) and columns (outputs)
+constexpr int kOperandBytes = kBig * kRowBytes;        // one operand's rows of one K step: 32 KB
+constexpr int kStageBytes = 2 * kOperandBytes;         // A then B
+constexpr int kCopiesPerWave = kStageBytes / 1024 / 8;  // 1 KB copy instructions per wave per stage
+
+template <int YDT, bool ROPE>
+__global__ __launch_bounds__(512) void gemm_dma_kernel(const uint8_t* __restrict__ x, int64_t ldx,
+                                                       const uint8_t* __restrict__ w, int T, int N, int K, int ntn,
+                                                       const int32_t* __restrict__ pos, const float* __restrict__ cos_t,
+                                                       const float* __restrict__ sin_t, int head_dim,
+                                                       void* __restrict__ y, int64_t ldy) {
+  using namespace smla_attn;
+  extern __shared__ __align__(16) uint8_t lds_g[];
+  lds_u8_t* lds = (lds_u8_t*)lds_g;
+  const uint32_t lds_base = (uint32_t)(uintptr_t)lds;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int g = blockIdx.x / ntn;
+  const int n0 = (blockIdx.x % ntn) * kBig;
+  const int t0 = blockIdx.y * kBig;
+  const int wm = wave & 1, wn = wave >> 1;  // 128-row half, 64-column quarter
+  // copy instruction q = 8 wave + i covers stage bytes [1024 q, 1024 q + 1024): rows 8 (q mod 32)
+  // .. +7 of A (q < 32) or of B; lane L takes row + L / 8, slot L mod 8 <- chunk
+  // (L mod 8) ^ ((row / 2) mod 8)
+  const uint8_t* src[kCopiesPerWave];
+#pragma unroll
+  for (int i = 0; i < kCopiesPerWave; i++) {
+    const int q = wave * kCopiesPerWave + i;
+    const int r = 8 * (q & 31) + (lane >> 3);
+    const int c = (lane & 7) ^ ((r >> 1) & 7);
+    if (q < 32) {
+      const int t = min(t0 + r, T - 1);
+      src[i] = x + ((int64_t)t * ldx + (int64_t)g * K) * 2 + 16 * c;
+    } else {
+      const int n = min(n0 + r, N - 1);
+      src[i] = w + ((int64_t)g * N + n) * (int64_t)K * 2 + 16 * c;
+    }
+  }
+  auto issue = [&](int stage, int ks) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < kCopiesPerWave; i++) {
+      const uint32_t ld =
+          __builtin_amdgcn_readfirstlane(lds_base + stage * kStageBytes + (wave * kCopiesPerWave + i) * 1024);
+      dma16(src[i] + (int64_t)ks * kRowBytes, ld);
+    }
+  };
+
+  f32x16_t_g acc[4][2];
+#pragma unroll
+  for (int mb = 0; mb < 4; mb++)
+#pragma unroll
+    for (int nb = 0; nb < 2; nb++)
+#pragma unroll
+      for (int r = 0; r < 16; r++) acc[mb][nb][r] = 0.f;
+  // fragment rows of this lane: A row 128 wm + 32 mb + lane % 32, B row 64 wn + 32 nb + lane % 32;
+  // the lane half h holds k 16 kk + 8 h .. +7, chunk 2 kk + h of the row
+  const int r32 = lane & 31, khalf = lane >> 5;
+  // ROPE: the A chunks this thread rotates in a RoPE step, j = tid + 512 i (row j / 8, slot j mod 8),
+  // and their rows' offsets in the cos / sin tables (32 pairs per position)
+  int prow[4] = {0, 0, 0, 0};
+  if constexpr (ROPE) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) prow[i] = pos[min(t0 + ((tid + 512 * i) >> 3), T - 1)] * 32;
+  }
+  const int nk = K / 64;
+  issue(0, 0);
+  for (int ks = 0; ks < nk; ks++) {
+    wait_vm(0);     // this wave's copies of step ks
+    lds_barrier();  // everyone's copies of step ks landed; step ks - 1 is read by every wave
+    if (ks + 1 < nk) issue((ks + 1) & 1, ks + 1);
+    const lds_u8_t* A = lds + (ks & 1) * kStageBytes;
+    const lds_u8_t* B = A + kOperandBytes;
+    if constexpr (ROPE) {
+      // the step holding a head's last 64 dims: every A chunk (4 (x0, x1) pairs, pairs 4c .. 4c + 3
+      // of its row's position, c = slot ^ ((row / 2) mod 8)) rotated back in place, then a barrier
+      if ((ks * 64) % head_dim == head_dim - 64) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          const int j = tid + 512 * i, r = j >> 3, sl = j & 7, c = sl ^ ((r >> 1) & 7);
+          lds_u32x4_t* pa = (lds_u32x4_t*)(lds + (ks & 1) * kStageBytes + r * kRowBytes + 16 * sl);
+          *pa = inv_rope4(*pa, cos_t + prow[i] + 4 * c, sin_t + prow[i] + 4 * c);
+        }
+        lds_barrier();
+      }
+    }
+#pragma unroll
+    for (int kk = 0; kk < 4; kk++) {
+      const int c = 2 * kk + khalf;
+      bf16x8_t a[4], b[2];
+#pragma unroll
+      for (int mb = 0; mb < 4; mb++) {
+        const int r = 128 * wm + 32 * mb + r32;
+        a[mb] = as_bf16x8(*(const lds_u32x4_t*)(A + r * kRowBytes + 16 * (c ^ ((r >> 1) & 7))));
+      }
+#pragma unroll
+      for (int nb = 0; nb < 2; nb++) {
+        const int r = 64 * wn + 32 * nb + r32;
+        b[nb] = as_bf16x8(*(const lds_u32x4_t*)(B + r * kRowBytes + 16 * (c ^ ((r >> 1) & 7))));
+      }
+#pragma unroll
+      for (int mb = 0; mb < 4; mb++)
+#pragma unroll
+        for (int nb = 0; nb < 2; nb++)
+          acc[mb][nb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[mb], b[nb], acc[mb][nb], 0, 0, 0);
+    }
+  }
+
+  // accumulator r of block (mb, nb): token 128 wm + 32 mb + 8 (r / 4) + 4 (lane / 32) + r % 4,
+  // output 64 wn + 32 nb + lane % 32
+#pragma unroll
+  for (int mb = 0; mb < 4; mb++)
+#pragma unroll
+    for (int nb = 0; nb < 2; nb++) {
+      const int n = n0 + 64 * wn + 32 * nb + r32;
+      if (n >= N) continue;
+#pragma unroll
+      for (int r = 0; r < 16; r++) {
+        const int t = t0 + 128 * wm + 32 * mb + 8 * (r >> 2) + 4 * khalf + (r & 3);
+        if (t < T) {
+          const int64_t o = (int64_t)t * ldy + (int64_t)g * N + n;
+          if constexpr (YDT == SMLA_BF16)
+            ((uint16_t*)y)[o] = bf16_rne(acc[mb][nb][r]);
+          else
+            ((float*)y)[o] = acc[mb][nb][r];
+        }
+      }
+    }
+}
+
 }  // namespace
 
 // y [T, G*N] (row stride G*N) = grouped x [T, G*K] (row stride ldx elements) times w [G*N, K]^T.
@@ -208,9 +351,28 @@ __global__ __launch_bounds__(256) void gemm_kernel(const uint8_t* __restrict__ x
 int launch_gemm_tiled(const void* x, int64_t ldx, bool f32_operands, const void* w, int64_t T, int64_t G, int64_t N,
                       int64_t K, const int32_t* pos, const float* cos_t, const float* sin_t, int64_t head_dim,
                       void* y, int y_dtype, hipStream_t st) {
+  const int64_t ldy = G * N;
+  // bf16 operands, K a multiple of 64 (and the RoPE dims one K step per head) and enough 256 x 256
+  // tiles for every CU: the DMA form
+  if (!f32_operands && K % 64 == 0 && ldx % 8 == 0 && (!pos || head_dim % 64 == 0) &&
+      (T + kBig - 1) / kBig * G * ((N + kBig - 1) / kBig) >= smla_num_cus()) {
+    const int64_t ntb = (N + kBig - 1) / kBig;
+    const dim3 gb((unsigned)(ntb * G), (unsigned)((T + kBig - 1) / kBig));
+    auto kern = pos ? (y_dtype == SMLA_BF16 ? gemm_dma_kernel<SMLA_BF16, true> : gemm_dma_kernel<SMLA_F32, true>)
+                    : (y_dtype == SMLA_BF16 ? gemm_dma_kernel<SMLA_BF16, false> : gemm_dma_kernel<SMLA_F32, false>);
+    // devices whose LDS limit is raised, one set per kernel (RoPE form x output type)
+    static std::atomic<uint64_t> lds_attr[4] = {{0}, {0}, {0}, {0}};
+    if (hipError_t e = smla_set_dynamic_lds((const void*)kern, 2 * kStageBytes,
+                                            lds_attr[(pos ? 2 : 0) + (y_dtype == SMLA_BF16 ? 1 : 0)]);
+        e != hipSuccess)
+      return (int)e;
+    hipLaunchKernelGGL(kern, gb, dim3(512), 2 * kStageBytes, st, (const uint8_t*)x, ldx, (const uint8_t*)w, (int)T,
+                       (int)N, (int)K, (int)ntb, pos, cos_t, sin_t, (int)head_dim, y, ldy);
+    SMLA_HIP_CHECK_LAUNCH();
+    return SMLA_OK;
+  }
   const int64_t ntn = (N + kBN - 1) / kBN;
   const dim3 grid((unsigned)(ntn * G), (unsigned)((T + kBM - 1) / kBM)), blk(256);
-  const int64_t ldy = G * N;
 #define SMLA_GEMM(BF, YD, RP)                                                                                   \
   hipLaunchKernelGGL((gemm_kernel<BF, YD, RP>), grid, blk, 0, st, (const uint8_t*)x, ldx, (const uint8_t*)w,   \
                      (int)T, (int)N, (int)K, (int)ntn, pos, cos_t, sin_t, (int)head_dim, y, ldy)

@@ -51,6 +51,8 @@ def _check_linear(got, x, w, G, out_dtype):
     (8, 4, 2048, 2048, torch.bfloat16),
     (2, 1, 8192, 512, torch.float32),
     # the tiled MFMA GEMM
+    (768, 1, 21760, 512, torch.float32),       # 256 x 256 DMA tiles: 3 x 85 of them
+    (520, 2, 11000, 576, torch.bfloat16),      # the same, ragged tokens and outputs, two groups
     (64, 1, 1024, 4096, torch.float32),
     (4096, 1, 1024, 4096, torch.bfloat16),     # prefill's q_down
     (300, 1, 200, 520, torch.float32),         # ragged token and output tiles, a K tail
@@ -114,6 +116,31 @@ def test_o_proj_fused_rope(dev, T):
     # against the oracle (float64 products, bf16 intermediate)
     ref = omla.o_project(o, pos, cos_t.cpu(), sin_t.cpu(), wa.float().numpy(), wb.float().numpy(), G)
     np.testing.assert_allclose(fused.cpu().double().numpy(), ref, rtol=1e-2, atol=2e-2 * np.abs(ref).max())
+
+
+def test_o_proj_fused_rope_wide(dev):
+    """2048 tokens: the grouped product runs the 256 x 256 DMA tiles with the inverse RoPE applied in
+    LDS; it equals the standalone rotation followed by the plain product bit for bit, and the
+    oracle on a sample of tokens (each token's output depends on that token alone)."""
+    from smla import norm_rope as snr
+    from smla import ops
+    announce("o_proj T=2048 (DMA tiles with RoPE)")
+    g = torch.Generator().manual_seed(2048)
+    T, H, D, rd, G, R, dim = 2048, 64, 512, 64, 8, 1024, 4096
+    o = torch.randn(T, H, D, generator=g).to(torch.bfloat16)
+    wa = (torch.randn(G * R, H * D // G, generator=g) * 0.02).to(torch.bfloat16)
+    wb = (torch.randn(dim, G * R, generator=g) * 0.02).to(torch.bfloat16)
+    pos = torch.randint(0, 65536, (T,), generator=g, dtype=torch.int32)
+    cos_t, sin_t = snr.rope_tables(rd, 65536, device=dev)
+    od, wad, wbd, posd = o.to(dev), wa.to(dev), wb.to(dev), pos.to(dev)
+    fused = ops.o_proj_op(od, posd, cos_t, sin_t, wad, wbd, G, torch.float32)
+    rot = od.clone()
+    ops.rope_op_(rot, posd, cos_t, sin_t, True)
+    two = ops.o_proj_op(rot, None, None, None, wad, wbd, G, torch.float32)
+    assert torch.equal(fused, two)
+    idx = torch.tensor([0, 1, 255, 256, 1023, 1500, 2046, 2047])
+    ref = omla.o_project(o[idx], pos[idx], cos_t.cpu(), sin_t.cpu(), wa.float().numpy(), wb.float().numpy(), G)
+    np.testing.assert_allclose(fused.cpu()[idx].double().numpy(), ref, rtol=1e-2, atol=2e-2 * np.abs(ref).max())
 
 
 def test_mla_mirror_routes(dev):
