@@ -355,6 +355,7 @@ int launch_gemm_tiled(const void* x, int64_t ldx, bool f32_operands, const void*
   // bf16 operands, K a multiple of 64 (and the RoPE dims one K step per head) and enough 256 x 256
   // tiles for every CU: the DMA form
   if (!f32_operands && K % 64 == 0 && ldx % 8 == 0 && (!pos || head_dim % 64 == 0) &&
+      (((uintptr_t)x | (uintptr_t)w) & 15) == 0 &&
       (T + kBig - 1) / kBig * G * ((N + kBig - 1) / kBig) >= smla_num_cus()) {
     const int64_t ntb = (N + kBig - 1) / kBig;
     const dim3 gb((unsigned)(ntb * G), (unsigned)((T + kBig - 1) / kBig));
