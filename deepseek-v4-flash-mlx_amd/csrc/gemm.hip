@@ -18,8 +18,9 @@
 // is loaded (inverse RoPE at pos[t], every product and sum rounded in float32, then bf16), the
 // arithmetic of smla_rope.
 //
-// Large bf16 products (gemm_dma_kernel: enough 256 x 256 tiles for every CU, K a multiple of 64):
-// 8 waves per workgroup, each a 128 x 64 quarter-octant as 4 x 2 blocks of
+// Large bf16 products (gemm_dma_kernel: K a multiple of 64 and enough 256 x 256 tiles for every
+// CU, else 128 x 128 tiles of 4 waves, two workgroups per CU, when those suffice):
+// 8 waves per 256 x 256 workgroup, each a 128 x 64 quarter-octant as 4 x 2 blocks of
 // v_mfma_f32_32x32x16_bf16.  Operands go HBM -> LDS by global_load_lds_dwordx4 (no register
 // staging) into a ring of two 64 KB stages; a K step (64 k) is 32 MFMAs per wave, two waves per
 // SIMD, long enough to cover the next step's copies, with one barrier per step.  A copy
@@ -214,36 +215,46 @@ __global__ __launch_bounds__(256) void gemm_kernel(const uint8_t* __restrict__ x
     }
 }
 
-constexpr int kBig = 256;                              // tile rows (tokens) and columns (outputs)
-constexpr int kOperandBytes = kBig * kRowBytes;        // one operand's rows of one K step: 32 KB
-constexpr int kStageBytes = 2 * kOperandBytes;         // A then B
-constexpr int kCopiesPerWave = kStageBytes / 1024 / 8;  // 1 KB copy instructions per wave per stage
+// BT x BT tiles (tokens x outputs): BT = 256 with 8 waves of 128 x 64, or BT = 128 with 4 waves of
+// 64 x 64 (two workgroups per CU); either way 8 one-KB copy instructions per wave per stage
+template <int BT>
+struct DmaTile {
+  static constexpr int NW = BT == 256 ? 8 : 4;        // waves
+  static constexpr int WROWS = BT / 2;                 // rows per wave (2 row halves)
+  static constexpr int MB = WROWS / 32;                // 32-row MFMA blocks per wave
+  static constexpr int OPB = BT * kRowBytes;           // one operand's rows of one K step
+  static constexpr int STAGE = 2 * OPB;                // A then B
+  static constexpr int COPIES = STAGE / 1024 / NW;     // per wave per stage (8)
+  static constexpr int ACH = BT * 8 / (64 * NW);       // A chunks per thread (rotation of a RoPE step: 4)
+};
 
-template <int YDT, bool ROPE>
-__global__ __launch_bounds__(512) void gemm_dma_kernel(const uint8_t* __restrict__ x, int64_t ldx,
+template <int YDT, bool ROPE, int BT>
+__global__ __launch_bounds__(DmaTile<BT>::NW * 64) void gemm_dma_kernel(const uint8_t* __restrict__ x, int64_t ldx,
                                                        const uint8_t* __restrict__ w, int T, int N, int K, int ntn,
                                                        const int32_t* __restrict__ pos, const float* __restrict__ cos_t,
                                                        const float* __restrict__ sin_t, int head_dim,
                                                        void* __restrict__ y, int64_t ldy) {
   using namespace smla_attn;
+  using L = DmaTile<BT>;
+  constexpr int kStageBytes = L::STAGE, kOperandBytes = L::OPB, kCopiesPerWave = L::COPIES;
   extern __shared__ __align__(16) uint8_t lds_g[];
   lds_u8_t* lds = (lds_u8_t*)lds_g;
   const uint32_t lds_base = (uint32_t)(uintptr_t)lds;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int g = blockIdx.x / ntn;
-  const int n0 = (blockIdx.x % ntn) * kBig;
-  const int t0 = blockIdx.y * kBig;
-  const int wm = wave & 1, wn = wave >> 1;  // 128-row half, 64-column quarter
-  // copy instruction q = 8 wave + i covers stage bytes [1024 q, 1024 q + 1024): rows 8 (q mod 32)
-  // .. +7 of A (q < 32) or of B; lane L takes row + L / 8, slot L mod 8 <- chunk
+  const int n0 = (blockIdx.x % ntn) * BT;
+  const int t0 = blockIdx.y * BT;
+  const int wm = wave & 1, wn = wave >> 1;  // row half, 64-column slice
+  // copy instruction q = 8 wave + i covers stage bytes [1024 q, 1024 q + 1024): rows
+  // 8 (q mod BT/8) .. +7 of A (q < BT/8) or of B; lane L takes row + L / 8, slot L mod 8 <- chunk
   // (L mod 8) ^ ((row / 2) mod 8)
   const uint8_t* src[kCopiesPerWave];
 #pragma unroll
   for (int i = 0; i < kCopiesPerWave; i++) {
     const int q = wave * kCopiesPerWave + i;
-    const int r = 8 * (q & 31) + (lane >> 3);
+    const int r = 8 * (q % (BT / 8)) + (lane >> 3);
     const int c = (lane & 7) ^ ((r >> 1) & 7);
-    if (q < 32) {
+    if (q < BT / 8) {
       const int t = min(t0 + r, T - 1);
       src[i] = x + ((int64_t)t * ldx + (int64_t)g * K) * 2 + 16 * c;
     } else {
@@ -260,9 +271,9 @@ __global__ __launch_bounds__(512) void gemm_dma_kernel(const uint8_t* __restrict
     }
   };
 
-  f32x16_t_g acc[4][2];
+  f32x16_t_g acc[L::MB][2];
 #pragma unroll
-  for (int mb = 0; mb < 4; mb++)
+  for (int mb = 0; mb < L::MB; mb++)
 #pragma unroll
     for (int nb = 0; nb < 2; nb++)
 #pragma unroll
@@ -272,10 +283,10 @@ __global__ __launch_bounds__(512) void gemm_dma_kernel(const uint8_t* __restrict
   const int r32 = lane & 31, khalf = lane >> 5;
   // ROPE: the A chunks this thread rotates in a RoPE step, j = tid + 512 i (row j / 8, slot j mod 8),
   // and their rows' offsets in the cos / sin tables (32 pairs per position)
-  int prow[4] = {0, 0, 0, 0};
+  int prow[L::ACH] = {};
   if constexpr (ROPE) {
 #pragma unroll
-    for (int i = 0; i < 4; i++) prow[i] = pos[min(t0 + ((tid + 512 * i) >> 3), T - 1)] * 32;
+    for (int i = 0; i < L::ACH; i++) prow[i] = pos[min(t0 + ((tid + 64 * L::NW * i) >> 3), T - 1)] * 32;
   }
   const int nk = K / 64;
   issue(0, 0);
@@ -290,8 +301,8 @@ __global__ __launch_bounds__(512) void gemm_dma_kernel(const uint8_t* __restrict
       // of its row's position, c = slot ^ ((row / 2) mod 8)) rotated back in place, then a barrier
       if ((ks * 64) % head_dim == head_dim - 64) {
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-          const int j = tid + 512 * i, r = j >> 3, sl = j & 7, c = sl ^ ((r >> 1) & 7);
+        for (int i = 0; i < L::ACH; i++) {
+          const int j = tid + 64 * L::NW * i, r = j >> 3, sl = j & 7, c = sl ^ ((r >> 1) & 7);
           lds_u32x4_t* pa = (lds_u32x4_t*)(lds + (ks & 1) * kStageBytes + r * kRowBytes + 16 * sl);
           *pa = inv_rope4(*pa, cos_t + prow[i] + 4 * c, sin_t + prow[i] + 4 * c);
         }
@@ -301,10 +312,10 @@ __global__ __launch_bounds__(512) void gemm_dma_kernel(const uint8_t* __restrict
 #pragma unroll
     for (int kk = 0; kk < 4; kk++) {
       const int c = 2 * kk + khalf;
-      bf16x8_t a[4], b[2];
+      bf16x8_t a[L::MB], b[2];
 #pragma unroll
-      for (int mb = 0; mb < 4; mb++) {
-        const int r = 128 * wm + 32 * mb + r32;
+      for (int mb = 0; mb < L::MB; mb++) {
+        const int r = L::WROWS * wm + 32 * mb + r32;
         a[mb] = as_bf16x8(*(const lds_u32x4_t*)(A + r * kRowBytes + 16 * (c ^ ((r >> 1) & 7))));
       }
 #pragma unroll
@@ -313,24 +324,24 @@ __global__ __launch_bounds__(512) void gemm_dma_kernel(const uint8_t* __restrict
         b[nb] = as_bf16x8(*(const lds_u32x4_t*)(B + r * kRowBytes + 16 * (c ^ ((r >> 1) & 7))));
       }
 #pragma unroll
-      for (int mb = 0; mb < 4; mb++)
+      for (int mb = 0; mb < L::MB; mb++)
 #pragma unroll
         for (int nb = 0; nb < 2; nb++)
           acc[mb][nb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[mb], b[nb], acc[mb][nb], 0, 0, 0);
     }
   }
 
-  // accumulator r of block (mb, nb): token 128 wm + 32 mb + 8 (r / 4) + 4 (lane / 32) + r % 4,
+  // accumulator r of block (mb, nb): token WROWS wm + 32 mb + 8 (r / 4) + 4 (lane / 32) + r % 4,
   // output 64 wn + 32 nb + lane % 32
 #pragma unroll
-  for (int mb = 0; mb < 4; mb++)
+  for (int mb = 0; mb < L::MB; mb++)
 #pragma unroll
     for (int nb = 0; nb < 2; nb++) {
       const int n = n0 + 64 * wn + 32 * nb + r32;
       if (n >= N) continue;
 #pragma unroll
       for (int r = 0; r < 16; r++) {
-        const int t = t0 + 128 * wm + 32 * mb + 8 * (r >> 2) + 4 * khalf + (r & 3);
+        const int t = t0 + L::WROWS * wm + 32 * mb + 8 * (r >> 2) + 4 * khalf + (r & 3);
         if (t < T) {
           const int64_t o = (int64_t)t * ldy + (int64_t)g * N + n;
           if constexpr (YDT == SMLA_BF16)
@@ -344,6 +355,27 @@ __global__ __launch_bounds__(512) void gemm_dma_kernel(const uint8_t* __restrict
 
 }  // namespace
 
+template <int BT>
+static int launch_gemm_dma(const void* x, int64_t ldx, const void* w, int64_t T, int64_t G, int64_t N, int64_t K,
+                           const int32_t* pos, const float* cos_t, const float* sin_t, int64_t head_dim, void* y,
+                           int y_dtype, hipStream_t st) {
+  using L = DmaTile<BT>;
+  const int64_t ntb = (N + BT - 1) / BT;
+  const dim3 gb((unsigned)(ntb * G), (unsigned)((T + BT - 1) / BT));
+  auto kern = pos ? (y_dtype == SMLA_BF16 ? gemm_dma_kernel<SMLA_BF16, true, BT> : gemm_dma_kernel<SMLA_F32, true, BT>)
+                  : (y_dtype == SMLA_BF16 ? gemm_dma_kernel<SMLA_BF16, false, BT> : gemm_dma_kernel<SMLA_F32, false, BT>);
+  // devices whose LDS limit is raised, one set per kernel (RoPE form x output type)
+  static std::atomic<uint64_t> lds_attr[4] = {{0}, {0}, {0}, {0}};
+  if (hipError_t e = smla_set_dynamic_lds((const void*)kern, 2 * L::STAGE,
+                                          lds_attr[(pos ? 2 : 0) + (y_dtype == SMLA_BF16 ? 1 : 0)]);
+      e != hipSuccess)
+    return (int)e;
+  hipLaunchKernelGGL(kern, gb, dim3(L::NW * 64), 2 * L::STAGE, st, (const uint8_t*)x, ldx, (const uint8_t*)w, (int)T,
+                     (int)N, (int)K, (int)ntb, pos, cos_t, sin_t, (int)head_dim, y, G * N);
+  SMLA_HIP_CHECK_LAUNCH();
+  return SMLA_OK;
+}
+
 // y [T, G*N] (row stride G*N) = grouped x [T, G*K] (row stride ldx elements) times w [G*N, K]^T.
 // x and w both bf16 (x_f32 false) or both fp32; y bf16 or fp32.  With pos (bf16 only), inverse RoPE
 // of the last 64 dims of every head_dim-wide head of x on load.  16-byte aligned rows (K % 8 for
@@ -352,25 +384,16 @@ int launch_gemm_tiled(const void* x, int64_t ldx, bool f32_operands, const void*
                       int64_t K, const int32_t* pos, const float* cos_t, const float* sin_t, int64_t head_dim,
                       void* y, int y_dtype, hipStream_t st) {
   const int64_t ldy = G * N;
-  // bf16 operands, K a multiple of 64 (and the RoPE dims one K step per head) and enough 256 x 256
-  // tiles for every CU: the DMA form
+  // bf16 operands, 16-byte aligned, K a multiple of 64 (and the RoPE dims one K step per head): the
+  // DMA tiles, 256 x 256 when they give every CU one, else 128 x 128 when those do
   if (!f32_operands && K % 64 == 0 && ldx % 8 == 0 && (!pos || head_dim % 64 == 0) &&
-      (((uintptr_t)x | (uintptr_t)w) & 15) == 0 &&
-      (T + kBig - 1) / kBig * G * ((N + kBig - 1) / kBig) >= smla_num_cus()) {
-    const int64_t ntb = (N + kBig - 1) / kBig;
-    const dim3 gb((unsigned)(ntb * G), (unsigned)((T + kBig - 1) / kBig));
-    auto kern = pos ? (y_dtype == SMLA_BF16 ? gemm_dma_kernel<SMLA_BF16, true> : gemm_dma_kernel<SMLA_F32, true>)
-                    : (y_dtype == SMLA_BF16 ? gemm_dma_kernel<SMLA_BF16, false> : gemm_dma_kernel<SMLA_F32, false>);
-    // devices whose LDS limit is raised, one set per kernel (RoPE form x output type)
-    static std::atomic<uint64_t> lds_attr[4] = {{0}, {0}, {0}, {0}};
-    if (hipError_t e = smla_set_dynamic_lds((const void*)kern, 2 * kStageBytes,
-                                            lds_attr[(pos ? 2 : 0) + (y_dtype == SMLA_BF16 ? 1 : 0)]);
-        e != hipSuccess)
-      return (int)e;
-    hipLaunchKernelGGL(kern, gb, dim3(512), 2 * kStageBytes, st, (const uint8_t*)x, ldx, (const uint8_t*)w, (int)T,
-                       (int)N, (int)K, (int)ntb, pos, cos_t, sin_t, (int)head_dim, y, ldy);
-    SMLA_HIP_CHECK_LAUNCH();
-    return SMLA_OK;
+      (((uintptr_t)x | (uintptr_t)w) & 15) == 0) {
+    const int64_t cus = smla_num_cus();
+    auto tiles = [&](int64_t bt) { return (T + bt - 1) / bt * G * ((N + bt - 1) / bt); };
+    if (tiles(256) >= cus)
+      return launch_gemm_dma<256>(x, ldx, w, T, G, N, K, pos, cos_t, sin_t, head_dim, y, y_dtype, st);
+    if (tiles(128) >= cus)
+      return launch_gemm_dma<128>(x, ldx, w, T, G, N, K, pos, cos_t, sin_t, head_dim, y, y_dtype, st);
   }
   const int64_t ntn = (N + kBN - 1) / kBN;
   const dim3 grid((unsigned)(ntn * G), (unsigned)((T + kBM - 1) / kBM)), blk(256);

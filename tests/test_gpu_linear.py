@@ -118,15 +118,17 @@ def test_o_proj_fused_rope(dev, T):
     np.testing.assert_allclose(fused.cpu().double().numpy(), ref, rtol=1e-2, atol=2e-2 * np.abs(ref).max())
 
 
-def test_o_proj_fused_rope_wide(dev):
-    """2048 tokens: the grouped product runs the 256 x 256 DMA tiles with the inverse RoPE applied in
-    LDS; it equals the standalone rotation followed by the plain product bit for bit, and the
-    oracle on a sample of tokens (each token's output depends on that token alone)."""
+@pytest.mark.parametrize("T", [600, 2048])
+def test_o_proj_fused_rope_wide(dev, T):
+    """The grouped product on the DMA tiles (600 tokens: 128 x 128, 2048: 256 x 256) with the
+    inverse RoPE applied in LDS: equal to the standalone rotation followed by the plain product bit
+    for bit, and to the oracle on a sample of tokens (each token's output depends on that token
+    alone)."""
     from smla import norm_rope as snr
     from smla import ops
-    announce("o_proj T=2048 (DMA tiles with RoPE)")
-    g = torch.Generator().manual_seed(2048)
-    T, H, D, rd, G, R, dim = 2048, 64, 512, 64, 8, 1024, 4096
+    announce(f"o_proj T={T} (DMA tiles with RoPE)")
+    g = torch.Generator().manual_seed(T)
+    H, D, rd, G, R, dim = 64, 512, 64, 8, 1024, 4096
     o = torch.randn(T, H, D, generator=g).to(torch.bfloat16)
     wa = (torch.randn(G * R, H * D // G, generator=g) * 0.02).to(torch.bfloat16)
     wb = (torch.randn(dim, G * R, generator=g) * 0.02).to(torch.bfloat16)
@@ -138,7 +140,7 @@ def test_o_proj_fused_rope_wide(dev):
     ops.rope_op_(rot, posd, cos_t, sin_t, True)
     two = ops.o_proj_op(rot, None, None, None, wad, wbd, G, torch.float32)
     assert torch.equal(fused, two)
-    idx = torch.tensor([0, 1, 255, 256, 1023, 1500, 2046, 2047])
+    idx = torch.tensor([0, 1, 127, 128, 255, 256, T // 2, T - 2, T - 1])
     ref = omla.o_project(o[idx], pos[idx], cos_t.cpu(), sin_t.cpu(), wa.float().numpy(), wb.float().numpy(), G)
     np.testing.assert_allclose(fused.cpu()[idx].double().numpy(), ref, rtol=1e-2, atol=2e-2 * np.abs(ref).max())
 
