@@ -100,6 +100,31 @@ def test_ring_vs_oracle_ring(dev, fp8_sim):
                 np.testing.assert_allclose(got.numpy(), row.numpy(), rtol=1e-4, atol=2e-5)
 
 
+def test_quant_fp8_encoder_every_code(dev):
+    """The quantiser's e4m3 encoding on the device over every finite e4m3 value, every midpoint
+    between neighbours and the floats next to each midpoint, tiny values, signed zeros and random
+    values: blocks that open with 448 have scale 1, so their codes are the plain encoding."""
+    from smla import ops
+    announce("quant fp8 encoder")
+    ref = ofp8.e4m3_decode(np.arange(256, dtype=np.uint8))
+    vals = ref[np.isfinite(ref)]
+    pos = np.unique(np.abs(vals))
+    mids = ((pos[1:].astype(np.float64) + pos[:-1]) / 2).astype(np.float32)
+    rnd = np.clip(np.random.default_rng(5).standard_normal(4000).astype(np.float32) * 50, -448, 448)
+    x = np.concatenate([vals, mids, -mids, np.nextafter(mids, 0), np.nextafter(mids, 1),
+                        np.nextafter(-mids, 0), np.nextafter(-mids, -1), rnd,
+                        np.float32([2.0 ** -10, -(2.0 ** -10), 3 * 2.0 ** -10, 1e-30, -1e-30, 0.0, -0.0,
+                                    2.0 ** -9, 448.0, -448.0])]).astype(np.float32)
+    nb = (x.size + 62) // 63
+    blocks = np.zeros((nb, 64), dtype=np.float32)
+    blocks[:, 0] = 448.0
+    blocks[:, 1:].flat[:x.size] = x
+    codes, scales = ops.quant_fp8_pow2_op(torch.from_numpy(blocks).to(dev))
+    assert torch.all(scales.cpu() == 1.0)
+    got = codes.cpu().numpy().reshape(nb, 64)[:, 1:].reshape(-1)[:x.size]
+    np.testing.assert_array_equal(got, ofp8.e4m3_encode(x).astype(np.uint8))
+
+
 def test_quant_fp8_bit_exact(dev):
     from smla import ops
     announce("quant fp8")
