@@ -198,27 +198,26 @@ __global__ __launch_bounds__(kPoolThreads) void gated_pool_kernel(
   const int64_t b = bg / G, g = bg % G;
   const int t = threadIdx.x;
   const int64_t two_d = 2 * (int64_t)d;
+  // channels c0 = 2t and c0 + 1 of every slot in one 8-byte load each (kv, score, ape)
+  const int c0 = 2 * t;
+  float v0[2 * kMaxRatio], s0[2 * kMaxRatio], v1[2 * kMaxRatio], s1[2 * kMaxRatio];
+  int ns = 0;
+  auto slot = [&](int64_t row, int64_t off, int j) __attribute__((always_inline)) {
+    const f32x2_t kvv = *(const f32x2_t*)(kv + row * two_d + off + c0);
+    const f32x2_t sc = *(const f32x2_t*)(score + row * two_d + off + c0);
+    const f32x2_t ap = *(const f32x2_t*)(ape + j * two_d + off + c0);
+    v0[ns] = kvv[0];
+    v1[ns] = kvv[1];
+    s0[ns] = sc[0] + ap[0];
+    s1[ns] = sc[1] + ap[1];
+    ns++;
+  };
+  if (g > 0)
+    for (int j = 0; j < ratio; j++) slot(b * N + (g - 1) * ratio + j, 0, j);
+  for (int j = 0; j < ratio; j++) slot(b * N + g * ratio + j, d, j);
   float pooled[2];
-  for (int k = 0; k < 2; k++) {
-    const int c = 2 * t + k;
-    float v[2 * kMaxRatio], s[2 * kMaxRatio];
-    int ns = 0;
-    if (g > 0) {
-      for (int j = 0; j < ratio; j++) {
-        int64_t row = b * N + (g - 1) * ratio + j;
-        v[ns] = kv[row * two_d + c];
-        s[ns] = score[row * two_d + c] + ape[j * two_d + c];
-        ns++;
-      }
-    }
-    for (int j = 0; j < ratio; j++) {
-      int64_t row = b * N + g * ratio + j;
-      v[ns] = kv[row * two_d + d + c];
-      s[ns] = score[row * two_d + d + c] + ape[j * two_d + d + c];
-      ns++;
-    }
-    pooled[k] = softmax_pool<2 * kMaxRatio>(v, s, ns);
-  }
+  pooled[0] = softmax_pool<2 * kMaxRatio>(v0, s0, ns);
+  pooled[1] = softmax_pool<2 * kMaxRatio>(v1, s1, ns);
   pool_epilogue(pooled[0], pooled[1], d, rd, eps, sim, norm_w, cos_t, sin_t, g * ratio, red, xch,
                 out + bg * (int64_t)d);
 }
@@ -370,6 +369,8 @@ extern "C" int smla_gated_pool(const float* kv, const float* score, const float*
   int rc = check_pool_dims(d, ratio, rd, sim);
   if (rc) return rc;
   if (N % ratio != 0) return SMLA_E_SHAPE;
+  // the kernel reads two adjacent channels of kv, score and ape in one 8-byte load
+  if ((((uintptr_t)kv | (uintptr_t)score | (uintptr_t)ape) & 7) != 0) return SMLA_E_UNSUPPORTED;
   int64_t rows = B * (N / ratio);
   if (rows <= 0) return SMLA_OK;
   hipLaunchKernelGGL(gated_pool_kernel, dim3((unsigned)rows), dim3((unsigned)(d / 2)), 0, (hipStream_t)stream, kv,

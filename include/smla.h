@@ -294,7 +294,8 @@ enum { SMLA_SIM_NONE = 0, SMLA_SIM_FP8 = 1, SMLA_SIM_ROTATE_FP4 = 2 };
  *   kv, score [B,N,2d] fp32 (N a multiple of ratio);  ape [ratio,2d];  norm_w [d];
  *   cos, sin [>= N, rd/2] fp32 rotation tables indexed by token position (row g uses position
  *   g*ratio);  out [B, N/ratio, d] fp32, quantised as `sim` says (SMLA_SIM_*).
- *   d is 128, 256 or 512; (d - rd) % 64 == 0; ratio <= 8.
+ *   d is 128, 256 or 512; (d - rd) % 64 == 0; ratio <= 8; kv, score and ape 8-byte aligned
+ *   (SMLA_E_UNSUPPORTED otherwise).
  */
 int smla_gated_pool(const float* kv, const float* score, const float* ape, const float* norm_w,
                     const float* cos_t, const float* sin_t, int64_t B, int64_t N, int64_t d,

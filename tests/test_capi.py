@@ -83,6 +83,9 @@ def test_host_validation_rejects_bad_arguments():
     assert lib.smla_gated_pool(fake, fake, fake, fake, fake, fake, 1, 8, 512, 4, 63, 1e-6, 0, fake, None) == -2
     assert lib.smla_gated_pool(fake, fake, fake, fake, fake, fake, 1, 8, 192, 4, 64, 1e-6, 0, fake, None) == -4
     assert lib.smla_gated_pool(fake, fake, fake, fake, fake, fake, 1, 8, 256, 4, 64, 1e-6, 3, fake, None) == -6
+    odd = ctypes.c_void_p(4100)                                                  # kv/score/ape not 8-byte aligned
+    assert lib.smla_gated_pool(odd, fake, fake, fake, fake, fake, 1, 8, 256, 4, 64, 1e-6, 0, fake, None) == -4
+    assert lib.smla_gated_pool(fake, fake, odd, fake, fake, fake, 1, 8, 256, 4, 64, 1e-6, 0, fake, None) == -4
     # rotate_fp4: row length, flags, codes without scales, dtype, alignment
     assert lib.smla_rotate_fp4(fake, 0, 4, 48, 3, fake, None, None, None) == -4
     assert lib.smla_rotate_fp4(fake, 0, 4, 2048, 3, fake, None, None, None) == -4
