@@ -237,28 +237,87 @@ __global__ __launch_bounds__(kPoolThreads) void ring_step_kernel(
   if (pos < 0 || pos + 1 - ratio >= n_pos) return;  // block-uniform guard
   float* rk = ring_kv + b * (2 * ratio) * two_d;
   float* rs = ring_sc + b * (2 * ratio) * two_d;
-  const int slot = ratio + (int)(pos % ratio);
-  // thread t owns channels {2t, 2t+1} and {d+2t, d+2t+1} of every slot
-  for (int k = 0; k < 2; k++) {
-    const int c = 2 * t + k;
+  const int ph = (int)(pos % ratio);
+  const int slot = ratio + ph;
+  // thread t owns channels c0 = 2t, 2t+1 of both halves (h = 0: c0, h = 1: d + c0) of every slot,
+  // so no other thread reads or writes what it touches: every ring value it needs is loaded up
+  // front (8-byte loads of its two channels, all independent) and the emit, pool and shift run
+  // from registers
+  const int c0 = 2 * t;
+  f32x2_t nk[2], ns[2];  // the new token's slot
+#pragma unroll
+  for (int h = 0; h < 2; h++) {
+    const int64_t cc = c0 + h * (int64_t)d;
+    nk[h] = *(const f32x2_t*)(kv_p + b * ldp + cc);
+    const f32x2_t sp = *(const f32x2_t*)(score_p + b * ldp + cc);
+    const f32x2_t ap = *(const f32x2_t*)(ape + ph * two_d + cc);
+    ns[h][0] = sp[0] + ap[0];
+    ns[h][1] = sp[1] + ap[1];
+  }
+  if ((pos + 1) % ratio != 0) {  // block-uniform: no row completes, store the slot
+#pragma unroll
     for (int h = 0; h < 2; h++) {
-      int64_t cc = c + h * (int64_t)d;
-      rk[slot * two_d + cc] = kv_p[b * ldp + cc];
-      rs[slot * two_d + cc] = score_p[b * ldp + cc] + ape[(pos % ratio) * two_d + cc];
+      const int64_t cc = c0 + h * (int64_t)d;
+      *(f32x2_t*)(rk + slot * two_d + cc) = nk[h];
+      *(f32x2_t*)(rs + slot * two_d + cc) = ns[h];
+    }
+    return;
+  }
+  // a row completes: slot 2r-1 is the new token; the pool reads the first halves of slots
+  // 0..r-1 and the second halves of slots r..2r-1, the shift moves both halves of slots r..2r-1
+  f32x2_t ok[kMaxRatio], os[kMaxRatio];                // first halves of slots 0..r-1
+  f32x2_t hk[2][kMaxRatio], hs[2][kMaxRatio];          // both halves of slots r..2r-1
+#pragma unroll
+  for (int j = 0; j < kMaxRatio; j++) {
+    if (j < ratio) {
+      ok[j] = *(const f32x2_t*)(rk + j * two_d + c0);
+      os[j] = *(const f32x2_t*)(rs + j * two_d + c0);
+#pragma unroll
+      for (int h = 0; h < 2; h++) {
+        const int64_t cc = c0 + h * (int64_t)d;
+        if (j < ratio - 1) {
+          hk[h][j] = *(const f32x2_t*)(rk + (ratio + j) * two_d + cc);
+          hs[h][j] = *(const f32x2_t*)(rs + (ratio + j) * two_d + cc);
+        } else {
+          hk[h][j] = nk[h];
+          hs[h][j] = ns[h];
+        }
+      }
     }
   }
-  if ((pos + 1) % ratio != 0) return;  // block-uniform
   float pooled[2];
+#pragma unroll
   for (int k = 0; k < 2; k++) {
-    const int c = 2 * t + k;
-    float v[2 * kMaxRatio], s[2 * kMaxRatio];
-    for (int j = 0; j < ratio; j++) {
-      v[j] = rk[j * two_d + c];
-      s[j] = rs[j * two_d + c];
-      v[ratio + j] = rk[(ratio + j) * two_d + d + c];
-      s[ratio + j] = rs[(ratio + j) * two_d + d + c];
+    float v[2 * kMaxRatio], sc[2 * kMaxRatio];
+#pragma unroll
+    for (int j = 0; j < kMaxRatio; j++) {
+      if (j < ratio) {
+        v[j] = ok[j][k];
+        sc[j] = os[j][k];
+        v[ratio + j] = hk[1][j][k];
+        sc[ratio + j] = hs[1][j][k];
+      }
     }
-    pooled[k] = softmax_pool<2 * kMaxRatio>(v, s, 2 * ratio);
+    pooled[k] = softmax_pool<2 * kMaxRatio>(v, sc, 2 * ratio);
+  }
+  // shift: slots r..2r-1 -> 0..r-1 (own channels only); slots r..2r-1 keep their values, the new
+  // token included in slot 2r-1, as after a store-then-copy
+#pragma unroll
+  for (int j = 0; j < kMaxRatio; j++) {
+    if (j < ratio) {
+#pragma unroll
+      for (int h = 0; h < 2; h++) {
+        const int64_t cc = c0 + h * (int64_t)d;
+        *(f32x2_t*)(rk + j * two_d + cc) = hk[h][j];
+        *(f32x2_t*)(rs + j * two_d + cc) = hs[h][j];
+      }
+    }
+  }
+#pragma unroll
+  for (int h = 0; h < 2; h++) {
+    const int64_t cc = c0 + h * (int64_t)d;
+    *(f32x2_t*)(rk + (2 * ratio - 1) * two_d + cc) = nk[h];
+    *(f32x2_t*)(rs + (2 * ratio - 1) * two_d + cc) = ns[h];
   }
   const int64_t grp = (pos + 1) / ratio - 1;
   __shared__ float rowbuf[2 * kPoolThreads];
@@ -267,17 +326,6 @@ __global__ __launch_bounds__(kPoolThreads) void ring_step_kernel(
     float* dst = comp + (b * comp_cap + grp) * (int64_t)d;
     dst[2 * t] = rowbuf[2 * t];
     dst[2 * t + 1] = rowbuf[2 * t + 1];
-  }
-  // shift: slots r..2r-1 -> 0..r-1 (own channels only)
-  for (int k = 0; k < 2; k++) {
-    const int c = 2 * t + k;
-    for (int h = 0; h < 2; h++) {
-      int64_t cc = c + h * (int64_t)d;
-      for (int j = 0; j < ratio; j++) {
-        rk[j * two_d + cc] = rk[(ratio + j) * two_d + cc];
-        rs[j * two_d + cc] = rs[(ratio + j) * two_d + cc];
-      }
-    }
   }
 }
 
@@ -449,6 +497,10 @@ extern "C" int smla_ring_step(float* ring_kv, float* ring_sc, const float* kv_p,
   if (B <= 0 || comp_cap < 0 || n_pos <= 0 || (ld_p != 0 && ld_p < 2 * d)) return SMLA_E_SHAPE;
   int rc = check_pool_dims(d, ratio, rd, sim);
   if (rc) return rc;
+  // two adjacent channels move in one 8-byte access
+  if ((((uintptr_t)ring_kv | (uintptr_t)ring_sc | (uintptr_t)kv_p | (uintptr_t)score_p | (uintptr_t)ape) & 7) != 0 ||
+      ld_p % 2 != 0)
+    return SMLA_E_UNSUPPORTED;
   hipLaunchKernelGGL(ring_step_kernel, dim3((unsigned)B), dim3((unsigned)(d / 2)), 0, (hipStream_t)stream, ring_kv,
                      ring_sc, kv_p, score_p, pos, ape, norm_w, cos_t, sin_t, n_pos, (int)d, (int)ratio, (int)rd,
                      eps, sim, comp_cache, comp_cap, ld_p ? ld_p : 2 * d);

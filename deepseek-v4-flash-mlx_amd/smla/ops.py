@@ -335,8 +335,10 @@ def ring_step_op(ring_kv: torch.Tensor, ring_sc: torch.Tensor, kv_p: torch.Tenso
     B = ring_kv.shape[0]
     d = ring_kv.shape[-1] // 2
     # row-strided fp32 views (slices of one wider projection) pass as they are; anything else is packed
+    # (8-byte aligned with an even row stride: the kernel moves two channels per access)
     strided = (kv_p.dtype == score_p.dtype == torch.float32 and kv_p.dim() == score_p.dim() == 2
-               and kv_p.stride(1) == score_p.stride(1) == 1 and kv_p.stride(0) == score_p.stride(0))
+               and kv_p.stride(1) == score_p.stride(1) == 1 and kv_p.stride(0) == score_p.stride(0)
+               and kv_p.stride(0) % 2 == 0 and kv_p.data_ptr() % 8 == 0 and score_p.data_ptr() % 8 == 0)
     if not strided:
         kv_p, score_p = kv_p.float().contiguous(), score_p.float().contiguous()
     ld = kv_p.stride(0) if kv_p.dim() == 2 else 0

@@ -86,6 +86,14 @@ def test_host_validation_rejects_bad_arguments():
     odd = ctypes.c_void_p(4100)                                                  # kv/score/ape not 8-byte aligned
     assert lib.smla_gated_pool(odd, fake, fake, fake, fake, fake, 1, 8, 256, 4, 64, 1e-6, 0, fake, None) == -4
     assert lib.smla_gated_pool(fake, fake, odd, fake, fake, fake, 1, 8, 256, 4, 64, 1e-6, 0, fake, None) == -4
+    ring_args = [fake] * 9 + [64, 2, 256, 4, 64, 1e-6, 0, fake, 8, 0, None]
+    for i in (0, 2, 5):                                                          # ring_kv, kv_p, ape unaligned
+        a = list(ring_args)
+        a[i] = odd
+        assert lib.smla_ring_step(*a) == -4
+    a = list(ring_args)
+    a[18] = 513                                                                  # odd projection row stride
+    assert lib.smla_ring_step(*a) == -4
     # rotate_fp4: row length, flags, codes without scales, dtype, alignment
     assert lib.smla_rotate_fp4(fake, 0, 4, 48, 3, fake, None, None, None) == -4
     assert lib.smla_rotate_fp4(fake, 0, 4, 2048, 3, fake, None, None, None) == -4

@@ -98,6 +98,8 @@ def test_ring_vs_oracle_ring(dev, fp8_sim):
                 assert diff.max().item() <= row[: d - rd].abs().max().item() * 0.13
             else:
                 np.testing.assert_allclose(got.numpy(), row.numpy(), rtol=1e-4, atol=2e-5)
+        # the ring itself (moves and the score + ape adds only): bit for bit
+        assert torch.equal(ring.ring_kv[b].cpu(), kvs) and torch.equal(ring.ring_sc[b].cpu(), scs)
 
 
 def test_quant_fp8_encoder_every_code(dev):
