@@ -92,24 +92,49 @@ __device__ inline float block_sum(float v, float* red) {
   return s;
 }
 
-// Epilogue shared by the prefill pool and the ring step: RMSNorm(norm_w), RoPE of the last rd
-// channels at position `pos`, then the `sim` quantisation (SMLA_SIM_*).  Thread t owns channels 2t
+// Epilogue shared by the prefill pool, the ring step and the row epilogue: RMSNorm with the
+// weights in `e`, RoPE of the last rd channels by the pair in `e` (the row's position), then the
+// `sim` quantisation (SMLA_SIM_*).  Thread t owns channels 2t
 // and 2t+1 (d == 2*blockDim.x).  `v0,v1` are the pooled values; the result is written to dst[2t],
 // dst[2t+1].  `xch` (d floats of LDS) carries the rotation stages that cross waves.
-__device__ inline void pool_epilogue(float v0, float v1, int d, int rd, float eps, int sim,
-                                     const float* __restrict__ norm_w, const float* __restrict__ cos_t,
-                                     const float* __restrict__ sin_t, int64_t pos, float* red, float* xch,
-                                     float* dst) {
+struct EpiOperands {
+  float w0, w1;  // norm weights of channels 2t, 2t+1 (1 for the weightless norm: an exact product)
+  float cs, sn;  // rotation of the pair when it is a rope channel pair
+};
+
+// The epilogue's operands from memory, loaded by the caller ahead of (or beside) its own loads so
+// that their latency overlaps them rather than following the norm's reduction.
+__device__ inline EpiOperands epilogue_weights(const float* __restrict__ norm_w) {
+  const int c0 = 2 * threadIdx.x;
+  EpiOperands e{1.f, 1.f, 1.f, 0.f};
+  if (norm_w) {
+    e.w0 = norm_w[c0];
+    e.w1 = norm_w[c0 + 1];
+  }
+  return e;
+}
+
+__device__ inline void epilogue_rotation(EpiOperands& e, int d, int rd, const float* __restrict__ cos_t,
+                                         const float* __restrict__ sin_t, int64_t pos) {
+  const int c0 = 2 * threadIdx.x;
+  if (c0 >= d - rd) {
+    const int64_t i = pos * (rd / 2) + ((c0 - (d - rd)) >> 1);
+    e.cs = cos_t[i];
+    e.sn = sin_t[i];
+  }
+}
+
+__device__ inline void pool_epilogue(float v0, float v1, int d, int rd, float eps, int sim, const EpiOperands& e,
+                                     float* red, float* xch, float* dst) {
   const int t = threadIdx.x;
   const int c0 = 2 * t;
   float ss = block_sum(v0 * v0 + v1 * v1, red);
   float inv = rsqrtf(ss / (float)d + eps);
-  float y0 = (norm_w ? norm_w[c0] : 1.f) * (v0 * inv);   // no weight: the weightless per-head norm
-  float y1 = (norm_w ? norm_w[c0 + 1] : 1.f) * (v1 * inv);
+  float y0 = e.w0 * (v0 * inv);
+  float y1 = e.w1 * (v1 * inv);
   const int nope = d - rd;
   if (c0 >= nope) {
-    int pi = (c0 - nope) >> 1;
-    float cs = cos_t[pos * (rd / 2) + pi], sn = sin_t[pos * (rd / 2) + pi];
+    const float cs = e.cs, sn = e.sn;
     float r0 = y0 * cs - y1 * sn;
     float r1 = y0 * sn + y1 * cs;
     y0 = r0;
@@ -200,6 +225,8 @@ __global__ __launch_bounds__(kPoolThreads) void gated_pool_kernel(
   const int64_t two_d = 2 * (int64_t)d;
   // channels c0 = 2t and c0 + 1 of every slot in one 8-byte load each (kv, score, ape)
   const int c0 = 2 * t;
+  EpiOperands eo = epilogue_weights(norm_w);
+  epilogue_rotation(eo, d, rd, cos_t, sin_t, g * ratio);
   float v0[2 * kMaxRatio], s0[2 * kMaxRatio], v1[2 * kMaxRatio], s1[2 * kMaxRatio];
   int ns = 0;
   auto slot = [&](int64_t row, int64_t off, int j) __attribute__((always_inline)) {
@@ -218,7 +245,7 @@ __global__ __launch_bounds__(kPoolThreads) void gated_pool_kernel(
   float pooled[2];
   pooled[0] = softmax_pool<2 * kMaxRatio>(v0, s0, ns);
   pooled[1] = softmax_pool<2 * kMaxRatio>(v1, s1, ns);
-  pool_epilogue(pooled[0], pooled[1], d, rd, eps, sim, norm_w, cos_t, sin_t, g * ratio, red, xch,
+  pool_epilogue(pooled[0], pooled[1], d, rd, eps, sim, eo, red, xch,
                 out + bg * (int64_t)d);
 }
 
@@ -263,6 +290,8 @@ __global__ __launch_bounds__(kPoolThreads) void ring_step_kernel(
     }
     return;
   }
+  EpiOperands eo = epilogue_weights(norm_w);
+  epilogue_rotation(eo, d, rd, cos_t, sin_t, pos + 1 - ratio);
   // a row completes: slot 2r-1 is the new token; the pool reads the first halves of slots
   // 0..r-1 and the second halves of slots r..2r-1, the shift moves both halves of slots r..2r-1
   f32x2_t ok[kMaxRatio], os[kMaxRatio];                // first halves of slots 0..r-1
@@ -321,7 +350,7 @@ __global__ __launch_bounds__(kPoolThreads) void ring_step_kernel(
   }
   const int64_t grp = (pos + 1) / ratio - 1;
   __shared__ float rowbuf[2 * kPoolThreads];
-  pool_epilogue(pooled[0], pooled[1], d, rd, eps, sim, norm_w, cos_t, sin_t, pos + 1 - ratio, red, xch, rowbuf);
+  pool_epilogue(pooled[0], pooled[1], d, rd, eps, sim, eo, red, xch, rowbuf);
   if (grp < comp_cap) {
     float* dst = comp + (b * comp_cap + grp) * (int64_t)d;
     dst[2 * t] = rowbuf[2 * t];
@@ -445,12 +474,16 @@ __global__ __launch_bounds__(512) void row_epilogue_kernel(const float* __restri
   __shared__ float res[1024];
   const int64_t r = blockIdx.x;
   const int t = threadIdx.x;
+  // the row and the norm weights do not depend on the position: loaded beside it
+  const float* xr = x + r * ldx;
+  const float v0 = xr[2 * t], v1 = xr[2 * t + 1];
+  EpiOperands eo = epilogue_weights(norm_w);
   const int64_t s = r / rows_per_pos;
   const int64_t p = pos ? (int64_t)pos[s] : 0;
   const bool ok = (rd == 0 || (p >= 0 && p < n_pos)) && (cache_rows == 0 || (p >= 0 && p < cache_rows));
   if (!ok) return;  // uniform over the workgroup
-  const float* xr = x + r * ldx;
-  pool_epilogue(xr[2 * t], xr[2 * t + 1], d, rd, eps, sim, norm_w, cos_t, sin_t, rd ? p : 0, red, xch, res);
+  if (rd) epilogue_rotation(eo, d, rd, cos_t, sin_t, p);
+  pool_epilogue(v0, v1, d, rd, eps, sim, eo, red, xch, res);
   const int64_t orow = cache_rows > 0 ? s * cache_rows + p : r;
   if (out_dtype == SMLA_BF16)
     ((uint32_t*)out)[(orow * d) / 2 + t] = pack_bf16x2(res[2 * t], res[2 * t + 1]);
