@@ -249,7 +249,8 @@ __global__ __launch_bounds__(kPoolThreads) void gated_pool_kernel(
                 out + bg * (int64_t)d);
 }
 
-__global__ __launch_bounds__(kPoolThreads) void ring_step_kernel(
+// the ring step of sequence b, run by one workgroup of d/2 threads
+__device__ __attribute__((always_inline)) inline void ring_step_body(int64_t b,
     float* __restrict__ ring_kv, float* __restrict__ ring_sc, const float* __restrict__ kv_p,
     const float* __restrict__ score_p, const int32_t* __restrict__ pos_arr, const float* __restrict__ ape,
     const float* __restrict__ norm_w, const float* __restrict__ cos_t, const float* __restrict__ sin_t,
@@ -257,7 +258,6 @@ __global__ __launch_bounds__(kPoolThreads) void ring_step_kernel(
     int64_t ldp) {
   __shared__ float red[kPoolThreads / 64];
   __shared__ float xch[2 * kPoolThreads];
-  const int64_t b = blockIdx.x;
   const int t = threadIdx.x;
   const int64_t two_d = 2 * (int64_t)d;
   const int64_t pos = pos_arr[b];
@@ -356,6 +356,15 @@ __global__ __launch_bounds__(kPoolThreads) void ring_step_kernel(
     dst[2 * t] = rowbuf[2 * t];
     dst[2 * t + 1] = rowbuf[2 * t + 1];
   }
+}
+
+__global__ __launch_bounds__(kPoolThreads) void ring_step_kernel(
+    float* __restrict__ ring_kv, float* __restrict__ ring_sc, const float* __restrict__ kv_p,
+    const float* __restrict__ score_p, const int32_t* __restrict__ pos_arr, const float* __restrict__ ape,
+    const float* __restrict__ norm_w, const float* __restrict__ cos_t, const float* __restrict__ sin_t,
+    int64_t n_pos, int d, int ratio, int rd, float eps, int sim, float* __restrict__ comp, int64_t comp_cap,
+    int64_t ldp) {
+  ring_step_body(blockIdx.x, ring_kv, ring_sc, kv_p, score_p, pos_arr, ape, norm_w, cos_t, sin_t, n_pos, d, ratio, rd, eps, sim, comp, comp_cap, ldp);
 }
 
 // 16 lanes per 64-element block (one DPP row), 4 elements per lane: vector loads, the block's
@@ -461,18 +470,15 @@ extern "C" int smla_gated_pool(const float* kv, const float* score, const float*
 // the `sim` quantisation), written in out_dtype to row r of `out` or, when cache_rows > 0, to row
 // pos of sequence r / rows_per_pos of a cache [.., cache_rows, d].  A position outside the rotation
 // table or the cache leaves the row unwritten.
-__global__ __launch_bounds__(512) void row_epilogue_kernel(const float* __restrict__ x, int d, int64_t ldx,
-                                                           int rows_per_pos,
-                                                           const int32_t* __restrict__ pos,
-                                                           const float* __restrict__ norm_w,
-                                                           const float* __restrict__ cos_t,
-                                                           const float* __restrict__ sin_t, int64_t n_pos, int rd,
-                                                           float eps, int sim, void* __restrict__ out, int out_dtype,
-                                                           int64_t cache_rows) {
+// input row r, run by one workgroup of d/2 threads
+__device__ __attribute__((always_inline)) inline void row_epilogue_body(int64_t r,
+    const float* __restrict__ x, int d, int64_t ldx, int rows_per_pos,
+    const int32_t* __restrict__ pos, const float* __restrict__ norm_w, const float* __restrict__ cos_t,
+    const float* __restrict__ sin_t, int64_t n_pos, int rd, float eps, int sim, void* __restrict__ out, int out_dtype,
+    int64_t cache_rows) {
   __shared__ float red[8];
   __shared__ float xch[1024];
   __shared__ float res[1024];
-  const int64_t r = blockIdx.x;
   const int t = threadIdx.x;
   // the row and the norm weights do not depend on the position: loaded beside it
   const float* xr = x + r * ldx;
@@ -489,6 +495,32 @@ __global__ __launch_bounds__(512) void row_epilogue_kernel(const float* __restri
     ((uint32_t*)out)[(orow * d) / 2 + t] = pack_bf16x2(res[2 * t], res[2 * t + 1]);
   else
     ((f32x2_t*)out)[(orow * d) / 2 + t] = f32x2_t{res[2 * t], res[2 * t + 1]};
+}
+
+__global__ __launch_bounds__(512) void row_epilogue_kernel(const float* __restrict__ x, int d, int64_t ldx, int rows_per_pos,
+    const int32_t* __restrict__ pos, const float* __restrict__ norm_w, const float* __restrict__ cos_t,
+    const float* __restrict__ sin_t, int64_t n_pos, int rd, float eps, int sim, void* __restrict__ out, int out_dtype,
+    int64_t cache_rows) {
+  row_epilogue_body(blockIdx.x, x, d, ldx, rows_per_pos, pos, norm_w, cos_t, sin_t, n_pos, rd, eps, sim, out, out_dtype, cache_rows);
+}
+
+// The decode step's kv row epilogue (into the window cache) and compressor ring step in one
+// launch: both read only the input projection and share the thread layout (d/2 threads, channels
+// 2t and 2t+1).  Workgroups 0..B-1 step the rings, workgroups B..2B-1 write the kv rows.
+__global__ __launch_bounds__(kPoolThreads) void ring_kv_kernel(
+    float* __restrict__ ring_kv, float* __restrict__ ring_sc, const float* __restrict__ kv_p,
+    const float* __restrict__ score_p, const int32_t* __restrict__ pos_arr, const float* __restrict__ ape,
+    const float* __restrict__ norm_w, const float* __restrict__ cos_t, const float* __restrict__ sin_t,
+    int64_t n_pos, int d, int ratio, int rd, float eps, int sim, float* __restrict__ comp, int64_t comp_cap,
+    int64_t ldp, int64_t B,
+    const float* __restrict__ kx, int64_t ldk, const float* __restrict__ k_norm, const float* __restrict__ k_cos,
+    const float* __restrict__ k_sin, int64_t k_n_pos, int k_rd, float k_eps, int k_sim, void* __restrict__ k_cache,
+    int k_dtype, int64_t k_cache_rows) {
+  if ((int64_t)blockIdx.x < B)
+    ring_step_body(blockIdx.x, ring_kv, ring_sc, kv_p, score_p, pos_arr, ape, norm_w, cos_t, sin_t, n_pos, d, ratio, rd, eps, sim, comp, comp_cap, ldp);
+  else
+    row_epilogue_body((int64_t)blockIdx.x - B, kx, d, ldk, 1, pos_arr, k_norm, k_cos, k_sin, k_n_pos, k_rd, k_eps,
+                      k_sim, k_cache, k_dtype, k_cache_rows);
 }
 
 // ids [B, T] for sequences at positions pos[b]: columns 0..window-1 hold the window rows
@@ -521,10 +553,10 @@ __global__ __launch_bounds__(256) void decode_ids_kernel(const int32_t* __restri
   }
 }
 
-extern "C" int smla_ring_step(float* ring_kv, float* ring_sc, const float* kv_p, const float* score_p,
-                              const int32_t* pos, const float* ape, const float* norm_w, const float* cos_t,
-                              const float* sin_t, int64_t n_pos, int64_t B, int64_t d, int64_t ratio, int64_t rd,
-                              float eps, int sim, float* comp_cache, int64_t comp_cap, int64_t ld_p, void* stream) {
+static int check_ring_step(const float* ring_kv, const float* ring_sc, const float* kv_p, const float* score_p,
+                           const int32_t* pos, const float* ape, const float* norm_w, const float* cos_t,
+                           const float* sin_t, int64_t n_pos, int64_t B, int64_t d, int64_t ratio, int64_t rd,
+                           int sim, const float* comp_cache, int64_t comp_cap, int64_t ld_p) {
   if (!ring_kv || !ring_sc || !kv_p || !score_p || !pos || !ape || !norm_w || !cos_t || !sin_t || !comp_cache)
     return SMLA_E_NULL;
   if (B <= 0 || comp_cap < 0 || n_pos <= 0 || (ld_p != 0 && ld_p < 2 * d)) return SMLA_E_SHAPE;
@@ -534,6 +566,16 @@ extern "C" int smla_ring_step(float* ring_kv, float* ring_sc, const float* kv_p,
   if ((((uintptr_t)ring_kv | (uintptr_t)ring_sc | (uintptr_t)kv_p | (uintptr_t)score_p | (uintptr_t)ape) & 7) != 0 ||
       ld_p % 2 != 0)
     return SMLA_E_UNSUPPORTED;
+  return SMLA_OK;
+}
+
+extern "C" int smla_ring_step(float* ring_kv, float* ring_sc, const float* kv_p, const float* score_p,
+                              const int32_t* pos, const float* ape, const float* norm_w, const float* cos_t,
+                              const float* sin_t, int64_t n_pos, int64_t B, int64_t d, int64_t ratio, int64_t rd,
+                              float eps, int sim, float* comp_cache, int64_t comp_cap, int64_t ld_p, void* stream) {
+  int rc = check_ring_step(ring_kv, ring_sc, kv_p, score_p, pos, ape, norm_w, cos_t, sin_t, n_pos, B, d, ratio, rd,
+                           sim, comp_cache, comp_cap, ld_p);
+  if (rc) return rc;
   hipLaunchKernelGGL(ring_step_kernel, dim3((unsigned)B), dim3((unsigned)(d / 2)), 0, (hipStream_t)stream, ring_kv,
                      ring_sc, kv_p, score_p, pos, ape, norm_w, cos_t, sin_t, n_pos, (int)d, (int)ratio, (int)rd,
                      eps, sim, comp_cache, comp_cap, ld_p ? ld_p : 2 * d);
@@ -558,11 +600,9 @@ extern "C" int smla_quant_fp8_pow2(const void* x, int x_dtype, int64_t rows, int
   return SMLA_OK;
 }
 
-extern "C" int smla_row_epilogue(const float* x, int64_t rows, int64_t d, int64_t ldx, int64_t rows_per_pos,
-                                 const int32_t* pos,
-                                 const float* norm_w, const float* cos_t, const float* sin_t, int64_t n_pos,
-                                 int64_t rd, float eps, int sim, void* out, int out_dtype, int64_t cache_rows,
-                                 void* stream) {
+static int check_row_epilogue(const float* x, int64_t rows, int64_t d, int64_t ldx, int64_t rows_per_pos,
+                              const int32_t* pos, const float* cos_t, const float* sin_t, int64_t n_pos, int64_t rd,
+                              float eps, int sim, const void* out, int out_dtype, int64_t cache_rows) {
   if (!x || !out) return SMLA_E_NULL;
   if (rows <= 0 || d < 128 || d > 1024 || d % 64 != 0 || rows_per_pos <= 0 || rd < 0 || rd > d || rd % 2 != 0 ||
       cache_rows < 0 || rows > (int64_t)INT32_MAX || (ldx != 0 && ldx < d))
@@ -573,9 +613,42 @@ extern "C" int smla_row_epilogue(const float* x, int64_t rows, int64_t d, int64_
   if (sim == SMLA_SIM_FP8 && (d - rd) % 64 != 0) return SMLA_E_SHAPE;
   if (out_dtype != SMLA_F32 && out_dtype != SMLA_BF16) return SMLA_E_DTYPE;
   if (!(eps >= 0.f)) return SMLA_E_RANGE;
+  return SMLA_OK;
+}
+
+extern "C" int smla_row_epilogue(const float* x, int64_t rows, int64_t d, int64_t ldx, int64_t rows_per_pos,
+                                 const int32_t* pos,
+                                 const float* norm_w, const float* cos_t, const float* sin_t, int64_t n_pos,
+                                 int64_t rd, float eps, int sim, void* out, int out_dtype, int64_t cache_rows,
+                                 void* stream) {
+  int rc = check_row_epilogue(x, rows, d, ldx, rows_per_pos, pos, cos_t, sin_t, n_pos, rd, eps, sim, out, out_dtype,
+                              cache_rows);
+  if (rc) return rc;
   hipLaunchKernelGGL(row_epilogue_kernel, dim3((unsigned)rows), dim3((unsigned)(d / 2)), 0, (hipStream_t)stream, x,
                      (int)d, ldx ? ldx : d, (int)rows_per_pos, pos, norm_w, cos_t, sin_t, n_pos, (int)rd, eps, sim, out, out_dtype,
                      cache_rows);
+  SMLA_HIP_CHECK_LAUNCH();
+  return SMLA_OK;
+}
+
+extern "C" int smla_ring_step_kv(float* ring_kv, float* ring_sc, const float* kv_p, const float* score_p,
+                                 const int32_t* pos, const float* ape, const float* norm_w, const float* cos_t,
+                                 const float* sin_t, int64_t n_pos, int64_t B, int64_t d, int64_t ratio, int64_t rd,
+                                 float eps, int sim, float* comp_cache, int64_t comp_cap, int64_t ld_p,
+                                 const float* kv_x, int64_t ld_kv, const float* kv_norm, const float* kv_cos,
+                                 const float* kv_sin, int64_t kv_n_pos, int64_t kv_rd, float kv_eps, int kv_sim,
+                                 void* kv_cache, int kv_cache_dtype, int64_t kv_cache_rows, void* stream) {
+  int rc = check_ring_step(ring_kv, ring_sc, kv_p, score_p, pos, ape, norm_w, cos_t, sin_t, n_pos, B, d, ratio, rd,
+                           sim, comp_cache, comp_cap, ld_p);
+  if (rc) return rc;
+  rc = check_row_epilogue(kv_x, B, d, ld_kv, 1, pos, kv_cos, kv_sin, kv_n_pos, kv_rd, kv_eps, kv_sim, kv_cache,
+                          kv_cache_dtype, kv_cache_rows);
+  if (rc) return rc;
+  if (kv_cache_rows <= 0 || B > (int64_t)INT32_MAX / 2) return SMLA_E_SHAPE;
+  hipLaunchKernelGGL(ring_kv_kernel, dim3((unsigned)(2 * B)), dim3((unsigned)(d / 2)), 0, (hipStream_t)stream, ring_kv,
+                     ring_sc, kv_p, score_p, pos, ape, norm_w, cos_t, sin_t, n_pos, (int)d, (int)ratio, (int)rd, eps,
+                     sim, comp_cache, comp_cap, ld_p ? ld_p : 2 * d, B, kv_x, ld_kv ? ld_kv : d, kv_norm, kv_cos,
+                     kv_sin, kv_n_pos, (int)kv_rd, kv_eps, kv_sim, kv_cache, kv_cache_dtype, kv_cache_rows);
   SMLA_HIP_CHECK_LAUNCH();
   return SMLA_OK;
 }

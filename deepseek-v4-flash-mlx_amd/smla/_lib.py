@@ -52,6 +52,8 @@ _SIGNATURES = {
                                _int, _vp, _vp]),
     "smla_ring_step": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64,
                               _f32, _int, _vp, _i64, _i64, _vp]),
+    "smla_ring_step_kv": (_int, [_vp] * 9 + [_i64] * 5 + [_f32, _int, _vp, _i64, _i64, _vp, _i64, _vp, _vp, _vp,
+                                                           _i64, _i64, _f32, _int, _vp, _int, _i64, _vp]),
     "smla_quant_fp8_pow2": (_int, [_vp, _int, _i64, _i64, _vp, _vp, _vp]),
     "smla_row_epilogue": (_int, [_vp, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _i64, _i64, _f32, _int, _vp,
                                  _int, _i64, _vp]),

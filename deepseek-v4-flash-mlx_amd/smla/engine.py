@@ -22,7 +22,8 @@ sequences:
 RoPE tables: layers with a nonzero ratio (4 or 128) use YaRN (base 160000, factor 16 over 65536
 positions), ratio-0 layers plain base 10000 (``decode_engine.py:47,73``).  Every step runs on the HIP kernels:
 ``smla_linear`` (projections, fp32 results), ``smla_row_epilogue`` (the norms, RoPE, the fp8 round
-trip and the window-cache write), ``smla_ring_step``, ``smla_decode_ids``, ``smla_sparse_attn`` and
+trip and the window-cache write), ``smla_ring_step`` (with the kv row's epilogue as
+``smla_ring_step_kv`` in a step), ``smla_decode_ids``, ``smla_sparse_attn`` and
 ``smla_o_proj``.  Caches are device-resident and owned by the layer object.
 """
 from dataclasses import dataclass
@@ -208,9 +209,13 @@ class DecodeLayer:
         y = _proj(xn, self.w_in)                     # [B, sum of the projection widths] fp32
         c = self.cuts
         q = self.q_path(y[:, c[0]:c[1]], pos)
-        self.kv_append(y[:, c[1]:c[2]], pos)
         if self.ring_ratio:
-            self.ring_step(y[:, c[2]:c[3]], y[:, c[3]:c[4]], pos)
+            # the kv row's epilogue and the ring step in one launch (kv_append + ring_step)
+            ops.ring_step_kv(self.ring, y[:, c[2]:c[3]], y[:, c[3]:c[4]], pos, self.comp32, y[:, c[1]:c[2]],
+                             self.kv_a_norm, self.cos_t, self.sin_t, ROPE_HD, _lib.SIM_FP8, self.raw,
+                             cache_rows=self.max_pos)
+        else:
+            self.kv_append(y[:, c[1]:c[2]], pos)
         ids = self.index_list(pos, scores, k)
         o = _sa.sparse_attn_two_source(q[:, None], self.raw, self.comp, self.w.sinks.float(), ids[:, None],
                                        HEAD_DIM ** -0.5, dv=HEAD_DIM)

@@ -524,6 +524,44 @@ def row_epilogue(x, norm_w, pos, cos_t, sin_t, rd, sim, out, rows_per_pos=1, cac
     return out
 
 
+def ring_step_kv(ring, kv_p, score_p, pos, comp_cache, kv_x, kv_norm, cos_t, sin_t, rd, sim, kv_cache,
+                 cache_rows=None, eps=1e-6):
+    """``smla_ring_step_kv``: ``ring.step(kv_p, score_p, pos, comp_cache)`` and
+    ``row_epilogue(kv_x, kv_norm, pos, cos_t, sin_t, rd, sim, kv_cache, cache_rows=cache_rows)`` in
+    one launch (``oracle/decode_engine.py:81-84,96-105``), bit for bit the two calls' results.
+    kv_p/score_p [B, 2d] and kv_x [B, d] fp32: row-strided views pass as they are when 8-byte aligned
+    with even row strides (slices of one projection), anything else is packed.  kv_cache
+    [B, rows, d] bf16/fp32; cache_rows defaults to its rows.  Stream-ordered."""
+    _on_gpu(kv_p, score_p, pos, comp_cache, kv_x, kv_norm, cos_t, sin_t, kv_cache, ring.ring_kv)
+    for t in (ring.ring_kv, ring.ring_sc, comp_cache):
+        if not t.is_contiguous() or t.dtype != torch.float32:
+            raise ValueError("ring and compressed-cache tensors must be contiguous fp32")
+    if not kv_cache.is_contiguous():
+        raise ValueError("kv_cache must be contiguous")
+    B = ring.ring_kv.shape[0]
+    d = ring.ring_kv.shape[-1] // 2
+    if kv_cache.shape[0] != B or kv_cache.shape[-1] != d or comp_cache.shape[0] != B:
+        raise ValueError(f"kv_cache and comp_cache must hold {B} sequences of {d}-wide rows")
+
+    def rows(t, w):
+        if (t.dtype != torch.float32 or t.dim() != 2 or tuple(t.shape) != (B, w) or t.stride(1) != 1
+                or t.stride(0) % 2 or t.data_ptr() % 8):
+            t = t.float().reshape(B, w).contiguous()
+        return t
+
+    kv_p, score_p, kv_x = rows(kv_p, 2 * d), rows(score_p, 2 * d), rows(kv_x, d)
+    if kv_p.stride(0) != score_p.stride(0):
+        kv_p, score_p = kv_p.contiguous(), score_p.contiguous()
+    pos = pos.to(torch.int32).contiguous()
+    kv_norm = kv_norm.float().contiguous()
+    cos_t, sin_t = cos_t.float().contiguous(), sin_t.float().contiguous()
+    _lib.call("smla_ring_step_kv", _p(ring.ring_kv), _p(ring.ring_sc), _p(kv_p), _p(score_p), _p(pos), _p(ring.ape),
+              _p(ring.norm_w), _p(ring.cos_t), _p(ring.sin_t), ring.cos_t.shape[0], B, d, ring.ratio, ring.rd, 1e-6,
+              int(ring.sim), _p(comp_cache), comp_cache.shape[1], kv_p.stride(0), _p(kv_x), kv_x.stride(0),
+              _p(kv_norm), _p(cos_t), _p(sin_t), cos_t.shape[0], rd, float(eps), int(sim), _p(kv_cache),
+              dtype_code(kv_cache), kv_cache.shape[1] if cache_rows is None else cache_rows, _stream(kv_p))
+
+
 def decode_ids(pos, window, ratio, n_raw, ncomp, T, out=None, comp32=None, comp_out=None):
     """``smla_decode_ids``: [B, T] int32 ids (window rows, then the visible compressed rows offset
     by n_raw); with comp32/comp_out, an emitted compressed row is copied to bf16."""

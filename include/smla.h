@@ -27,6 +27,7 @@
  *   smla_ring_step            oracle/decode_engine.py:96-105   decode compressor ring step and cache append
  *   smla_quant_fp8_pow2       v4mlx/compressor.py:11-20        act_quant_sim (stored form: codes + pow2 scales)
  *   smla_row_epilogue         oracle/decode_engine.py:78-83    q/kv row norms, RoPE, fp8 sim, window-cache write
+ *   smla_ring_step_kv         oracle/decode_engine.py:81-84,96-105  kv window append + ring step in one launch
  *   smla_decode_ids           oracle/decode_engine.py:110-114  decode id list (window + visible compressed rows)
  *   smla_rotate_fp4           v4mlx/qat.py:8-31                hadamard_rotate, fp4_act_quant (and stored form)
  *                             v4mlx/compressor.py:57-59        the indexer compressor's key transform
@@ -330,6 +331,23 @@ int smla_row_epilogue(const float* x, int64_t rows, int64_t d, int64_t ldx, int6
                       const float* norm_w, const float* cos_t, const float* sin_t, int64_t n_pos,
                       int64_t rd, float eps, int sim, void* out, int out_dtype, int64_t cache_rows,
                       void* stream);
+
+/* smla_ring_step_kv: smla_ring_step and smla_row_epilogue for the same B sequences at positions
+ * pos[b], in one launch: the decode step's kv row (oracle/decode_engine.py:81-84) and its
+ * compressor ring (:96-105) both follow the input projection and read nothing else.  The ring
+ * arguments are smla_ring_step's.  kv_x [B, d] fp32 (the ring's d) rows ld_kv elements apart
+ * (0: d) are normed with kv_norm, their last kv_rd channels rotated with kv_cos/kv_sin
+ * [kv_n_pos, kv_rd/2], quantised as kv_sim says (SMLA_SIM_NONE / SMLA_SIM_FP8), and written to row
+ * pos[b] of kv_cache [B, kv_cache_rows, d] (kv_cache_rows > 0) in kv_cache_dtype (SMLA_F32 /
+ * SMLA_BF16).  Arguments are checked as the two entry points check them; the results are theirs
+ * bit for bit. */
+int smla_ring_step_kv(float* ring_kv, float* ring_sc, const float* kv_p, const float* score_p,
+                      const int32_t* pos, const float* ape, const float* norm_w, const float* cos_t,
+                      const float* sin_t, int64_t n_pos, int64_t B, int64_t d, int64_t ratio, int64_t rd,
+                      float eps, int sim, float* comp_cache, int64_t comp_cap, int64_t ld_p,
+                      const float* kv_x, int64_t ld_kv, const float* kv_norm, const float* kv_cos,
+                      const float* kv_sin, int64_t kv_n_pos, int64_t kv_rd, float kv_eps, int kv_sim,
+                      void* kv_cache, int kv_cache_dtype, int64_t kv_cache_rows, void* stream);
 
 /* smla_decode_ids: the decode id list of oracle/decode_engine.py:110-114 for B sequences at
  * positions pos [B]: ids [B, T] int32 (T >= window), columns 0..window-1 = window rows

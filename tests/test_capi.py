@@ -94,6 +94,13 @@ def test_host_validation_rejects_bad_arguments():
     a = list(ring_args)
     a[18] = 513                                                                  # odd projection row stride
     assert lib.smla_ring_step(*a) == -4
+    # ring_step_kv: the ring's checks, the row epilogue's, and a window cache with rows
+    rk = [fake] * 9 + [64, 2, 512, 4, 64, 1e-6, 0, fake, 8, 0]
+    kv = [fake, 0, fake, fake, fake, 64, 64, 1e-6, 1, fake, 1, 64, None]
+    assert lib.smla_ring_step_kv(*rk, *(kv[:11] + [0, None])) == -2             # kv_cache_rows 0
+    assert lib.smla_ring_step_kv(*rk, *(kv[:8] + [2] + kv[9:])) == -4           # rotate-fp4 sim on the kv row
+    assert lib.smla_ring_step_kv(*rk, *([None] + kv[1:])) == -1                 # kv_x missing
+    assert lib.smla_ring_step_kv(*(rk[:18] + [1025]), *kv) == -4                # odd projection row stride
     # rotate_fp4: row length, flags, codes without scales, dtype, alignment
     assert lib.smla_rotate_fp4(fake, 0, 4, 48, 3, fake, None, None, None) == -4
     assert lib.smla_rotate_fp4(fake, 0, 4, 2048, 3, fake, None, None, None) == -4

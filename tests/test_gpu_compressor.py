@@ -102,6 +102,42 @@ def test_ring_vs_oracle_ring(dev, fp8_sim):
         assert torch.equal(ring.ring_kv[b].cpu(), kvs) and torch.equal(ring.ring_sc[b].cpu(), scs)
 
 
+def test_ring_step_kv_equals_separate_calls(dev):
+    """smla_ring_step_kv (the kv row's epilogue and the ring step in one launch) against
+    smla_row_epilogue then smla_ring_step on the same inputs: ring state, compressed rows and
+    window-cache rows bit for bit, over steps that emit and steps that do not, with one sequence
+    at a negative position (left untouched by both)."""
+    from smla import _lib, ops
+    from smla import compressor as sc
+    announce("ring step + kv row epilogue in one launch")
+    g = torch.Generator().manual_seed(11)
+    B, d, r, rd, rows = 3, 512, 4, 64, 64
+    ape = torch.randn(r, 2 * d, generator=g)
+    nw = 1 + 0.1 * torch.randn(d, generator=g)
+    kvn = (1 + 0.1 * torch.randn(d, generator=g)).to(dev)
+    pre_kv, pre_sc = torch.randn(B, 6, 2 * d, generator=g), torch.randn(B, 6, 2 * d, generator=g)
+    rings, comps, caches = [], [], []
+    for _ in range(2):
+        ring = sc.Ring(B, d, ape, nw, ratio=r, rope_head_dim=rd, max_pos=4096, fp8_sim=True, device=dev)
+        ring.init_from_prefill(pre_kv.to(dev), pre_sc.to(dev))
+        rings.append(ring)
+        comps.append(torch.zeros(B, 16, d, device=dev))
+        caches.append(torch.zeros(B, rows, d, dtype=torch.bfloat16, device=dev))
+    cos_t, sin_t = rings[0].cos_t, rings[0].sin_t
+    for p in range(6, 16):
+        y = torch.randn(B, 5 * d, generator=g).to(dev)        # [kv row | kv proj | score proj], one projection
+        kv_x, kvp, scp = y[:, :d], y[:, d:3 * d], y[:, 3 * d:]
+        pos = torch.tensor([p, p + 1, -1 if p == 9 else p + 2], dtype=torch.int32, device=dev)
+        ops.row_epilogue(kv_x, kvn, pos, cos_t, sin_t, rd, _lib.SIM_FP8, caches[0], cache_rows=rows)
+        rings[0].step(kvp, scp, pos, comps[0])
+        ops.ring_step_kv(rings[1], kvp, scp, pos, comps[1], kv_x, kvn, cos_t, sin_t, rd, _lib.SIM_FP8, caches[1])
+    torch.cuda.synchronize()
+    assert torch.equal(rings[0].ring_kv, rings[1].ring_kv) and torch.equal(rings[0].ring_sc, rings[1].ring_sc)
+    assert torch.equal(comps[0], comps[1])
+    assert torch.equal(caches[0].view(torch.int16), caches[1].view(torch.int16))
+    assert comps[0].abs().sum() > 0 and caches[0].float().abs().sum() > 0   # rows were written
+
+
 def test_quant_fp8_encoder_every_code(dev):
     """The quantiser's e4m3 encoding on the device over every finite e4m3 value, every midpoint
     between neighbours and the floats next to each midpoint, tiny values, signed zeros and random
