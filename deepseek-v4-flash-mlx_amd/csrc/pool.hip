@@ -527,13 +527,12 @@ __global__ __launch_bounds__(kPoolThreads) void ring_kv_kernel(
 // max(0, p-window+1)..p (then -1), the rest n_raw + j for the (p+1)/ratio visible compressed rows
 // j (then -1).  Workgroup column 0 also copies a row the ring emitted at this step
 // ((p+1) % ratio == 0) from comp32 to comp_out in bf16.
-__global__ __launch_bounds__(256) void decode_ids_kernel(const int32_t* __restrict__ pos, int window, int ratio,
-                                                         int64_t n_raw, int64_t ncomp, int64_t T,
-                                                         int32_t* __restrict__ ids, const float* __restrict__ comp32,
-                                                         uint16_t* __restrict__ comp_out, int d) {
-  const int64_t b = blockIdx.y;
+// column block bx of sequence b's ids, run by one workgroup of 256 threads
+__device__ __attribute__((always_inline)) inline void decode_ids_body(int64_t bx, int64_t b,
+    const int32_t* __restrict__ pos, int window, int ratio, int64_t n_raw, int64_t ncomp, int64_t T,
+    int32_t* __restrict__ ids, const float* __restrict__ comp32, uint16_t* __restrict__ comp_out, int d) {
   const int64_t p = pos[b];
-  const int64_t j = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t j = bx * 256 + threadIdx.x;
   if (j < T) {
     int64_t id;
     if (j < window) {
@@ -545,11 +544,35 @@ __global__ __launch_bounds__(256) void decode_ids_kernel(const int32_t* __restri
     }
     ids[b * T + j] = (int32_t)id;
   }
-  if (blockIdx.x == 0 && comp_out && ratio > 0 && p >= 0 && (p + 1) % ratio == 0) {
+  if (bx == 0 && comp_out && ratio > 0 && p >= 0 && (p + 1) % ratio == 0) {
     const int64_t row = (p + 1) / ratio - 1;
     if (row < ncomp)
       for (int c = threadIdx.x; c < d; c += 256)
         comp_out[(b * ncomp + row) * d + c] = bf16_rne(comp32[(b * ncomp + row) * d + c]);
+  }
+}
+
+__global__ __launch_bounds__(256) void decode_ids_kernel(const int32_t* __restrict__ pos, int window, int ratio, int64_t n_raw, int64_t ncomp, int64_t T,
+    int32_t* __restrict__ ids, const float* __restrict__ comp32, uint16_t* __restrict__ comp_out, int d) {
+  decode_ids_body(blockIdx.x, blockIdx.y, pos, window, ratio, n_raw, ncomp, T, ids, comp32, comp_out, d);
+}
+
+// The decode step's per-head q epilogue (d = 512: 256 threads) and its id build in one launch:
+// workgroups 0..rows-1 take the q rows, the next nx * B the id column blocks (nx = ceil(T/256)),
+// sequence-major.
+__global__ __launch_bounds__(256) void q_ids_kernel(
+    const float* __restrict__ x, int d, int64_t ldx, int rows_per_pos, const int32_t* __restrict__ qpos,
+    const float* __restrict__ norm_w, const float* __restrict__ cos_t, const float* __restrict__ sin_t, int64_t n_pos,
+    int rd, float eps, int sim, void* __restrict__ out, int out_dtype, int64_t cache_rows, int64_t rows, int64_t nx,
+    const int32_t* __restrict__ pos, int window, int ratio, int64_t n_raw, int64_t ncomp, int64_t T,
+    int32_t* __restrict__ ids, const float* __restrict__ comp32, uint16_t* __restrict__ comp_out, int comp_d) {
+  const int64_t blk = blockIdx.x;
+  if (blk < rows) {
+    row_epilogue_body(blk, x, d, ldx, rows_per_pos, qpos, norm_w, cos_t, sin_t, n_pos, rd, eps, sim, out, out_dtype,
+                      cache_rows);
+  } else {
+    const int64_t i = blk - rows;
+    decode_ids_body(i % nx, i / nx, pos, window, ratio, n_raw, ncomp, T, ids, comp32, comp_out, comp_d);
   }
 }
 
@@ -653,18 +676,48 @@ extern "C" int smla_ring_step_kv(float* ring_kv, float* ring_sc, const float* kv
   return SMLA_OK;
 }
 
-extern "C" int smla_decode_ids(const int32_t* pos, int64_t B, int64_t window, int64_t ratio, int64_t n_raw,
-                               int64_t ncomp, int32_t* ids, int64_t T, const float* comp32, uint16_t* comp_out,
-                               int64_t d, void* stream) {
+static int check_decode_ids(const int32_t* pos, int64_t B, int64_t window, int64_t ratio, int64_t n_raw,
+                            int64_t ncomp, const int32_t* ids, int64_t T, const float* comp32,
+                            const uint16_t* comp_out, int64_t d) {
   if (!pos || !ids) return SMLA_E_NULL;
   if (B <= 0 || B > 65535 || window <= 0 || ratio < 0 || n_raw <= 0 || ncomp < 0 || T < window || d < 0)
     return SMLA_E_SHAPE;
   if ((comp32 == nullptr) != (comp_out == nullptr)) return SMLA_E_NULL;
   if (comp_out && (ratio == 0 || d <= 0)) return SMLA_E_SHAPE;
   if (n_raw + ncomp > (int64_t)INT32_MAX) return SMLA_E_RANGE;
+  return SMLA_OK;
+}
+
+extern "C" int smla_decode_ids(const int32_t* pos, int64_t B, int64_t window, int64_t ratio, int64_t n_raw,
+                               int64_t ncomp, int32_t* ids, int64_t T, const float* comp32, uint16_t* comp_out,
+                               int64_t d, void* stream) {
+  int rc = check_decode_ids(pos, B, window, ratio, n_raw, ncomp, ids, T, comp32, comp_out, d);
+  if (rc) return rc;
   const dim3 grid((unsigned)((T + 255) / 256), (unsigned)B);
   hipLaunchKernelGGL(decode_ids_kernel, grid, dim3(256), 0, (hipStream_t)stream, pos, (int)window, (int)ratio, n_raw,
                      ncomp, T, ids, comp32, comp_out, (int)d);
+  SMLA_HIP_CHECK_LAUNCH();
+  return SMLA_OK;
+}
+
+extern "C" int smla_row_epilogue_ids(const float* x, int64_t rows, int64_t d, int64_t ldx, int64_t rows_per_pos,
+                                     const int32_t* pos, const float* norm_w, const float* cos_t, const float* sin_t,
+                                     int64_t n_pos, int64_t rd, float eps, int sim, void* out, int out_dtype,
+                                     int64_t cache_rows, const int32_t* ids_pos, int64_t B, int64_t window,
+                                     int64_t ratio, int64_t n_raw, int64_t ncomp, int32_t* ids, int64_t T,
+                                     const float* comp32, uint16_t* comp_out, int64_t comp_d, void* stream) {
+  int rc = check_row_epilogue(x, rows, d, ldx, rows_per_pos, pos, cos_t, sin_t, n_pos, rd, eps, sim, out, out_dtype,
+                              cache_rows);
+  if (rc) return rc;
+  rc = check_decode_ids(ids_pos, B, window, ratio, n_raw, ncomp, ids, T, comp32, comp_out, comp_d);
+  if (rc) return rc;
+  if (d != 512) return SMLA_E_UNSUPPORTED;  // the id blocks' 256 threads are the rows' d/2
+  const int64_t nx = (T + 255) / 256;
+  if (rows + nx * B > (int64_t)INT32_MAX) return SMLA_E_SHAPE;
+  hipLaunchKernelGGL(q_ids_kernel, dim3((unsigned)(rows + nx * B)), dim3(256), 0, (hipStream_t)stream, x, (int)d,
+                     ldx ? ldx : d, (int)rows_per_pos, pos, norm_w, cos_t, sin_t, n_pos, (int)rd, eps, sim, out,
+                     out_dtype, cache_rows, rows, nx, ids_pos, (int)window, (int)ratio, n_raw, ncomp, T, ids, comp32,
+                     comp_out, (int)comp_d);
   SMLA_HIP_CHECK_LAUNCH();
   return SMLA_OK;
 }

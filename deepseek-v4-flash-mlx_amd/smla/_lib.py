@@ -57,6 +57,8 @@ _SIGNATURES = {
     "smla_quant_fp8_pow2": (_int, [_vp, _int, _i64, _i64, _vp, _vp, _vp]),
     "smla_row_epilogue": (_int, [_vp, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _i64, _i64, _f32, _int, _vp,
                                  _int, _i64, _vp]),
+    "smla_row_epilogue_ids": (_int, [_vp, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _i64, _i64, _f32, _int, _vp,
+                                     _int, _i64, _vp, _i64, _i64, _i64, _i64, _i64, _vp, _i64, _vp, _vp, _i64, _vp]),
     "smla_decode_ids": (_int, [_vp, _i64, _i64, _i64, _i64, _i64, _vp, _i64, _vp, _vp, _i64, _vp]),
     "smla_rotate_fp4": (_int, [_vp, _int, _i64, _i64, _int, _vp, _vp, _vp, _vp]),
     "smla_rope": (_int, [_vp, _int, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _i64, _int, _vp]),

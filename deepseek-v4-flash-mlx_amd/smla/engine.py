@@ -141,6 +141,29 @@ class DecodeLayer:
                              comp_out=comp[1])
         if take_all:
             return ids
+        return self._select(pos, scores, k)
+
+    def q_and_ids(self, qa_f, pos, scores=None, k=2048):
+        """``q_path`` and ``index_list`` of one decode step, with the per-head q epilogue and the id
+        build in one launch (``smla_row_epilogue_ids``): the same q and ids.  Runs after the ring
+        step, whose emitted row the id build copies."""
+        rows = qa_f.shape[0]
+        qa = torch.empty(rows, qa_f.shape[1], dtype=torch.bfloat16, device=qa_f.device)
+        ops.row_epilogue(qa_f, self.q_a_norm, None, None, None, 0, _lib.SIM_NONE, qa)
+        q = torch.empty(rows, N_HEADS, HEAD_DIM, dtype=torch.bfloat16, device=qa_f.device)
+        comp = (self.comp32, self.comp) if self.ring_ratio else (None, None)
+        take_all = scores is None or not self.ring_ratio
+        T = WINDOW + (self.ncap if take_all else 0)
+        ids = torch.empty(self.B, T, dtype=torch.int32, device=qa_f.device)
+        ops.row_epilogue_ids(_proj(qa, self.w.wq_b).view(rows * N_HEADS, HEAD_DIM), None, pos, self.cos_t,
+                             self.sin_t, ROPE_HD, _lib.SIM_NONE, q, N_HEADS, pos, WINDOW, self.ring_ratio,
+                             self.max_pos, self.ncap, T, ids, comp32=comp[0], comp_out=comp[1])
+        if take_all:
+            return q, ids
+        return q, self._select(pos, scores, k)
+
+    def _select(self, pos, scores, k):
+        """Window + top-k ids from indexer scores [B, ncap] (``decode_engine.py:110-114``)."""
         if scores.shape != (self.B, self.ncap):
             raise ValueError(f"scores must be [{self.B}, {self.ncap}] (one per compressed slot)")
         # visible compressed rows at p: (p+1)//4 (decode_engine.py:112), at most the cache's rows
@@ -208,7 +231,6 @@ class DecodeLayer:
                 raise ValueError(f"positions must lie in [0, {self.max_pos}); got {int(lo)}..{int(hi)}")
         y = _proj(xn, self.w_in)                     # [B, sum of the projection widths] fp32
         c = self.cuts
-        q = self.q_path(y[:, c[0]:c[1]], pos)
         if self.ring_ratio:
             # the kv row's epilogue and the ring step in one launch (kv_append + ring_step)
             ops.ring_step_kv(self.ring, y[:, c[2]:c[3]], y[:, c[3]:c[4]], pos, self.comp32, y[:, c[1]:c[2]],
@@ -216,7 +238,7 @@ class DecodeLayer:
                              cache_rows=self.max_pos)
         else:
             self.kv_append(y[:, c[1]:c[2]], pos)
-        ids = self.index_list(pos, scores, k)
+        q, ids = self.q_and_ids(y[:, c[0]:c[1]], pos, scores, k)
         o = _sa.sparse_attn_two_source(q[:, None], self.raw, self.comp, self.w.sinks.float(), ids[:, None],
                                        HEAD_DIM ** -0.5, dv=HEAD_DIM)
         return mla.o_project(o[:, 0].contiguous(), pos, self.cos_t, self.sin_t, self.w.wo_a, self.w.wo_b)

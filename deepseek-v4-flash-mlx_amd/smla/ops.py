@@ -524,6 +524,28 @@ def row_epilogue(x, norm_w, pos, cos_t, sin_t, rd, sim, out, rows_per_pos=1, cac
     return out
 
 
+def row_epilogue_ids(x, norm_w, pos, cos_t, sin_t, rd, sim, out, rows_per_pos, ids_pos, window, ratio, n_raw,
+                     ncomp, T, ids, comp32=None, comp_out=None, cache_rows=0, eps=1e-6):
+    """``smla_row_epilogue_ids``: ``row_epilogue(x, norm_w, pos, cos_t, sin_t, rd, sim, out,
+    rows_per_pos, cache_rows, eps)`` on rows of d = 512 and ``decode_ids(ids_pos, window, ratio,
+    n_raw, ncomp, T, ids, comp32, comp_out)`` in one launch, bit for bit the two calls' results."""
+    _on_gpu(x, out, ids_pos, ids, *(t for t in (norm_w, pos, cos_t, sin_t, comp32, comp_out) if t is not None))
+    if x.dtype != torch.float32 or x.stride(-1) != 1 or not out.is_contiguous():
+        raise ValueError("row_epilogue_ids: x must be fp32 with unit column stride and out contiguous")
+    if x.dim() != 2:
+        x = x.reshape(-1, x.shape[-1])
+    ids_pos = ids_pos.to(torch.int32).contiguous()
+    B = ids_pos.numel()
+    if ids.dtype != torch.int32 or not ids.is_contiguous() or tuple(ids.shape) != (B, T):
+        raise ValueError(f"ids must be a contiguous int32 [{B}, {T}] tensor")
+    n_pos = cos_t.shape[0] if cos_t is not None else 0
+    d_comp = comp32.shape[-1] if comp32 is not None else 0
+    _lib.call("smla_row_epilogue_ids", _p(x), x.shape[0], x.shape[-1], x.stride(0), rows_per_pos, _p(pos), _p(norm_w),
+              _p(cos_t), _p(sin_t), n_pos, rd, float(eps), int(sim), _p(out), dtype_code(out), cache_rows,
+              _p(ids_pos), B, window, ratio, n_raw, ncomp, _p(ids), T, _p(comp32), _p(comp_out), d_comp, _stream(x))
+    return out, ids
+
+
 def ring_step_kv(ring, kv_p, score_p, pos, comp_cache, kv_x, kv_norm, cos_t, sin_t, rd, sim, kv_cache,
                  cache_rows=None, eps=1e-6):
     """``smla_ring_step_kv``: ``ring.step(kv_p, score_p, pos, comp_cache)`` and

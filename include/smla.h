@@ -28,6 +28,7 @@
  *   smla_quant_fp8_pow2       v4mlx/compressor.py:11-20        act_quant_sim (stored form: codes + pow2 scales)
  *   smla_row_epilogue         oracle/decode_engine.py:78-83    q/kv row norms, RoPE, fp8 sim, window-cache write
  *   smla_ring_step_kv         oracle/decode_engine.py:81-84,96-105  kv window append + ring step in one launch
+ *   smla_row_epilogue_ids     oracle/decode_engine.py:78-80,110-114  per-head q epilogue + decode ids in one launch
  *   smla_decode_ids           oracle/decode_engine.py:110-114  decode id list (window + visible compressed rows)
  *   smla_rotate_fp4           v4mlx/qat.py:8-31                hadamard_rotate, fp4_act_quant (and stored form)
  *                             v4mlx/compressor.py:57-59        the indexer compressor's key transform
@@ -341,6 +342,19 @@ int smla_row_epilogue(const float* x, int64_t rows, int64_t d, int64_t ldx, int6
  * pos[b] of kv_cache [B, kv_cache_rows, d] (kv_cache_rows > 0) in kv_cache_dtype (SMLA_F32 /
  * SMLA_BF16).  Arguments are checked as the two entry points check them; the results are theirs
  * bit for bit. */
+/* smla_row_epilogue_ids: smla_row_epilogue (rows of d = 512; its arguments first) and
+ * smla_decode_ids (its arguments after cache_rows, with its own position array ids_pos and
+ * row width comp_d) in one launch: the decode step's per-head q norm and RoPE
+ * (oracle/decode_engine.py:78-80) and its id list (:110-114) share no data.  Arguments are
+ * checked as the two entry points check them (d other than 512: SMLA_E_UNSUPPORTED); the results
+ * are theirs bit for bit. */
+int smla_row_epilogue_ids(const float* x, int64_t rows, int64_t d, int64_t ldx, int64_t rows_per_pos,
+                          const int32_t* pos, const float* norm_w, const float* cos_t, const float* sin_t,
+                          int64_t n_pos, int64_t rd, float eps, int sim, void* out, int out_dtype,
+                          int64_t cache_rows, const int32_t* ids_pos, int64_t B, int64_t window,
+                          int64_t ratio, int64_t n_raw, int64_t ncomp, int32_t* ids, int64_t T,
+                          const float* comp32, uint16_t* comp_out, int64_t comp_d, void* stream);
+
 int smla_ring_step_kv(float* ring_kv, float* ring_sc, const float* kv_p, const float* score_p,
                       const int32_t* pos, const float* ape, const float* norm_w, const float* cos_t,
                       const float* sin_t, int64_t n_pos, int64_t B, int64_t d, int64_t ratio, int64_t rd,

@@ -101,6 +101,13 @@ def test_host_validation_rejects_bad_arguments():
     assert lib.smla_ring_step_kv(*rk, *(kv[:8] + [2] + kv[9:])) == -4           # rotate-fp4 sim on the kv row
     assert lib.smla_ring_step_kv(*rk, *([None] + kv[1:])) == -1                 # kv_x missing
     assert lib.smla_ring_step_kv(*(rk[:18] + [1025]), *kv) == -4                # odd projection row stride
+    # row_epilogue_ids: the row epilogue's checks, decode_ids', and rows of 512 only
+    re = [fake, 64, 512, 0, 64, fake, None, fake, fake, 64, 64, 1e-6, 0, fake, 1, 0]
+    di = [fake, 1, 128, 4, 1024, 256, fake, 384, None, None, 0, None]
+    assert lib.smla_row_epilogue_ids(*(re[:2] + [256] + re[3:]), *di) == -4      # d 256
+    assert lib.smla_row_epilogue_ids(*re, *(di[:2] + [0] + di[3:])) == -2       # window 0
+    assert lib.smla_row_epilogue_ids(*re, *(di[:6] + [None] + di[7:])) == -1    # ids missing
+    assert lib.smla_row_epilogue_ids(*(re[:12] + [2] + re[13:]), *di) == -4     # rotate-fp4 sim on q rows
     # rotate_fp4: row length, flags, codes without scales, dtype, alignment
     assert lib.smla_rotate_fp4(fake, 0, 4, 48, 3, fake, None, None, None) == -4
     assert lib.smla_rotate_fp4(fake, 0, 4, 2048, 3, fake, None, None, None) == -4

@@ -133,3 +133,38 @@ def test_decode_ids_brute_force(dev, ratio):
                 assert torch.equal(got[r], comp32[b, r].to(torch.bfloat16))
                 got[r] = 0
             assert torch.all(got.float() == 0)
+
+
+def test_row_epilogue_ids_equals_separate_calls(dev):
+    """smla_row_epilogue_ids (the per-head q epilogue and the decode id build in one launch) against
+    smla_row_epilogue then smla_decode_ids on the same inputs: q rows, ids and the emitted
+    compressed rows' bf16 copies bit for bit, with positions that emit, that do not, and one
+    negative position."""
+    from smla import _lib, ops
+    announce("row epilogue + decode ids in one launch")
+    g = torch.Generator().manual_seed(12)
+    B, H, d, rd, n_pos, ncomp, n_raw, window = 4, 64, 512, 64, 4096, 300, 4096, 128
+    T = window + ncomp
+    x = torch.randn(B * H, d, generator=g).to(dev)
+    cos_t = torch.randn(n_pos, rd // 2, generator=g).to(dev)
+    sin_t = torch.randn(n_pos, rd // 2, generator=g).to(dev)
+    comp32 = torch.randn(B, ncomp, d, generator=g).to(dev)
+    pos = torch.tensor([3, 1000, -1, 1199], dtype=torch.int32, device=dev)   # 3, 1199: a row completes
+    outs = []
+    for fused in (False, True):
+        q = torch.zeros(B, H, d, dtype=torch.bfloat16, device=dev)
+        ids = torch.zeros(B, T, dtype=torch.int32, device=dev)
+        comp_out = torch.zeros(B, ncomp, d, dtype=torch.bfloat16, device=dev)
+        if fused:
+            ops.row_epilogue_ids(x, None, pos, cos_t, sin_t, rd, _lib.SIM_NONE, q, H, pos, window, 4, n_raw, ncomp, T,
+                                 ids, comp32=comp32, comp_out=comp_out)
+        else:
+            ops.row_epilogue(x, None, pos, cos_t, sin_t, rd, _lib.SIM_NONE, q, rows_per_pos=H)
+            ops.decode_ids(pos, window, 4, n_raw, ncomp, T, out=ids, comp32=comp32, comp_out=comp_out)
+        outs.append((q, ids, comp_out))
+    torch.cuda.synchronize()
+    (q0, i0, c0), (q1, i1, c1) = outs
+    assert torch.equal(q0.view(torch.int16), q1.view(torch.int16))
+    assert torch.equal(i0, i1)
+    assert torch.equal(c0.view(torch.int16), c1.view(torch.int16))
+    assert q0.float().abs().sum() > 0 and c0.float().abs().sum() > 0 and (i0 >= 0).any()
