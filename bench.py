@@ -64,7 +64,7 @@ def parse():
     ap.add_argument("--rot", type=int, default=24, help="cache copies rotated across steps")
     ap.add_argument("--kernel-iters", type=int, default=96)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-steps", type=int, default=3)
+    ap.add_argument("--cpu-steps", type=int, default=5, help="CPU baseline: median of this many runs after 1 warm-up")
     ap.add_argument("--rows-per-split", type=int, default=0,
                     help="attention split plan: index-list rows per split, a multiple of 32 (0 = the default plan)")
     ap.add_argument("--decode-path", choices=("lists", "select-in-attn"), default="lists",
@@ -134,6 +134,7 @@ def prefill_measure(dev, reps):
                         "window 128 + causal compressed rows (smla_prefill_attn)",
             "ms": round(ms, 4), "flops": flops, "query_row_pairs": pairs, "tflops": round(tflops, 1),
             "mfma_peak_tflops": BF16_PEAK_TFLOPS, "mfma_util": round(tflops / BF16_PEAK_TFLOPS, 4),
+            "ms_method": f"the better of two timed rounds of {reps} passes each (5 untimed passes before each)",
             "ms_index_lists": round(ms_lists, 4)}
 
 
@@ -183,6 +184,23 @@ def other_workloads(dev, reps):
     from smla import workloads as wl
     res = {}
 
+    # ---- fp32_plumbing: B=1, H=16, fp32 q/rows [4096,576], fp32 indexer keys [4096,64], top-512,
+    # the fp32 attention (the vector-ALU kernel: fp32 operands keep the reference's precision)
+    w = wl.fp32_plumbing()
+    q1, kv1, qi1, ki1, w1 = (w[t].to(dev) for t in ("q", "kv", "q_idx", "k_idx", "w"))
+
+    def run_c1():
+        sc = sidx.indexer_score(qi1[None], ki1[None], None, w1[None])
+        sel = sidx.topk(sc[0], w["k"])
+        return ssa.sparse_attn(q1, kv1, None, sel, w["scale"], dv=w["dv"])
+    ms = _time_graph_ms(run_c1, reps)
+    gather = w["k"] * 576 * 4 + 16 * 576 * 4 + 16 * 512 * 4 + w["k"] * 4
+    res["fp32_plumbing"] = {"workload": "fp32_plumbing: B=1 H=16, fp32 q [16,576] and rows [4096,576], fp32 indexer "
+                                        "keys [4096,64] (16 heads), top-512, fp32 attention",
+                            "us_per_step": round(ms * 1e3, 3), "gather_bytes": gather,
+                            "achieved_gbs": round(gather / (ms * 1e-3) / 1e9, 1)}
+    del q1, kv1, qi1, ki1, w1
+
     # ---- decode_64k: one sequence, 20 consecutive positions 65516..65535; per step: indexer over
     # the (p+1)//4 visible compressed keys, window + top-2048 ids, attention, merge
     w = wl.decode_64k()
@@ -203,10 +221,15 @@ def other_workloads(dev, reps):
     ms = _time_graph_ms(run64, max(1, reps // 4), inner=1)
     per = ms / w["steps"]
     step_bytes = algorithmic_attention_bytes(1, 64, win + k)
+    nk = keys.shape[1]
+    idx_bytes = nk * (64 + 4) + nk * 4          # fp8 keys + scales read, scores written
     res["decode_64k"] = {"workload": "decode_64k: B=1 H=64, raw [65536,576] + mean-pooled [16384,576] bf16, fp8 keys "
                                      "[16384,64], 20 steps at positions 65516..65535, top-k 2048 + window 128",
                          "tok_s": round(w["steps"] / (ms * 1e-3), 1), "ms_per_step": round(per, 4),
-                         "attention_bytes_per_step": step_bytes}
+                         "attention_bytes_per_step": step_bytes, "indexer_bytes_per_step": idx_bytes,
+                         "achieved_gbs": round((step_bytes + idx_bytes) / (per * 1e-3) / 1e9, 1),
+                         "achieved_gbs_note": "attention + indexer algorithmic bytes over the whole step "
+                                              "(indexer, selection, attention, merge): a latency-bound step"}
 
     # ---- batched_fp8: 64 sequences, e4m3 rows with pow2 scales, 2048 ids each (attention + merge)
     w = wl.batched_fp8()
@@ -342,8 +365,8 @@ def other_workloads(dev, reps):
     ms = _time_graph_ms(lambda: layer.step(xn, pos), reps, inner=5)
     wbytes = sum(t.numel() * t.element_size() for t in (lw.wq_a, lw.wq_b, lw.wkv, lw.wo_a, lw.wo_b, lw.wkv_c,
                                                          lw.wgate_c))
-    res["decode_layer"] = {"workload": "decode_layer: one attention layer, B=8 tokens at position 32767, 32K window "
-                                       "cache + 8192 compressed rows (take-all: 128 + 8192 ids), 231 MB of bf16 "
+    res["decode_layer"] = {"workload": "decode_layer: one attention layer, B=8 tokens at position 32767, 128-row window "
+                                       "ring + 8192 compressed rows (take-all: 128 + 8192 ids), 231 MB of bf16 "
                                        "weights; graph of 5 steps",
                            "us": round(ms * 1e3, 3), "tok_s": round(B / (ms * 1e-3), 1), "weight_bytes": wbytes}
     del layer, lw
@@ -409,6 +432,101 @@ def cpu_baseline(w, nthreads, reps):
         times.append(time.perf_counter() - t0)
     med = float(np.median(times))
     return med
+
+
+def _median_time(fn, reps):
+    """Median wall time of `reps` calls of fn after one warm-up call."""
+    import numpy as np
+    fn()
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return float(np.median(times))
+
+
+def cpu_legs(nthreads, reps):
+    """The oracle on the other configurations, on the host's cores (median of `reps` after one
+    warm-up each): fp32_plumbing (whole step), prefill_4k (a sample of 8 of its 64 query chunks of
+    64, every 8th, extrapolated by query-row pairs), decode_64k (4 of its 20 steps) and batched_fp8
+    (all 64 sequences, each sequence's gathered rows dequantised)."""
+    import numpy as np
+    import torch
+    sys.path.insert(0, ROOT)
+    from oracle import compressor as ocomp
+    from oracle import indexer as oidx
+    from oracle import sparse_attn as osa
+    from smla import workloads as wl
+    torch.set_num_threads(nthreads)
+    res = {}
+
+    w = wl.fp32_plumbing()
+    qi, ki, wt = w["q_idx"].numpy(), w["k_idx"].numpy(), w["w"].numpy()
+
+    def c1():
+        sc = oidx.indexer_score(qi, ki, None, wt)
+        sel = oidx.topk(sc, w["k"])
+        osa.sparse_attn(w["q"], w["kv"], None, torch.from_numpy(sel), w["scale"], dv=w["dv"])
+    t = _median_time(c1, reps)
+    res["fp32_plumbing"] = {"ms_per_step": round(t * 1e3, 3), "sample": "the whole step (indexer, top-512, attention)"}
+
+    w = wl.prefill_4k()
+    q = w["q"][0].float()
+    raw = w["raw"]
+    comp = ocomp.mean_pool(raw, 4).to(torch.bfloat16)
+    kv = torch.cat([raw[0].float(), comp[0].float()])
+    idx = wl.prefill_indices(4096, ratio=4, window=128, n_raw=4096)
+    chunks = list(range(0, 64, 8))
+    pairs_all = int((idx >= 0).sum())
+    pairs_s = sum(int((idx[64 * c:64 * c + 64] >= 0).sum()) for c in chunks)
+
+    def c3():
+        for c in chunks:
+            osa.sparse_attn(q[64 * c:64 * c + 64], kv, None, idx[64 * c:64 * c + 64], w["scale"], dv=512)
+    t = _median_time(c3, reps)
+    res["prefill_4k"] = {"ms_sample": round(t * 1e3, 2), "sample_query_row_pairs": pairs_s,
+                         "ms_full_extrapolated": round(t * 1e3 * pairs_all / pairs_s, 1),
+                         "gflops": round(2.0 * pairs_s * 64 * 1088 / t / 1e9, 1),
+                         "sample": "8 of the 64 chunks of 64 queries (every 8th), extrapolated to the whole "
+                                   "prompt by query-row pairs"}
+    del q, raw, comp, kv
+
+    w = wl.decode_64k()
+    comp = ocomp.mean_pool(w["raw"], 4).to(torch.bfloat16)[0].float()
+    raw_f = w["raw"][0].float()
+    keys = w["k_codes"][0].view(torch.float8_e4m3fn).float().numpy()
+    ks = w["kscale"][0].numpy()
+    n_raw, win, k = raw_f.shape[0], w["window"], w["k"]
+
+    def c4():
+        for i in range(4):
+            p = w["pos0"] + i
+            nv = (p + 1) // 4
+            sc = oidx.indexer_score(w["q_idx"][i].float().numpy()[None], keys, ks, w["w"][i].numpy()[None],
+                                    np.array([nv], dtype=np.int32))
+            sel = oidx.topk(sc, k, np.array([nv], dtype=np.int32))[0]
+            kvb = torch.cat([raw_f[p - win + 1:p + 1], comp[torch.from_numpy(sel[sel >= 0]).long()]])
+            osa.sparse_attn(w["q"][i].float(), kvb, None, torch.arange(kvb.shape[0], dtype=torch.int32)[None],
+                            w["scale"], dv=512)
+    t = _median_time(c4, reps)
+    res["decode_64k"] = {"ms_per_step": round(t * 1e3 / 4, 3), "sample": "4 of the 20 steps (indexer over 16384 "
+                                                                         "keys, top-2048, attention)"}
+    del comp, raw_f, keys
+
+    w = wl.batched_fp8()
+
+    def c5():
+        for b in range(w["q"].shape[0]):
+            ids = w["idx"][b, 0]
+            ids = ids[ids >= 0].long()
+            rows = wl.dequant_e4m3(w["codes"][b, ids], w["scales"][b, ids])
+            osa.sparse_attn(w["q"][b].float(), rows, None, torch.arange(rows.shape[0], dtype=torch.int32)[None],
+                            w["scale"], dv=512)
+    t = _median_time(c5, reps)
+    res["batched_fp8"] = {"ms_per_step": round(t * 1e3, 2), "tok_s": round(64 / t, 1),
+                          "sample": "all 64 sequences (gathered rows dequantised, then attention)"}
+    return res
 
 
 def main():
@@ -632,6 +750,18 @@ def main():
                "cpu_model": _cpu_model(),
                "sample": f"one full decode step (8 sequences: indexer chain + top-k + attention), "
                          f"median of {args.cpu_steps} after 1 warm-up; {med * 1e3:.1f} ms/step"}
+        print("[bench] cpu legs of the other configurations", file=sys.stderr, flush=True)
+        legs = cpu_legs(ncores, args.cpu_steps)
+        for name, leg in legs.items():
+            leg.update(cores=ncores, kind="port", median_of=args.cpu_steps)
+        if prefill is not None:
+            prefill["cpu_baseline"] = legs.pop("prefill_4k")
+        if others is not None:
+            for name in list(legs):
+                if name in others:
+                    others[name]["cpu_baseline"] = legs.pop(name)
+        if legs:
+            cpu["other_configs"] = legs
 
     line = {
         "metric": METRIC,

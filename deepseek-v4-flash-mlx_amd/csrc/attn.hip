@@ -507,6 +507,7 @@ extern "C" int smla_decode_attn(const void* q, int q_dtype, const void* kv_raw, 
                                 void* workspace, size_t workspace_bytes, void* stream) {
   if (!scores || !pos) return SMLA_E_NULL;
   if (N <= 0 || window < 0 || k <= 0 || window + k > 0x7fffffff || N > 0x7fffffff) return SMLA_E_SHAPE;
+  if (window > n_raw) return SMLA_E_SHAPE;  // the raw ring must hold the window
   const int64_t T = window + k;
   // the list arguments are checked with a stand-in for the list pointer
   int rc = check_attn_args(q, q_dtype, kv_raw, n_raw, kv_comp, n_comp, kv_dtype, nullptr, nullptr, (const int32_t*)pos,

@@ -244,9 +244,12 @@ __global__ __launch_bounds__(768) void attn_decode_kernel(
     SL& sm = *(SL*)lds_generic;
     const int p = sr.pos[bs];
     auto valid = [&](int64_t r) -> int { return (r >= 0 && r < ntot) ? (int)r : -1; };
+    // window entry e: the row of position pp = p - window + 1 + e in the raw ring of n0 >= window
+    // rows (row pp mod n0), -1 before the sequence start
     for (int t = tid; t < nt; t += 768) {
       const int e = t_begin + t;
-      ids_s[t] = (t < nrows && e < sr.window) ? valid((int64_t)p - sr.window + 1 + e) : -1;
+      const int64_t pp = (int64_t)p - sr.window + 1 + e;
+      ids_s[t] = (t < nrows && e < sr.window && pp >= 0) ? (int)((uint32_t)pp % (uint32_t)n0) : -1;
     }
     if (t_end > sr.window) {  // uniform over the workgroup
       int nv = sr.nvis ? sr.nvis[bs] : sr.N;

@@ -468,8 +468,10 @@ extern "C" int smla_gated_pool(const float* kv, const float* score, const float*
 // One workgroup of d/2 threads per input row r (fp32, d channels): pool_epilogue (RMSNorm with
 // norm_w, or weightless when it is null; RoPE of the last rd channels at pos[r / rows_per_pos];
 // the `sim` quantisation), written in out_dtype to row r of `out` or, when cache_rows > 0, to row
-// pos of sequence r / rows_per_pos of a cache [.., cache_rows, d].  A position outside the rotation
-// table or the cache leaves the row unwritten.
+// pos mod cache_rows of sequence r / rows_per_pos of a cache [.., cache_rows, d]: a cache with a
+// row per position keeps every row, a shorter one is a ring of the last cache_rows positions (the
+// bounded window of oracle/v4_fast.py:93-96, winr[p % 128]).  A negative position, or one outside
+// the rotation table, leaves the row unwritten.
 // input row r, run by one workgroup of d/2 threads
 __device__ __attribute__((always_inline)) inline void row_epilogue_body(int64_t r,
     const float* __restrict__ x, int d, int64_t ldx, int rows_per_pos,
@@ -486,11 +488,11 @@ __device__ __attribute__((always_inline)) inline void row_epilogue_body(int64_t 
   EpiOperands eo = epilogue_weights(norm_w);
   const int64_t s = r / rows_per_pos;
   const int64_t p = pos ? (int64_t)pos[s] : 0;
-  const bool ok = (rd == 0 || (p >= 0 && p < n_pos)) && (cache_rows == 0 || (p >= 0 && p < cache_rows));
+  const bool ok = (rd == 0 || (p >= 0 && p < n_pos)) && (cache_rows == 0 || p >= 0);
   if (!ok) return;  // uniform over the workgroup
   if (rd) epilogue_rotation(eo, d, rd, cos_t, sin_t, p);
   pool_epilogue(v0, v1, d, rd, eps, sim, eo, red, xch, res);
-  const int64_t orow = cache_rows > 0 ? s * cache_rows + p : r;
+  const int64_t orow = cache_rows > 0 ? s * cache_rows + p % cache_rows : r;
   if (out_dtype == SMLA_BF16)
     ((uint32_t*)out)[(orow * d) / 2 + t] = pack_bf16x2(res[2 * t], res[2 * t + 1]);
   else
@@ -523,9 +525,10 @@ __global__ __launch_bounds__(kPoolThreads) void ring_kv_kernel(
                       k_sim, k_cache, k_dtype, k_cache_rows);
 }
 
-// ids [B, T] for sequences at positions pos[b]: columns 0..window-1 hold the window rows
-// max(0, p-window+1)..p (then -1), the rest n_raw + j for the (p+1)/ratio visible compressed rows
-// j (then -1).  Workgroup column 0 also copies a row the ring emitted at this step
+// ids [B, T] for sequences at positions pos[b]: columns 0..window-1 hold the rows of positions
+// max(0, p-window+1)..p (then -1) in the raw source of n_raw rows, where position pp lives at row
+// pp mod n_raw (a ring of n_raw >= window rows; the identity for a cache with a row per position),
+// the rest n_raw + j for the (p+1)/ratio visible compressed rows j (then -1).  Workgroup column 0 also copies a row the ring emitted at this step
 // ((p+1) % ratio == 0) from comp32 to comp_out in bf16.
 // column block bx of sequence b's ids, run by one workgroup of 256 threads
 __device__ __attribute__((always_inline)) inline void decode_ids_body(int64_t bx, int64_t b,
@@ -537,7 +540,7 @@ __device__ __attribute__((always_inline)) inline void decode_ids_body(int64_t bx
     int64_t id;
     if (j < window) {
       const int64_t lo = p - window + 1 > 0 ? p - window + 1 : 0;
-      id = lo + j <= p ? lo + j : -1;
+      id = lo + j <= p ? (int64_t)((uint64_t)(lo + j) % (uint64_t)n_raw) : -1;
     } else {
       const int64_t c = j - window;
       id = (ratio > 0 && c < ncomp && c < (p + 1) / ratio) ? n_raw + c : -1;
@@ -682,6 +685,7 @@ static int check_decode_ids(const int32_t* pos, int64_t B, int64_t window, int64
   if (!pos || !ids) return SMLA_E_NULL;
   if (B <= 0 || B > 65535 || window <= 0 || ratio < 0 || n_raw <= 0 || ncomp < 0 || T < window || d < 0)
     return SMLA_E_SHAPE;
+  if (window > n_raw) return SMLA_E_SHAPE;  // a ring shorter than the window would alias its rows
   if ((comp32 == nullptr) != (comp_out == nullptr)) return SMLA_E_NULL;
   if (comp_out && (ratio == 0 || d <= 0)) return SMLA_E_SHAPE;
   if (n_raw + ncomp > (int64_t)INT32_MAX) return SMLA_E_RANGE;

@@ -59,10 +59,12 @@ __global__ __launch_bounds__(NT) void topk_kernel(const float* scores, int64_t N
   if (nv < 0) nv = 0;
   int32_t* orow = out + r * out_stride;
   if (wpos) {
+    // position v of the window lives at raw row v mod id_offset (the raw source is a ring of
+    // id_offset >= window rows; the identity for a cache with a row per position)
     const int64_t p = wpos[r];
     for (int j = tid; j < window; j += NT) {
       const int64_t v = p - window + 1 + j;
-      orow[j] = v < 0 ? -1 : (int32_t)v;
+      orow[j] = v < 0 ? -1 : (int32_t)(id_offset > 0 ? (uint32_t)v % (uint32_t)id_offset : (uint32_t)v);
     }
     orow += window;
   }
@@ -166,6 +168,7 @@ extern "C" int smla_select_decode(const float* scores, int64_t R, int64_t N, con
   if (!scores || !out || !pos) return SMLA_E_NULL;
   if (R <= 0 || N <= 0 || k <= 0 || window < 0 || out_stride < k + window) return SMLA_E_SHAPE;
   if (R > 0x7fffffff || k > 0x7fffffff || window > 0x7fffffff) return SMLA_E_UNSUPPORTED;
+  if (id_offset > 0 && window > id_offset) return SMLA_E_SHAPE;  // a raw ring shorter than the window
   if ((N + kTopkThreads - 1) / kTopkThreads > 64) return SMLA_E_UNSUPPORTED;
   return launch_select(scores, R, N, nvis, k, out, out_stride, id_offset, pos, (int)window, (hipStream_t)stream);
 }
@@ -185,6 +188,7 @@ extern "C" int smla_index_decode(const void* q, int q_dtype, const void* keys, i
   if (B <= 0 || S <= 0 || Hi <= 0 || Di <= 0 || N <= 0 || k <= 0 || window < 0 || out_stride < k + window)
     return SMLA_E_SHAPE;
   if (flags & ~SMLA_INDEX_EXACT) return SMLA_E_RANGE;
+  if (window > 0 && id_offset > 0 && window > id_offset) return SMLA_E_SHAPE;
   if (!workspace || workspace_bytes < smla_index_decode_workspace(B, S, N)) return SMLA_E_WORKSPACE;
   const int64_t R = B * S;
   if (R > 65535 || k > 0x7fffffff || window > 0x7fffffff || (N + kTopkThreads - 1) / kTopkThreads > 64)

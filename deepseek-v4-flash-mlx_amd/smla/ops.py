@@ -505,11 +505,47 @@ def decode_window_idxs(pos, window, out=None):
     return out
 
 
+def _check_row_epilogue(x, norm_w, pos, cos_t, rd, out, rows_per_pos, cache_rows):
+    """Sizes the row epilogue's kernel relies on (the C entry cannot see tensor extents): one
+    position per rows_per_pos input rows, a norm weight per channel, rd/2 table columns, and room
+    in out for every row (row r, or row pos mod cache_rows of sequence r // rows_per_pos)."""
+    rows, d = (x.shape[0], x.shape[-1]) if x.dim() == 2 else (x.numel() // x.shape[-1], x.shape[-1])
+    if rows_per_pos < 1 or rows % rows_per_pos:
+        raise ValueError(f"row_epilogue: {rows} rows are not a whole number of {rows_per_pos}-row positions")
+    seqs = rows // rows_per_pos
+    if pos is not None and pos.numel() != seqs:
+        raise ValueError(f"row_epilogue: pos must hold {seqs} positions, got {pos.numel()}")
+    if (rd or cache_rows) and pos is None:
+        raise ValueError("row_epilogue: RoPE and the cache write need positions")
+    if norm_w is not None and norm_w.numel() != d:
+        raise ValueError(f"row_epilogue: norm_w must hold {d} weights, got {norm_w.numel()}")
+    if rd and (cos_t is None or cos_t.dim() != 2 or cos_t.shape[1] != rd // 2):
+        raise ValueError(f"row_epilogue: cos/sin tables must be [n_pos, {rd // 2}]")
+    need = seqs * cache_rows * d if cache_rows > 0 else rows * d
+    if out.numel() < need:
+        raise ValueError(f"row_epilogue: out holds {out.numel()} elements, the rows need {need}")
+
+
+def _check_decode_ids(B, ncomp, T, ids, comp32, comp_out):
+    """The id list and the emitted-row copy address ids [B, T] and comp32 / comp_out [B, ncomp, d]."""
+    if ids is not None and (ids.dtype != torch.int32 or not ids.is_contiguous() or tuple(ids.shape) != (B, T)):
+        raise ValueError(f"ids must be a contiguous int32 [{B}, {T}] tensor")
+    if (comp32 is None) != (comp_out is None):
+        raise ValueError("comp32 and comp_out go together")
+    if comp32 is not None:
+        for t in (comp32, comp_out):
+            if t.dim() != 3 or tuple(t.shape[:2]) != (B, ncomp) or not t.is_contiguous():
+                raise ValueError(f"comp32 / comp_out must be contiguous [{B}, {ncomp}, d] tensors")
+        if comp32.shape != comp_out.shape:
+            raise ValueError("comp32 and comp_out must have the same shape")
+
+
 def row_epilogue(x, norm_w, pos, cos_t, sin_t, rd, sim, out, rows_per_pos=1, cache_rows=0, eps=1e-6):
     """``smla_row_epilogue``: rows of x [rows, d] fp32 -> RMSNorm (norm_w [d], or None for the
     weightless norm) -> RoPE of the last rd channels at pos[row // rows_per_pos] -> `sim` -> out
-    (bf16 or fp32): row r of out [rows, d], or with cache_rows > 0 row pos of sequence
-    r // rows_per_pos of a cache [.., cache_rows, d].  Stream-ordered; returns out."""
+    (bf16 or fp32): row r of out [rows, d], or with cache_rows > 0 row pos mod cache_rows of
+    sequence r // rows_per_pos of a cache [.., cache_rows, d].  Stream-ordered; returns out."""
+    _check_row_epilogue(x, norm_w, pos, cos_t, rd, out, rows_per_pos, cache_rows)
     _on_gpu(x, out, *(t for t in (norm_w, pos, cos_t, sin_t) if t is not None))
     if x.dtype != torch.float32 or x.stride(-1) != 1 or not out.is_contiguous():
         raise ValueError("row_epilogue: x must be fp32 with unit column stride and out contiguous")
@@ -529,6 +565,8 @@ def row_epilogue_ids(x, norm_w, pos, cos_t, sin_t, rd, sim, out, rows_per_pos, i
     """``smla_row_epilogue_ids``: ``row_epilogue(x, norm_w, pos, cos_t, sin_t, rd, sim, out,
     rows_per_pos, cache_rows, eps)`` on rows of d = 512 and ``decode_ids(ids_pos, window, ratio,
     n_raw, ncomp, T, ids, comp32, comp_out)`` in one launch, bit for bit the two calls' results."""
+    _check_row_epilogue(x, norm_w, pos, cos_t, rd, out, rows_per_pos, cache_rows)
+    _check_decode_ids(ids_pos.numel(), ncomp, T, ids, comp32, comp_out)
     _on_gpu(x, out, ids_pos, ids, *(t for t in (norm_w, pos, cos_t, sin_t, comp32, comp_out) if t is not None))
     if x.dtype != torch.float32 or x.stride(-1) != 1 or not out.is_contiguous():
         raise ValueError("row_epilogue_ids: x must be fp32 with unit column stride and out contiguous")
@@ -536,8 +574,6 @@ def row_epilogue_ids(x, norm_w, pos, cos_t, sin_t, rd, sim, out, rows_per_pos, i
         x = x.reshape(-1, x.shape[-1])
     ids_pos = ids_pos.to(torch.int32).contiguous()
     B = ids_pos.numel()
-    if ids.dtype != torch.int32 or not ids.is_contiguous() or tuple(ids.shape) != (B, T):
-        raise ValueError(f"ids must be a contiguous int32 [{B}, {T}] tensor")
     n_pos = cos_t.shape[0] if cos_t is not None else 0
     d_comp = comp32.shape[-1] if comp32 is not None else 0
     _lib.call("smla_row_epilogue_ids", _p(x), x.shape[0], x.shape[-1], x.stride(0), rows_per_pos, _p(pos), _p(norm_w),
@@ -554,6 +590,11 @@ def ring_step_kv(ring, kv_p, score_p, pos, comp_cache, kv_x, kv_norm, cos_t, sin
     kv_p/score_p [B, 2d] and kv_x [B, d] fp32: row-strided views pass as they are when 8-byte aligned
     with even row strides (slices of one projection), anything else is packed.  kv_cache
     [B, rows, d] bf16/fp32; cache_rows defaults to its rows.  Stream-ordered."""
+    B0 = ring.ring_kv.shape[0]
+    if pos.numel() != B0:
+        raise ValueError(f"ring_step_kv: pos must hold {B0} positions, got {pos.numel()}")
+    if cache_rows is not None and not 0 < cache_rows <= kv_cache.shape[1]:
+        raise ValueError(f"ring_step_kv: cache_rows must lie in 1..{kv_cache.shape[1]}")
     _on_gpu(kv_p, score_p, pos, comp_cache, kv_x, kv_norm, cos_t, sin_t, kv_cache, ring.ring_kv)
     for t in (ring.ring_kv, ring.ring_sc, comp_cache):
         if not t.is_contiguous() or t.dtype != torch.float32:
@@ -587,6 +628,7 @@ def ring_step_kv(ring, kv_p, score_p, pos, comp_cache, kv_x, kv_norm, cos_t, sin
 def decode_ids(pos, window, ratio, n_raw, ncomp, T, out=None, comp32=None, comp_out=None):
     """``smla_decode_ids``: [B, T] int32 ids (window rows, then the visible compressed rows offset
     by n_raw); with comp32/comp_out, an emitted compressed row is copied to bf16."""
+    _check_decode_ids(pos.numel(), ncomp, T, out, comp32, comp_out)
     _on_gpu(pos, *(t for t in (out, comp32, comp_out) if t is not None))
     pos = pos.to(torch.int32).contiguous()
     B = pos.numel()

@@ -97,6 +97,13 @@ int smla_api_version(void);
  *   p_t = exp(scale q.kv[idx_t] - m), m = max over valid t.  No valid index -> NaN.
  * Duplicate ids count once per occurrence.
  *
+ * Kernels: q BF16 with BF16 or FP8 rows, H % 16 == 0, D 576 or 512, DV 512, B*S <= 65535 and a
+ * plan of at most 1024 splits (index lists up to 8192 rows per split) run the split-K MFMA kernel
+ * plus the merge; every other call (F32 / F16 operands, other H / D / DV, more query rows or
+ * splits) runs the vector-ALU kernel, one workgroup per (query row, head), with the same results
+ * to the tolerance of its dtype (both kernels are tested against the oracle for F32, BF16 and FP8
+ * rows).
+ *
  * workspace: smla_sparse_attn_workspace() bytes (split-K partial states), may be 0.
  */
 int smla_sparse_attn(const void* q, int q_dtype,
@@ -178,7 +185,9 @@ int smla_prefill_attn(const void* q, int q_dtype, const void* kv_raw, int64_t n_
  * Decode attention over the engine's index build in one call.  Replaces
  * oracle/decode_engine.py:110-117 (widx + cidx, then sparse_attn over [window; compressed]) with
  * the compressed part ranked by indexer scores: query row r (of R = B*S) attends
- *   raw rows pos[r]-window+1 .. pos[r] (those >= 0)  (ids 0 .. n_raw-1)
+ *   the raw rows of positions pos[r]-window+1 .. pos[r] (those >= 0), position pp at row
+ *   pp mod n_raw (ids 0 .. n_raw-1; kv_raw is a ring of n_raw >= window rows, e.g. the 128-row
+ *   window of oracle/v4_fast.py:93-96, or a cache with a row per position)
  *   the min(k, nvis[r]) best of scores[r, 0 .. nvis[r]-1] (score descending, index ascending,
  *   -0 == +0), compressed row c as id n_raw + c
  * i.e. the list smla_select_decode(scores, R, N, nvis, k, pos, window, ids, window+k, n_raw)
@@ -189,7 +198,7 @@ int smla_prefill_attn(const void* q, int q_dtype, const void* kv_raw, int64_t n_
  *   q [B,S,H,D] BF16, kv_raw [B,n_raw,D], kv_comp [B,n_comp,D] BF16 (or F32 / F16: list path),
  *   scores [R,N] F32, nvis [R] int32 or NULL (all N), pos [R] int32, out [B,S,H,DV] BF16 or F32.
  * workspace: smla_decode_attn_workspace(B, S, H, D, DV, window, k, q_dtype, kv_dtype, out_dtype)
- * bytes.  Requires N <= 65536. */
+ * bytes.  Requires N <= 65536 and window <= n_raw (else SMLA_E_SHAPE). */
 size_t smla_decode_attn_workspace(int64_t B, int64_t S, int64_t H, int64_t D, int64_t DV, int64_t window,
                                   int64_t k, int q_dtype, int kv_dtype, int out_dtype);
 int smla_decode_attn(const void* q, int q_dtype, const void* kv_raw, int64_t n_raw, const void* kv_comp,
@@ -249,9 +258,12 @@ int smla_topk(const float* scores, int64_t R, int64_t N, const int32_t* nvis, in
               int32_t* out, int64_t out_stride, int32_t id_offset, void* stream);
 
 /* The whole decode index build of oracle/decode_engine.py:110-114 in one launch: for row r,
- * out[r*out_stride + j] = pos[r]-window+1+j (or -1 where negative) for j < window, then the
- * smla_topk selection of scores row r (ids + id_offset, -1 padded) at columns window..window+k-1.
- * pos: [R] int32 on the device; out_stride >= window + k. */
+ * out[r*out_stride + j] = the raw row of position pp = pos[r]-window+1+j (or -1 where pp < 0) for
+ * j < window, then the smla_topk selection of scores row r (ids + id_offset, -1 padded) at columns
+ * window..window+k-1.  The raw row of position pp is pp mod id_offset when id_offset > 0 (the
+ * raw source is a ring of id_offset rows, the ring order of ref_torch/sparse_attn.py:11-13; a cache
+ * with a row per position is the identity), else pp.  pos: [R] int32 on the device;
+ * out_stride >= window + k; window <= id_offset when id_offset > 0 (else SMLA_E_SHAPE). */
 int smla_select_decode(const float* scores, int64_t R, int64_t N, const int32_t* nvis, int64_t k,
                        const int32_t* pos, int64_t window, int32_t* out, int64_t out_stride,
                        int32_t id_offset, void* stream);
@@ -324,10 +336,11 @@ int smla_ring_step(float* ring_kv, float* ring_sc, const float* kv_p, const floa
  * 26-28), RoPE of the last rd channels (ref_torch/norm_rope.py:53-62, interleaved pairs, cos/sin
  * [n_pos, rd/2]) at position pos[r / rows_per_pos], then `sim` (SMLA_SIM_NONE or SMLA_SIM_FP8: the
  * d-rd other channels fp8 round-tripped, v4mlx/compressor.py:11-20).  Row r goes to row r of out
- * [rows, d] (SMLA_F32 / SMLA_BF16), or, with cache_rows > 0, to row pos of sequence r / rows_per_pos
- * of a cache [.., cache_rows, d] (the window append, decode_engine.py:84).  eps: the RMSNorm eps.
- * ldx: elements between consecutive input rows (0: d).  A row whose position lies outside
- * [0, n_pos) (when rd > 0) or [0, cache_rows) is not written. */
+ * [rows, d] (SMLA_F32 / SMLA_BF16), or, with cache_rows > 0, to row pos mod cache_rows of sequence
+ * r / rows_per_pos of a cache [.., cache_rows, d] (the window append, decode_engine.py:84; a cache
+ * shorter than the positions is the ring of oracle/v4_fast.py:93-96, winr[p % 128]).  eps: the
+ * RMSNorm eps.  ldx: elements between consecutive input rows (0: d).  A row whose position is
+ * negative or lies outside [0, n_pos) (when rd > 0) is not written. */
 int smla_row_epilogue(const float* x, int64_t rows, int64_t d, int64_t ldx, int64_t rows_per_pos, const int32_t* pos,
                       const float* norm_w, const float* cos_t, const float* sin_t, int64_t n_pos,
                       int64_t rd, float eps, int sim, void* out, int out_dtype, int64_t cache_rows,
@@ -339,7 +352,7 @@ int smla_row_epilogue(const float* x, int64_t rows, int64_t d, int64_t ldx, int6
  * arguments are smla_ring_step's.  kv_x [B, d] fp32 (the ring's d) rows ld_kv elements apart
  * (0: d) are normed with kv_norm, their last kv_rd channels rotated with kv_cos/kv_sin
  * [kv_n_pos, kv_rd/2], quantised as kv_sim says (SMLA_SIM_NONE / SMLA_SIM_FP8), and written to row
- * pos[b] of kv_cache [B, kv_cache_rows, d] (kv_cache_rows > 0) in kv_cache_dtype (SMLA_F32 /
+ * pos[b] mod kv_cache_rows of kv_cache [B, kv_cache_rows, d] (kv_cache_rows > 0) in kv_cache_dtype (SMLA_F32 /
  * SMLA_BF16).  Arguments are checked as the two entry points check them; the results are theirs
  * bit for bit. */
 /* smla_row_epilogue_ids: smla_row_epilogue (rows of d = 512; its arguments first) and
@@ -364,9 +377,11 @@ int smla_ring_step_kv(float* ring_kv, float* ring_sc, const float* kv_p, const f
                       void* kv_cache, int kv_cache_dtype, int64_t kv_cache_rows, void* stream);
 
 /* smla_decode_ids: the decode id list of oracle/decode_engine.py:110-114 for B sequences at
- * positions pos [B]: ids [B, T] int32 (T >= window), columns 0..window-1 = window rows
- * max(0, p-window+1)..p then -1, columns window.. = n_raw + j for the (p+1)/ratio visible
- * compressed rows j < ncomp (ratio 0: none), then -1.  With comp32 / comp_out (both or neither;
+ * positions pos [B]: ids [B, T] int32 (T >= window), columns 0..window-1 = the raw rows of
+ * positions max(0, p-window+1)..p (position pp at row pp mod n_raw: a ring of n_raw >= window
+ * rows, or a cache with a row per position) then -1, columns window.. = n_raw + j for the (p+1)/ratio visible
+ * compressed rows j < ncomp (ratio 0: none), then -1 (window <= n_raw, else SMLA_E_SHAPE).
+ * With comp32 / comp_out (both or neither;
  * [B, ncomp, d] fp32 / bf16), a row the ring emitted at this step ((p+1) % ratio == 0) is copied
  * to comp_out as bf16. */
 int smla_decode_ids(const int32_t* pos, int64_t B, int64_t window, int64_t ratio, int64_t n_raw, int64_t ncomp,

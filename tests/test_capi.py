@@ -137,6 +137,9 @@ def test_host_validation_rejects_bad_arguments():
     assert lib.smla_decode_ids(fake, 2, 128, 4, 512, 16, fake, 100, None, None, 0, None) == -2
     assert lib.smla_decode_ids(fake, 2, 128, 4, 512, 16, fake, 144, fake, None, 512, None) == -1
     assert lib.smla_decode_ids(fake, 2, 128, 0, 512, 16, fake, 144, fake, fake, 512, None) == -2
+    # a raw ring shorter than the window would alias its rows: decode_ids, select_decode
+    assert lib.smla_decode_ids(fake, 2, 128, 4, 100, 16, fake, 144, None, None, 0, None) == -2
+    assert lib.smla_select_decode(fake, 2, 1024, None, 64, fake, 128, fake, 192, 100, None) == -2
 
 
 def _cpu_decode_layer():
@@ -253,3 +256,57 @@ def test_device_fp4_codec_matches_oracle(codec):
     np.testing.assert_array_equal(got, qat.fp4_scale_exponent(amax))
     for lg in range(5, 11):
         assert codec.host_hadamard_scale(lg) == qat.rotate_scale(2 ** lg)
+
+
+def test_layer_wrappers_check_sizes():
+    """The fused layer wrappers check the extents the C entries cannot see before anything reaches a
+    kernel: one position per sequence, norm weights per channel, table width, room in out (rows or
+    the cache), the ids and emitted-row buffers, and ring_step_kv's position count and cache rows.
+    The checks come before the device check, so CPU tensors show them."""
+    from smla import _lib, ops
+    x = torch.zeros(4, 512)
+    out = torch.zeros(4, 512)
+    pos = torch.zeros(4, dtype=torch.int32)
+    cs = torch.zeros(64, 32)
+    re = lambda **kw: ops.row_epilogue(**{**dict(x=x, norm_w=None, pos=pos, cos_t=cs, sin_t=cs, rd=64,
+                                                 sim=_lib.SIM_NONE, out=out), **kw})
+    with pytest.raises(ValueError, match="positions"):
+        re(pos=torch.zeros(3, dtype=torch.int32))                        # pos count != rows
+    with pytest.raises(ValueError, match="whole number"):
+        re(rows_per_pos=3)                                               # 4 rows, 3 per position
+    with pytest.raises(ValueError, match="norm_w"):
+        re(norm_w=torch.ones(256))
+    with pytest.raises(ValueError, match="tables"):
+        re(cos_t=torch.zeros(64, 16), sin_t=torch.zeros(64, 16))
+    with pytest.raises(ValueError, match="out holds"):
+        re(out=torch.zeros(3, 512))                                      # too few rows
+    with pytest.raises(ValueError, match="out holds"):
+        re(out=torch.zeros(4, 8, 512), cache_rows=16)                    # cache of 8 rows, 16 claimed
+    with pytest.raises(ValueError, match="need positions"):
+        re(pos=None)
+    # decode_ids: ids shape, emitted-row buffers
+    ids_pos = torch.zeros(2, dtype=torch.int32)
+    with pytest.raises(ValueError, match="ids must be"):
+        ops.decode_ids(ids_pos, 128, 4, 128, 16, 144, out=torch.zeros(2, 100, dtype=torch.int32))
+    with pytest.raises(ValueError, match="comp32 / comp_out"):
+        ops.decode_ids(ids_pos, 128, 4, 128, 16, 144, comp32=torch.zeros(2, 8, 512),
+                       comp_out=torch.zeros(2, 8, 512, dtype=torch.bfloat16))
+    with pytest.raises(ValueError, match="go together"):
+        ops.decode_ids(ids_pos, 128, 4, 128, 16, 144, comp32=torch.zeros(2, 16, 512))
+    # row_epilogue_ids: both sets of checks
+    with pytest.raises(ValueError, match="ids must be"):
+        ops.row_epilogue_ids(x, None, ids_pos, cs, cs, 64, _lib.SIM_NONE, out, 2, ids_pos, 128, 4, 128, 16, 144,
+                             torch.zeros(2, 128, dtype=torch.int32))
+    with pytest.raises(ValueError, match="positions"):
+        ops.row_epilogue_ids(x, None, pos[:3], cs, cs, 64, _lib.SIM_NONE, out, 1, ids_pos, 128, 4, 128, 16, 144,
+                             torch.zeros(2, 144, dtype=torch.int32))
+
+    # ring_step_kv: one position per sequence, cache rows within the cache
+    class _Ring:
+        ring_kv = torch.zeros(2, 8, 1024)
+    with pytest.raises(ValueError, match="positions"):
+        ops.ring_step_kv(_Ring, None, None, torch.zeros(3, dtype=torch.int32), None, None, None, None, None, 64,
+                         _lib.SIM_FP8, torch.zeros(2, 128, 512))
+    with pytest.raises(ValueError, match="cache_rows"):
+        ops.ring_step_kv(_Ring, None, None, torch.zeros(2, dtype=torch.int32), None, None, None, None, None, 64,
+                         _lib.SIM_FP8, torch.zeros(2, 128, 512), cache_rows=256)

@@ -180,6 +180,36 @@ def test_fp8_rows_vs_oracle(dev, B, T, n, sharp, H, D, pow2):
     _check_bf16(out, ref, "fp8 rows")
 
 
+@pytest.mark.parametrize("kind,S,H,D,dv,T,n", [("bf16", 3, 8, 128, 128, 300, 500),      # H % 16 != 0
+                                               ("bf16", 2, 16, 256, 200, 90, 400),      # D, DV off the MFMA shapes
+                                               ("fp8", 2, 8, 128, 128, 257, 600),       # fp8 rows, H = 8
+                                               ("fp8", 1, 20, 192, 64, 70, 300)])
+def test_generic_kernel_bf16_fp8_rows(dev, kind, S, H, D, dv, T, n):
+    """Shapes the MFMA split kernel does not take (H not a multiple of 16, D other than 576 / 512,
+    DV other than 512) run the vector-ALU kernel for bf16 and fp8 rows as well as fp32: the same
+    results as the oracle on the exact bf16 / dequantised fp8 values, to the bf16 tolerance."""
+    from smla import sparse_attn as ssa
+    from smla import workloads as wl
+    announce(f"generic kernel {kind} S={S} H={H} D={D} dv={dv} T={T} n={n}")
+    g = torch.Generator().manual_seed(S * 100 + H)
+    B = 2
+    q = (torch.randn(B, S, H, D, generator=g) * 0.3).to(torch.bfloat16)
+    x = torch.randn(B, n, D, generator=g) * 0.3
+    idx = torch.randint(-1, n, (B, S, T), generator=g, dtype=torch.int32)
+    sink = torch.randn(H, generator=g)
+    if kind == "bf16":
+        kv = x.to(torch.bfloat16)
+        out = ssa.sparse_attn_batched(q.to(dev), kv.to(dev), sink.to(dev), idx.to(dev), D ** -0.5, dv=dv)
+        rows = kv.float()
+    else:
+        codes, scales = wl.quant_e4m3_pow2(x)
+        out = ssa.sparse_attn_batched(q.to(dev), codes.to(dev), sink.to(dev), idx.to(dev), D ** -0.5, dv=dv,
+                                      kv_scale=scales.to(dev))
+        rows = wl.dequant_e4m3(codes, scales)
+    ref = _oracle_two_source(q, rows, None, sink, idx, D ** -0.5, dv)
+    _check_bf16(out, ref, f"generic kernel {kind}")
+
+
 def test_fp32_plumbing_workload(dev):
     """The fp32 plumbing case: H=16, 4096 rows, indexer top-512, fp32 attention, 1e-5."""
     from smla import indexer as sidx

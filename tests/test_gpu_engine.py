@@ -66,7 +66,7 @@ def test_decode_layer_vs_oracle(dev, ratio, steps):
             r = _rel(y[b], yr)
             worst = max(worst, r)
             assert r <= 1e-2, f"step {p} seq {b}: output rel err {r:.3e}"
-            _check_row(layer.raw[b, p].float().cpu(), kv, 1e-2, f"step {p} seq {b}: window row")
+            _check_row(layer.raw[b, p % 128].float().cpu(), kv, 1e-2, f"step {p} seq {b}: window row")
             if ratio == 4 and (p + 1) % 4 == 0:
                 j = (p + 1) // 4 - 1
                 assert len(states[b].comp) == j + 1
@@ -105,8 +105,9 @@ def test_decode_layer_indexer_topk_vs_oracle(dev, k, steps):
         for b in range(B):
             yr, _, ids_ref, _ = oe.decode_step(states[b], wo, xn[b].float(), p, scores=sc[b].numpy(), k=k)
             got = ids[b][ids[b] >= 0].tolist()
-            # window ids are cache positions in both; compressed ids: max_pos + j here, (p + 1) + j there
-            got = sorted(i if i < max_pos else (p + 1) + (i - max_pos) for i in got)
+            # window ids: ring rows here (position pp at row pp % 128), positions there; compressed
+            # ids: 128 + j here, (p + 1) + j there
+            got = sorted(p - (p - i) % 128 if i < 128 else (p + 1) + (i - 128) for i in got)
             assert got == sorted(ids_ref.tolist()), f"step {p} seq {b}: id sets differ"
             assert len(ids_ref) == min(p + 1, 128) + min(nv, k)
             r = _rel(y[b], yr)
@@ -136,7 +137,9 @@ def test_prefill_then_decode_vs_oracle(dev, ratio, S, steps):
         for i in range(S):
             r = _rel(y[b, i], yr[i])
             assert r <= 1e-2, f"prefill seq {b} position {i}: output rel err {r:.3e}"
-            _check_row(layer.raw[b, i].float().cpu(), states[b].win[i], 1e-2, f"prefill seq {b}: window row {i}")
+            if i >= S - 128:   # the ring keeps the prompt's last 128 window rows, position i at row i % 128
+                _check_row(layer.raw[b, i % 128].float().cpu(), states[b].win[i], 1e-2,
+                           f"prefill seq {b}: window row {i}")
         assert len(states[b].comp) == (S // 4 if ratio == 4 else 0)
         for j in range(len(states[b].comp)):
             _check_row(layer.comp32[b, j].cpu(), states[b].comp[j], 2e-2, f"prefill seq {b}: compressed row {j}")
@@ -150,6 +153,35 @@ def test_prefill_then_decode_vs_oracle(dev, ratio, S, steps):
             if ratio == 4 and (p + 1) % 4 == 0:
                 j = (p + 1) // 4 - 1
                 _check_row(layer.comp32[b, j].cpu(), states[b].comp[j], 2e-2, f"step {p} seq {b}: compressed row {j}")
+
+
+def test_decode_layer_window_ring_wraps(dev):
+    """The window ring over 320 decode steps of a ratio-4 layer (the 128-row ring wraps twice and a
+    half, and the compressed list grows to 80 rows): every step's output within 1e-2 of the
+    oracle, whose window list is unbounded, and the row written at p lands at ring row p % 128.
+    The ring's size does not depend on max_pos."""
+    from smla import engine
+    announce("decode layer window ring, 320 steps")
+    t = _make_weights(4, seed=31)
+    w = engine.LayerWeights(**{k: v.to(dev) for k, v in t.items()})
+    wo = oe.OracleWeights(**{k: (v.double().numpy() if v.dtype == torch.bfloat16 else v.float())
+                             for k, v in t.items()})
+    B, max_pos, steps = 1, 512, 320
+    layer = engine.DecodeLayer(w, B, 4, max_pos=max_pos, device=dev)
+    assert tuple(layer.raw.shape) == (B, 128, 512)
+    assert tuple(engine.DecodeLayer(w, B, 4, max_pos=4096, device=dev).raw.shape) == (B, 128, 512)
+    st = oe.LayerState(4, max_pos=max_pos)
+    g = torch.Generator().manual_seed(400)
+    worst = 0.0
+    for p in range(steps):
+        xn = torch.randn(B, 4096, generator=g).to(torch.bfloat16)
+        y = layer.step(xn.to(dev), torch.full((B,), p, dtype=torch.int32, device=dev)).float().cpu()
+        yr, kv, ids, _ = oe.decode_step(st, wo, xn[0].float(), p)
+        r = _rel(y[0], yr)
+        worst = max(worst, r)
+        assert r <= 1e-2, f"step {p}: output rel err {r:.3e}"
+        _check_row(layer.raw[0, p % 128].float().cpu(), kv, 1e-2, f"step {p}: window row")
+    announce(f"worst output rel err {worst:.3e}")
 
 
 def test_prefill_rejects_bad_shapes(dev):

@@ -94,24 +94,32 @@ def test_q_a_norm_d1024(dev):
     assert torch.allclose(out.cpu(), onr.rmsnorm(x, w), rtol=1e-5, atol=1e-6)
 
 
-def test_out_of_range_position_writes_nothing(dev):
+def test_cache_position_wraps_and_invalid_writes_nothing(dev):
+    """A cache of cache_rows rows is a ring: position p lands at row p mod cache_rows (40 -> 8 of 32,
+    the bounded window of oracle/v4_fast.py:93-96); a negative position, or one past the rotation
+    table, writes nothing."""
     from smla import _lib, ops
     from smla import norm_rope as snr
-    announce("row_epilogue position past the cache")
+    announce("row_epilogue cache ring positions")
     cos_d, sin_d = snr.rope_tables(64, 64, *YARN, device=dev)
-    cache = torch.zeros(2, 32, 512, dtype=torch.bfloat16, device=dev)
-    x = torch.ones(2, 512, device=dev)
-    ops.row_epilogue(x, None, torch.tensor([5, 40], dtype=torch.int32, device=dev), cos_d, sin_d, 64,
+    cache = torch.zeros(4, 32, 512, dtype=torch.bfloat16, device=dev)
+    x = torch.ones(4, 512, device=dev)
+    ops.row_epilogue(x, None, torch.tensor([5, 40, -1, 70], dtype=torch.int32, device=dev), cos_d, sin_d, 64,
                      _lib.SIM_FP8, cache, cache_rows=32)
     c = cache.float().cpu()
-    assert c[0, 5].abs().sum() > 0 and c[1].abs().sum() == 0
+    assert c[0, 5].abs().sum() > 0 and c[1, 8].abs().sum() > 0
+    c[0, 5] = 0
+    c[1, 8] = 0
+    assert c.abs().sum() == 0
 
 
-@pytest.mark.parametrize("ratio", [4, 0])
-def test_decode_ids_brute_force(dev, ratio):
+@pytest.mark.parametrize("ratio,n_raw", [(4, 512), (0, 512), (4, 128), (0, 200)])
+def test_decode_ids_brute_force(dev, ratio, n_raw):
+    """Window ids: position pp at raw row pp mod n_raw (a cache with a row per position, or a ring
+    of 128 or 200 rows that positions up to 511 wrap), then the visible compressed rows."""
     from smla import ops
-    announce(f"decode_ids ratio={ratio}")
-    n_raw, ncomp, d, W = 512, 128, 512, 128
+    announce(f"decode_ids ratio={ratio} n_raw={n_raw}")
+    ncomp, d, W = 128, 512, 128
     pos = torch.tensor([0, 3, 126, 127, 128, 300, 511], dtype=torch.int32)
     B = pos.numel()
     T = W + (ncomp if ratio else 0)
@@ -122,7 +130,7 @@ def test_decode_ids_brute_force(dev, ratio):
     for b in range(B):
         p = int(pos[b])
         lo = max(0, p - W + 1)
-        win = [t for t in range(lo, p + 1)] + [-1] * (W - (p + 1 - lo))
+        win = [t % n_raw for t in range(lo, p + 1)] + [-1] * (W - (p + 1 - lo))
         comp = [n_raw + j for j in range(ncomp) if ratio and j < (p + 1) // ratio]
         comp += [-1] * (T - W - len(comp))
         assert ids[b].tolist() == win + comp
