@@ -20,7 +20,9 @@
 // tiles' and the score waves read Q^T with the K-read pattern (free of bank conflicts).  Masked ids and rows past
 // the split load row 0, so every LDS value an MFMA reads is finite.
 //
-// Output: final rows (one split) or (m, l, O) partial states in the layout attn_merge_kernel reads.
+// Output: final rows (one split) or (m, l, O) partial states in the layout the merge kernels read.
+// bf16 partials leave the value waves' registers in MFMA fragment order (attn_merge_frag_kernel):
+// no staging through LDS and no barrier after the tile loop.
 #include "attn_common.h"
 #include "select_row.h"
 
@@ -449,6 +451,8 @@ __global__ __launch_bounds__(768) void attn_decode_kernel(
   // output staging after the loop (the ring is free then): 64 head rows of 512 values in the output
   // element type (bf16 for bf16 output or bf16 partials, else fp32), padded against bank conflicts
   const bool out_bf16 = out_dtype == SMLA_BF16;
+  // bf16 partial states: written in MFMA fragment order, no staging (attn_merge_frag_kernel)
+  const bool frag_out = nsplit > 1 && out_bf16;
   const int row_bytes = out_bf16 ? 1024 : 2048;
   const int srow_bytes = row_bytes + 16;
   // the workgroup's nh x 512 output block is contiguous: final rows [bs][hb..][512] or the split's
@@ -574,10 +578,10 @@ __global__ __launch_bounds__(768) void attn_decode_kernel(
       ml_s[hl * 2 + 1] = l_tot;
       if (nsplit > 1 && hl < nh) {
         const int64_t rec = (bs * nsplit + split) * (int64_t)H + hb + hl;
-        part[rec * 2] = m_ref;
-        part[rec * 2 + 1] = l_tot;
+        *(f32x2_t*)(part + rec * 2) = f32x2_t{m_ref, l_tot};
       }
     }
+    if (frag_out) return;  // the value waves write their partial O without these values
     lds_barrier();  // (m, l) in LDS
     lds_barrier();  // the value waves' output block is staged
     copy_out();
@@ -632,6 +636,31 @@ __global__ __launch_bounds__(768) void attn_decode_kernel(
       }
     }
     end_iteration(it);
+  }
+  if (frag_out) {
+    // bf16 partial O^T straight from the accumulators: block (query row, split, head group) of
+    // 64 KB holds, for value wave vw (head pair hp, value quarter dq), value block mb and half h,
+    // 1 KB pieces at ((vw * 4 + mb) * 2 + h) * 1024 in which lane l's 16 bytes are the 8 values
+    // 128 dq + 32 mb + 16 h + 8 (l >> 5) .. +7 of head 32 hp + (l & 31).  The accumulator holds
+    // value columns 8 (r >> 2) + 4 (l >> 5) + (r & 3) of register r; one lane swap per register
+    // pair gives each lane 8 contiguous columns.
+    uint8_t* blk = (uint8_t*)(part + (int64_t)gridDim.y * H * nsplit * 2) +
+                   ((bs * nsplit + split) * (int64_t)gridDim.z + (hb >> 6)) * 65536 + (int64_t)vw * 8192 + 16 * lane;
+#pragma unroll
+    for (int mb = 0; mb < 4; mb++) {
+      uint32_t d[8];
+#pragma unroll
+      for (int k = 0; k < 8; k++) d[k] = pack2(o[mb][2 * k], o[mb][2 * k + 1]);
+#pragma unroll
+      for (int k = 0; k < 8; k += 4) {
+        // lanes 32-63 of d[k], d[k+1] <-> lanes 0-31 of d[k+2], d[k+3]
+        const auto s0 = __builtin_amdgcn_permlane32_swap(d[k], d[k + 2], false, false);
+        const auto s1 = __builtin_amdgcn_permlane32_swap(d[k + 1], d[k + 3], false, false);
+        const u32x4_t v4 = {s0[0], s1[0], s0[1], s1[1]};
+        *(u32x4_t*)(blk + (mb * 2 + (k >> 2)) * 1024) = v4;
+      }
+    }
+    return;
   }
   lds_barrier();  // the score waves' (m, l) are in LDS
 
