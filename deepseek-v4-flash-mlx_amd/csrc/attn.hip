@@ -5,8 +5,9 @@
 // denominator, output = weighted sum of the first DV columns of the gathered rows.
 //
 // This file holds:
-//  * attn_generic_kernel — fp32 VALU, any dtype / shape; one workgroup per (b, s, head).  This
-//    is the fp32 path (1e-5 parity) and the path for shapes the MFMA kernel does not cover.
+//  * attn_generic_kernel — fp32 VALU, any dtype / shape; one workgroup of 16 waves per (b, s, head),
+//    a wave per gathered row at a time.  This is the fp32 path (1e-5 parity) and the path for
+//    shapes the MFMA kernel does not cover.
 //  * attn_merge_kernel   — log-sum-exp merge of the split partial states that the MFMA split
 //    kernel (attn_decode.hip) writes.
 //  * the split plan and the C entry points.
@@ -18,7 +19,6 @@
 namespace {
 
 using smla_attn::kRescaleSlack;
-using smla_attn::kThreads;
 using smla_attn::kTileRows;
 using smla_attn::RowSrc;
 
@@ -34,109 +34,253 @@ __device__ inline const uint8_t* row_ptr(const RowSrc& src, int64_t b, int64_t r
   return (const uint8_t*)src.kv1 + (b * src.n1 + r1) * D * es;
 }
 
-__device__ inline int dtype_size(int dt) { return dt == SMLA_F32 ? 4 : (dt == SMLA_FP8_E4M3 ? 1 : 2); }
-
 // ---------------------------------------------------------------------------------------------
-// Generic VALU kernel.
-__global__ __launch_bounds__(kThreads) void attn_generic_kernel(
-    const void* __restrict__ q, int q_dtype, RowSrc src, int kv_dtype,
-    const float* __restrict__ sink, const int32_t* __restrict__ idx, int64_t T, int64_t S,
-    int64_t H, int64_t D, int64_t DV, float scale, void* __restrict__ out, int out_dtype) {
-  extern __shared__ float smem[];
-  float* sq = smem;                 // [D]
-  float* sp = sq + D;               // [256]
-  int* sid = (int*)(sp + kThreads); // [256]
-  __shared__ float red[kThreads / 64];
+// Generic VALU kernel: one workgroup of 16 waves per (query row, head).  Each wave takes a
+// contiguous sixteenth of the index list and walks it R rows at a time: lane l holds columns
+// l, l+64, ... of each row (coalesced row loads, 64 columns per load instruction), the dot with q
+// is a DPP wave sum, and the wave keeps its own online-softmax state (m, l, O).  The 16 states merge
+// through LDS at the end in a fixed order, so the result does not depend on timing.
+constexpr int kGenWaves = 16;
+constexpr int kGenThreads = 64 * kGenWaves;
 
-  const int tid = threadIdx.x;
+template <int KT>
+__device__ inline float load_elem(const uint8_t* row, int64_t i) {
+  if constexpr (KT == SMLA_F32) return ((const float*)row)[i];
+  else if constexpr (KT == SMLA_BF16) return bf16_bits_to_f32(((const uint16_t*)row)[i]);
+  else if constexpr (KT == SMLA_F16) return (float)((const _Float16*)row)[i];
+  else return e4m3_to_f32(row[i]);
+}
+
+// KT: row dtype; NC: 64-column chunks of a row held in registers; ONE: the whole row fits NC chunks
+// (D <= 64 NC), so the value columns are taken from the registers the dot used; otherwise the dot
+// runs over the row in blocks of NC chunks and the value columns (DV <= 1024) are loaded again.
+template <int KT, int NC, bool ONE>
+__global__ __launch_bounds__(kGenThreads) void attn_generic_kernel(
+    const void* __restrict__ q, int q_dtype, RowSrc src, const float* __restrict__ sink,
+    const int32_t* __restrict__ idx, int64_t T, int64_t S, int64_t H, int64_t D, int64_t DV, float scale,
+    void* __restrict__ out, int out_dtype) {
+  constexpr int R = NC <= 4 ? 8 : (NC <= 9 ? 4 : 2);  // rows in flight per wave
+  constexpr int NA = ONE ? NC : 16;                   // value chunks held (DV <= 1024)
+  constexpr int ES = KT == SMLA_F32 ? 4 : (KT == SMLA_FP8_E4M3 ? 1 : 2);
+  constexpr int HW = kGenWaves / 2;
+  extern __shared__ float smem[];
+  float* sq = smem;     // [D] the query row
+  float* buf = sq + D;  // [HW][DV] weighted partial outputs
+  __shared__ float sm[kGenWaves], sl[kGenWaves];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int64_t h = blockIdx.x % H;
   const int64_t bs = blockIdx.x / H;
   const int64_t b = batch_of(bs, S);
   const int64_t ntot = src.n0 + src.n1;
-  const int es = dtype_size(kv_dtype);
+  const int nch = (int)((D + 63) >> 6);
 
-  for (int64_t d = tid; d < D; d += kThreads) sq[d] = load_as_f32(q, (bs * H + h) * D + d, q_dtype);
+  for (int64_t d = tid; d < D; d += kGenThreads) sq[d] = load_as_f32(q, (bs * H + h) * D + d, q_dtype);
   __syncthreads();
-
-  constexpr int kMaxDvPerThread = 4;  // DV <= 1024
-  float acc[kMaxDvPerThread];
+  float qv[ONE ? NC : 1];
+  if constexpr (ONE) {
 #pragma unroll
-  for (int j = 0; j < kMaxDvPerThread; j++) acc[j] = 0.f;
+    for (int c = 0; c < NC; c++) qv[c] = 64 * c + lane < D ? sq[64 * c + lane] : 0.f;
+  }
+  float acc[NA];
+#pragma unroll
+  for (int c = 0; c < NA; c++) acc[c] = 0.f;
   float m_run = -SMLA_INF, l_run = 0.f;
-  const int32_t* ids = idx + bs * T;
 
-  for (int64_t t0 = 0; t0 < T; t0 += kThreads) {
-    int64_t t = t0 + tid;
-    float sc = -SMLA_INF;
-    int rid = -1;
-    if (t < T) {
-      int64_t r = ids[t];
-      if (r >= 0 && r < ntot) {
-        const float* srow = nullptr;
-        const uint8_t* row = row_ptr(src, b, r, D, es, &srow);
-        float dot = 0.f;
-        for (int64_t d = 0; d < D; d++) {
-          float v = load_as_f32(row, d, kv_dtype);
-          if (srow) v *= srow[d / 64];
-          dot = fmaf(sq[d], v, dot);
-        }
-        sc = scale * dot;
-        rid = (int)r;
+  const int32_t* ids = idx + bs * T;
+  const int64_t per = (T + kGenWaves - 1) / kGenWaves;
+  const int64_t t_beg = wv * per;
+  const int64_t t_end = t_beg + per < T ? t_beg + per : T;
+  for (int64_t tb = t_beg; tb < t_end; tb += 64) {
+    const int nb = (int)(t_end - tb < 64 ? t_end - tb : 64);
+    const int idv = lane < nb ? ids[tb + lane] : -1;
+    for (int j = 0; j < nb; j += R) {
+      const uint8_t* rp[R];
+      const float* sp[R];
+      bool ok[R];
+#pragma unroll
+      for (int k = 0; k < R; k++) {
+        const int r = j + k < nb ? __builtin_amdgcn_readlane(idv, (j + k) & 63) : -1;
+        ok[k] = r >= 0 && r < ntot;
+        sp[k] = nullptr;
+        rp[k] = ok[k] ? row_ptr(src, b, r, D, ES, &sp[k]) : nullptr;
       }
-    }
-    // block max
-    float mx = wave_max(sc);
-    if ((tid & 63) == 0) red[tid >> 6] = mx;
-    __syncthreads();
-    float mt = red[0];
-    for (int w = 1; w < kThreads / 64; w++) mt = fmaxf(mt, red[w]);
-    __syncthreads();
-    float m_new = fmaxf(m_run, mt);
-    float p = (rid >= 0 && m_new > -SMLA_INF) ? __expf(sc - m_new) : 0.f;
-    sp[tid] = p;
-    sid[tid] = rid;
-    float ps = wave_sum(p);
-    if ((tid & 63) == 0) red[tid >> 6] = ps;
-    __syncthreads();
-    float psum = 0.f;
-    for (int w = 0; w < kThreads / 64; w++) psum += red[w];
-    if (m_new > -SMLA_INF) {
-      float alpha = (m_run > -SMLA_INF) ? __expf(m_run - m_new) : 0.f;
-      l_run = l_run * alpha + psum;
+      float dot[R];
+      float v[ONE ? R : 1][ONE ? NC : 1];
+      if constexpr (ONE) {
 #pragma unroll
-      for (int j = 0; j < kMaxDvPerThread; j++) acc[j] *= alpha;
-      int64_t nt = (T - t0) < kThreads ? (T - t0) : kThreads;
-      for (int64_t tt = 0; tt < nt; tt++) {
-        int r = sid[tt];
-        if (r < 0) continue;
-        float pt = sp[tt];
-        const float* srow = nullptr;
-        const uint8_t* row = row_ptr(src, b, r, D, es, &srow);
+        for (int k = 0; k < R; k++)
 #pragma unroll
-        for (int j = 0; j < kMaxDvPerThread; j++) {
-          int64_t dv = tid + j * kThreads;
-          if (dv < DV) {
-            float v = load_as_f32(row, dv, kv_dtype);
-            if (srow) v *= srow[dv / 64];
-            acc[j] = fmaf(pt, v, acc[j]);
+          for (int c = 0; c < NC; c++) {
+            const int64_t d = 64 * c + lane;
+            float x = 0.f;
+            if (ok[k] && c < nch && d < D) {
+              x = load_elem<KT>(rp[k], d);
+              if constexpr (KT == SMLA_FP8_E4M3) x *= sp[k][c];
+            }
+            v[k][c] = x;
+          }
+#pragma unroll
+        for (int k = 0; k < R; k++) {
+          float s = 0.f;
+#pragma unroll
+          for (int c = 0; c < NC; c++) s = fmaf(qv[c], v[k][c], s);
+          dot[k] = s;
+        }
+      } else {
+#pragma unroll
+        for (int k = 0; k < R; k++) dot[k] = 0.f;
+        for (int c0 = 0; c0 < nch; c0 += NC) {
+          float w[R][NC];
+#pragma unroll
+          for (int k = 0; k < R; k++)
+#pragma unroll
+            for (int c = 0; c < NC; c++) {
+              const int cc = c0 + c;
+              const int64_t d = 64 * (int64_t)cc + lane;
+              float x = 0.f;
+              if (ok[k] && cc < nch && d < D) {
+                x = load_elem<KT>(rp[k], d);
+                if constexpr (KT == SMLA_FP8_E4M3) x *= sp[k][cc];
+              }
+              w[k][c] = x;
+            }
+#pragma unroll
+          for (int c = 0; c < NC; c++) {
+            const int64_t d = 64 * (int64_t)(c0 + c) + lane;
+            const float qd = d < D ? sq[d] : 0.f;
+#pragma unroll
+            for (int k = 0; k < R; k++) dot[k] = fmaf(qd, w[k][c], dot[k]);
           }
         }
       }
-      m_run = m_new;
-    }
-    __syncthreads();
-  }
-  float snk = sink ? sink[h] : -SMLA_INF;
-  float den = l_run + ((m_run > -SMLA_INF) ? __expf(snk - m_run) : 0.f);
-  bool empty = !(m_run > -SMLA_INF);
+      float s[R];
+      float mx = m_run;
 #pragma unroll
-  for (int j = 0; j < kMaxDvPerThread; j++) {
-    int64_t dv = tid + j * kThreads;
-    if (dv < DV) {
-      float o = empty ? __builtin_nanf("") : acc[j] / den;
-      store_from_f32(out, (bs * H + h) * DV + dv, out_dtype, o);
+      for (int k = 0; k < R; k++) {
+        const float tot = wave_sum_dpp(dot[k]);
+        s[k] = ok[k] ? scale * tot : -SMLA_INF;
+        mx = fmaxf(mx, s[k]);
+      }
+      if (mx > -SMLA_INF) {
+        const float alpha = m_run > -SMLA_INF ? __expf(m_run - mx) : 0.f;
+        float p[R];
+        float ps = 0.f;
+#pragma unroll
+        for (int k = 0; k < R; k++) {
+          p[k] = ok[k] ? __expf(s[k] - mx) : 0.f;
+          ps += p[k];
+        }
+        l_run = l_run * alpha + ps;
+        if constexpr (ONE) {
+#pragma unroll
+          for (int c = 0; c < NA; c++) {
+            float a = acc[c] * alpha;
+#pragma unroll
+            for (int k = 0; k < R; k++) a = fmaf(p[k], v[k][c], a);
+            acc[c] = a;
+          }
+        } else {
+#pragma unroll
+          for (int c = 0; c < NA; c++) {
+            const int64_t d = 64 * c + lane;
+            float a = acc[c] * alpha;
+#pragma unroll
+            for (int k = 0; k < R; k++) {
+              float x = 0.f;
+              if (ok[k] && d < DV) {
+                x = load_elem<KT>(rp[k], d);
+                if constexpr (KT == SMLA_FP8_E4M3) x *= sp[k][c];
+              }
+              a = fmaf(p[k], x, a);
+            }
+            acc[c] = a;
+          }
+        }
+        m_run = mx;
+      }
     }
   }
+
+  // merge of the 16 wave states: weights exp(m_w - M), partial outputs summed in wave order
+  if (lane == 0) {
+    sm[wv] = m_run;
+    sl[wv] = l_run;
+  }
+  __syncthreads();
+  float M = -SMLA_INF;
+#pragma unroll
+  for (int w = 0; w < kGenWaves; w++) M = fmaxf(M, sm[w]);
+  const float wt = m_run > -SMLA_INF ? __expf(m_run - M) : 0.f;
+  if (wv >= HW) {
+#pragma unroll
+    for (int c = 0; c < NA; c++)
+      if (64 * c + lane < DV) buf[(wv - HW) * DV + 64 * c + lane] = acc[c] * wt;
+  }
+  __syncthreads();
+  if (wv < HW) {
+#pragma unroll
+    for (int c = 0; c < NA; c++)
+      if (64 * c + lane < DV) buf[wv * DV + 64 * c + lane] = fmaf(acc[c], wt, buf[wv * DV + 64 * c + lane]);
+  }
+  __syncthreads();
+  float den = 0.f;
+#pragma unroll
+  for (int w = 0; w < kGenWaves; w++) den += (sm[w] > -SMLA_INF ? __expf(sm[w] - M) : 0.f) * sl[w];
+  const bool empty = !(M > -SMLA_INF);
+  const float snk = sink ? sink[h] : -SMLA_INF;
+  if (!empty) den += __expf(snk - M);
+  for (int64_t d = tid; d < DV; d += kGenThreads) {
+    float o = 0.f;
+#pragma unroll
+    for (int w = 0; w < HW; w++) o += buf[w * DV + d];
+    store_from_f32(out, (bs * H + h) * DV + d, out_dtype, empty ? __builtin_nanf("") : o / den);
+  }
+}
+
+template <int KT>
+void launch_generic_kt(int64_t D, dim3 grid, size_t lds, hipStream_t st, const void* q, int q_dtype, RowSrc src,
+                       const float* sink, const int32_t* idx, int64_t T, int64_t S, int64_t H, int64_t DV,
+                       float scale, void* out, int out_dtype) {
+  const int64_t nch = (D + 63) / 64;
+  if (nch <= 4)
+    hipLaunchKernelGGL((attn_generic_kernel<KT, 4, true>), grid, dim3(kGenThreads), lds, st, q, q_dtype, src, sink,
+                       idx, T, S, H, D, DV, scale, out, out_dtype);
+  else if (nch <= 9)
+    hipLaunchKernelGGL((attn_generic_kernel<KT, 9, true>), grid, dim3(kGenThreads), lds, st, q, q_dtype, src, sink,
+                       idx, T, S, H, D, DV, scale, out, out_dtype);
+  else if (nch <= 16)
+    hipLaunchKernelGGL((attn_generic_kernel<KT, 16, true>), grid, dim3(kGenThreads), lds, st, q, q_dtype, src, sink,
+                       idx, T, S, H, D, DV, scale, out, out_dtype);
+  else
+    hipLaunchKernelGGL((attn_generic_kernel<KT, 16, false>), grid, dim3(kGenThreads), lds, st, q, q_dtype, src, sink,
+                       idx, T, S, H, D, DV, scale, out, out_dtype);
+}
+
+// the generic kernel over B*S*H workgroups; LDS: the query row and half the waves' partial outputs
+int launch_generic(const void* q, int q_dtype, RowSrc src, int kv_dtype, const float* sink, const int32_t* idx,
+                   int64_t T, int64_t B, int64_t S, int64_t H, int64_t D, int64_t DV, float scale, void* out,
+                   int out_dtype, hipStream_t st) {
+  const size_t lds = (size_t)D * 4 + (size_t)(kGenWaves / 2) * DV * 4;
+  if (lds > 64 * 1024 || B * S * H > 0xffffffffll) return SMLA_E_UNSUPPORTED;
+  const dim3 grid((unsigned)(B * S * H));
+  switch (kv_dtype) {
+    case SMLA_F32:
+      launch_generic_kt<SMLA_F32>(D, grid, lds, st, q, q_dtype, src, sink, idx, T, S, H, DV, scale, out, out_dtype);
+      break;
+    case SMLA_BF16:
+      launch_generic_kt<SMLA_BF16>(D, grid, lds, st, q, q_dtype, src, sink, idx, T, S, H, DV, scale, out, out_dtype);
+      break;
+    case SMLA_F16:
+      launch_generic_kt<SMLA_F16>(D, grid, lds, st, q, q_dtype, src, sink, idx, T, S, H, DV, scale, out, out_dtype);
+      break;
+    default:
+      launch_generic_kt<SMLA_FP8_E4M3>(D, grid, lds, st, q, q_dtype, src, sink, idx, T, S, H, DV, scale, out,
+                                      out_dtype);
+  }
+  SMLA_HIP_CHECK_LAUNCH();
+  return SMLA_OK;
 }
 
 // Merge of split partial states.  The nsplit states (m_j, l_j, O_j) of one (query row, head) are
@@ -528,12 +672,8 @@ static int attn_launch(const Plan& p, int phases, const void* q, int q_dtype, Ro
                      smla_attn::SelectRows sr = smla_attn::SelectRows{}) {
   if (!p.mfma) {
     if (!(phases & SMLA_ATTN_SPLIT)) return SMLA_OK;
-    const size_t lds = (size_t)D * 4 + kThreads * 8;
-    if (lds > 64 * 1024) return SMLA_E_UNSUPPORTED;
-    hipLaunchKernelGGL(attn_generic_kernel, dim3((unsigned)(B * S * H)), dim3(kThreads), lds, st, q, q_dtype, src,
-                       kv_dtype, attn_sink, topk_idxs, T, S, H, D, DV, scale, out, out_dtype);
-    SMLA_HIP_CHECK_LAUNCH();
-    return SMLA_OK;
+    return launch_generic(q, q_dtype, src, kv_dtype, attn_sink, topk_idxs, T, B, S, H, D, DV, scale, out, out_dtype,
+                          st);
   }
   if (phases & SMLA_ATTN_SPLIT) {
     const int rc = smla_attn::launch_decode_v6((int)D, kv_dtype == SMLA_FP8_E4M3, p.nsplit, p.rows_per_split, q, src,
