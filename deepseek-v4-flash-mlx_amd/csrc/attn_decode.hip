@@ -49,17 +49,18 @@ struct Geo6 {
   static constexpr int AL_OFF = P_OFF + 2 * PBUF;        // rescale factors: 2 x 64 floats
   static constexpr int IDS_OFF = AL_OFF + 2 * 64 * 4;
   static constexpr int MAX_ROWS = MAXROWS_;             // rows per split (index table in LDS; 0: none)
-  static constexpr int ML_OFF = IDS_OFF + MAX_ROWS * 4;  // (m, l) per head after the loop
+  static constexpr int LOOP_END = IDS_OFF + MAX_ROWS * 4;  // end of what the tile loop uses
+  static constexpr int STAGE_BF16 = 64 * (1024 + 16);   // output staging after the loop
+  static constexpr int STAGE_F32 = 64 * (2048 + 16);
+  // (m, l) per head after the loop, past the output staging (which may reach past LOOP_END)
+  static constexpr int ML_OFF = LOOP_END > STAGE_F32 ? LOOP_END : STAGE_F32;
   static constexpr int LDS_BYTES = ML_OFF + 64 * 2 * 4;
   static constexpr int NW = 12;
   static constexpr int KSTEPS = D / 32;                 // 18 / 16
   static constexpr int NDMA = kTileRows + (TAIL ? kTileRows / 8 : 0);   // 36 / 32 per tile
-  static constexpr int STAGE_BF16 = 64 * (1024 + 16);   // output staging after the loop
-  static constexpr int STAGE_F32 = 64 * (2048 + 16);
   static_assert(LDS_BYTES <= 160 * 1024, "LDS budget");
   static_assert(NBUF >= 3, "Q takes the last two slots; tile 0 needs one more");
-  static_assert(STAGE_BF16 <= ML_OFF, "bf16 staging below the (m, l) table");
-  static constexpr bool STAGE_F32_FITS = STAGE_F32 <= ML_OFF;
+  static_assert(STAGE_F32 <= ML_OFF, "output staging below the (m, l) table");
 };
 
 __device__ inline uint32_t pack2(float a, float b) { return pack_bf16x2(a, b); }
@@ -355,21 +356,36 @@ __global__ __launch_bounds__(768) void attn_decode_kernel(
   // ---- fp8 rows (e4m3 codes + one fp32 power-of-two scale per 64 columns): the value waves load
   // a tile's 32 x D codes into registers (16 codes per lane-chunk, chunks dealt over the 512
   // value lanes) and write them to the ring slot as bf16 (exact: 4 significant bits times a power
-  // of two), in the layout the DMA gives bf16 rows
+  // of two), in the layout the DMA gives bf16 rows.  A wave's chunks are all main columns or all
+  // rope columns (f8_chunk), so no wave runs both store paths (6 % faster on the 64-sequence fp8
+  // batch than chunks dealt in row order); 8-code pieces, whose 16-byte stores are contiguous
+  // over the lanes, measured 9 % slower (twice the load instructions).
   constexpr int F8_CH = D / 16;                       // 16-code chunks per row (36 / 32)
   constexpr int F8_K = (kTileRows * F8_CH + 511) / 512;  // chunks per value lane (3 / 2)
   struct F8Regs {
     u32x4_t v[F8_K];
     float s[F8_K];
   };
+  // chunk k of value lane vl: k < 2 the main columns (row ci / 32, chunk ci % 32 with ci = vl + 512 k),
+  // k = 2 the rope tail (lanes vl < 128: row vl / 4, chunk 32 + vl % 4), so no wave mixes the two
+  auto f8_chunk = [&](int vl, int k, int& r, int& cc) -> bool {
+    if (k < 2) {
+      const int ci = vl + 512 * k;
+      r = ci >> 5;
+      cc = ci & 31;
+      return true;
+    }
+    r = vl >> 2;
+    cc = 32 + (vl & 3);
+    return vl < 128;
+  };
   auto f8_load = [&](int tl, F8Regs& fr) {
     const lds_i32_t* tid_s = ids_s + tl * kTileRows;
     const int vl = (wave - 4) * 64 + lane;
 #pragma unroll
     for (int k = 0; k < F8_K; k++) {
-      const int ci = vl + 512 * k;
-      const int r = ci / F8_CH, cc = ci - r * F8_CH;
-      if (ci < kTileRows * F8_CH) {
+      int r, cc;
+      if (f8_chunk(vl, k, r, cc)) {
         const int rid = tid_s[r];
         const int64_t row = rid < 0 ? (n0 > 0 ? b * n0 : b * n1) : (rid < n0 ? b * n0 + rid : b * n1 + (rid - n0));
         const bool in0 = rid < 0 ? n0 > 0 : rid < n0;
@@ -385,9 +401,8 @@ __global__ __launch_bounds__(768) void attn_decode_kernel(
     const int vl = (wave - 4) * 64 + lane;
 #pragma unroll
     for (int k = 0; k < F8_K; k++) {
-      const int ci = vl + 512 * k;
-      const int r = ci / F8_CH, cc = ci - r * F8_CH;
-      if (ci < kTileRows * F8_CH) {
+      int r, cc;
+      if (f8_chunk(vl, k, r, cc)) {
         uint32_t w[8];
         // a normal power-of-two scale (the fp8 simulation's form): code x scale is a bf16 value,
         // which the scaled converter gives exactly, two per instruction (it applies the scale's
@@ -410,7 +425,7 @@ __global__ __launch_bounds__(768) void attn_decode_kernel(
           }
         }
         const u32x4_t w0 = {w[0], w[1], w[2], w[3]}, w1 = {w[4], w[5], w[6], w[7]};
-        if (cc < 32) {
+        if (k < 2) {
           *(lds_u32x4_t*)(slot + r * G::MSTRIDE + 32 * cc) = w0;
           *(lds_u32x4_t*)(slot + r * G::MSTRIDE + 32 * cc + 16) = w1;
         } else {  // rope dims: 16-byte chunks 2(cc-32), 2(cc-32)+1 of the row's tail, swizzled

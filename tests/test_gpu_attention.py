@@ -180,6 +180,32 @@ def test_fp8_rows_vs_oracle(dev, B, T, n, sharp, H, D, pow2):
     _check_bf16(out, ref, "fp8 rows")
 
 
+
+@pytest.mark.parametrize("D", [576, 512])
+def test_fp8_split_plans_and_fp32_out(dev, D):
+    """fp8 rows under every kind of split plan (splits of up to 256 rows: the 4-slot ring, longer:
+    the 3-slot ring with the long index table), with bf16 and fp32 outputs (one split: the
+    kernel's own epilogue, whose fp32 rows are staged in LDS past the tile loop's data; more: the
+    merge of bf16 or fp32 partial states): every combination gives the oracle's answer."""
+    from smla import ops
+    from smla import workloads as wl
+    g = torch.Generator().manual_seed(D)
+    B, H, n, T = 2, 64, 3000, 1500
+    q = (torch.randn(B, 1, H, D, generator=g) * 0.3).to(torch.bfloat16)
+    codes, scales = wl.quant_e4m3_pow2(torch.randn(B, n, D, generator=g) * 0.05)
+    idx = torch.randint(0, n, (B, 1, T), generator=g, dtype=torch.int32)
+    idx[..., ::11] = -1
+    ref = _oracle_two_source(q, wl.dequant_e4m3(codes, scales), None, None, idx, D ** -0.5, 512)
+    qd, cd, sd, idxd = q.to(dev), codes.to(dev), scales.to(dev), idx.to(dev)
+    for rps in (32, 96, 512, 544, 1504):
+        ns, got_rps, _ = ops.attn_plan(B, 1, H, D, 512, T, torch.bfloat16, torch.uint8, rows_per_split=rps)
+        for odt in (torch.bfloat16, torch.float32):
+            announce(f"fp8 D={D} rows_per_split={rps} (nsplit {ns}) out {odt}")
+            out = torch.empty(B, 1, H, 512, dtype=odt, device=dev)
+            ops.sparse_attn_ex(qd, cd, None, sd, None, None, idxd, D ** -0.5, 512, rows_per_split=rps, out=out)
+            _check_bf16(out, ref, f"fp8 rows_per_split {rps} out {odt}")
+
+
 @pytest.mark.parametrize("kind,S,H,D,dv,T,n", [("bf16", 3, 8, 128, 128, 300, 500),      # H % 16 != 0
                                                ("bf16", 2, 16, 256, 200, 90, 400),      # D, DV off the MFMA shapes
                                                ("fp8", 2, 8, 128, 128, 257, 600),       # fp8 rows, H = 8

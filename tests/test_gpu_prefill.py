@@ -111,6 +111,32 @@ def test_prefill_attn_implicit_rows(dev, n_raw, q_pos0, S, H, ratio, use_sink):
     _check(out[0], ref, "prefill_attn")
 
 
+def test_prefill_attn_fp32_out(dev):
+    """fp32 output (64 head rows of 2048 bytes staged in LDS after the tile loop): the bf16
+    output's values before their rounding, so rounding them to bf16 gives the bf16 output bit for
+    bit, and every head (the last ones included) within tolerance of the oracle."""
+    from smla import compressor as scomp
+    from smla import sparse_attn as ssa
+    from smla import workloads as wl
+    n_raw, q_pos0, S, H = 1024, 900, 40, 64
+    announce(f"prefill_attn fp32 out n_raw={n_raw} q_pos0={q_pos0} S={S}")
+    q, raw = _inputs(n_raw, S, H, seed=31)
+    raw_d = raw.to(dev)
+    comp_d = scomp.block_mean_pool(raw_d, 4)
+    sink = torch.randn(H, generator=torch.Generator().manual_seed(8))
+    scale = 576 ** -0.5
+    out16 = ssa.prefill_attn(q.to(dev), raw_d, comp_d, sink.to(dev), scale, q_pos0=q_pos0, window=128, ratio=4)
+    out32 = ssa.prefill_attn(q.to(dev), raw_d, comp_d, sink.to(dev), scale, q_pos0=q_pos0, window=128, ratio=4,
+                             out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    assert out32.dtype == torch.float32
+    assert torch.equal(out32.to(torch.bfloat16).view(torch.int16), out16.view(torch.int16))
+    idx = wl.prefill_indices(n_raw, ratio=4, window=128, n_raw=n_raw)[q_pos0:q_pos0 + S]
+    kv = torch.cat([raw[0].float(), comp_d.cpu()[0].float()])
+    ref = osa.sparse_attn(q[0].float(), kv, sink, idx, scale, dv=512)
+    _check(out32[0], ref, "prefill_attn fp32 out")
+
+
 def test_prefill_attn_long_lists(dev):
     """Lists past the 8192 rows an index table holds (positions near 40000: 128 window rows and up
     to 10000 compressed rows per query) against the oracle; the queries straddle the point where
