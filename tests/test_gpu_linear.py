@@ -39,7 +39,7 @@ def _check_linear(got, x, w, G, out_dtype):
 @pytest.mark.parametrize("T,G,N,K,out_dtype", [
     (8, 8, 1024, 4096, torch.bfloat16),      # o_grouped's grouped product at decode (LDS form)
     (12, 8, 1024, 4096, torch.bfloat16),     # the same width in the register form (T > 8)
-    (8, 1, 4096, 8192, torch.float32),       # its second product (16 waves)
+    (8, 1, 4096, 8192, torch.float32),       # its second product (8 waves x 16 steps)
     (9, 1, 4096, 8192, torch.float32),       # register form
     (1, 1, 256, 4096, torch.float32),
     (3, 2, 48, 512, torch.float32),          # one wave per workgroup
