@@ -135,6 +135,27 @@ def test_many_splits_merge(dev):
     _check_bf16(out, ref, "many splits")
 
 
+@pytest.mark.parametrize("nsplit", [2, 8, 9, 16, 17, 24, 25, 33])
+def test_merge_split_counts(dev, nsplit):
+    """Split counts on both sides of the merge's chunk sizes (8, 16, 24 and 32 splits per pass,
+    more in several passes with an online rescale): 32-row splits of bf16 rows, a sink, two
+    64-head groups, bf16 partials in fragment order, against the oracle."""
+    from smla import ops
+    g = torch.Generator().manual_seed(100 + nsplit)
+    B, H, D, n = 2, 128, 576, 3000
+    T = 32 * nsplit - 5
+    announce(f"merge nsplit={nsplit} T={T} H={H}")
+    q = (torch.randn(B, 1, H, D, generator=g) * 0.3).to(torch.bfloat16)
+    kv = (torch.randn(B, n, D, generator=g) * 0.5).to(torch.bfloat16)
+    idx = torch.randint(0, n, (B, 1, T), generator=g, dtype=torch.int32)
+    sink = torch.randn(H, generator=g)
+    ns, rps, _ = ops.attn_plan(B, 1, H, D, 512, T, rows_per_split=32)
+    assert ns == nsplit and rps == 32, (ns, rps)
+    out = ops.sparse_attn_ex(q.to(dev), kv.to(dev), None, None, None, sink.to(dev), idx.to(dev), D ** -0.5, 512,
+                             rows_per_split=32)
+    _check_bf16(out, _oracle_two_source(q, kv, None, sink, idx, D ** -0.5, 512), f"merge of {nsplit} splits")
+
+
 def test_all_masked_rows_are_nan(dev):
     from smla import sparse_attn as ssa
     announce("all-masked rows")
