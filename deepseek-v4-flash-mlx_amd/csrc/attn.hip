@@ -8,8 +8,8 @@
 //  * attn_generic_kernel — fp32 VALU, any dtype / shape; one workgroup of 16 waves per (b, s, head),
 //    a wave per gathered row at a time.  This is the fp32 path (1e-5 parity) and the path for
 //    shapes the MFMA kernel does not cover.
-//  * attn_merge_kernel   — log-sum-exp merge of the split partial states that the MFMA split
-//    kernel (attn_decode.hip) writes.
+//  * attn_merge_kernel / attn_merge_frag_kernel — log-sum-exp merge of the split partial states
+//    that the MFMA split kernel (attn_decode.hip) writes (fp32 rows / bf16 in MFMA fragment order).
 //  * the split plan and the C entry points.
 #include <algorithm>
 #include <mutex>
@@ -443,92 +443,88 @@ __global__ __launch_bounds__(WAVES * 64) void attn_merge_kernel(const float* __r
 // them from their accumulators): per (query row bs, split j, head group hg) a 64 KB block in which
 // the 1 KB piece ((vw * 4 + mb) * 2 + h) holds, in lane l's 16 bytes, value columns
 // 128 (vw >> 1) + 32 mb + 16 h + 8 (l >> 5) .. +7 of head 64 hg + 32 (vw & 1) + (l & 31).
-// One workgroup of 4 waves per (query row, head group, 1 KB piece): wave qt takes a quarter of the
-// piece, lane m 4 bytes of source lane sl = 16 qt + (m >> 2), i.e. value columns
-// 8 (sl >> 5) + 2 (m & 3) + {0, 1} of the piece for head 32 (vw & 1) + (sl & 31); every split's
-// piece is 1 KB read by the workgroup at once.  The (m, l) records of the piece's 32 heads (the
-// split kernel's [row][split][head] fp32 pairs) go through LDS once per chunk of CH splits, read as
-// 256 contiguous bytes per split.  The O loads of a chunk are issued first, then its (m, l) loads
-// (for at most CH splits, the common case, one round trip); a later chunk whose maximum exceeds M
-// rescales the running sums first.  Per split the weight and the sums follow attn_merge_kernel's
-// formula.
+// One wave per (query row, head group, 1 KB piece): lane l reads source lane l's 16 bytes of the
+// piece in every split (8 values of one head) and the (m, l) record of that head (the split
+// kernel's [row][split][head] fp32 pairs), with no LDS and no barrier.  A chunk's O loads are
+// issued first, then its (m, l) loads (for at most CH splits, the common case, one round trip); a
+// later chunk whose maximum exceeds M rescales the running sums first.  Per split the weight and
+// the sums follow attn_merge_kernel's formula.  (Against 4-wave workgroups reading 4 bytes per
+// lane with the records staged in LDS: equal at 23 splits, 44.7 -> 42.4 us on the 64-sequence fp8
+// batch, whose 4 splits per row take CH = 8.)
 template <int CH>
-__global__ __launch_bounds__(256) void attn_merge_frag_kernel(const float* __restrict__ part, int nsplit, int64_t BS,
-                                                              int H, int HG, const float* __restrict__ sink,
-                                                              void* __restrict__ out, int out_dtype) {
-  __shared__ f32x2_t ml_s[CH][32];
+__global__ __launch_bounds__(64) void attn_merge_frag_kernel(const float* __restrict__ part, int nsplit, int64_t BS,
+                                                               int H, int HG, const float* __restrict__ sink,
+                                                               void* __restrict__ out, int out_dtype) {
   {
     const uint32_t gx = gridDim.x, gy = gridDim.y, gz = gridDim.z;
     asm volatile("" ::"s"(gx), "s"(gy), "s"(gz), "s"(part), "s"(nsplit), "s"(BS), "s"(H), "s"(HG), "s"(sink),
                  "s"(out), "s"(out_dtype));
   }
-  const int tid = threadIdx.x, lane = tid & 63, qt = tid >> 6;
-  // every piece of query row bs on XCD bs mod 8, where the split kernel left its partials
+  const int lane = threadIdx.x;
   int64_t bs, item;
   xcd_row_item(BS, (int64_t)HG * 64, bs, item);
   const int hg = (int)((uint32_t)item >> 6), piece = (int)((uint32_t)item & 63u);
   const int vw = piece >> 3, mb = (piece >> 1) & 3, h = piece & 1;
-  const int sl = 16 * qt + (lane >> 2);                        // source lane within the piece
-  const int hl = 32 * (vw & 1);                               // first head of the piece, in the group
-  const int head = 64 * hg + hl + (sl & 31);
-  const int dv0 = 128 * (vw >> 1) + 32 * mb + 16 * h + 8 * (sl >> 5) + 2 * (lane & 3);
+  const int hl = 32 * (vw & 1) + (lane & 31);  // head within the group
+  const int head = 64 * hg + hl;
+  const int dv0 = 128 * (vw >> 1) + 32 * mb + 16 * h + 8 * (lane >> 5);
   const uint8_t* ob = (const uint8_t*)(part + BS * H * nsplit * 2) + (bs * nsplit * (int64_t)HG + hg) * 65536 +
-                      piece * 1024 + 256 * qt + 4 * lane;      // split j: + j * HG * 64 KB
+                      piece * 1024 + 16 * lane;  // split j: + j * HG * 64 KB
   const int64_t job = (int64_t)HG * 65536;
-  const float* mlb = part + (bs * nsplit * (int64_t)H + 64 * hg + hl) * 2;
-  const int nh = min(32, H - (64 * hg + hl));                 // heads of the piece that exist
-  float M = -SMLA_INF, L = 0.f, a0 = 0.f, a1 = 0.f;
+  const float* mlb = part + (bs * nsplit * (int64_t)H + min(head, H - 1)) * 2;  // split j: + j * H * 2
+  float M = -SMLA_INF, L = 0.f, acc[8];
+#pragma unroll
+  for (int e = 0; e < 8; e++) acc[e] = 0.f;
   for (int j0 = 0; j0 < nsplit; j0 += CH) {
-    if (j0 > 0) __syncthreads();  // the previous chunk's (m, l) reads are done
-    uint32_t v[CH];
-    // unconditional loads (an index past the last split re-reads it and is masked below), the
-    // O values first
+    u32x4_t v[CH];
+    f32x2_t ml[CH];
 #pragma unroll
-    for (int u = 0; u < CH; u++) v[u] = *(const uint32_t*)(ob + min(j0 + u, nsplit - 1) * job);
-    f32x2_t st[CH * 32 / 256];
+    for (int u = 0; u < CH; u++) v[u] = *(const u32x4_t*)(ob + min(j0 + u, nsplit - 1) * job);
 #pragma unroll
-    for (int k = 0; k < CH * 32 / 256; k++) {
-      const int e = tid + 256 * k, jj = e >> 5, c = e & 31;
-      const int j = min(j0 + jj, nsplit - 1);
-      st[k] = *(const f32x2_t*)(mlb + ((int64_t)j * H + min(c, nh - 1)) * 2);
-    }
-#pragma unroll
-    for (int k = 0; k < CH * 32 / 256; k++) {
-      const int e = tid + 256 * k;
-      ml_s[e >> 5][e & 31] = st[k];
-    }
-    __syncthreads();
+    for (int u = 0; u < CH; u++) ml[u] = *(const f32x2_t*)(mlb + (int64_t)min(j0 + u, nsplit - 1) * H * 2);
     float mc = M;
 #pragma unroll
-    for (int u = 0; u < CH; u++) mc = fmaxf(mc, j0 + u < nsplit ? ml_s[u][sl & 31][0] : -SMLA_INF);
+    for (int u = 0; u < CH; u++) mc = fmaxf(mc, j0 + u < nsplit ? ml[u][0] : -SMLA_INF);
     if (mc > M && M > -SMLA_INF) {  // a later chunk raised the maximum (only past CH splits)
       const float r = __expf(M - mc);
       L *= r;
-      a0 *= r;
-      a1 *= r;
+#pragma unroll
+      for (int e = 0; e < 8; e++) acc[e] *= r;
     }
     M = mc;
 #pragma unroll
     for (int u = 0; u < CH; u++) {
-      const f32x2_t t = ml_s[u][sl & 31];
-      const float m = j0 + u < nsplit ? t[0] : -SMLA_INF;
+      const float m = j0 + u < nsplit ? ml[u][0] : -SMLA_INF;
       const float w = m > -SMLA_INF ? __expf(m - M) : 0.f;
-      L += w * t[1];
-      a0 += w * __uint_as_float(v[u] << 16);
-      a1 += w * __uint_as_float(v[u] & 0xffff0000u);
+      L += w * ml[u][1];
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        acc[2 * e] += w * __uint_as_float(v[u][e] << 16);
+        acc[2 * e + 1] += w * __uint_as_float(v[u][e] & 0xffff0000u);
+      }
     }
   }
-  const bool empty = !(M > -SMLA_INF);
   if (head >= H) return;
+  const bool empty = !(M > -SMLA_INF);
   const float snk = sink ? sink[head] : -SMLA_INF;
   if (!empty) L += __expf(snk - M);
   const float inv = 1.0f / L;
   const int64_t o = (bs * H + head) * 512 + dv0;
   if (out_dtype == SMLA_BF16) {
-    *(uint32_t*)((uint16_t*)out + o) = empty ? 0x7fc07fc0u : pack_bf16x2(a0 * inv, a1 * inv);
+    u32x4_t w4;
+#pragma unroll
+    for (int e = 0; e < 4; e++) w4[e] = empty ? 0x7fc07fc0u : pack_bf16x2(acc[2 * e] * inv, acc[2 * e + 1] * inv);
+    *(u32x4_t*)((uint16_t*)out + o) = w4;
   } else {
     const float nan = __builtin_nanf("");
-    *(f32x2_t*)((float*)out + o) = empty ? f32x2_t{nan, nan} : f32x2_t{a0 * inv, a1 * inv};
+    f32x4_t a, c;
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      a[e] = empty ? nan : acc[e] * inv;
+      c[e] = empty ? nan : acc[4 + e] * inv;
+    }
+    *(f32x4_t*)((float*)out + o) = a;
+    *(f32x4_t*)((float*)out + o + 4) = c;
   }
 }
 
@@ -592,16 +588,16 @@ int launch_merge(const Plan& p, int64_t B, int64_t S, int64_t H, const float* si
   if (part_bf16) {  // fragment-order partials: one workgroup per (query row, head group, 1 KB piece)
     const dim3 grid((unsigned)(B * S * p.hgroups * 64));
     if (p.nsplit <= 8)
-      hipLaunchKernelGGL(attn_merge_frag_kernel<8>, grid, dim3(256), 0, stream, (const float*)ws, p.nsplit, B * S,
+      hipLaunchKernelGGL(attn_merge_frag_kernel<8>, grid, dim3(64), 0, stream, (const float*)ws, p.nsplit, B * S,
                          (int)H, p.hgroups, sink, out, out_dtype);
     else if (p.nsplit <= 16)
-      hipLaunchKernelGGL(attn_merge_frag_kernel<16>, grid, dim3(256), 0, stream, (const float*)ws, p.nsplit, B * S,
+      hipLaunchKernelGGL(attn_merge_frag_kernel<16>, grid, dim3(64), 0, stream, (const float*)ws, p.nsplit, B * S,
                          (int)H, p.hgroups, sink, out, out_dtype);
     else if (p.nsplit <= 24)
-      hipLaunchKernelGGL(attn_merge_frag_kernel<24>, grid, dim3(256), 0, stream, (const float*)ws, p.nsplit, B * S,
+      hipLaunchKernelGGL(attn_merge_frag_kernel<24>, grid, dim3(64), 0, stream, (const float*)ws, p.nsplit, B * S,
                          (int)H, p.hgroups, sink, out, out_dtype);
     else
-      hipLaunchKernelGGL(attn_merge_frag_kernel<32>, grid, dim3(256), 0, stream, (const float*)ws, p.nsplit, B * S,
+      hipLaunchKernelGGL(attn_merge_frag_kernel<32>, grid, dim3(64), 0, stream, (const float*)ws, p.nsplit, B * S,
                          (int)H, p.hgroups, sink, out, out_dtype);
     SMLA_HIP_CHECK_LAUNCH();
     return SMLA_OK;
