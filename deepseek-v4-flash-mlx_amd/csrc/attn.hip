@@ -39,9 +39,25 @@ __device__ inline const uint8_t* row_ptr(const RowSrc& src, int64_t b, int64_t r
 // contiguous sixteenth of the index list and walks it R rows at a time: lane l holds columns
 // l, l+64, ... of each row (coalesced row loads, 64 columns per load instruction), the dot with q
 // is a DPP wave sum, and the wave keeps its own online-softmax state (m, l, O).  The 16 states merge
-// through LDS at the end in a fixed order, so the result does not depend on timing.
+// through LDS at the end in a fixed order, so the result does not depend on timing.  The kernel is
+// bound by each workgroup's own gather: every (query row, head) reads all T rows (1.2 MB for 512
+// fp32 rows of 576), about the rate one CU takes in.
 constexpr int kGenWaves = 16;
 constexpr int kGenThreads = 64 * kGenWaves;
+
+// a row element in its storage type (the register a load lands in) and its fp32 value
+template <int KT>
+using RawElem = typename std::conditional<
+    KT == SMLA_F32, float,
+    typename std::conditional<KT == SMLA_BF16, uint16_t,
+                              typename std::conditional<KT == SMLA_F16, _Float16, uint8_t>::type>::type>::type;
+template <int KT>
+__device__ inline float raw_to_f32(RawElem<KT> x) {
+  if constexpr (KT == SMLA_F32) return x;
+  else if constexpr (KT == SMLA_BF16) return bf16_bits_to_f32(x);
+  else if constexpr (KT == SMLA_F16) return (float)x;
+  else return e4m3_to_f32(x);
+}
 
 template <int KT>
 __device__ inline float load_elem(const uint8_t* row, int64_t i) {
@@ -59,7 +75,10 @@ __global__ __launch_bounds__(kGenThreads) void attn_generic_kernel(
     const void* __restrict__ q, int q_dtype, RowSrc src, const float* __restrict__ sink,
     const int32_t* __restrict__ idx, int64_t T, int64_t S, int64_t H, int64_t D, int64_t DV, float scale,
     void* __restrict__ out, int out_dtype) {
-  constexpr int R = NC <= 4 ? 8 : (NC <= 9 ? 4 : 2);  // rows in flight per wave
+  // rows per batch: two batches in flight per wave when the row fits NC chunks (ONE), one
+  // otherwise; sized to the 128 registers of a 16-wave workgroup (3 rows per batch at NC = 9
+  // spill, and measured no faster)
+  constexpr int R = ONE ? (NC <= 4 ? 8 : (NC <= 9 ? 2 : 1)) : 2;
   constexpr int NA = ONE ? NC : 16;                   // value chunks held (DV <= 1024)
   constexpr int ES = KT == SMLA_F32 ? 4 : (KT == SMLA_FP8_E4M3 ? 1 : 2);
   constexpr int HW = kGenWaves / 2;
@@ -92,43 +111,105 @@ __global__ __launch_bounds__(kGenThreads) void attn_generic_kernel(
   const int64_t per = (T + kGenWaves - 1) / kGenWaves;
   const int64_t t_beg = wv * per;
   const int64_t t_end = t_beg + per < T ? t_beg + per : T;
-  for (int64_t tb = t_beg; tb < t_end; tb += 64) {
-    const int nb = (int)(t_end - tb < 64 ? t_end - tb : 64);
-    const int idv = lane < nb ? ids[tb + lane] : -1;
-    for (int j = 0; j < nb; j += R) {
-      const uint8_t* rp[R];
-      const float* sp[R];
-      bool ok[R];
+  // online-softmax update of the wave's state with R rows: scores s (-inf: masked), values in
+  // x(k, c) for the NA value chunks
+  auto update = [&](const float (&s)[R], auto&& x) {
+    float mx = m_run;
+#pragma unroll
+    for (int k = 0; k < R; k++) mx = fmaxf(mx, s[k]);
+    if (mx > -SMLA_INF) {
+      const float alpha = m_run > -SMLA_INF ? __expf(m_run - mx) : 0.f;
+      float p[R];
+      float ps = 0.f;
 #pragma unroll
       for (int k = 0; k < R; k++) {
-        const int r = j + k < nb ? __builtin_amdgcn_readlane(idv, (j + k) & 63) : -1;
-        ok[k] = r >= 0 && r < ntot;
-        sp[k] = nullptr;
-        rp[k] = ok[k] ? row_ptr(src, b, r, D, ES, &sp[k]) : nullptr;
+        p[k] = s[k] > -SMLA_INF ? __expf(s[k] - mx) : 0.f;
+        ps += p[k];
       }
-      float dot[R];
-      float v[ONE ? R : 1][ONE ? NC : 1];
-      if constexpr (ONE) {
+      l_run = l_run * alpha + ps;
 #pragma unroll
-        for (int k = 0; k < R; k++)
+      for (int c = 0; c < NA; c++) {
+        float a = acc[c] * alpha;
 #pragma unroll
-          for (int c = 0; c < NC; c++) {
-            const int64_t d = 64 * c + lane;
-            float x = 0.f;
-            if (ok[k] && c < nch && d < D) {
-              x = load_elem<KT>(rp[k], d);
-              if constexpr (KT == SMLA_FP8_E4M3) x *= sp[k][c];
-            }
-            v[k][c] = x;
-          }
+        for (int k = 0; k < R; k++) a = fmaf(p[k], x(k, c), a);
+        acc[c] = a;
+      }
+      m_run = mx;
+    }
+  };
+  if constexpr (ONE) {
+    // Two batches of R rows in flight: a batch's loads are issued one batch ahead of their use.
+    // Every fetch issues the same loads (masked rows read row 0, columns past D column D - 1,
+    // rows past the block are masked), so the compiler's wait counts stay exact.
+    struct Batch {
+      RawElem<KT> v[R][NC];
+      float sc[R][KT == SMLA_FP8_E4M3 ? NC : 1];
+      bool ok[R];
+    };
+    for (int64_t tb = t_beg; tb < t_end; tb += 64) {
+      const int nb = (int)(t_end - tb < 64 ? t_end - tb : 64);
+      const int idv = lane < nb ? ids[tb + lane] : -1;
+      auto fetch = [&](int j, Batch& bt) {
 #pragma unroll
         for (int k = 0; k < R; k++) {
-          float s = 0.f;
+          const int r = j + k < nb ? __builtin_amdgcn_readlane(idv, (j + k) & 63) : -1;
+          bt.ok[k] = r >= 0 && r < ntot;
+          const float* sp = nullptr;
+          const uint8_t* rp = row_ptr(src, b, bt.ok[k] ? r : 0, D, ES, &sp);
 #pragma unroll
-          for (int c = 0; c < NC; c++) s = fmaf(qv[c], v[k][c], s);
-          dot[k] = s;
+          for (int c = 0; c < NC; c++) {
+            const int64_t d = 64 * c + lane < D ? 64 * c + lane : D - 1;
+            bt.v[k][c] = ((const RawElem<KT>*)rp)[d];
+            if constexpr (KT == SMLA_FP8_E4M3) bt.sc[k][c] = sp[c < nch ? c : nch - 1];
+          }
         }
-      } else {
+      };
+      // element (k, c) of a fetched batch as fp32 (0 for masked rows and columns past D); computed
+      // where it is used, so a batch holds only its loaded registers
+      auto elem = [&](const Batch& bt, int k, int c) -> float {
+        float x = 64 * c + lane < D ? raw_to_f32<KT>(bt.v[k][c]) : 0.f;
+        if constexpr (KT == SMLA_FP8_E4M3) x *= bt.sc[k][c];
+        return bt.ok[k] ? x : 0.f;
+      };
+      auto consume = [&](const Batch& bt) {
+        float s[R];
+#pragma unroll
+        for (int k = 0; k < R; k++) {
+          float dt = 0.f;
+#pragma unroll
+          for (int c = 0; c < NC; c++) dt = fmaf(qv[c], elem(bt, k, c), dt);
+          const float tot = wave_sum_dpp(dt);
+          s[k] = bt.ok[k] ? scale * tot : -SMLA_INF;
+        }
+        update(s, [&](int k, int c) { return elem(bt, k, c); });
+      };
+      Batch ba, bb;
+      fetch(0, ba);
+      for (int j = 0; j < nb; j += 2 * R) {
+        fetch(j + R, bb);
+        consume(ba);
+        fetch(j + 2 * R, ba);
+        if (j + R < nb) consume(bb);
+      }
+    }
+  }
+  if constexpr (!ONE) {
+    // rows longer than NC chunks: the dot in blocks of NC chunks, the value columns loaded again
+    for (int64_t tb = t_beg; tb < t_end; tb += 64) {
+      const int nb = (int)(t_end - tb < 64 ? t_end - tb : 64);
+      const int idv = lane < nb ? ids[tb + lane] : -1;
+      for (int j = 0; j < nb; j += R) {
+        const uint8_t* rp[R];
+        const float* sp[R];
+        bool ok[R];
+#pragma unroll
+        for (int k = 0; k < R; k++) {
+          const int r = j + k < nb ? __builtin_amdgcn_readlane(idv, (j + k) & 63) : -1;
+          ok[k] = r >= 0 && r < ntot;
+          sp[k] = nullptr;
+          rp[k] = ok[k] ? row_ptr(src, b, r, D, ES, &sp[k]) : nullptr;
+        }
+        float dot[R];
 #pragma unroll
         for (int k = 0; k < R; k++) dot[k] = 0.f;
         for (int c0 = 0; c0 < nch; c0 += NC) {
@@ -154,51 +235,21 @@ __global__ __launch_bounds__(kGenThreads) void attn_generic_kernel(
             for (int k = 0; k < R; k++) dot[k] = fmaf(qd, w[k][c], dot[k]);
           }
         }
-      }
-      float s[R];
-      float mx = m_run;
-#pragma unroll
-      for (int k = 0; k < R; k++) {
-        const float tot = wave_sum_dpp(dot[k]);
-        s[k] = ok[k] ? scale * tot : -SMLA_INF;
-        mx = fmaxf(mx, s[k]);
-      }
-      if (mx > -SMLA_INF) {
-        const float alpha = m_run > -SMLA_INF ? __expf(m_run - mx) : 0.f;
-        float p[R];
-        float ps = 0.f;
+        float s[R];
 #pragma unroll
         for (int k = 0; k < R; k++) {
-          p[k] = ok[k] ? __expf(s[k] - mx) : 0.f;
-          ps += p[k];
+          const float tot = wave_sum_dpp(dot[k]);
+          s[k] = ok[k] ? scale * tot : -SMLA_INF;
         }
-        l_run = l_run * alpha + ps;
-        if constexpr (ONE) {
-#pragma unroll
-          for (int c = 0; c < NA; c++) {
-            float a = acc[c] * alpha;
-#pragma unroll
-            for (int k = 0; k < R; k++) a = fmaf(p[k], v[k][c], a);
-            acc[c] = a;
+        update(s, [&](int k, int c) {
+          const int64_t d = 64 * c + lane;
+          float x = 0.f;
+          if (ok[k] && d < DV) {
+            x = load_elem<KT>(rp[k], d);
+            if constexpr (KT == SMLA_FP8_E4M3) x *= sp[k][c];
           }
-        } else {
-#pragma unroll
-          for (int c = 0; c < NA; c++) {
-            const int64_t d = 64 * c + lane;
-            float a = acc[c] * alpha;
-#pragma unroll
-            for (int k = 0; k < R; k++) {
-              float x = 0.f;
-              if (ok[k] && d < DV) {
-                x = load_elem<KT>(rp[k], d);
-                if constexpr (KT == SMLA_FP8_E4M3) x *= sp[k][c];
-              }
-              a = fmaf(p[k], x, a);
-            }
-            acc[c] = a;
-          }
-        }
-        m_run = mx;
+          return x;
+        });
       }
     }
   }
