@@ -122,9 +122,9 @@ size_t smla_sparse_attn_workspace(int64_t B, int64_t S, int64_t H, int64_t D, in
 /* The split plan of the attention path for these sizes, a pure function of the arguments and the
  * device's compute-unit count.  rows_per_split: index-list rows per split requested (a multiple of
  * 32), or 0 for the default plan (enough splits to give every compute unit a workgroup, at least
- * two 32-row tiles each).  Writes the number of splits (0 when the fp32 generic kernel runs, which
- * does not split) and the rows per split, either pointer may be NULL; returns the workspace bytes
- * that plan needs for out_dtype (0: none). */
+ * two 32-row tiles each).  Writes the number of splits (0 when the vector-ALU kernel runs: F32 /
+ * F16 operands or shapes the MFMA kernel does not take; it does not split) and the rows per split,
+ * either pointer may be NULL; returns the workspace bytes that plan needs for out_dtype (0: none). */
 size_t smla_sparse_attn_plan(int64_t B, int64_t S, int64_t H, int64_t D, int64_t DV, int64_t T,
                              int q_dtype, int kv_dtype, int out_dtype, int64_t rows_per_split,
                              int64_t* nsplit, int64_t* rows_per_split_out);
