@@ -52,7 +52,10 @@ def _lib():
 def test_fp32_generic_path_small(dev):
     from smla import sparse_attn as ssa
     g = torch.Generator().manual_seed(0)
-    for (s, h, d, n, T, dv) in [(1, 16, 576, 300, 100, 512), (3, 5, 40, 50, 33, 40), (2, 2, 64, 10, 300, 32)]:
+    # D 576 / 40 / 64: rows held in registers; 700: 16 register chunks; 1100: the dot in blocks of
+    # 16 chunks, value columns loaded again
+    for (s, h, d, n, T, dv) in [(1, 16, 576, 300, 100, 512), (3, 5, 40, 50, 33, 40), (2, 2, 64, 10, 300, 32),
+                                (2, 3, 700, 400, 150, 512), (1, 4, 1100, 300, 77, 700)]:
         announce(f"fp32 generic s={s} h={h} d={d} n={n} T={T}")
         q = torch.randn(s, h, d, generator=g)
         kv = torch.randn(n, d, generator=g)
