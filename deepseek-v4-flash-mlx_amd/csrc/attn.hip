@@ -593,7 +593,7 @@ Plan make_plan(int64_t B, int64_t S, int64_t H, int64_t D, int64_t DV, int64_t T
                int64_t rps_req) {
   Plan p{};
   p.mfma = q_dtype == SMLA_BF16 && (kv_dtype == SMLA_BF16 || kv_dtype == SMLA_FP8_E4M3) &&
-           H % 16 == 0 && DV == 512 && (D == 576 || D == 512) && T > 0 && T < (1ll << 30) && B * S <= 65535;
+           H % 16 == 0 && DV == 512 && (D == 576 || D == 512) && T > 0 && T < (1ll << 30);
   if (!p.mfma) return p;
   p.hgroups = (int)((H + 63) / 64);
   const int64_t rows = B * S * p.hgroups;
@@ -630,6 +630,41 @@ size_t plan_workspace(const Plan& p, int64_t B, int64_t S, int64_t H, int64_t DV
   const size_t ml = recs * (size_t)H * 2 * sizeof(float);
   if (out_dtype == SMLA_BF16) return ml + recs * (size_t)p.hgroups * 65536;
   return ml + recs * (size_t)H * (size_t)DV * 4;
+}
+
+// The split kernel's grid holds at most kChunkRows query rows (its y dimension, 65535 at most; a
+// multiple of 8 keeps the XCD pinning of rows).  Longer calls run as launches over row chunks:
+// whole batch entries while one sequence fits, else pieces of one sequence.  f(b0, s0, nb, ns)
+// runs the chunk of query rows b0*S + s0 .. as a call of nb entries of ns rows; the first nonzero
+// return ends the walk.
+constexpr int64_t kChunkRows = 65528;
+
+template <class F>
+int for_row_chunks(int64_t B, int64_t S, F&& f) {
+  if (B * S <= kChunkRows) return f((int64_t)0, (int64_t)0, B, S);
+  if (S <= kChunkRows) {
+    const int64_t per = kChunkRows / S;
+    for (int64_t b0 = 0; b0 < B; b0 += per)
+      if (const int rc = f(b0, (int64_t)0, std::min(per, B - b0), S); rc != SMLA_OK) return rc;
+    return SMLA_OK;
+  }
+  for (int64_t b = 0; b < B; b++)
+    for (int64_t s0 = 0; s0 < S; s0 += kChunkRows)
+      if (const int rc = f(b, s0, (int64_t)1, std::min(kChunkRows, S - s0)); rc != SMLA_OK) return rc;
+  return SMLA_OK;
+}
+
+// the row sources of batch entries b0.. (rows of row_bytes bytes; fp8 rows with D/64 scales each)
+RowSrc rows_from(const RowSrc& s, int64_t b0, int64_t row_bytes, int64_t scales_per_row) {
+  auto adv = [](const void* p, int64_t bytes) -> const void* {
+    return p ? (const void*)((const uint8_t*)p + bytes) : nullptr;
+  };
+  RowSrc r = s;
+  r.kv0 = adv(s.kv0, b0 * s.n0 * row_bytes);
+  r.kv1 = adv(s.kv1, b0 * s.n1 * row_bytes);
+  r.sc0 = (const float*)adv(s.sc0, b0 * s.n0 * scales_per_row * (int64_t)sizeof(float));
+  r.sc1 = (const float*)adv(s.sc1, b0 * s.n1 * scales_per_row * (int64_t)sizeof(float));
+  return r;
 }
 
 int launch_merge(const Plan& p, int64_t B, int64_t S, int64_t H, const float* sink, void* out, int out_dtype,
@@ -712,7 +747,9 @@ int check_attn_args(const void* q, int q_dtype, const void* kv0, int64_t n0, con
 
 // The launches of one attention call under plan p (phases: SMLA_ATTN_SPLIT and / or
 // SMLA_ATTN_MERGE), with `ws` holding at least plan_workspace(p, ...) bytes.  Arguments are
-// checked by the caller.
+// checked by the caller.  Calls of more query rows than one grid holds run chunk by chunk
+// (for_row_chunks), each chunk's partial states in its own stretch of the workspace, so a merge
+// alone finds what a split alone left.
 static int attn_launch(const Plan& p, int phases, const void* q, int q_dtype, RowSrc src, int kv_dtype,
                      const float* attn_sink, const int32_t* topk_idxs, int64_t T, int64_t B, int64_t S, int64_t H,
                      int64_t D, int64_t DV, float scale, void* out, int out_dtype, void* ws, hipStream_t st,
@@ -722,14 +759,31 @@ static int attn_launch(const Plan& p, int phases, const void* q, int q_dtype, Ro
     return launch_generic(q, q_dtype, src, kv_dtype, attn_sink, topk_idxs, T, B, S, H, D, DV, scale, out, out_dtype,
                           st);
   }
-  if (phases & SMLA_ATTN_SPLIT) {
-    const int rc = smla_attn::launch_decode_v6((int)D, kv_dtype == SMLA_FP8_E4M3, p.nsplit, p.rows_per_split, q, src,
-                                               attn_sink, topk_idxs, T, B, S, H, scale, out, out_dtype, (float*)ws,
-                                               st, smla_attn::ImplicitRows{}, sr);
-    if (rc != SMLA_OK) return rc;
-  }
-  if (phases & SMLA_ATTN_MERGE) return launch_merge(p, B, S, H, attn_sink, out, out_dtype, ws, st);
-  return SMLA_OK;
+  const bool fp8 = kv_dtype == SMLA_FP8_E4M3;
+  const int64_t row_bytes = fp8 ? D : 2 * D;
+  const int64_t out_row = H * DV * (out_dtype == SMLA_BF16 ? 2 : 4);
+  return for_row_chunks(B, S, [&](int64_t b0, int64_t s0, int64_t nb, int64_t ns) -> int {
+    const int64_t r0 = b0 * S + s0;  // first query row of the chunk
+    const void* cq = (const uint16_t*)q + r0 * H * D;
+    const RowSrc csrc = rows_from(src, b0, row_bytes, fp8 ? D / 64 : 0);
+    const int32_t* cidx = topk_idxs ? topk_idxs + r0 * T : nullptr;
+    void* cout = (uint8_t*)out + r0 * out_row;
+    void* cws = ws ? (uint8_t*)ws + plan_workspace(p, 1, r0, H, DV, out_dtype) : nullptr;
+    smla_attn::SelectRows csr = sr;
+    if (sr.enabled) {
+      csr.scores = sr.scores + r0 * (int64_t)sr.N;
+      csr.nvis = sr.nvis ? sr.nvis + r0 : nullptr;
+      csr.pos = sr.pos + r0;
+    }
+    if (phases & SMLA_ATTN_SPLIT) {
+      const int rc = smla_attn::launch_decode_v6((int)D, fp8, p.nsplit, p.rows_per_split, cq, csrc, attn_sink, cidx, T,
+                                                 nb, ns, H, scale, cout, out_dtype, (float*)cws, st,
+                                                 smla_attn::ImplicitRows{}, csr);
+      if (rc != SMLA_OK) return rc;
+    }
+    if (phases & SMLA_ATTN_MERGE) return launch_merge(p, nb, ns, H, attn_sink, cout, out_dtype, cws, st);
+    return SMLA_OK;
+  });
 }
 
 // the checks and plan of one call, then its launches on `ws` (ws_bytes of it)
@@ -769,12 +823,19 @@ extern "C" int smla_prefill_attn(const void* q, int q_dtype, const void* kv_raw,
   const int64_t nc_max = ratio > 0 ? std::min((q_pos0 + S) / ratio, n_comp) : 0;
   const int64_t T = window + nc_max;
   const int64_t rows = (T + kTileRows - 1) / kTileRows * kTileRows;
-  if (rows > (1 << 24) || B * S > 65535 || window > (1 << 24)) return SMLA_E_UNSUPPORTED;
+  if (rows > (1 << 24) || window > (1 << 24)) return SMLA_E_UNSUPPORTED;
   const smla_attn::RowSrc src{kv_raw, nc_max > 0 ? kv_comp : nullptr, nullptr, nullptr, n_raw,
                               nc_max > 0 ? n_comp : 0};
-  const smla_attn::ImplicitRows ir{q_pos0, (int)window, (int)ratio, 1};
-  return smla_attn::launch_decode_v6((int)D, false, 1, (int)rows, q, src, attn_sink, nullptr, T, B, S, H, scale, out,
-                                     out_dtype, nullptr, (hipStream_t)stream, ir);
+  const int64_t out_row = H * DV * (out_dtype == SMLA_BF16 ? 2 : 4);
+  // more query rows than one grid holds: launches over row chunks, the positions of a piece of a
+  // sequence starting at q_pos0 + s0
+  return for_row_chunks(B, S, [&](int64_t b0, int64_t s0, int64_t nb, int64_t ns) -> int {
+    const int64_t r0 = b0 * S + s0;
+    const smla_attn::ImplicitRows ir{q_pos0 + s0, (int)window, (int)ratio, 1};
+    return smla_attn::launch_decode_v6((int)D, false, 1, (int)rows, (const uint16_t*)q + r0 * H * D,
+                                       rows_from(src, b0, 2 * D, 0), attn_sink, nullptr, T, nb, ns, H, scale,
+                                       (uint8_t*)out + r0 * out_row, out_dtype, nullptr, (hipStream_t)stream, ir);
+  });
 }
 
 // Decode attention over the engine's index build (window ids of pos, then the top-k of the

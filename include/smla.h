@@ -97,12 +97,12 @@ int smla_api_version(void);
  *   p_t = exp(scale q.kv[idx_t] - m), m = max over valid t.  No valid index -> NaN.
  * Duplicate ids count once per occurrence.
  *
- * Kernels: q BF16 with BF16 or FP8 rows, H % 16 == 0, D 576 or 512, DV 512, B*S <= 65535 and a
- * plan of at most 1024 splits (index lists up to 8192 rows per split) run the split-K MFMA kernel
- * plus the merge; every other call (F32 / F16 operands, other H / D / DV, more query rows or
- * splits) runs the vector-ALU kernel, one workgroup per (query row, head), with the same results
- * to the tolerance of its dtype (both kernels are tested against the oracle for F32, BF16 and FP8
- * rows).
+ * Kernels: q BF16 with BF16 or FP8 rows, H % 16 == 0, D 576 or 512, DV 512 and a plan of at
+ * most 1024 splits (index lists up to 8192 rows per split) run the split-K MFMA kernel plus the
+ * merge, in launches of at most 65528 query rows (whole sequences while one fits, else pieces of
+ * one); every other call (F32 / F16 operands, other H / D / DV, more splits) runs the vector-ALU
+ * kernel, one workgroup per (query row, head), with the same results to the tolerance of its
+ * dtype (both kernels are tested against the oracle for F32, BF16 and FP8 rows).
  *
  * workspace: smla_sparse_attn_workspace() bytes (split-K partial states), may be 0.
  */
@@ -173,8 +173,9 @@ int smla_sparse_attn_noalloc(const void* q, int q_dtype,
  * exactly the sparse_attn call of the reference for that position (same result as
  * smla_sparse_attn over those index lists, bit for bit).  No index tensor and no workspace.
  *   q [B,S,H,D] BF16, kv_raw [B,n_raw,D] BF16, kv_comp [B,n_comp,D] BF16 or NULL (ratio 0),
- *   D 576 or 512, DV 512, H % 16 == 0, q_pos0 + S <= n_raw, B*S <= 65535,
- *   out [B,S,H,DV] BF16 or F32.  Workgroups take the queries longest list first. */
+ *   D 576 or 512, DV 512, H % 16 == 0, q_pos0 + S <= n_raw,
+ *   out [B,S,H,DV] BF16 or F32.  Workgroups take the queries longest list first, in launches of
+ *   at most 65528 queries (whole sequences while one fits, else pieces of one). */
 int smla_prefill_attn(const void* q, int q_dtype, const void* kv_raw, int64_t n_raw,
                       const void* kv_comp, int64_t n_comp, int kv_dtype, const float* attn_sink,
                       int64_t q_pos0, int64_t window, int64_t ratio, int64_t B, int64_t S,
