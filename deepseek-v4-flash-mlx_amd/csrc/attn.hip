@@ -632,28 +632,6 @@ size_t plan_workspace(const Plan& p, int64_t B, int64_t S, int64_t H, int64_t DV
   return ml + recs * (size_t)H * (size_t)DV * 4;
 }
 
-// The split kernel's grid holds at most kChunkRows query rows (its y dimension, 65535 at most; a
-// multiple of 8 keeps the XCD pinning of rows).  Longer calls run as launches over row chunks:
-// whole batch entries while one sequence fits, else pieces of one sequence.  f(b0, s0, nb, ns)
-// runs the chunk of query rows b0*S + s0 .. as a call of nb entries of ns rows; the first nonzero
-// return ends the walk.
-constexpr int64_t kChunkRows = 65528;
-
-template <class F>
-int for_row_chunks(int64_t B, int64_t S, F&& f) {
-  if (B * S <= kChunkRows) return f((int64_t)0, (int64_t)0, B, S);
-  if (S <= kChunkRows) {
-    const int64_t per = kChunkRows / S;
-    for (int64_t b0 = 0; b0 < B; b0 += per)
-      if (const int rc = f(b0, (int64_t)0, std::min(per, B - b0), S); rc != SMLA_OK) return rc;
-    return SMLA_OK;
-  }
-  for (int64_t b = 0; b < B; b++)
-    for (int64_t s0 = 0; s0 < S; s0 += kChunkRows)
-      if (const int rc = f(b, s0, (int64_t)1, std::min(kChunkRows, S - s0)); rc != SMLA_OK) return rc;
-  return SMLA_OK;
-}
-
 // the row sources of batch entries b0.. (rows of row_bytes bytes; fp8 rows with D/64 scales each)
 RowSrc rows_from(const RowSrc& s, int64_t b0, int64_t row_bytes, int64_t scales_per_row) {
   auto adv = [](const void* p, int64_t bytes) -> const void* {

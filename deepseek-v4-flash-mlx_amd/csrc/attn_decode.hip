@@ -125,8 +125,8 @@ __global__ __launch_bounds__(768) void attn_decode_kernel(
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   // grid (nsplit, B*S, head groups).  One split per query row and one head group (prefill): query
   // rows in XCD chunks (query_row_of); otherwise every split and head group of query row bs on XCD
-  // bs mod 8 (when B*S is a multiple of 8), where the selection left its index list and where the
-  // merge reads the partials back
+  // bs mod 8 (when B*S is a multiple of 8), so that they share the row's q block and index list in
+  // one L2
   const int nsplit = gridDim.x;
   int split = 0, hb = 0;  // hb: first head of this workgroup
   int64_t bs;

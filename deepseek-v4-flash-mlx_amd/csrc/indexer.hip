@@ -467,17 +467,31 @@ int indexer_score_any(const void* q, int q_dtype, const void* keys, int k_dtype,
   if (!q || !keys || !weights || !scores || (k_dtype == kFp4 && !kbs)) return SMLA_E_NULL;
   if (B <= 0 || S <= 0 || Hi <= 0 || Di <= 0 || N <= 0) return SMLA_E_SHAPE;
   if (q_dtype != SMLA_F32 && q_dtype != SMLA_BF16) return SMLA_E_DTYPE;
-  if (Hi > 256 || (Hi <= 64 && Hi * Di > kMaxQ) || (N + 63) / 64 > 0x7fffffff || B * S > 65535)
-    return SMLA_E_UNSUPPORTED;
+  if (Hi > 256 || (Hi <= 64 && Hi * Di > kMaxQ) || (N + 63) / 64 > 0x7fffffff) return SMLA_E_UNSUPPORTED;
+  if (Di != 32 && Di != 64 && Di != 128) return SMLA_E_UNSUPPORTED;
   // q rows and key rows are read as 16-byte words, fp4 scale bytes of a row as one 2-byte word
   if (((uintptr_t)q & 15) || ((uintptr_t)keys & 15) || ((uintptr_t)kbs & 1)) return SMLA_E_UNSUPPORTED;
   hipStream_t st = (hipStream_t)stream;
-  switch (Di) {
-    case 32: return launch_di<32>(q, q_dtype, keys, k_dtype, kbs, kscale, weights, nvis, B, S, Hi, N, scores, st);
-    case 64: return launch_di<64>(q, q_dtype, keys, k_dtype, kbs, kscale, weights, nvis, B, S, Hi, N, scores, st);
-    case 128: return launch_di<128>(q, q_dtype, keys, k_dtype, kbs, kscale, weights, nvis, B, S, Hi, N, scores, st);
-  }
-  return SMLA_E_UNSUPPORTED;
+  // bytes of one key row and of one q element
+  const int64_t krow = k_dtype == SMLA_F32 ? 4 * Di : k_dtype == SMLA_BF16 ? 2 * Di : k_dtype == kFp4 ? Di / 2 : Di;
+  const int64_t qel = q_dtype == SMLA_BF16 ? 2 : 4;
+  // the grid's y dimension is the query row: longer calls run as launches over row chunks, each
+  // with its q rows, weights, nvis and scores and its sequences' keys
+  return for_row_chunks(B, S, [&](int64_t b0, int64_t s0, int64_t nb, int64_t ns) -> int {
+    const int64_t r0 = b0 * S + s0;
+    const void* cq = (const uint8_t*)q + r0 * Hi * Di * qel;
+    const void* ck = (const uint8_t*)keys + b0 * N * krow;
+    const uint8_t* ckbs = kbs ? kbs + b0 * N * (Di / 32) : nullptr;
+    const float* cks = kscale ? kscale + b0 * N : nullptr;
+    const float* cw = weights + r0 * Hi;
+    const int32_t* cnv = nvis ? nvis + r0 : nullptr;
+    float* csc = scores + r0 * N;
+    switch (Di) {
+      case 32: return launch_di<32>(cq, q_dtype, ck, k_dtype, ckbs, cks, cw, cnv, nb, ns, Hi, N, csc, st);
+      case 64: return launch_di<64>(cq, q_dtype, ck, k_dtype, ckbs, cks, cw, cnv, nb, ns, Hi, N, csc, st);
+      default: return launch_di<128>(cq, q_dtype, ck, k_dtype, ckbs, cks, cw, cnv, nb, ns, Hi, N, csc, st);
+    }
+  });
 }
 }  // namespace
 

@@ -219,13 +219,15 @@ __device__ inline int wave_incl_scan(int x) {
 
 // ---------------------------------------------------------------------------------------------
 // XCD pinning.  The workgroups of a launch are dealt to the 8 XCDs round-robin in linear order
-// (workgroup L = x + gx (y + gy z) runs on XCD L mod 8), each XCD has its own L2, and what a kernel
-// leaves in an XCD's L2 is still there for the next kernel (a reader on the writer's XCD sees L2
-// latency, about half the latency of data another XCD wrote and a third of HBM's).  A launch over
-// `rows` x `items` workgroups (rows a multiple of 8) that places every item of row r on XCD
-// r mod 8 therefore hands row r's data to the next kernel that pins rows the same way in one L2:
-// the decode step pins its query rows in the indexer, the selection (one workgroup per row), the
-// attention splits and the merge.
+// (workgroup L = x + gx (y + gy z) runs on XCD L mod 8) and each XCD has its own L2 (a hit in
+// it costs about half the latency of a line served from another XCD's side and a third of HBM's).
+// A launch over `rows` x `items` workgroups (rows a multiple of 8) that places every item of row r
+// on XCD r mod 8 has all items of row r share its data in one L2: the attention splits of a query
+// row fetch its q block and index list once per sequence instead of once per XCD.  Across kernel
+// boundaries lines a kernel read stay in the L2; lines a kernel wrote are read back from memory
+// (the merge fetches as many bytes as the split kernel wrote), so pinning a consumer to its
+// producer's XCD saves no memory traffic.  The decode step pins its query rows the same way in
+// the indexer, the selection, the attention splits and the merge.
 constexpr int kXcds = 8;
 __device__ inline int64_t linear_block_id() {
   return (int64_t)blockIdx.x + (int64_t)gridDim.x * ((int64_t)blockIdx.y + (int64_t)gridDim.y * blockIdx.z);
@@ -250,6 +252,28 @@ __device__ inline void xcd_row_item(int64_t rows, int64_t items, int64_t& row, i
 // batch entry of query row bs with S query rows per entry (bs < 2^32: a grid dimension)
 __device__ inline int64_t batch_of(int64_t bs, int64_t S) {
   return S == 1 ? bs : (int64_t)((uint32_t)bs / (uint32_t)S);
+}
+
+// Launches whose grid has a query-row dimension (y: at most 65535) take at most kChunkRows query
+// rows (a multiple of 8 keeps the XCD pinning of rows).  Longer calls run as launches over row
+// chunks: whole batch entries while one entry fits, else pieces of one entry.  f(b0, s0, nb, ns)
+// runs the chunk of query rows b0*S + s0 .. as a call of nb entries of ns rows each; the first
+// nonzero return ends the walk.
+constexpr int64_t kChunkRows = 65528;
+
+template <class F>
+inline int for_row_chunks(int64_t B, int64_t S, F&& f) {
+  if (B * S <= kChunkRows) return f((int64_t)0, (int64_t)0, B, S);
+  if (S <= kChunkRows) {
+    const int64_t per = kChunkRows / S;
+    for (int64_t b0 = 0; b0 < B; b0 += per)
+      if (const int rc = f(b0, (int64_t)0, per < B - b0 ? per : B - b0, S); rc != 0) return rc;
+    return 0;
+  }
+  for (int64_t b = 0; b < B; b++)
+    for (int64_t s0 = 0; s0 < S; s0 += kChunkRows)
+      if (const int rc = f(b, s0, (int64_t)1, kChunkRows < S - s0 ? kChunkRows : S - s0); rc != 0) return rc;
+  return 0;
 }
 
 // ---------------------------------------------------------------------------------------------

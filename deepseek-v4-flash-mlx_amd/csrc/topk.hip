@@ -191,7 +191,7 @@ extern "C" int smla_index_decode(const void* q, int q_dtype, const void* keys, i
   if (window > 0 && id_offset > 0 && window > id_offset) return SMLA_E_SHAPE;
   if (!workspace || workspace_bytes < smla_index_decode_workspace(B, S, N)) return SMLA_E_WORKSPACE;
   const int64_t R = B * S;
-  if (R > 65535 || k > 0x7fffffff || window > 0x7fffffff || (N + kTopkThreads - 1) / kTopkThreads > 64)
+  if (R > 0x7fffffff || k > 0x7fffffff || window > 0x7fffffff || (N + kTopkThreads - 1) / kTopkThreads > 64)
     return SMLA_E_UNSUPPORTED;
   // the fixed-order scores (matrix-core chains for 64 heads x 64 dims) into the workspace, then the
   // exact selection; SMLA_INDEX_EXACT changes nothing (the scores are always the fixed-order ones)

@@ -274,8 +274,8 @@ int smla_select_decode(const float* scores, int64_t R, int64_t N, const int32_t*
  * R = B*S query rows, with the same output bit for bit.  Replaces the compressed index selection
  * of oracle/decode_engine.py:110-114 with an indexer-ranked one.
  * workspace: smla_index_decode_workspace(B, S, N) bytes (the B*S*N fp32 scores).  Requires
- * ceil(N / 1024) <= 64 and B*S <= 65535.  flags: 0 or SMLA_INDEX_EXACT (accepted, no effect:
- * the scores are always the fixed-order ones).
+ * ceil(N / 1024) <= 64.  flags: 0 or SMLA_INDEX_EXACT (accepted, no effect: the scores are always
+ * the fixed-order ones).
  */
 enum { SMLA_INDEX_EXACT = 1 };
 int smla_index_decode(const void* q, int q_dtype, const void* keys, int k_dtype, const float* kscale,

@@ -163,3 +163,89 @@ def test_decode_attn_pieces_of_one_sequence(dev):
     rows = _rows_near(S, [CHUNK])
     ref = _oracle_two_source(q[:, rows].cpu(), raw.cpu(), comp.cpu(), sink.cpu(), idx[:, rows].cpu(), scale, 512)
     _check_bf16(out[:, rows], ref, "long decode_attn")
+
+
+def _f32_bits(t):
+    return t.contiguous().view(torch.int32)
+
+
+def test_indexer_pieces_of_one_sequence(dev):
+    """Indexer scores for 66000 query rows of one sequence (64 heads x 64 dims: the matrix-core
+    kernel; launches of 65528 + 472 rows), fp8 keys with scales, ragged nvis: every row equal to
+    calls of fewer rows, the boundary rows bit-identical to the oracle."""
+    from oracle import indexer as oidx
+    from smla import indexer as sidx
+    from smla import workloads as wl
+    S, Hi, Di, N = 66000, 64, 64, 300
+    announce(f"long indexer S={S} Hi={Hi} Di={Di} N={N} fp8 keys")
+    gc = torch.Generator().manual_seed(6)
+    codes, ks = wl.quant_e4m3_pow2(torch.randn(1, N, Di, generator=gc), block=Di)
+    ks = ks.reshape(1, N)
+    g = torch.Generator(device=dev).manual_seed(6)
+    q = torch.randn(1, S, Hi, Di, generator=g, device=dev).to(torch.bfloat16)
+    w = torch.randn(1, S, Hi, generator=g, device=dev)
+    nvis = torch.randint(0, N + 1, (1, S), generator=g, device=dev, dtype=torch.int32)
+    cd, ksd = codes.to(dev), ks.to(dev)
+    out = sidx.indexer_score(q, cd, ksd, w, nvis)
+    for lo, hi in ((0, 40000), (40000, S)):
+        part = sidx.indexer_score(q[:, lo:hi].contiguous(), cd, ksd, w[:, lo:hi].contiguous(),
+                                  nvis[:, lo:hi].contiguous())
+        torch.cuda.synchronize()
+        assert torch.equal(_f32_bits(out[:, lo:hi]), _f32_bits(part)), f"rows {lo}..{hi}"
+    rows = _rows_near(S, [CHUNK])
+    ref = oidx.indexer_score(q[0, rows].float().cpu().numpy(), codes[0].view(torch.float8_e4m3fn).float().numpy(),
+                             ks[0].numpy(), w[0, rows].cpu().numpy(), nvis[0, rows].cpu().numpy())
+    assert torch.equal(_f32_bits(out[0, rows].cpu()), _f32_bits(torch.from_numpy(ref)))
+
+
+def test_indexer_whole_sequences_fp4(dev):
+    """Indexer scores for three sequences of 30000 query rows (launches of two sequences, then
+    one: keys, block scales and key scales offset per chunk), 16 heads (the vector-ALU kernel),
+    fp32 q, keys in the stored fp4 form."""
+    from oracle import indexer as oidx
+    from oracle import qat
+    from smla import indexer as sidx
+    B, S, Hi, Di, N = 3, 30000, 16, 64, 200
+    announce(f"long indexer B={B} S={S} Hi={Hi} N={N} fp4 keys")
+    gc = torch.Generator().manual_seed(7)
+    codes, scales = qat.fp4_quantize(qat.hadamard_rotate(torch.randn(B, N, Di, generator=gc).numpy()))
+    kvals = qat.fp4_dequantize(codes, scales)
+    ks = torch.rand(B, N, generator=gc) + 0.5
+    g = torch.Generator(device=dev).manual_seed(7)
+    q = torch.randn(B, S, Hi, Di, generator=g, device=dev)
+    w = torch.randn(B, S, Hi, generator=g, device=dev)
+    nvis = torch.randint(0, N + 1, (B, S), generator=g, device=dev, dtype=torch.int32)
+    cd, sd, ksd = torch.from_numpy(codes).to(dev), torch.from_numpy(scales).to(dev), ks.to(dev)
+    out = sidx.indexer_score_fp4(q, cd, sd, ksd, w, nvis)
+    for b in range(B):
+        part = sidx.indexer_score_fp4(q[b:b + 1].contiguous(), cd[b:b + 1].contiguous(), sd[b:b + 1].contiguous(),
+                                      ksd[b:b + 1].contiguous(), w[b:b + 1].contiguous(), nvis[b:b + 1].contiguous())
+        torch.cuda.synchronize()
+        assert torch.equal(_f32_bits(out[b:b + 1]), _f32_bits(part)), f"sequence {b}"
+    rows = _rows_near(S, [])
+    for b in (1, 2):
+        ref = oidx.indexer_score(q[b, rows].cpu().numpy(), kvals[b], ks[b].numpy(), w[b, rows].cpu().numpy(),
+                                 nvis[b, rows].cpu().numpy())
+        assert torch.equal(_f32_bits(out[b, rows].cpu()), _f32_bits(torch.from_numpy(ref))), f"sequence {b}"
+
+
+def test_index_decode_pieces_of_one_sequence(dev):
+    """Indexer scores and the decode index build in one call over 66000 query rows of one
+    sequence: equal to the scores followed by the selection."""
+    from smla import indexer as sidx
+    from smla import workloads as wl
+    S, Hi, Di, N, k, window, n_raw = 66000, 64, 64, 512, 64, 16, 4096
+    announce(f"long index_decode S={S} N={N} k={k}")
+    gc = torch.Generator().manual_seed(8)
+    codes, ks = wl.quant_e4m3_pow2(torch.randn(1, N, Di, generator=gc), block=Di)
+    cd, ksd = codes.to(dev), ks.reshape(1, N).to(dev)
+    g = torch.Generator(device=dev).manual_seed(8)
+    q = torch.randn(1, S, Hi, Di, generator=g, device=dev).to(torch.bfloat16)
+    w = torch.randn(1, S, Hi, generator=g, device=dev)
+    nvis = torch.randint(1, N + 1, (1, S), generator=g, device=dev, dtype=torch.int32)
+    pos = torch.randint(0, n_raw, (S,), generator=g, device=dev, dtype=torch.int32)
+    fused = sidx.index_decode(q, cd, ksd, w, nvis, k, pos, window, n_raw)
+    sc = sidx.indexer_score(q, cd, ksd, w, nvis)
+    two = sidx.select_decode_indices(sc[0], k, pos, window, n_raw, nvis=nvis[0])
+    torch.cuda.synchronize()
+    assert torch.equal(fused, two)
