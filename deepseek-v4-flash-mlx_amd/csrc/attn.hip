@@ -494,24 +494,31 @@ __global__ __launch_bounds__(WAVES * 64) void attn_merge_kernel(const float* __r
 // them from their accumulators): per (query row bs, split j, head group hg) a 64 KB block in which
 // the 1 KB piece ((vw * 4 + mb) * 2 + h) holds, in lane l's 16 bytes, value columns
 // 128 (vw >> 1) + 32 mb + 16 h + 8 (l >> 5) .. +7 of head 64 hg + 32 (vw & 1) + (l & 31).
-// One wave per (query row, head group, 1 KB piece): lane l reads source lane l's 16 bytes of the
-// piece in every split (8 values of one head) and the (m, l) record of that head (the split
-// kernel's [row][split][head] fp32 pairs), with no LDS and no barrier.  A chunk's O loads are
-// issued first, then its (m, l) loads (for at most CH splits, the common case, one round trip); a
-// later chunk whose maximum exceeds M rescales the running sums first.  Per split the weight and
-// the sums follow attn_merge_kernel's formula.  (Against 4-wave workgroups reading 4 bytes per
-// lane with the records staged in LDS: equal at 23 splits, 44.7 -> 42.4 us on the 64-sequence fp8
-// batch, whose 4 splits per row take CH = 8.)
-template <int CH>
-__global__ __launch_bounds__(64) void attn_merge_frag_kernel(const float* __restrict__ part, int nsplit, int64_t BS,
-                                                               int H, int HG, const float* __restrict__ sink,
-                                                               void* __restrict__ out, int out_dtype) {
+// One workgroup of NW waves per (query row, head group, 1 KB piece): lane l reads source lane l's
+// 16 bytes of the piece in every split (8 values of one head) and the (m, l) record of that head
+// (the split kernel's [row][split][head] fp32 pairs).  Wave w takes the w-th of NW equal runs of
+// the splits; a run's O loads are issued CH at a time, then their (m, l) loads, so up to NW * CH
+// splits cost one round trip; a later chunk whose maximum exceeds M rescales the running sums
+// first.  Loads past the end of a run read its last split again (weight 0; spreading them over
+// other splits costs SGPR spills of the per-load offsets and measured slower).  With NW > 1 the
+// waves' states meet in LDS and wave 0 combines them in wave order.  Per split the weight and the
+// sums follow attn_merge_kernel's formula.  (Against 4-wave workgroups reading 4 bytes per lane
+// with the records staged in LDS: equal at 23 splits, 44.7 -> 42.4 us on the 64-sequence fp8
+// batch, whose 4 splits per row take CH = 8.  Two waves of 17 splits instead of one wave taking
+// 32 then 2 on the one-sequence 16384-key decode step, 34 splits per row: 32.9 -> 29.7 us per
+// step.)
+template <int CH, int NW = 1>
+__global__ __launch_bounds__(64 * NW) void attn_merge_frag_kernel(const float* __restrict__ part, int nsplit,
+                                                                    int64_t BS, int H, int HG,
+                                                                    const float* __restrict__ sink,
+                                                                    void* __restrict__ out, int out_dtype) {
   {
     const uint32_t gx = gridDim.x, gy = gridDim.y, gz = gridDim.z;
     asm volatile("" ::"s"(gx), "s"(gy), "s"(gz), "s"(part), "s"(nsplit), "s"(BS), "s"(H), "s"(HG), "s"(sink),
                  "s"(out), "s"(out_dtype));
   }
-  const int lane = threadIdx.x;
+  const int lane = threadIdx.x & 63;
+  const int wq = NW > 1 ? __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) : 0;
   int64_t bs, item;
   xcd_row_item(BS, (int64_t)HG * 64, bs, item);
   const int hg = (int)((uint32_t)item >> 6), piece = (int)((uint32_t)item & 63u);
@@ -523,19 +530,24 @@ __global__ __launch_bounds__(64) void attn_merge_frag_kernel(const float* __rest
                       piece * 1024 + 16 * lane;  // split j: + j * HG * 64 KB
   const int64_t job = (int64_t)HG * 65536;
   const float* mlb = part + (bs * nsplit * (int64_t)H + min(head, H - 1)) * 2;  // split j: + j * H * 2
+  // this wave's run of splits [jb, je)
+  const int per = (nsplit + NW - 1) / NW;
+  const int jb = wq * per, je = min(nsplit, jb + per);
   float M = -SMLA_INF, L = 0.f, acc[8];
 #pragma unroll
   for (int e = 0; e < 8; e++) acc[e] = 0.f;
-  for (int j0 = 0; j0 < nsplit; j0 += CH) {
+  for (int j0 = jb; j0 < je; j0 += CH) {
     u32x4_t v[CH];
     f32x2_t ml[CH];
+    // split read by load u (past the run: its last split again)
+    auto src = [&](int u) -> int64_t { return min(j0 + u, je - 1); };
 #pragma unroll
-    for (int u = 0; u < CH; u++) v[u] = *(const u32x4_t*)(ob + min(j0 + u, nsplit - 1) * job);
+    for (int u = 0; u < CH; u++) v[u] = *(const u32x4_t*)(ob + src(u) * job);
 #pragma unroll
-    for (int u = 0; u < CH; u++) ml[u] = *(const f32x2_t*)(mlb + (int64_t)min(j0 + u, nsplit - 1) * H * 2);
+    for (int u = 0; u < CH; u++) ml[u] = *(const f32x2_t*)(mlb + src(u) * H * 2);
     float mc = M;
 #pragma unroll
-    for (int u = 0; u < CH; u++) mc = fmaxf(mc, j0 + u < nsplit ? ml[u][0] : -SMLA_INF);
+    for (int u = 0; u < CH; u++) mc = fmaxf(mc, j0 + u < je ? ml[u][0] : -SMLA_INF);
     if (mc > M && M > -SMLA_INF) {  // a later chunk raised the maximum (only past CH splits)
       const float r = __expf(M - mc);
       L *= r;
@@ -545,7 +557,7 @@ __global__ __launch_bounds__(64) void attn_merge_frag_kernel(const float* __rest
     M = mc;
 #pragma unroll
     for (int u = 0; u < CH; u++) {
-      const float m = j0 + u < nsplit ? ml[u][0] : -SMLA_INF;
+      const float m = j0 + u < je ? ml[u][0] : -SMLA_INF;
       const float w = m > -SMLA_INF ? __expf(m - M) : 0.f;
       L += w * ml[u][1];
 #pragma unroll
@@ -553,6 +565,29 @@ __global__ __launch_bounds__(64) void attn_merge_frag_kernel(const float* __rest
         acc[2 * e] += w * __uint_as_float(v[u][e] << 16);
         acc[2 * e + 1] += w * __uint_as_float(v[u][e] & 0xffff0000u);
       }
+    }
+  }
+  if constexpr (NW > 1) {
+    // waves 1.. hand their (M, L, acc) to wave 0, which folds them in wave order
+    __shared__ float xs[NW - 1][10][64];
+    if (wq > 0) {
+      xs[wq - 1][0][lane] = M;
+      xs[wq - 1][1][lane] = L;
+#pragma unroll
+      for (int e = 0; e < 8; e++) xs[wq - 1][2 + e][lane] = acc[e];
+    }
+    __syncthreads();
+    if (wq > 0) return;
+#pragma unroll
+    for (int w = 0; w < NW - 1; w++) {
+      const float m2 = xs[w][0][lane];
+      const float mn = fmaxf(M, m2);
+      const float r1 = M > -SMLA_INF ? __expf(M - mn) : 0.f;
+      const float r2 = m2 > -SMLA_INF ? __expf(m2 - mn) : 0.f;
+      L = L * r1 + xs[w][1][lane] * r2;
+#pragma unroll
+      for (int e = 0; e < 8; e++) acc[e] = acc[e] * r1 + xs[w][2 + e][lane] * r2;
+      M = mn;
     }
   }
   if (head >= H) return;
@@ -650,19 +685,29 @@ int launch_merge(const Plan& p, int64_t B, int64_t S, int64_t H, const float* si
   if (p.nsplit <= 1) return SMLA_OK;
   const bool part_bf16 = out_dtype == SMLA_BF16;
   if (part_bf16) {  // fragment-order partials: one workgroup per (query row, head group, 1 KB piece)
+    // waves per piece: one run of at most 32 splits each, up to 4 (more splits: 4 waves, several
+    // chunks); CH: the smallest of 8 / 16 / 24 / 32 that covers a wave's run
     const dim3 grid((unsigned)(B * S * p.hgroups * 64));
-    if (p.nsplit <= 8)
-      hipLaunchKernelGGL(attn_merge_frag_kernel<8>, grid, dim3(64), 0, stream, (const float*)ws, p.nsplit, B * S,
-                         (int)H, p.hgroups, sink, out, out_dtype);
-    else if (p.nsplit <= 16)
-      hipLaunchKernelGGL(attn_merge_frag_kernel<16>, grid, dim3(64), 0, stream, (const float*)ws, p.nsplit, B * S,
-                         (int)H, p.hgroups, sink, out, out_dtype);
-    else if (p.nsplit <= 24)
-      hipLaunchKernelGGL(attn_merge_frag_kernel<24>, grid, dim3(64), 0, stream, (const float*)ws, p.nsplit, B * S,
-                         (int)H, p.hgroups, sink, out, out_dtype);
-    else
-      hipLaunchKernelGGL(attn_merge_frag_kernel<32>, grid, dim3(64), 0, stream, (const float*)ws, p.nsplit, B * S,
-                         (int)H, p.hgroups, sink, out, out_dtype);
+    const int nw = p.nsplit <= 32 ? 1 : p.nsplit <= 64 ? 2 : 4;
+    const int run = (p.nsplit + nw - 1) / nw;
+    const int ch = run <= 8 ? 8 : run <= 16 ? 16 : run <= 24 ? 24 : 32;
+#define SMLA_MERGE_FRAG(C, W)                                                                                      \
+  hipLaunchKernelGGL((attn_merge_frag_kernel<C, W>), grid, dim3(64 * W), 0, stream, (const float*)ws, p.nsplit, \
+                     B * S, (int)H, p.hgroups, sink, out, out_dtype)
+#define SMLA_MERGE_FRAG_CH(W)        \
+  if (ch == 8) SMLA_MERGE_FRAG(8, W); \
+  else if (ch == 16) SMLA_MERGE_FRAG(16, W); \
+  else if (ch == 24) SMLA_MERGE_FRAG(24, W); \
+  else SMLA_MERGE_FRAG(32, W)
+    if (nw == 1) {
+      SMLA_MERGE_FRAG_CH(1);
+    } else if (nw == 2) {
+      SMLA_MERGE_FRAG_CH(2);
+    } else {
+      SMLA_MERGE_FRAG_CH(4);
+    }
+#undef SMLA_MERGE_FRAG_CH
+#undef SMLA_MERGE_FRAG
     SMLA_HIP_CHECK_LAUNCH();
     return SMLA_OK;
   }

@@ -138,11 +138,12 @@ def test_many_splits_merge(dev):
     _check_bf16(out, ref, "many splits")
 
 
-@pytest.mark.parametrize("nsplit", [2, 8, 9, 16, 17, 24, 25, 33])
+@pytest.mark.parametrize("nsplit", [2, 8, 9, 16, 17, 24, 25, 32, 33, 48, 64, 65, 97, 128, 129])
 def test_merge_split_counts(dev, nsplit):
-    """Split counts on both sides of the merge's chunk sizes (8, 16, 24 and 32 splits per pass,
-    more in several passes with an online rescale): 32-row splits of bf16 rows, a sink, two
-    64-head groups, bf16 partials in fragment order, against the oracle."""
+    """Split counts on both sides of the merge's chunk sizes (8, 16, 24 and 32 splits per load
+    chunk) and wave counts (one wave per piece up to 32 splits, two up to 64, four beyond, several
+    chunks per wave past 128): 32-row splits of bf16 rows, a sink, two 64-head groups, bf16
+    partials in fragment order, against the oracle."""
     from smla import ops
     g = torch.Generator().manual_seed(100 + nsplit)
     B, H, D, n = 2, 128, 576, 3000
