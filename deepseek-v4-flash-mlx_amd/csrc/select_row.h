@@ -93,12 +93,20 @@ __device__ inline void row_threshold(const float (&fv)[PER], int nloc, int base,
       before += c[i];
     }
   };
-  // rank of candidate c among the first `total` in the order (key asc, index asc)
+  // rank of candidate c among the first `total` in the order (key asc, index asc).  The slots
+  // from total up to the next multiple of 8 hold the largest pair (never below a candidate), so
+  // the loads go 8 at a time and their latencies overlap (a loop over `total` alone runs its
+  // remainder one dependent load at a time: ≈1.3 K cycles for the ≈10 candidates of a row)
   auto rank_of = [&](int c, int total) -> int {
     const uint64_t me = sm.cand_pair[c];
     int rank = 0;
-#pragma unroll 16
-    for (int j = 0; j < total; j++) rank += sm.cand_pair[j] < me;
+    for (int j0 = 0; j0 < total; j0 += 8) {
+      uint64_t v[8];
+#pragma unroll
+      for (int u = 0; u < 8; u++) v[u] = sm.cand_pair[j0 + u];
+#pragma unroll
+      for (int u = 0; u < 8; u++) rank += v[u] < me;
+    }
     return rank;
   };
 
@@ -202,6 +210,7 @@ __device__ inline void row_threshold(const float (&fv)[PER], int nloc, int base,
           slot++;
         }
       }
+      if (tid >= cb && tid < ((cb + 7) & ~7)) sm.cand_pair[tid] = ~0ull;  // rank_of's padding
       __syncthreads();
       if (tid < cb && rank_of(tid, cb) == need - 1) {
         const uint64_t pr = sm.cand_pair[tid];
