@@ -243,9 +243,8 @@ __global__ __launch_bounds__(256) void indexer_mfma_kernel(const void* __restric
   const int64_t b = batch_of(bs, S);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int64_t kb = chunk * KEYS + wave * KT;  // first key of this wave's tile
-  const int64_t nv = nvis ? (int64_t)nvis[bs] : N;
 
-  // the row of key kb + lane mod KT in its storage type, then the q row of head `lane`
+  // the row of key kb + lane mod KT in its storage type
   constexpr int KW = KDT == kFp4 ? 2 : KDT == SMLA_FP8_E4M3 ? 4 : (KDT == SMLA_BF16 ? 8 : 16);
   u32x4_t kr[KW];
   uint32_t ksb = 0;  // fp4: the row's two scale bytes
@@ -257,14 +256,48 @@ __global__ __launch_bounds__(256) void indexer_mfma_kernel(const void* __restric
     for (int v = 0; v < KW; v++) kr[v] = pk[v];
     if constexpr (KDT == kFp4) ksb = ((const uint16_t*)kbs)[row];
   }
+  // The row's q block (64 heads), its head weights and the key's scale come in once per workgroup
+  // through LDS: each wave loading the whole q block itself moved 8 KB per wave through L2 (16 MB
+  // per decode step), and the compiler placed each of those loads next to its first MFMA, a round
+  // trip per 16 bytes inside the chain; the weights and the scale were loaded after the chain.  q
+  // rows sit at a stride of QW + 1 16-byte words, so the 64 lanes' row reads spread over the banks.
   constexpr int QW = QDT == SMLA_BF16 ? 8 : 16;  // 16-byte words per head row
-  u32x4_t qw[QW];
+  constexpr int QV = 64 * QW / 256;              // words of the q block per thread
+  __shared__ u32x4_t q_s[64 * (QW + 1)];
+  __shared__ float w_s[64];
+  float ksc = 1.f;  // the scale of key kb + lane (lanes < KT write)
+  int nvl = 0;      // the row's visible count (nvis given)
   {
-    const u32x4_t* qp = (const u32x4_t*)((const uint8_t*)q + (bs * 64 + lane) * (int64_t)(QW * 16));
+    const u32x4_t* qp = (const u32x4_t*)((const uint8_t*)q + bs * 64 * (int64_t)(QW * 16));
+    u32x4_t qv[QV];
 #pragma unroll
-    for (int v = 0; v < QW; v++) qw[v] = qp[v];
+    for (int i = 0; i < QV; i++) qv[i] = qp[threadIdx.x + 256 * i];
+    const float wv = weights[bs * 64 + lane];
+    float ksc0 = 1.f;
+    if (kscale) ksc0 = kscale[b * N + min(kb + (lane & (KT - 1)), N - 1)];
+    if (nvis) nvl = nvis[bs];
+    // one wait for every load of the wave (the keys were requested first)
+#pragma unroll
+    for (int v = 0; v < KW; v++) asm volatile("" ::"v"(kr[v]));
+#pragma unroll
+    for (int i = 0; i < QV; i++) asm volatile("" ::"v"(qv[i]));
+    asm volatile("" ::"v"(wv), "v"(ksc0), "v"(nvl), "v"(ksb));
+    ksc = ksc0;
+#pragma unroll
+    for (int i = 0; i < QV; i++) {
+      const int k = threadIdx.x + 256 * i;  // word k: head k / QW, word k % QW
+      q_s[(k / QW) * (QW + 1) + k % QW] = qv[i];
+    }
+    if (wave == 0) w_s[lane] = wv;
   }
-  const float* wrow = weights + bs * 64;  // uniform: scalar loads
+  const int64_t nv = nvis ? (int64_t)nvl : N;
+  __syncthreads();
+  u32x4_t qw[QW];  // head `lane`'s q row, read whole before the chain starts
+#pragma unroll
+  for (int v = 0; v < QW; v++) qw[v] = q_s[lane * (QW + 1) + v];
+#pragma unroll
+  for (int v = 0; v < QW; v++) asm volatile("" : "+v"(qw[v]));
+  auto wrow = [&](int h) -> float { return w_s[h]; };
   float qf[DI];
 #pragma unroll
   for (int v = 0; v < QW; v++)
@@ -348,10 +381,10 @@ __global__ __launch_bounds__(256) void indexer_mfma_kernel(const void* __restric
 #pragma unroll
       for (int rr = 0; rr < 4; rr++) r[rr] = acc[R + rr] > 0.f ? acc[R + rr] : 0.f;
 #pragma unroll
-      for (int rr = 0; rr < 4; rr++) sum = __builtin_fmaf(wrow[8 * tt + rr], r[rr], sum);
+      for (int rr = 0; rr < 4; rr++) sum = __builtin_fmaf(wrow(8 * tt + rr), r[rr], sum);
       sum = __uint_as_float(__builtin_amdgcn_permlane32_swap(__float_as_uint(sum), __float_as_uint(sum), false, false)[0]);
 #pragma unroll
-      for (int rr = 0; rr < 4; rr++) sum = __builtin_fmaf(wrow[8 * tt + 4 + rr], r[rr], sum);
+      for (int rr = 0; rr < 4; rr++) sum = __builtin_fmaf(wrow(8 * tt + 4 + rr), r[rr], sum);
       sum = __uint_as_float(__builtin_amdgcn_permlane32_swap(__float_as_uint(sum), __float_as_uint(sum), false, false)[1]);
     }
   } else {
@@ -366,7 +399,7 @@ __global__ __launch_bounds__(256) void indexer_mfma_kernel(const void* __restric
 #pragma unroll
       for (int g = 0; g < 4; g++) {
 #pragma unroll
-        for (int rr = 0; rr < 4; rr++) sum = __builtin_fmaf(wrow[16 * bk + 4 * g + rr], r[rr], sum);
+        for (int rr = 0; rr < 4; rr++) sum = __builtin_fmaf(wrow(16 * bk + 4 * g + rr), r[rr], sum);
         const uint32_t y =
             __builtin_amdgcn_permlane16_swap(__float_as_uint(sum), __float_as_uint(sum), false, false)[g & 1];
         sum = __uint_as_float(__builtin_amdgcn_permlane32_swap(y, y, false, false)[g >> 1]);
@@ -374,7 +407,7 @@ __global__ __launch_bounds__(256) void indexer_mfma_kernel(const void* __restric
     }
   }
   const int64_t n = kb + lane;
-  if (lane < KT && n < N) scores[bs * N + n] = n < nv ? (kscale ? sum * kscale[b * N + n] : sum) : -SMLA_INF;
+  if (lane < KT && n < N) scores[bs * N + n] = n < nv ? (kscale ? sum * ksc : sum) : -SMLA_INF;
 }
 
 // Hi > 64: one thread per key, sequential over all heads (same arithmetic order)
