@@ -34,16 +34,20 @@ __global__ __launch_bounds__(NT) void topk_kernel(const float* scores, int64_t N
   const int64_t r = blockIdx.x;
   // N <= 65536 (PER * NT): every index of the row fits 32 bits
   const int base = tid * PER;
-  // this thread's PER contiguous scores: 16-byte loads when the run lies inside the row and is
-  // 16-byte aligned (rows of N floats: N % 4 == 0), element loads otherwise.  Issued first: the
-  // window-id stores below may alias the scores, so loads placed after them would wait for them.
+  // the row's visible count and this thread's PER contiguous scores, requested together (one
+  // round trip): 16-byte loads when rows are 16-byte aligned (N % 4 == 0; a quad past the row end
+  // reads the row's last quad, never visible), element loads otherwise.  No branch per thread
+  // between the loads and their first use, so no wait lands before the window-id stores (issued
+  // after the loads: they may alias the scores).
+  int nv = nvis ? nvis[r] : (int)N;
   float fv[PER];
   {
     const float* row = scores + r * N;
-    if (PER % 4 == 0 && (N & 3) == 0 && base + PER <= N) {
+    if (PER % 4 == 0 && (N & 3) == 0 && N >= 4) {  // uniform
 #pragma unroll
       for (int j = 0; j < PER; j += 4) {
-        const f32x4_t v4 = *(const f32x4_t*)(row + base + j);
+        const int64_t a = base + j < N ? base + j : N - 4;
+        const f32x4_t v4 = *(const f32x4_t*)(row + a);
         fv[j] = v4[0];
         fv[j + 1] = v4[1];
         fv[j + 2] = v4[2];
@@ -51,10 +55,9 @@ __global__ __launch_bounds__(NT) void topk_kernel(const float* scores, int64_t N
       }
     } else {
 #pragma unroll
-      for (int j = 0; j < PER; j++) fv[j] = base + j < N ? row[base + j] : 0.f;
+      for (int j = 0; j < PER; j++) fv[j] = row[base + j < N ? base + j : N - 1];
     }
   }
-  int nv = nvis ? nvis[r] : (int)N;
   if (nv > (int)N) nv = (int)N;
   if (nv < 0) nv = 0;
   int32_t* orow = out + r * out_stride;
