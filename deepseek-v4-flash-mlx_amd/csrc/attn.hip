@@ -70,11 +70,14 @@ __device__ inline float load_elem(const uint8_t* row, int64_t i) {
 // KT: row dtype; NC: 64-column chunks of a row held in registers; ONE: the whole row fits NC chunks
 // (D <= 64 NC), so the value columns are taken from the registers the dot used; otherwise the dot
 // runs over the row in blocks of NC chunks and the value columns (DV <= 1024) are loaded again.
+// Grid (B*S*H, nsplit): with nsplit > 1 workgroup (row, head, split j) takes the j-th of nsplit
+// equal runs of the index list and writes its partial state (m, l, unnormalised O) to `part`
+// ([row, head][split] records of (m, l), then of DV values) for attn_generic_merge_kernel.
 template <int KT, int NC, bool ONE>
 __global__ __launch_bounds__(kGenThreads) void attn_generic_kernel(
     const void* __restrict__ q, int q_dtype, RowSrc src, const float* __restrict__ sink,
     const int32_t* __restrict__ idx, int64_t T, int64_t S, int64_t H, int64_t D, int64_t DV, float scale,
-    void* __restrict__ out, int out_dtype) {
+    void* __restrict__ out, int out_dtype, float* __restrict__ part) {
   // rows per batch: two batches in flight per wave when the row fits NC chunks (ONE), one
   // otherwise; sized to the 128 registers of a 16-wave workgroup (3 rows per batch at NC = 9
   // spill, and measured no faster)
@@ -108,9 +111,12 @@ __global__ __launch_bounds__(kGenThreads) void attn_generic_kernel(
   float m_run = -SMLA_INF, l_run = 0.f;
 
   const int32_t* ids = idx + bs * T;
-  const int64_t per = (T + kGenWaves - 1) / kGenWaves;
-  const int64_t t_beg = wv * per;
-  const int64_t t_end = t_beg + per < T ? t_beg + per : T;
+  const int nsplit = gridDim.y, split = blockIdx.y;
+  const int64_t tps = (T + nsplit - 1) / nsplit;  // list entries per split
+  const int64_t t0 = split * tps, t1 = t0 + tps < T ? t0 + tps : T;
+  const int64_t per = (t1 - t0 + kGenWaves - 1) / kGenWaves;
+  const int64_t t_beg = t0 + wv * per;
+  const int64_t t_end = t_beg + per < t1 ? t_beg + per : t1;
   // online-softmax update of the wave's state with R rows: scores s (-inf: masked), values in
   // x(k, c) for the NA value chunks
   auto update = [&](const float (&s)[R], auto&& x) {
@@ -279,6 +285,22 @@ __global__ __launch_bounds__(kGenThreads) void attn_generic_kernel(
   float den = 0.f;
 #pragma unroll
   for (int w = 0; w < kGenWaves; w++) den += (sm[w] > -SMLA_INF ? __expf(sm[w] - M) : 0.f) * sl[w];
+  const int64_t rh = bs * H + h;
+  if (nsplit > 1) {  // partial state: (M, l) and the unnormalised O of this split
+    const int64_t rec = rh * nsplit + split;
+    if (tid == 0) {
+      part[rec * 2] = M;
+      part[rec * 2 + 1] = den;
+    }
+    float* po = part + (int64_t)gridDim.x * nsplit * 2 + rec * DV;
+    for (int64_t d = tid; d < DV; d += kGenThreads) {
+      float o = 0.f;
+#pragma unroll
+      for (int w = 0; w < HW; w++) o += buf[w * DV + d];
+      po[d] = o;
+    }
+    return;
+  }
   const bool empty = !(M > -SMLA_INF);
   const float snk = sink ? sink[h] : -SMLA_INF;
   if (!empty) den += __expf(snk - M);
@@ -286,49 +308,84 @@ __global__ __launch_bounds__(kGenThreads) void attn_generic_kernel(
     float o = 0.f;
 #pragma unroll
     for (int w = 0; w < HW; w++) o += buf[w * DV + d];
-    store_from_f32(out, (bs * H + h) * DV + d, out_dtype, empty ? __builtin_nanf("") : o / den);
+    store_from_f32(out, rh * DV + d, out_dtype, empty ? __builtin_nanf("") : o / den);
+  }
+}
+
+// Merge of the generic kernel's split states: one workgroup per (query row, head); the weights
+// w_j = exp(m_j - M) go through LDS, then thread t sums columns t, t + 256, .. over the splits in
+// order: O = sum w_j O_j / (sum w_j l_j + exp(sink - M)), NaN when no split saw a valid row.
+constexpr int kGenMergeMax = 64;  // splits of the generic kernel at most
+__global__ __launch_bounds__(256) void attn_generic_merge_kernel(const float* __restrict__ part, int nsplit,
+                                                                 int64_t H, int64_t DV,
+                                                                 const float* __restrict__ sink,
+                                                                 void* __restrict__ out, int out_dtype) {
+  __shared__ float w_s[kGenMergeMax];
+  const int64_t rh = blockIdx.x;
+  const int h = (int)(rh % H);
+  const float* ml = part + rh * nsplit * 2;
+  float M = -SMLA_INF;
+  for (int j = 0; j < nsplit; j++) M = fmaxf(M, ml[2 * j]);
+  const bool empty = !(M > -SMLA_INF);
+  float L = 0.f;
+  for (int j = 0; j < nsplit; j++) {
+    const float w = ml[2 * j] > -SMLA_INF ? __expf(ml[2 * j] - M) : 0.f;
+    L += w * ml[2 * j + 1];
+    if (threadIdx.x == j) w_s[j] = w;
+  }
+  if (!empty && sink) L += __expf(sink[h] - M);
+  __syncthreads();
+  const float* ob = part + (int64_t)gridDim.x * nsplit * 2 + rh * nsplit * DV;
+  for (int64_t d = threadIdx.x; d < DV; d += 256) {
+    float o = 0.f;
+    for (int j = 0; j < nsplit; j++) o = fmaf(w_s[j], ob[j * DV + d], o);
+    store_from_f32(out, rh * DV + d, out_dtype, empty ? __builtin_nanf("") : o / L);
   }
 }
 
 template <int KT>
 void launch_generic_kt(int64_t D, dim3 grid, size_t lds, hipStream_t st, const void* q, int q_dtype, RowSrc src,
                        const float* sink, const int32_t* idx, int64_t T, int64_t S, int64_t H, int64_t DV,
-                       float scale, void* out, int out_dtype) {
+                       float scale, void* out, int out_dtype, float* part) {
   const int64_t nch = (D + 63) / 64;
   if (nch <= 4)
     hipLaunchKernelGGL((attn_generic_kernel<KT, 4, true>), grid, dim3(kGenThreads), lds, st, q, q_dtype, src, sink,
-                       idx, T, S, H, D, DV, scale, out, out_dtype);
+                       idx, T, S, H, D, DV, scale, out, out_dtype, part);
   else if (nch <= 9)
     hipLaunchKernelGGL((attn_generic_kernel<KT, 9, true>), grid, dim3(kGenThreads), lds, st, q, q_dtype, src, sink,
-                       idx, T, S, H, D, DV, scale, out, out_dtype);
+                       idx, T, S, H, D, DV, scale, out, out_dtype, part);
   else if (nch <= 16)
     hipLaunchKernelGGL((attn_generic_kernel<KT, 16, true>), grid, dim3(kGenThreads), lds, st, q, q_dtype, src, sink,
-                       idx, T, S, H, D, DV, scale, out, out_dtype);
+                       idx, T, S, H, D, DV, scale, out, out_dtype, part);
   else
     hipLaunchKernelGGL((attn_generic_kernel<KT, 16, false>), grid, dim3(kGenThreads), lds, st, q, q_dtype, src, sink,
-                       idx, T, S, H, D, DV, scale, out, out_dtype);
+                       idx, T, S, H, D, DV, scale, out, out_dtype, part);
 }
 
-// the generic kernel over B*S*H workgroups; LDS: the query row and half the waves' partial outputs
+// the generic kernel over B*S*H x nsplit workgroups (nsplit > 1: partial states into `part`);
+// LDS: the query row and half the waves' partial outputs
 int launch_generic(const void* q, int q_dtype, RowSrc src, int kv_dtype, const float* sink, const int32_t* idx,
                    int64_t T, int64_t B, int64_t S, int64_t H, int64_t D, int64_t DV, float scale, void* out,
-                   int out_dtype, hipStream_t st) {
+                   int out_dtype, int nsplit, float* part, hipStream_t st) {
   const size_t lds = (size_t)D * 4 + (size_t)(kGenWaves / 2) * DV * 4;
   if (lds > 64 * 1024 || B * S * H > 0xffffffffll) return SMLA_E_UNSUPPORTED;
-  const dim3 grid((unsigned)(B * S * H));
+  const dim3 grid((unsigned)(B * S * H), (unsigned)nsplit);
   switch (kv_dtype) {
     case SMLA_F32:
-      launch_generic_kt<SMLA_F32>(D, grid, lds, st, q, q_dtype, src, sink, idx, T, S, H, DV, scale, out, out_dtype);
+      launch_generic_kt<SMLA_F32>(D, grid, lds, st, q, q_dtype, src, sink, idx, T, S, H, DV, scale, out, out_dtype,
+                                  part);
       break;
     case SMLA_BF16:
-      launch_generic_kt<SMLA_BF16>(D, grid, lds, st, q, q_dtype, src, sink, idx, T, S, H, DV, scale, out, out_dtype);
+      launch_generic_kt<SMLA_BF16>(D, grid, lds, st, q, q_dtype, src, sink, idx, T, S, H, DV, scale, out, out_dtype,
+                                   part);
       break;
     case SMLA_F16:
-      launch_generic_kt<SMLA_F16>(D, grid, lds, st, q, q_dtype, src, sink, idx, T, S, H, DV, scale, out, out_dtype);
+      launch_generic_kt<SMLA_F16>(D, grid, lds, st, q, q_dtype, src, sink, idx, T, S, H, DV, scale, out, out_dtype,
+                                  part);
       break;
     default:
       launch_generic_kt<SMLA_FP8_E4M3>(D, grid, lds, st, q, q_dtype, src, sink, idx, T, S, H, DV, scale, out,
-                                      out_dtype);
+                                      out_dtype, part);
   }
   SMLA_HIP_CHECK_LAUNCH();
   return SMLA_OK;
@@ -626,12 +683,24 @@ struct Plan {
   int hgroups;
 };
 
+// splits of the vector-ALU kernel: enough (row, head, split) workgroups for about one per compute
+// unit, at least 32 list entries per split, at most kGenMergeMax
+int generic_splits(int64_t B, int64_t S, int64_t H, int64_t T) {
+  const int64_t rows = B * S * H, cus = smla_num_cus();
+  int64_t ns = rows >= cus ? 1 : (cus + rows - 1) / rows;
+  ns = std::min<int64_t>(ns, std::max<int64_t>(1, T / 32));
+  return (int)std::min<int64_t>(ns, kGenMergeMax);
+}
+
 Plan make_plan(int64_t B, int64_t S, int64_t H, int64_t D, int64_t DV, int64_t T, int q_dtype, int kv_dtype,
                int64_t rps_req) {
   Plan p{};
   p.mfma = q_dtype == SMLA_BF16 && (kv_dtype == SMLA_BF16 || kv_dtype == SMLA_FP8_E4M3) &&
            H % 16 == 0 && DV == 512 && (D == 576 || D == 512) && T > 0 && T < (1ll << 30);
-  if (!p.mfma) return p;
+  if (!p.mfma) {
+    p.nsplit = generic_splits(B, S, H, T);
+    return p;
+  }
   p.hgroups = (int)((H + 63) / 64);
   const int64_t rows = B * S * p.hgroups;
   const int64_t tiles = (T + kTileRows - 1) / kTileRows;
@@ -654,15 +723,21 @@ Plan make_plan(int64_t B, int64_t S, int64_t H, int64_t D, int64_t DV, int64_t T
   if (per > smla_attn::kDecodeV6MaxRows / kTileRows) per = smla_attn::kDecodeV6MaxRows / kTileRows;
   p.rows_per_split = (int)(per * kTileRows);
   p.nsplit = (int)((tiles + per - 1) / per);
-  if (p.nsplit > kMaxSplits) p.mfma = false;  // beyond the merge kernel's capacity: generic kernel
+  if (p.nsplit > kMaxSplits) {  // beyond the merge kernel's capacity: generic kernel
+    p.mfma = false;
+    p.nsplit = generic_splits(B, S, H, T);
+  }
   return p;
 }
 
-// bytes of split partial states for a plan: (m, l) fp32 per (query row, head, split), then the
-// partial O: bf16 blocks of 64 heads x 512 in fragment order per (query row, split, head group)
-// (bf16 output), or fp32 rows per (query row, split, head)
+// bytes of split partial states for a plan.  The MFMA kernel: (m, l) fp32 per (query row, head,
+// split), then the partial O: bf16 blocks of 64 heads x 512 in fragment order per (query row,
+// split, head group) (bf16 output), or fp32 rows per (query row, split, head).  The vector-ALU
+// kernel: (m, l) and DV fp32 values per (query row, head, split).
 size_t plan_workspace(const Plan& p, int64_t B, int64_t S, int64_t H, int64_t DV, int out_dtype) {
-  if (!p.mfma || p.nsplit <= 1) return 0;
+  if (p.nsplit <= 1) return 0;
+  if (!p.mfma)  // the vector-ALU kernel's split states: (m, l) then DV fp32 values per record
+    return (size_t)(B * S * H) * (size_t)p.nsplit * (size_t)(2 + DV) * sizeof(float);
   const size_t recs = (size_t)(B * S) * (size_t)p.nsplit;
   const size_t ml = recs * (size_t)H * 2 * sizeof(float);
   if (out_dtype == SMLA_BF16) return ml + recs * (size_t)p.hgroups * 65536;
@@ -780,9 +855,17 @@ static int attn_launch(const Plan& p, int phases, const void* q, int q_dtype, Ro
                      int64_t D, int64_t DV, float scale, void* out, int out_dtype, void* ws, hipStream_t st,
                      smla_attn::SelectRows sr = smla_attn::SelectRows{}) {
   if (!p.mfma) {
-    if (!(phases & SMLA_ATTN_SPLIT)) return SMLA_OK;
-    return launch_generic(q, q_dtype, src, kv_dtype, attn_sink, topk_idxs, T, B, S, H, D, DV, scale, out, out_dtype,
-                          st);
+    if (phases & SMLA_ATTN_SPLIT) {
+      const int rc = launch_generic(q, q_dtype, src, kv_dtype, attn_sink, topk_idxs, T, B, S, H, D, DV, scale, out,
+                                    out_dtype, p.nsplit, (float*)ws, st);
+      if (rc != SMLA_OK) return rc;
+    }
+    if ((phases & SMLA_ATTN_MERGE) && p.nsplit > 1) {
+      hipLaunchKernelGGL(attn_generic_merge_kernel, dim3((unsigned)(B * S * H)), dim3(256), 0, st, (const float*)ws,
+                         p.nsplit, H, DV, attn_sink, out, out_dtype);
+      SMLA_HIP_CHECK_LAUNCH();
+    }
+    return SMLA_OK;
   }
   const bool fp8 = kv_dtype == SMLA_FP8_E4M3;
   const int64_t row_bytes = fp8 ? D : 2 * D;

@@ -176,6 +176,46 @@ def test_all_masked_rows_are_nan(dev):
     assert torch.isnan(out32[1]).all() and not torch.isnan(out32[0]).any()
 
 
+@pytest.mark.parametrize("S,H,T,masked", [(1, 1, 4000, "none"), (2, 4, 300, "first"), (1, 3, 200, "all"),
+                                           (1, 16, 512, "scattered")])
+def test_generic_split_states(dev, S, H, T, masked):
+    """The vector-ALU kernel over list splits (up to 64: about one workgroup per compute unit for
+    few (row, head) pairs) and its merge: fp32 rows against the oracle at 1e-5 with a sink, splits
+    whose entries are all masked (weight zero), rows with no valid entry (NaN), and the split and
+    merge phases run as separate calls equal, bit for bit, to the call that runs both."""
+    from smla import _lib, ops
+    g = torch.Generator().manual_seed(T + H)
+    D, dv, n = 576, 512, 900
+    announce(f"generic split states S={S} H={H} T={T} masked={masked}")
+    q = torch.randn(1, S, H, D, generator=g)
+    kv = torch.randn(1, n, D, generator=g)
+    idx = torch.randint(0, n, (1, S, T), generator=g, dtype=torch.int32)
+    if masked == "first":
+        idx[..., : T // 2] = -1        # the first splits see no valid entry
+    elif masked == "all":
+        idx[...] = -1
+    elif masked == "scattered":
+        idx[..., ::3] = -1
+    sink = torch.randn(H, generator=g)
+    scale = D ** -0.5
+    ns, _, wsb = ops.attn_plan(1, S, H, D, dv, T, torch.float32, torch.float32, torch.float32)
+    assert ns == 0 and wsb > 0  # the vector-ALU kernel, with split states in the workspace
+    qd, kvd, idxd, sinkd = q.to(dev), kv.to(dev), idx.to(dev), sink.to(dev)
+    out = ops.sparse_attn_ex(qd, kvd, None, None, None, sinkd, idxd, scale, dv)
+    ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
+    o2 = torch.empty_like(out)
+    ops.sparse_attn_ex(qd, kvd, None, None, None, sinkd, idxd, scale, dv, phases=_lib.ATTN_SPLIT, out=o2, workspace=ws)
+    ops.sparse_attn_ex(qd, kvd, None, None, None, sinkd, idxd, scale, dv, phases=_lib.ATTN_MERGE, out=o2, workspace=ws)
+    torch.cuda.synchronize()
+    assert torch.equal(out, o2) or (torch.isnan(out).all() and torch.isnan(o2).all())
+    out = out.cpu()[0]
+    if masked == "all":
+        assert torch.isnan(out).all()
+        return
+    ref = osa.sparse_attn(q[0], kv[0], sink, idx[0], scale, dv=dv)
+    assert (out - ref).abs().max().item() <= F32_ABS
+
+
 @pytest.mark.parametrize("B,T,n,sharp,H,D,pow2", [(1, 64, 200, 1.0, 64, 576, True), (3, 700, 2000, 40.0, 64, 576, True),
                                                 (2, 2048, 2048, 1.0, 64, 576, True), (2, 333, 900, 10.0, 48, 576, True),
                                                 (2, 300, 500, 5.0, 64, 512, True), (2, 700, 1500, 10.0, 64, 576, False)])
