@@ -101,8 +101,9 @@ int smla_api_version(void);
  * most 1024 splits (index lists up to 8192 rows per split) run the split-K MFMA kernel plus the
  * merge, in launches of at most 65528 query rows (whole sequences while one fits, else pieces of
  * one); every other call (F32 / F16 operands, other H / D / DV, more splits) runs the vector-ALU
- * kernel, one workgroup per (query row, head), with the same results to the tolerance of its
- * dtype (both kernels are tested against the oracle for F32, BF16 and FP8 rows).
+ * kernel, one workgroup per (query row, head) -- with fewer of those than compute units, per run
+ * of the list (up to 64 runs and a merge) -- with the same results to the tolerance of its dtype
+ * (both kernels are tested against the oracle for F32, BF16 and FP8 rows).
  *
  * workspace: smla_sparse_attn_workspace() bytes (split-K partial states), may be 0.
  */
@@ -123,8 +124,9 @@ size_t smla_sparse_attn_workspace(int64_t B, int64_t S, int64_t H, int64_t D, in
  * device's compute-unit count.  rows_per_split: index-list rows per split requested (a multiple of
  * 32), or 0 for the default plan (enough splits to give every compute unit a workgroup, at least
  * two 32-row tiles each).  Writes the number of splits (0 when the vector-ALU kernel runs: F32 /
- * F16 operands or shapes the MFMA kernel does not take; it does not split) and the rows per split,
- * either pointer may be NULL; returns the workspace bytes that plan needs for out_dtype (0: none). */
+ * F16 operands or shapes the MFMA kernel does not take; its own list runs are not reported) and
+ * the rows per split, either pointer may be NULL; returns the workspace bytes that plan needs for
+ * out_dtype (0: none; for the vector-ALU kernel, its runs' states). */
 size_t smla_sparse_attn_plan(int64_t B, int64_t S, int64_t H, int64_t D, int64_t DV, int64_t T,
                              int q_dtype, int kv_dtype, int out_dtype, int64_t rows_per_split,
                              int64_t* nsplit, int64_t* rows_per_split_out);
