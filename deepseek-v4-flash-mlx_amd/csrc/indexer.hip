@@ -22,7 +22,9 @@ namespace {
 
 constexpr int kMaxQ = 64 * 128;  // Hi * Di fp32 in LDS (at most 32 KiB)
 constexpr int kKeys = 64;        // keys per workgroup (one per lane)
-constexpr int kHG = 16;          // heads per wave
+// heads per wave of indexer_kernel: 16, or 4 / 8 for few heads, so a 64-key workgroup still
+// spreads its dot products over four waves (at most 4 waves per workgroup)
+inline int heads_per_wave(int64_t Hi) { return Hi <= 16 ? 4 : (Hi <= 32 ? 8 : 16); }
 constexpr int kFp4 = 16;         // key type tag: packed e2m1 codes + one ue8m0 scale byte per 32
 
 // Two code words of the gfx950 scaled fp4 converter, lanes of byte SEL: elements 2 SEL, 2 SEL + 1.
@@ -56,7 +58,8 @@ __device__ inline void fp4_block16(uint32_t w0, uint32_t w1, uint32_t sb, float*
 }
 
 // One workgroup = 64 keys x all heads.  Wave w computes r_h = ReLU(dot_h) for heads
-// 16w .. 16w+15 (lane = key, key row in VGPRs, q rows read from LDS as wave-wide broadcasts);
+// hpw w .. hpw w + hpw - 1 (hpw = heads_per_wave: 4, 8 or 16; lane = key, key row in VGPRs, q rows
+// read from LDS as wave-wide broadcasts);
 // the r_h go through LDS and wave 0 runs the per-key chain over h = 0..Hi-1.  Each dot product is
 // the same sequential fma chain over d as the oracle's, so scores are bit-identical.
 template <int DI, int KDT, int QDT>
@@ -75,6 +78,7 @@ __global__ __launch_bounds__(256) void indexer_kernel(const void* __restrict__ q
   const int64_t b = batch_of(bs, S);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int nwaves = blockDim.x >> 6;
+  const int kHG = (Hi + nwaves - 1) / nwaves;  // heads per wave
   const int64_t n = chunk * kKeys + lane;
   const int64_t nv = nvis ? (int64_t)nvis[bs] : N;
   const bool live = n < N && n < nv;
@@ -466,7 +470,8 @@ int launch_k(const void* q, int q_dtype, const void* keys, const uint8_t* kbs, c
 #undef SMLA_IDX_MFMA
   } else if (Hi <= 64) {
     dim3 grid((unsigned)((N + kKeys - 1) / kKeys), (unsigned)(B * S));
-    const int threads = (int)(((Hi + kHG - 1) / kHG) * 64);
+    const int hpw = heads_per_wave(Hi);
+    const int threads = (int)(((Hi + hpw - 1) / hpw) * 64);
     if (q_dtype == SMLA_BF16)
       hipLaunchKernelGGL((indexer_kernel<DI, KDT, SMLA_BF16>), grid, dim3(threads), 0, st, q, q_dtype, keys, kbs,
                          kscale, w, nvis, S, (int)Hi, N, scores);
