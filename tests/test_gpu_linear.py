@@ -62,8 +62,6 @@ def _check_linear(got, x, w, G, out_dtype):
 @pytest.mark.parametrize("operands", [torch.bfloat16, torch.float32])
 def test_linear_vs_fp64(dev, T, G, N, K, out_dtype, operands):
     from smla import ops
-    if operands == torch.float32 and T <= 32 and K % 512 == 0 and N % 16 == 0 and T * N * K > 1 << 24:
-        pytest.skip("fp32 operands at a decode shape: covered by the smaller cases")
     announce(f"linear T={T} G={G} N={N} K={K} out={out_dtype} operands={operands}")
     g = torch.Generator().manual_seed(T * 7 + G + N + K)
     x = torch.randn(T, G * K, generator=g).to(operands)
