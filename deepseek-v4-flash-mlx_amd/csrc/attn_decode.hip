@@ -21,8 +21,9 @@
 // the split load row 0, so every LDS value an MFMA reads is finite.
 //
 // Output: final rows (one split) or (m, l, O) partial states in the layout the merge kernels read.
-// bf16 partials leave the value waves' registers in MFMA fragment order (attn_merge_frag_kernel):
-// no staging through LDS and no barrier after the tile loop.
+// bf16 partials leave the value waves' registers in MFMA fragment order (attn_merge_frag_kernel)
+// with nontemporal stores: no staging through LDS, no barrier after the tile loop, and no dirty L2
+// lines for the kernel's end to write back.
 #include "attn_common.h"
 #include "select_row.h"
 
