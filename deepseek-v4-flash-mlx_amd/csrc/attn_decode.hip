@@ -479,17 +479,12 @@ __global__ __launch_bounds__(768) void attn_decode_kernel(
         : (uint8_t*)(part + (int64_t)gridDim.y * H * nsplit * 2) + ((bs * nsplit + split) * (int64_t)H + hb) * row_bytes;
     const int chunks_per_row = row_bytes / 16;
     const int nchunks = nh * chunks_per_row;
-    if (nsplit == 1) {  // final rows are not read back by this launch
-      for (int i = tid; i < nchunks; i += G::NW * 64) {
-        const int hr = i / chunks_per_row, ch = i - hr * chunks_per_row;
-        __builtin_nontemporal_store(*(const lds_u32x4_t*)(lds + hr * srow_bytes + ch * 16),
-                                    (u32x4_t*)(dst + (int64_t)i * 16));
-      }
-    } else {
-      for (int i = tid; i < nchunks; i += G::NW * 64) {
-        const int hr = i / chunks_per_row, ch = i - hr * chunks_per_row;
-        *(u32x4_t*)(dst + (int64_t)i * 16) = *(const lds_u32x4_t*)(lds + hr * srow_bytes + ch * 16);
-      }
+    // nontemporal: neither final rows nor partial records are read back by this launch, and
+    // streamed out they leave no dirty L2 lines for the kernel's end to write back
+    for (int i = tid; i < nchunks; i += G::NW * 64) {
+      const int hr = i / chunks_per_row, ch = i - hr * chunks_per_row;
+      __builtin_nontemporal_store(*(const lds_u32x4_t*)(lds + hr * srow_bytes + ch * 16),
+                                  (u32x4_t*)(dst + (int64_t)i * 16));
     }
   };
 
