@@ -207,9 +207,9 @@ __global__ __launch_bounds__(256) void gemm_kernel(const uint8_t* __restrict__ x
         if (t < T) {
           const int64_t o = (int64_t)t * ldy + (int64_t)g * N + n;
           if constexpr (YDT == SMLA_BF16)
-            ((uint16_t*)y)[o] = bf16_rne(acc[mb][nb][r]);
+            __builtin_nontemporal_store((uint16_t)bf16_rne(acc[mb][nb][r]), (uint16_t*)y + o);
           else
-            ((float*)y)[o] = acc[mb][nb][r];
+            __builtin_nontemporal_store(acc[mb][nb][r], (float*)y + o);
         }
       }
     }
@@ -332,7 +332,9 @@ __global__ __launch_bounds__(DmaTile<BT>::NW * 64) void gemm_dma_kernel(const ui
   }
 
   // accumulator r of block (mb, nb): token WROWS wm + 32 mb + 8 (r / 4) + 4 (lane / 32) + r % 4,
-  // output 64 wn + 32 nb + lane % 32
+  // output 64 wn + 32 nb + lane % 32.  Nontemporal stores (the output is not read back by this
+  // launch; 64-byte runs per half wave): the grouped 4096 x 8 x 1024 x 4096 product 287 -> 275 us,
+  // the other prompt-size shapes equal.
 #pragma unroll
   for (int mb = 0; mb < L::MB; mb++)
 #pragma unroll
@@ -345,9 +347,9 @@ __global__ __launch_bounds__(DmaTile<BT>::NW * 64) void gemm_dma_kernel(const ui
         if (t < T) {
           const int64_t o = (int64_t)t * ldy + (int64_t)g * N + n;
           if constexpr (YDT == SMLA_BF16)
-            ((uint16_t*)y)[o] = bf16_rne(acc[mb][nb][r]);
+            __builtin_nontemporal_store((uint16_t)bf16_rne(acc[mb][nb][r]), (uint16_t*)y + o);
           else
-            ((float*)y)[o] = acc[mb][nb][r];
+            __builtin_nontemporal_store(acc[mb][nb][r], (float*)y + o);
         }
       }
     }
